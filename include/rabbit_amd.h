@@ -1,0 +1,212 @@
+/*
+ * rabbit_amd.h -- C ABI of the MI355X (gfx950) routed-expert dequant-matmul library.
+ *
+ * Drop-in boundary for ferrumox/rabbit's routed-expert path: the free functions of
+ * src/kernels.rs and src/quant.rs, the routers of src/qwen38/moe.rs and src/glm52/moe.rs,
+ * glm52::moe::apply_single_expert, the ExpertCache lookup (src/expert_cache.rs) and the per-family
+ * MoE layer (src/qwen38/generate.rs moe_forward, src/glm52/moe.rs moe). Each declaration cites
+ * the reference interface it replaces. Citations are path:line inside the reference repository.
+ *
+ * Conventions (mirroring the reference's slice conventions):
+ *  - Plain pointers and sizes; no C++ or torch types cross this boundary.
+ *  - Functions without a suffix take HOST buffers borrowed for the call and return after the
+ *    result is in the caller's buffer (the reference's &[f32] / &mut [f32] semantics).
+ *    Functions with the `_d` suffix take DEVICE pointers, enqueue on the context's stream and
+ *    return immediately; rbt_sync() waits.
+ *  - matmul-style calls overwrite y; rbt_apply_single_expert accumulates into out;
+ *    rbt_moe_forward overwrites out (the reference's moe zeroes out first).
+ *  - Nothing aborts or unwinds across the boundary: every call returns RBT_OK (0) or a negative
+ *    RBT_E_* status where the reference would panic or return Err; rbt_last_error() describes it.
+ *  - A context is not thread-safe (the reference's &mut ExpertCache); use one per host thread.
+ *  - Results are deterministic for fixed inputs (no float atomics).
+ */
+#ifndef RABBIT_AMD_H
+#define RABBIT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------------------- */
+#define RBT_OK 0
+#define RBT_E_INVALID (-1)      /* null pointer, zero/oversized dimension, bad enum */
+#define RBT_E_SHAPE (-2)        /* byte length does not match the shape (ModelError::ShapeMismatch,
+                                   expert_cache.rs:1245-1256) */
+#define RBT_E_HIP (-3)          /* HIP runtime error */
+#define RBT_E_NOT_RESIDENT (-4) /* routed expert missing from the pool (ExpertCache::get -> None) */
+#define RBT_E_NOMEM (-5)        /* device allocation failed */
+#define RBT_E_UNSUPPORTED (-6)  /* valid in the reference but not offered on this path */
+
+typedef struct rbt_ctx rbt_ctx;
+
+/* ---- weight containers: QT / QTKind (quant.rs:77-110) --------------------------------------- */
+typedef enum {
+    RBT_QT_F32 = 0,        /* QTKind::F32:       data f32[rows*cols] */
+    RBT_QT_I4_GROUPED = 1, /* QTKind::I4Grouped: data u8[rows*ceil(cols/2)] (value+8, low nibble
+                              first), scale f32[rows*ceil(cols/group_size)] (quant.rs:92-100) */
+    RBT_QT_MXFP4 = 2       /* QTKind::MxFp4:     data u8[rows*ceil(cols/2)] E2M1 (low nibble first),
+                              scale u8[rows*ceil(cols/32)] E8M0 (quant.rs:101-109) */
+} rbt_qt_kind;
+
+typedef struct {
+    size_t rows, cols;
+    int32_t kind;          /* rbt_qt_kind */
+    const void *data;
+    const void *scale;     /* NULL for RBT_QT_F32 */
+    size_t group_size;     /* RBT_QT_I4_GROUPED only */
+} rbt_qt;
+
+/* ExpertSlot + GateUp (expert_cache.rs:640-650). fused = 0: gate [i, d] and up [i, d];
+ * fused = 1: gate_up [2i, d] (gate rows first). down is [d, i]. */
+typedef struct {
+    uint32_t eid;
+    int32_t fused;
+    rbt_qt gate, up, gate_up, down;
+} rbt_expert_slot;
+
+/* ---- context ------------------------------------------------------------------------------- */
+/* Creates a context on HIP device `device`: its own stream (default priority), scratch, and the
+ * HBM-resident expert pool that replaces ExpertCache's storage (expert_cache.rs:1-52). */
+int rbt_init(rbt_ctx **out, int device);
+void rbt_destroy(rbt_ctx *ctx);
+const char *rbt_last_error(const rbt_ctx *ctx);
+int rbt_sync(rbt_ctx *ctx);
+/* The context's hipStream_t, for callers that enqueue their own work around the `_d` calls. */
+void *rbt_stream(rbt_ctx *ctx);
+/* Library version string. */
+const char *rbt_version(void);
+
+/* ---- quant.rs ------------------------------------------------------------------------------- */
+/* QT::resident_bytes (quant.rs:214-228). */
+size_t rbt_qt_resident_bytes(const rbt_qt *w);
+/* QT::row_f32 (quant.rs:280-341) for rows [row0, row0+nrows): out f32[nrows, cols], the dequantized
+ * weights bit-for-bit (e2m1_decode quant.rs:353, e8m0_decode quant.rs:391). */
+int rbt_dequant_rows(rbt_ctx *ctx, const rbt_qt *w, size_t row0, size_t nrows, float *out);
+int rbt_dequant_rows_d(rbt_ctx *ctx, const rbt_qt *w, size_t row0, size_t nrows, float *out);
+
+/* ---- kernels.rs: y[S,O] = x[S,I] . W^T ---------------------------------------------------- */
+/* matmul (kernels.rs:113), f32 weights W[O,I]. */
+int rbt_matmul(rbt_ctx *ctx, float *y, const float *x, const float *w, size_t s, size_t i, size_t o);
+int rbt_matmul_d(rbt_ctx *ctx, float *y, const float *x, const float *w, size_t s, size_t i, size_t o);
+/* matmul_mxfp4 (kernels.rs:233). */
+int rbt_matmul_mxfp4(rbt_ctx *ctx, float *y, const float *x, const uint8_t *data,
+                     const uint8_t *block_scale, size_t s, size_t i, size_t o);
+int rbt_matmul_mxfp4_d(rbt_ctx *ctx, float *y, const float *x, const uint8_t *data,
+                       const uint8_t *block_scale, size_t s, size_t i, size_t o);
+/* matmul_i4_grouped (kernels.rs:276). */
+int rbt_matmul_i4_grouped(rbt_ctx *ctx, float *y, const float *x, const uint8_t *q4, const float *scale,
+                          size_t group_size, size_t s, size_t i, size_t o);
+int rbt_matmul_i4_grouped_d(rbt_ctx *ctx, float *y, const float *x, const uint8_t *q4, const float *scale,
+                            size_t group_size, size_t s, size_t i, size_t o);
+/* matmul_qt (kernels.rs:1104): dispatch on w->kind (F32, I4Grouped, MxFp4). The rbt_qt's
+ * pointers are host memory for rbt_matmul_qt and device memory for rbt_matmul_qt_d. */
+int rbt_matmul_qt(rbt_ctx *ctx, float *y, const float *x, const rbt_qt *w, size_t s);
+int rbt_matmul_qt_d(rbt_ctx *ctx, float *y, const float *x, const rbt_qt *w, size_t s);
+
+/* ---- routers -------------------------------------------------------------------------------- */
+/* qwen38::moe::route (qwen38/moe.rs:41-76) for s tokens: logits f32[s, n] -> ids i32[s, k'],
+ * w f32[s, k'] with k' = min(k, n): top-k by logit (ties -> lower id), softmax over the winners,
+ * in descending order. */
+int rbt_route_softmax_topk(rbt_ctx *ctx, const float *logits, size_t s, size_t n, size_t k,
+                           int32_t *ids, float *w);
+int rbt_route_softmax_topk_d(rbt_ctx *ctx, const float *logits, size_t s, size_t n, size_t k,
+                             int32_t *ids, float *w);
+/* glm52::moe::route (glm52/moe.rs:131-260) for s tokens given router logits: p = sigmoid(logit),
+ * select by p + bias (bias may be NULL), lowest id on ties, weight = p, then optional norm_topk
+ * (w /= sum + 1e-20) and routed_scale. n_group > 1 selects rank_top_grouped (glm52/moe.rs:214). */
+int rbt_route_sigmoid_topk(rbt_ctx *ctx, const float *logits, const float *bias, size_t s, size_t n,
+                           size_t k, int32_t norm_topk, float routed_scale, size_t n_group,
+                           size_t topk_group, int32_t *ids, float *w);
+int rbt_route_sigmoid_topk_d(rbt_ctx *ctx, const float *logits, const float *bias, size_t s, size_t n,
+                             size_t k, int32_t norm_topk, float routed_scale, size_t n_group,
+                             size_t topk_group, int32_t *ids, float *w);
+/* unique_experts (glm52/moe.rs:333-344): ids i32[s, k] -> uniq (first-occurrence order).
+ * Returns the count (>= 0) or a negative status. */
+int rbt_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq);
+
+/* ---- one expert ------------------------------------------------------------------------------ */
+enum { RBT_ACT_SILU = 0 }; /* Activation::Silu (glm52/moe.rs:49-80) */
+/* apply_single_expert (glm52/moe.rs:463-513): the tokens that routed to slot->eid (ids/w are
+ * [s, k]) run gate, up, silu(gate)*up, down, and out[t, :] += w * result. Host buffers; the slot's
+ * weights may be host (uploaded for the call) or a pool slot from rbt_pool_get (device). */
+int rbt_apply_single_expert(rbt_ctx *ctx, const rbt_expert_slot *slot, const int32_t *ids, const float *w,
+                            size_t s, size_t k, const float *x, size_t d, size_t i, int32_t activation,
+                            float *out);
+int rbt_apply_single_expert_d(rbt_ctx *ctx, const rbt_expert_slot *slot, const int32_t *ids,
+                              const float *w, size_t s, size_t k, const float *x, size_t d, size_t i,
+                              int32_t activation, float *out);
+
+/* ---- HBM-resident expert pool (ExpertCache, expert_cache.rs) ---------------------------------- */
+/* ensure_loaded (expert_cache.rs:890) for one expert: copies a host slot's bytes into HBM,
+ * validating byte lengths as mxfp4_from_raw does (expert_cache.rs:1245-1256). Replaces an
+ * existing (layer, eid) entry. */
+int rbt_pool_put(rbt_ctx *ctx, uint32_t layer, const rbt_expert_slot *host_slot);
+/* Registers a slot whose pointers are already device memory owned by the caller. */
+int rbt_pool_put_device(rbt_ctx *ctx, uint32_t layer, const rbt_expert_slot *dev_slot);
+/* Allocates an uninitialised device slot of the given shape (MXFP4 or I4G, separate gate/up) in the
+ * pool and returns it, so a loader can fill the bytes in place (e.g. straight from a file read or
+ * a device-side generator) without a host staging copy. */
+const rbt_expert_slot *rbt_pool_alloc(rbt_ctx *ctx, uint32_t layer, uint32_t eid, int32_t kind,
+                                      size_t d, size_t i, size_t group_size);
+/* ExpertCache::get (expert_cache.rs:1010): the device-resident slot, or NULL when absent. */
+const rbt_expert_slot *rbt_pool_get(rbt_ctx *ctx, uint32_t layer, uint32_t eid);
+/* Bytes resident in the pool (all layers). */
+size_t rbt_pool_resident_bytes(rbt_ctx *ctx);
+
+/* ---- MoE layer: family dispatch (model.rs:22-140) and moe_forward / moe ------------------------ */
+typedef enum {
+    RBT_FAMILY_QWEN38 = 0, /* softmax top-k router, sigmoid-gated shared expert
+                              (qwen38/generate.rs:262-351) */
+    RBT_FAMILY_GLM52 = 1,  /* sigmoid(+bias) top-k, norm_topk, routed_scale, ungated shared expert
+                              (glm52/moe.rs:350-451) */
+    RBT_FAMILY_KIMI_K3 = 2 /* K3 routes through glm52::moe::route (kimi_k3/model.rs:426); plain
+                              (non-latent) MoE layer, ungated shared expert */
+} rbt_family;
+
+typedef struct {
+    int32_t family;          /* rbt_family */
+    size_t hidden, moe_inter, n_experts, topk;
+    const float *router;     /* host f32 [n_experts, hidden] (MoeWeights::router) */
+    const float *router_bias;/* host f32 [n_experts] post-sigmoid selection bias, or NULL */
+    const float *logit_bias; /* host f32 [n_experts] added to the router logits before the
+                                activation (synthetic workload skew; not in the reference), or NULL */
+    int32_t norm_topk;
+    float routed_scale;
+    size_t n_group, topk_group;
+    int32_t has_shared;
+    rbt_expert_slot shared;  /* host weights of the shared expert (uploaded) */
+    const float *shared_gate;/* host f32 [hidden] (Qwen shared_expert_gate) or NULL = ungated */
+} rbt_moe_layer_desc;
+
+/* Uploads a layer's router, biases and shared expert to HBM (Model::load_multi's dense part for
+ * the MoE block). Routed experts come from the pool (rbt_pool_put / rbt_pool_alloc). */
+int rbt_moe_layer_set(rbt_ctx *ctx, uint32_t layer, const rbt_moe_layer_desc *desc);
+/* Same, but the descriptor's pointers (router, biases, shared weights, shared gate) are device
+ * memory that stays owned by the caller. */
+int rbt_moe_layer_set_device(rbt_ctx *ctx, uint32_t layer, const rbt_moe_layer_desc *desc);
+
+/* moe_forward (qwen38/generate.rs:262) / moe (glm52/moe.rs:350): router, top-k, every routed
+ * expert in unique_experts order, then the shared expert added last. x f32[s, hidden] ->
+ * out f32[s, hidden] (overwritten). ids_out / w_out (optional, [s, topk]) receive the routing. */
+int rbt_moe_forward(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
+                    float *w_out);
+int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
+                      int32_t *ids_out, float *w_out);
+
+/* ---- synthetic workload generator (benchmarks and tests; bit-identical to oracle/) ------------ */
+/* Fills an MXFP4 [rows, cols] matrix in device memory: nibbles uniform over 0..15, E8M0 bytes
+ * uniform over exp_lo..exp_hi, from a counter-based hash of `seed`. */
+int rbt_synth_mxfp4_d(rbt_ctx *ctx, uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,
+                      uint32_t exp_lo, uint32_t exp_hi);
+/* Fills a grouped-int4 [rows, cols] matrix: nibbles uniform over 0..15 (values -8..7), scales
+ * uniform over [s_lo, s_hi). */
+int rbt_synth_i4g_d(rbt_ctx *ctx, uint8_t *data, float *scale, size_t rows, size_t cols, size_t group_size,
+                    uint64_t seed, float s_lo, float s_hi);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RABBIT_AMD_H */

@@ -1,0 +1,289 @@
+"""rabbit_amd -- MI355X (gfx950) routed-expert dequant-matmul for ferrumox/rabbit.
+
+Python front end over the C ABI (include/rabbit_amd.h, librabbit_amd.so), used by the tests and
+the benchmark. Names and argument meaning follow the reference's Rust functions:
+
+    kernels.rs   matmul, matmul_mxfp4, matmul_i4_grouped, matmul_qt      (y overwritten)
+    quant.rs     QT::row_f32 (dequant_rows), QT::resident_bytes
+    qwen38/moe.rs route (route_softmax_topk), glm52/moe.rs route (route_sigmoid_topk)
+    glm52/moe.rs  unique_experts, apply_single_expert                    (out accumulated)
+    expert_cache.rs ExpertCache::get / ensure_loaded  (pool_get / pool_put)
+    qwen38/generate.rs moe_forward, glm52/moe.rs moe   (moe_forward; out overwritten)
+
+Host numpy arrays go through the plain entry points (copied in and out per call, like the
+reference's borrowed slices); torch device tensors go through the `_d` entry points on the
+context's own HIP stream. Errors raise RbtError with the library's status and message; there is no
+CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+from .abi import (ACT_SILU, FAMILY_GLM52, FAMILY_KIMI_K3, FAMILY_QWEN38, QT_F32, QT_I4_GROUPED, QT_MXFP4,
+                  RbtExpertSlot, RbtMoeLayerDesc, RbtQT)
+
+__all__ = ["Context", "QT", "Slot", "RbtError", "load", "QT_F32", "QT_I4_GROUPED", "QT_MXFP4",
+           "FAMILY_QWEN38", "FAMILY_GLM52", "FAMILY_KIMI_K3", "ACT_SILU"]
+
+
+class RbtError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{abi.STATUS_NAMES.get(status, status)}: {msg}")
+        self.status = status
+
+
+def load():
+    return abi.load()
+
+
+def _is_torch(a) -> bool:
+    return hasattr(a, "data_ptr") and hasattr(a, "is_cuda")
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if _is_torch(a):
+        if not a.is_cuda:
+            raise ValueError("torch tensors passed to rabbit_amd must live on the GPU")
+        if not a.is_contiguous():
+            raise ValueError("tensor must be contiguous")
+        return a.data_ptr()
+    if isinstance(a, np.ndarray):
+        if not a.flags["C_CONTIGUOUS"]:
+            raise ValueError("array must be C-contiguous")
+        return a.ctypes.data
+    if isinstance(a, int):
+        return a
+    raise TypeError(f"unsupported buffer {type(a)}")
+
+
+class QT:
+    """One quantized matrix (mirrors QT / QTKind, quant.rs:77-110). data/scale are numpy arrays
+    (host) or torch GPU tensors (device)."""
+
+    def __init__(self, kind, rows, cols, data, scale=None, group_size=0):
+        self.kind, self.rows, self.cols = kind, rows, cols
+        self.data, self.scale, self.group_size = data, scale, group_size
+
+    @staticmethod
+    def mxfp4(data, scale, rows, cols):
+        return QT(QT_MXFP4, rows, cols, data, scale, 32)
+
+    @staticmethod
+    def i4g(data, scale, rows, cols, gs):
+        return QT(QT_I4_GROUPED, rows, cols, data, scale, gs)
+
+    @staticmethod
+    def f32(w, rows, cols):
+        return QT(QT_F32, rows, cols, w)
+
+    @property
+    def on_device(self) -> bool:
+        return _is_torch(self.data)
+
+    def c(self) -> RbtQT:
+        return RbtQT(self.rows, self.cols, self.kind, _ptr(self.data), _ptr(self.scale), self.group_size)
+
+    def resident_bytes(self) -> int:
+        q = self.c()
+        return abi.load().rbt_qt_resident_bytes(C.byref(q))
+
+
+class Slot:
+    """One expert (mirrors ExpertSlot / GateUp, expert_cache.rs:640-650)."""
+
+    def __init__(self, eid, down: QT, gate: QT | None = None, up: QT | None = None, gate_up: QT | None = None):
+        self.eid, self.down, self.gate, self.up, self.gate_up = eid, down, gate, up, gate_up
+
+    def c(self) -> RbtExpertSlot:
+        z = RbtQT()
+        return RbtExpertSlot(self.eid, int(self.gate_up is not None), self.gate.c() if self.gate else z,
+                             self.up.c() if self.up else z, self.gate_up.c() if self.gate_up else z, self.down.c())
+
+
+class Context:
+    """An rbt_ctx on one HIP device: stream, scratch, HBM-resident expert pool, MoE layers."""
+
+    def __init__(self, device: int = 0):
+        self.lib = abi.load()
+        h = C.c_void_p()
+        rc = self.lib.rbt_init(C.byref(h), device)
+        if rc != 0:
+            raise RbtError(rc, f"rbt_init(device={device}) failed")
+        self.h = h
+        self._keep = []  # host arrays referenced by device-layer descriptors
+
+    # -- plumbing ---------------------------------------------------------------------------
+    def close(self):
+        if self.h:
+            self.lib.rbt_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def check(self, rc: int):
+        if rc != 0:
+            raise RbtError(rc, (self.lib.rbt_last_error(self.h) or b"").decode())
+        return rc
+
+    def sync(self):
+        self.check(self.lib.rbt_sync(self.h))
+
+    @property
+    def stream(self) -> int:
+        return self.lib.rbt_stream(self.h) or 0
+
+    def torch_stream(self):
+        """The context's stream as a torch ExternalStream (for HIP events / interop)."""
+        import torch
+        return torch.cuda.ExternalStream(self.stream)
+
+    @staticmethod
+    def _torch_sync():
+        import torch
+        torch.cuda.synchronize()
+
+    # -- quant.rs ---------------------------------------------------------------------------
+    def dequant_rows(self, w: QT, row0: int, nrows: int, out=None):
+        q = w.c()
+        if w.on_device:
+            import torch
+            if out is None:
+                out = torch.empty(nrows * w.cols, dtype=torch.float32, device=w.data.device)
+            self._torch_sync()
+            self.check(self.lib.rbt_dequant_rows_d(self.h, C.byref(q), row0, nrows, _ptr(out)))
+            self.sync()
+            return out
+        if out is None:
+            out = np.empty(nrows * w.cols, np.float32)
+        self.check(self.lib.rbt_dequant_rows(self.h, C.byref(q), row0, nrows, _ptr(out)))
+        return out
+
+    # -- kernels.rs -------------------------------------------------------------------------
+    def matmul_qt(self, y, x, w: QT, s: int):
+        q = w.c()
+        if _is_torch(x):
+            self._torch_sync()
+            self.check(self.lib.rbt_matmul_qt_d(self.h, _ptr(y), _ptr(x), C.byref(q), s))
+            self.sync()
+        else:
+            self.check(self.lib.rbt_matmul_qt(self.h, _ptr(y), _ptr(x), C.byref(q), s))
+        return y
+
+    def matmul(self, y, x, w, s, i, o):
+        return self.matmul_qt(y, x, QT.f32(w, o, i), s)
+
+    def matmul_mxfp4(self, y, x, data, block_scale, s, i, o):
+        return self.matmul_qt(y, x, QT.mxfp4(data, block_scale, o, i), s)
+
+    def matmul_i4_grouped(self, y, x, q4, scale, group_size, s, i, o):
+        return self.matmul_qt(y, x, QT.i4g(q4, scale, o, i, group_size), s)
+
+    # -- routers ----------------------------------------------------------------------------
+    def route_softmax_topk(self, logits, s, n, k, ids, w):
+        if _is_torch(logits):
+            self._torch_sync()
+            self.check(self.lib.rbt_route_softmax_topk_d(self.h, _ptr(logits), s, n, k, _ptr(ids), _ptr(w)))
+            self.sync()
+        else:
+            self.check(self.lib.rbt_route_softmax_topk(self.h, _ptr(logits), s, n, k, _ptr(ids), _ptr(w)))
+        return ids, w
+
+    def route_sigmoid_topk(self, logits, bias, s, n, k, norm_topk, routed_scale, ids, w, n_group=1, topk_group=1):
+        args = (self.h, _ptr(logits), _ptr(bias), s, n, k, int(norm_topk), float(routed_scale), n_group,
+                topk_group, _ptr(ids), _ptr(w))
+        if _is_torch(logits):
+            self._torch_sync()
+            self.check(self.lib.rbt_route_sigmoid_topk_d(*args))
+            self.sync()
+        else:
+            self.check(self.lib.rbt_route_sigmoid_topk(*args))
+        return ids, w
+
+    def unique_experts(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        s, k = ids.shape
+        out = np.zeros(max(1, s * k), np.int32)
+        n = self.lib.rbt_unique_experts(_ptr(ids), s, k, _ptr(out))
+        if n < 0:
+            raise RbtError(n, "rbt_unique_experts")
+        return out[:n]
+
+    # -- experts ----------------------------------------------------------------------------
+    def apply_single_expert(self, slot, ids, w, s, k, x, d, i, out, activation=ACT_SILU):
+        """slot: a Slot (host or device weights) or a pool pointer from pool_get()."""
+        sc = slot if isinstance(slot, C._Pointer) else C.pointer(slot.c())
+        if _is_torch(x):
+            self._torch_sync()
+            self.check(self.lib.rbt_apply_single_expert_d(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i,
+                                                          activation, _ptr(out)))
+            self.sync()
+        else:
+            self.check(self.lib.rbt_apply_single_expert(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i,
+                                                        activation, _ptr(out)))
+        return out
+
+    # -- pool (ExpertCache) -----------------------------------------------------------------
+    def pool_put(self, layer: int, slot: Slot):
+        sc = slot.c()
+        if slot.down.on_device:
+            self.check(self.lib.rbt_pool_put_device(self.h, layer, C.byref(sc)))
+        else:
+            self.check(self.lib.rbt_pool_put(self.h, layer, C.byref(sc)))
+
+    def pool_alloc(self, layer, eid, kind, d, i, group_size=32):
+        p = self.lib.rbt_pool_alloc(self.h, layer, eid, kind, d, i, group_size)
+        if not p:
+            raise RbtError(-5, (self.lib.rbt_last_error(self.h) or b"").decode())
+        return p
+
+    def pool_get(self, layer, eid):
+        p = self.lib.rbt_pool_get(self.h, layer, eid)
+        return p if p else None
+
+    def pool_resident_bytes(self) -> int:
+        return self.lib.rbt_pool_resident_bytes(self.h)
+
+    def synth_mxfp4(self, data_ptr, scale_ptr, rows, cols, seed, exp_lo=119, exp_hi=123):
+        self.check(self.lib.rbt_synth_mxfp4_d(self.h, data_ptr, scale_ptr, rows, cols, seed, exp_lo, exp_hi))
+
+    def synth_i4g(self, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo=0.005, s_hi=0.02):
+        self.check(self.lib.rbt_synth_i4g_d(self.h, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo, s_hi))
+
+    # -- MoE layer ----------------------------------------------------------------------------
+    def moe_layer_set(self, layer, family, hidden, moe_inter, n_experts, topk, router, shared: Slot | None = None,
+                      shared_gate=None, router_bias=None, logit_bias=None, norm_topk=True, routed_scale=1.0,
+                      n_group=1, topk_group=1):
+        d = RbtMoeLayerDesc()
+        d.family, d.hidden, d.moe_inter, d.n_experts, d.topk = family, hidden, moe_inter, n_experts, topk
+        d.router, d.router_bias, d.logit_bias = _ptr(router), _ptr(router_bias), _ptr(logit_bias)
+        d.norm_topk, d.routed_scale, d.n_group, d.topk_group = int(norm_topk), routed_scale, n_group, topk_group
+        d.has_shared = int(shared is not None)
+        if shared is not None:
+            d.shared = shared.c()
+        d.shared_gate = _ptr(shared_gate)
+        if _is_torch(router):
+            self._keep.append((router, shared, shared_gate, router_bias, logit_bias))
+            self.check(self.lib.rbt_moe_layer_set_device(self.h, layer, C.byref(d)))
+        else:
+            self.check(self.lib.rbt_moe_layer_set(self.h, layer, C.byref(d)))
+
+    def moe_forward(self, layer, x, s, out, ids_out=None, w_out=None, sync=True):
+        if _is_torch(x):
+            if sync:
+                self._torch_sync()
+            self.check(self.lib.rbt_moe_forward_d(self.h, layer, _ptr(x), s, _ptr(out), _ptr(ids_out),
+                                                  _ptr(w_out)))
+            if sync:
+                self.sync()
+        else:
+            self.check(self.lib.rbt_moe_forward(self.h, layer, _ptr(x), s, _ptr(out), _ptr(ids_out), _ptr(w_out)))
+        return out

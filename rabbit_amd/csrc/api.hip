@@ -1,0 +1,950 @@
+// api.hip -- host side of the C ABI declared in include/rabbit_amd.h.
+//
+// Owns the per-context HIP stream, grow-only device scratch, the HBM-resident expert pool (the
+// storage half of ExpertCache, expert_cache.rs) and the per-layer MoE state (router, biases,
+// shared expert, device table of resident experts). Orchestrates the decode/prefill pipeline of
+// one MoE layer: router logits -> certified top-k -> grouping -> gate/up dequant-GEMV (+SiLU) ->
+// down dequant-GEMV -> ordered combine (+ shared expert).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <initializer_list>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "rbt_internal.h"
+
+namespace {
+
+enum ScratchSlot {
+  SC_X,
+  SC_Y,
+  SC_W,
+  SC_S,
+  SC_MID,
+  SC_BND,
+  SC_IDS,
+  SC_WTS,
+  SC_SHS,
+  SC_PJOB,
+  SC_PTOK,
+  SC_TPAIR,
+  SC_TW,
+  SC_H,
+  SC_YY,
+  SC_FLAGS,
+  SC_STAGE,
+  SC_OUT,
+  SC_IDS_OUT,
+  SC_W_OUT,
+  SC_N
+};
+
+struct PoolEntry {
+  rbt_expert_slot slot{};  // device pointers
+  void *alloc = nullptr;   // owned allocation (nullptr for caller-owned device slots)
+  size_t bytes = 0;
+};
+
+struct Layer {
+  rbt_moe_layer_desc desc{};  // device pointers
+  std::vector<void *> owned;
+  bool set = false;
+  bool dirty = true;
+  RbtExpertDev *d_table = nullptr;
+  size_t table_n = 0;
+  RbtExpertDev *d_shared = nullptr;
+  RbtExpertDev h_shared{};
+  int shared_kind = -1;
+  size_t shared_gs = 0, shared_inter = 0;
+  int routed_kind = -1;
+  size_t routed_gs = 0;
+};
+
+}  // namespace
+
+struct rbt_ctx : rbt::Ctx {
+  std::string err;
+  void *scratch[SC_N] = {};
+  size_t scratch_cap[SC_N] = {};
+  std::map<uint64_t, PoolEntry> pool;
+  std::map<uint32_t, Layer> layers;
+  int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts
+  int h_flags[8] = {};
+};
+
+namespace {
+
+constexpr int FLAG_ERR = 0, FLAG_AMB = 1, FLAG_UNIQ = 2, FLAG_NR = 3, FLAG_N = 8;
+
+int fail(rbt_ctx *c, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
+int fail(rbt_ctx *c, int code, const char *fmt, ...) {
+  if (c) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+  }
+  return code;
+}
+
+#define HIP_OK(c, expr)                                                                                   \
+  do {                                                                                                    \
+    hipError_t e_ = (expr);                                                                               \
+    if (e_ != hipSuccess) return fail((c), RBT_E_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),   \
+                                      __FILE__, __LINE__);                                                \
+  } while (0)
+
+#define RBT_TRY(expr)        \
+  do {                       \
+    int rc_ = (expr);        \
+    if (rc_ != RBT_OK) return rc_; \
+  } while (0)
+
+size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Grow-only device scratch. Growth synchronises the stream first, so in-flight work never sees a
+// freed buffer.
+int scratch(rbt_ctx *c, int slot, size_t bytes, void **out) {
+  if (bytes == 0) bytes = 256;
+  if (c->scratch_cap[slot] < bytes) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    if (c->scratch[slot]) HIP_OK(c, hipFree(c->scratch[slot]));
+    c->scratch[slot] = nullptr;
+    c->scratch_cap[slot] = 0;
+    size_t cap = align256(bytes + bytes / 4);
+    if (hipMalloc(&c->scratch[slot], cap) != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(c, RBT_E_NOMEM, "hipMalloc(%zu) for scratch slot %d failed", cap, slot);
+    }
+    c->scratch_cap[slot] = cap;
+  }
+  *out = c->scratch[slot];
+  return RBT_OK;
+}
+
+template <typename T>
+int scratch_t(rbt_ctx *c, int slot, size_t count, T **out) {
+  void *p;
+  RBT_TRY(scratch(c, slot, count * sizeof(T), &p));
+  *out = (T *)p;
+  return RBT_OK;
+}
+
+// Bytes of a QT's data and scale arrays.
+size_t qt_data_bytes(const rbt_qt &w) {
+  if (w.kind == RBT_QT_F32) return w.rows * w.cols * 4;
+  return w.rows * div_ceil(w.cols, 2);
+}
+size_t qt_scale_bytes(const rbt_qt &w) {
+  if (w.kind == RBT_QT_MXFP4) return w.rows * div_ceil(w.cols, 32);
+  if (w.kind == RBT_QT_I4_GROUPED) return w.rows * div_ceil(w.cols, w.group_size) * 4;
+  return 0;
+}
+
+int check_qt(rbt_ctx *c, const rbt_qt *w, const char *what) {
+  if (!w) return fail(c, RBT_E_INVALID, "%s: null rbt_qt", what);
+  if (w->kind != RBT_QT_F32 && w->kind != RBT_QT_MXFP4 && w->kind != RBT_QT_I4_GROUPED)
+    return fail(c, RBT_E_INVALID, "%s: unknown rbt_qt kind %d", what, (int)w->kind);
+  if (w->rows == 0 || w->cols == 0) return fail(c, RBT_E_INVALID, "%s: empty shape", what);
+  if (!w->data) return fail(c, RBT_E_INVALID, "%s: null data", what);
+  if (w->kind != RBT_QT_F32 && !w->scale) return fail(c, RBT_E_INVALID, "%s: null scale", what);
+  if (w->kind == RBT_QT_I4_GROUPED && w->group_size == 0)
+    return fail(c, RBT_E_INVALID, "%s: group_size 0", what);
+  if (w->rows > (1u << 30) || w->cols > (1u << 30)) return fail(c, RBT_E_INVALID, "%s: dimension too large", what);
+  return RBT_OK;
+}
+
+// Device view of an expert slot (fused gate_up presented as two halves).
+int slot_view(rbt_ctx *c, const rbt_expert_slot *s, size_t d, size_t i, RbtExpertDev *v, int *kind, size_t *gs) {
+  const rbt_qt &g = s->fused ? s->gate_up : s->gate;
+  RBT_TRY(check_qt(c, &g, s->fused ? "gate_up" : "gate"));
+  RBT_TRY(check_qt(c, &s->down, "down"));
+  if (!s->fused) RBT_TRY(check_qt(c, &s->up, "up"));
+  int k = g.kind;
+  if (k == RBT_QT_F32) return fail(c, RBT_E_UNSUPPORTED, "expert %u: f32 expert weights are not on this path", s->eid);
+  if (s->down.kind != k || (!s->fused && s->up.kind != k))
+    return fail(c, RBT_E_UNSUPPORTED, "expert %u: gate/up/down formats differ", s->eid);
+  size_t rows_g = s->fused ? 2 * i : i;
+  if (g.rows != rows_g || g.cols != d || s->down.rows != d || s->down.cols != i ||
+      (!s->fused && (s->up.rows != i || s->up.cols != d)))
+    return fail(c, RBT_E_SHAPE, "expert %u: weight shapes do not match hidden=%zu moe_inter=%zu", s->eid, d, i);
+  size_t g_gs = k == RBT_QT_I4_GROUPED ? g.group_size : 32;
+  if (k == RBT_QT_I4_GROUPED && (s->down.group_size != g_gs || (!s->fused && s->up.group_size != g_gs)))
+    return fail(c, RBT_E_UNSUPPORTED, "expert %u: group sizes differ", s->eid);
+  v->gd = (const uint8_t *)g.data;
+  v->gs = g.scale;
+  if (s->fused) {
+    // gate rows first, then up rows (glm52/moe.rs:494-503).
+    size_t row_scale = k == RBT_QT_MXFP4 ? div_ceil(d, 32) : div_ceil(d, g_gs) * 4;
+    v->ud = (const uint8_t *)g.data + i * div_ceil(d, 2);
+    v->us = (const uint8_t *)g.scale + i * row_scale;
+  } else {
+    v->ud = (const uint8_t *)s->up.data;
+    v->us = s->up.scale;
+  }
+  v->dd = (const uint8_t *)s->down.data;
+  v->ds = s->down.scale;
+  *kind = k;
+  *gs = g_gs;
+  return RBT_OK;
+}
+
+// Shape of an expert slot: d = hidden (gate cols), i = moe_inter (down cols).
+void slot_dims(const rbt_expert_slot *s, size_t *d, size_t *i) {
+  *d = s->down.rows;
+  *i = s->down.cols;
+}
+
+int sync_and_check(rbt_ctx *c) {
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
+  if (c->h_flags[FLAG_ERR]) {
+    HIP_OK(c, hipMemset(c->d_flags, 0, sizeof(int)));
+    return fail(c, RBT_E_NOT_RESIDENT, "a routed expert is not resident in the pool");
+  }
+  return RBT_OK;
+}
+
+// Copies n bytes host -> device scratch slot and returns the device pointer.
+int stage_in(rbt_ctx *c, int slot, const void *host, size_t n, void **dev) {
+  RBT_TRY(scratch(c, slot, n, dev));
+  if (n) HIP_OK(c, hipMemcpyAsync(*dev, host, n, hipMemcpyHostToDevice, c->stream));
+  return RBT_OK;
+}
+
+// Uploads a host QT into a contiguous staging region at *cursor, returning the device copy.
+int upload_qt(rbt_ctx *c, const rbt_qt &h, uint8_t *base, size_t *cursor, rbt_qt *d) {
+  *d = h;
+  size_t nd = qt_data_bytes(h), ns = qt_scale_bytes(h);
+  d->data = base + *cursor;
+  HIP_OK(c, hipMemcpyAsync(base + *cursor, h.data, nd, hipMemcpyHostToDevice, c->stream));
+  *cursor += align256(nd);
+  if (ns) {
+    d->scale = base + *cursor;
+    HIP_OK(c, hipMemcpyAsync(base + *cursor, h.scale, ns, hipMemcpyHostToDevice, c->stream));
+    *cursor += align256(ns);
+  } else {
+    d->scale = nullptr;
+  }
+  return RBT_OK;
+}
+
+size_t slot_bytes(const rbt_expert_slot *s) {
+  size_t n = 0;
+  auto add = [&](const rbt_qt &q) { n += align256(qt_data_bytes(q)) + align256(qt_scale_bytes(q)); };
+  if (s->fused) add(s->gate_up);
+  else {
+    add(s->gate);
+    add(s->up);
+  }
+  add(s->down);
+  return n;
+}
+
+int upload_slot(rbt_ctx *c, const rbt_expert_slot *h, uint8_t *base, rbt_expert_slot *d) {
+  size_t cur = 0;
+  *d = *h;
+  if (h->fused) RBT_TRY(upload_qt(c, h->gate_up, base, &cur, &d->gate_up));
+  else {
+    RBT_TRY(upload_qt(c, h->gate, base, &cur, &d->gate));
+    RBT_TRY(upload_qt(c, h->up, base, &cur, &d->up));
+  }
+  RBT_TRY(upload_qt(c, h->down, base, &cur, &d->down));
+  return RBT_OK;
+}
+
+const PoolEntry *find_pool_slot(rbt_ctx *c, const rbt_expert_slot *s) {
+  for (auto &kv : c->pool)
+    if (&kv.second.slot == s) return &kv.second;
+  return nullptr;
+}
+
+// y[S,O] = x . W^T for one QT whose pointers are device memory.
+int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) {
+  RBT_TRY(check_qt(c, w, "matmul"));
+  if (s == 0) return RBT_OK;
+  if (s > (1u << 24)) return fail(c, RBT_E_INVALID, "token count %zu too large", s);
+  const size_t i = w->cols, o = w->rows;
+  bool aligned = ((uintptr_t)w->data % 16 == 0) && ((uintptr_t)x % 16 == 0);
+  if (w->kind != RBT_QT_F32 && aligned && rbt::decode_shape_ok(i, w->kind, w->group_size)) {
+    RbtExpertDev one{};
+    one.dd = (const uint8_t *)w->data;
+    one.ds = w->scale;
+    HIP_OK(c, rbt::launch_decode(*c, false, w->kind, nullptr, one, (int)s, nullptr, x, nullptr, (long)i, (int)i,
+                                 (int)o, y, (long)o));
+    return RBT_OK;
+  }
+  HIP_OK(c, rbt::launch_generic(*c, w->kind, y, x, w->data, w->scale, w->group_size, s, i, o));
+  return RBT_OK;
+}
+
+// Runs gate/up (+SiLU) then down for `njobs` (expert, token) pairs.
+//   x: [tokens, d], x_index[p] = token of pair p; h: [njobs, i]; y: [njobs, d].
+int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
+                 const int *njobs_dev, const float *x, const int *x_index, size_t d, size_t i, float *h, float *y) {
+  bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
+  bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
+  if (fast_gu)
+    HIP_OK(c, rbt::launch_decode(*c, true, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d, (int)i,
+                                 h, (long)i));
+  else
+    HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
+                                       (int)i, h, (long)i));
+  if (fast_dn)
+    HIP_OK(c, rbt::launch_decode(*c, false, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i, (int)i, (int)d,
+                                 y, (long)d));
+  else
+    HIP_OK(c, rbt::launch_pair_generic(*c, false, kind, gs, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
+                                       (int)i, (int)d, y, (long)d));
+  return RBT_OK;
+}
+
+int refresh_table(rbt_ctx *c, uint32_t layer, Layer &L) {
+  size_t E = L.desc.n_experts;
+  if (!L.dirty && L.table_n == E) return RBT_OK;
+  std::vector<RbtExpertDev> t(E);
+  memset(t.data(), 0, E * sizeof(RbtExpertDev));
+  L.routed_kind = -1;
+  for (auto &kv : c->pool) {
+    if ((uint32_t)(kv.first >> 32) != layer) continue;
+    uint32_t eid = (uint32_t)kv.first;
+    if (eid >= E) continue;
+    int kind;
+    size_t gs;
+    RBT_TRY(slot_view(c, &kv.second.slot, L.desc.hidden, L.desc.moe_inter, &t[eid], &kind, &gs));
+    if (L.routed_kind >= 0 && (kind != L.routed_kind || gs != L.routed_gs))
+      return fail(c, RBT_E_UNSUPPORTED, "layer %u: routed experts mix weight formats", layer);
+    L.routed_kind = kind;
+    L.routed_gs = gs;
+  }
+  if (L.table_n < E) {
+    if (L.d_table) HIP_OK(c, hipFree(L.d_table));
+    L.d_table = nullptr;
+    HIP_OK(c, hipMalloc(&L.d_table, E * sizeof(RbtExpertDev)));
+  }
+  L.table_n = E;
+  HIP_OK(c, hipMemcpyAsync(L.d_table, t.data(), E * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  L.dirty = false;
+  return RBT_OK;
+}
+
+void free_layer(Layer &L) {
+  for (void *p : L.owned) (void)hipFree(p);
+  L.owned.clear();
+  if (L.d_table) (void)hipFree(L.d_table);
+  L.d_table = nullptr;
+  L.table_n = 0;
+  if (L.d_shared) (void)hipFree(L.d_shared);
+  L.d_shared = nullptr;
+}
+
+int dev_copy_of(rbt_ctx *c, Layer &L, const void *host, size_t bytes, const void **out) {
+  if (!host) {
+    *out = nullptr;
+    return RBT_OK;
+  }
+  void *p;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(c, RBT_E_NOMEM, "hipMalloc(%zu) failed", bytes);
+  }
+  L.owned.push_back(p);
+  HIP_OK(c, hipMemcpy(p, host, bytes, hipMemcpyHostToDevice));
+  *out = p;
+  return RBT_OK;
+}
+
+int layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d, bool device) {
+  if (!c || !d) return fail(c, RBT_E_INVALID, "null argument");
+  if (d->family < RBT_FAMILY_QWEN38 || d->family > RBT_FAMILY_KIMI_K3)
+    return fail(c, RBT_E_INVALID, "unknown family %d", (int)d->family);
+  if (d->hidden == 0 || d->moe_inter == 0 || d->n_experts == 0 || d->topk == 0 || !d->router)
+    return fail(c, RBT_E_INVALID, "layer %u: empty dimension or null router", layer);
+  if (d->n_experts > 2048) return fail(c, RBT_E_UNSUPPORTED, "n_experts > 2048");
+  if (std::min(d->topk, d->n_experts) > 64) return fail(c, RBT_E_UNSUPPORTED, "topk > 64");
+  if (d->n_group > 1 && (d->n_experts % d->n_group != 0 || d->n_group > 64))
+    return fail(c, RBT_E_INVALID, "n_experts %% n_group != 0 or n_group > 64");
+  Layer &L = c->layers[layer];
+  free_layer(L);
+  L = Layer{};
+  L.desc = *d;
+  size_t E = d->n_experts, H = d->hidden;
+  if (!device) {
+    const void *p;
+    RBT_TRY(dev_copy_of(c, L, d->router, E * H * 4, &p));
+    L.desc.router = (const float *)p;
+    RBT_TRY(dev_copy_of(c, L, d->router_bias, E * 4, &p));
+    L.desc.router_bias = (const float *)p;
+    RBT_TRY(dev_copy_of(c, L, d->logit_bias, E * 4, &p));
+    L.desc.logit_bias = (const float *)p;
+    RBT_TRY(dev_copy_of(c, L, d->shared_gate, H * 4, &p));
+    L.desc.shared_gate = (const float *)p;
+  }
+  if (d->has_shared) {
+    size_t sd, si;
+    slot_dims(&d->shared, &sd, &si);
+    if (sd != H) return fail(c, RBT_E_SHAPE, "shared expert hidden %zu != %zu", sd, H);
+    if (!device) {
+      void *p;
+      size_t nb = slot_bytes(&d->shared);
+      if (hipMalloc(&p, nb) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(c, RBT_E_NOMEM, "hipMalloc(%zu) failed", nb);
+      }
+      L.owned.push_back(p);
+      RBT_TRY(upload_slot(c, &d->shared, (uint8_t *)p, &L.desc.shared));
+      HIP_OK(c, hipStreamSynchronize(c->stream));
+    }
+    int kind;
+    size_t gs;
+    RBT_TRY(slot_view(c, &L.desc.shared, H, si, &L.h_shared, &kind, &gs));
+    L.shared_kind = kind;
+    L.shared_gs = gs;
+    L.shared_inter = si;
+    HIP_OK(c, hipMalloc(&L.d_shared, sizeof(RbtExpertDev)));
+    HIP_OK(c, hipMemcpy(L.d_shared, &L.h_shared, sizeof(RbtExpertDev), hipMemcpyHostToDevice));
+  } else {
+    HIP_OK(c, hipMalloc(&L.d_shared, sizeof(RbtExpertDev)));
+    HIP_OK(c, hipMemset(L.d_shared, 0, sizeof(RbtExpertDev)));
+  }
+  L.set = true;
+  L.dirty = true;
+  return RBT_OK;
+}
+
+int pool_insert(rbt_ctx *c, uint32_t layer, const rbt_expert_slot &slot, void *alloc, size_t bytes) {
+  uint64_t key = ((uint64_t)layer << 32) | slot.eid;
+  auto it = c->pool.find(key);
+  if (it != c->pool.end()) {
+    HIP_OK(c, hipStreamSynchronize(c->stream));
+    if (it->second.alloc) HIP_OK(c, hipFree(it->second.alloc));
+    c->pool.erase(it);
+  }
+  PoolEntry &e = c->pool[key];
+  e.slot = slot;
+  e.alloc = alloc;
+  e.bytes = bytes;
+  auto lit = c->layers.find(layer);
+  if (lit != c->layers.end()) lit->second.dirty = true;
+  return RBT_OK;
+}
+
+int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
+                    float *w_out) {
+  auto lit = c->layers.find(layer);
+  if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
+  Layer &L = lit->second;
+  if (s == 0) return RBT_OK;
+  if (!x || !out) return fail(c, RBT_E_INVALID, "null x or out");
+  if (s > 65536) return fail(c, RBT_E_UNSUPPORTED, "more than 65536 tokens per call");
+  RBT_TRY(refresh_table(c, layer, L));
+  const rbt_moe_layer_desc &D = L.desc;
+  const int S = (int)s, E = (int)D.n_experts, H = (int)D.hidden, I = (int)D.moe_inter;
+  const int k = (int)std::min(D.topk, D.n_experts);
+  if (L.routed_kind < 0) return fail(c, RBT_E_NOT_RESIDENT, "layer %u has no resident experts", layer);
+  const bool qwen = D.family == RBT_FAMILY_QWEN38;
+  const bool gated = qwen && D.has_shared && D.shared_gate;
+  const int erows = E + (gated ? 1 : 0);
+  const int P = S * k;
+  const int npairs = P + (D.has_shared ? S : 0);
+
+  double *mid, *bnd;
+  int32_t *ids;
+  float *wts, *shs, *tw, *h, *yy;
+  RbtExpertDev *pjob;
+  int *ptok, *tpair;
+  RBT_TRY(scratch_t(c, SC_MID, (size_t)S * erows, &mid));
+  RBT_TRY(scratch_t(c, SC_BND, (size_t)S * erows, &bnd));
+  RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
+  RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
+  RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
+  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)npairs, &pjob));
+  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)npairs, &ptok));
+  RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
+  RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
+  size_t hi = std::max((size_t)I, L.shared_inter);
+  RBT_TRY(scratch_t(c, SC_H, (size_t)npairs * hi, &h));
+  RBT_TRY(scratch_t(c, SC_YY, (size_t)npairs * H, &yy));
+  int *dflags = c->d_flags;
+
+  HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
+  rbt::RouterArgs ra{D.family, E,          erows,          k,     H, S, D.logit_bias, D.router_bias, D.norm_topk,
+                     D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB));
+  HIP_OK(c, rbt::launch_group(*c, ids, wts, S, k, E, L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
+                              dflags + FLAG_UNIQ));
+
+  const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
+                     L.shared_inter == (size_t)I;
+  RbtExpertDev none{};
+  if (merge || !D.has_shared) {
+    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy));
+  } else {
+    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, P, nullptr, x, ptok, H, I, h, yy));
+    // shared pairs [P, P+S): h rows at stride shared_inter after the routed block
+    float *hs = h + (size_t)P * I;
+    RBT_TRY(expert_pairs(c, L.shared_kind, L.shared_gs, pjob + P, none, S, nullptr, x, ptok + P, H, L.shared_inter, hs,
+                         yy + (size_t)P * H));
+  }
+  HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
+  if (ids_out)
+    HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, wts, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
+  return RBT_OK;
+}
+
+int route_dev(rbt_ctx *c, bool softmax, const float *logits, const float *bias, size_t s, size_t n, size_t k,
+              int32_t norm_topk, float routed_scale, size_t n_group, size_t topk_group, int32_t *ids, float *w) {
+  if (s == 0 || n == 0 || k == 0) return RBT_OK;
+  if (!logits || !ids || !w) return fail(c, RBT_E_INVALID, "null argument");
+  if (n > 2048) return fail(c, RBT_E_UNSUPPORTED, "more than 2048 experts");
+  size_t kk = std::min(k, n);
+  if (kk > 64) return fail(c, RBT_E_UNSUPPORTED, "topk > 64");
+  if (n_group > 1 && (n % n_group != 0 || n_group > 64)) return fail(c, RBT_E_INVALID, "bad n_group");
+  double *mid, *bnd;
+  RBT_TRY(scratch_t(c, SC_MID, s * n, &mid));
+  RBT_TRY(scratch_t(c, SC_BND, s * n, &bnd));
+  HIP_OK(c, rbt::launch_logits_to_mid(*c, logits, s * n, mid, bnd));
+  rbt::RouterArgs ra{softmax ? RBT_FAMILY_QWEN38 : RBT_FAMILY_GLM52, (int)n, (int)n, (int)kk, 0, (int)s, nullptr, bias,
+                     norm_topk, routed_scale, (int)n_group, (int)topk_group, nullptr, nullptr};
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, w, nullptr, nullptr));
+  return RBT_OK;
+}
+
+int apply_single_dev(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s, size_t k,
+                     const float *x, size_t d, size_t i, int32_t act, float *out) {
+  if (act != RBT_ACT_SILU) return fail(c, RBT_E_UNSUPPORTED, "activation %d", (int)act);
+  if (!slot || !ids || !w || !x || !out) return fail(c, RBT_E_INVALID, "null argument");
+  if (s == 0 || k == 0) return RBT_OK;
+  RbtExpertDev v;
+  int kind;
+  size_t gs;
+  RBT_TRY(slot_view(c, slot, d, i, &v, &kind, &gs));
+  int *ptok, *nr;
+  float *pw, *h, *yy;
+  RBT_TRY(scratch_t(c, SC_PTOK, s, &ptok));
+  RBT_TRY(scratch_t(c, SC_TW, s, &pw));
+  RBT_TRY(scratch_t(c, SC_FLAGS, 4, &nr));
+  RBT_TRY(scratch_t(c, SC_H, s * i, &h));
+  RBT_TRY(scratch_t(c, SC_YY, s * d, &yy));
+  HIP_OK(c, rbt::launch_single_rows(*c, ids, w, (int)s, (int)k, (int)slot->eid, ptok, pw, nr));
+  RBT_TRY(expert_pairs(c, kind, gs, nullptr, v, (int)s, nr, x, ptok, d, i, h, yy));
+  HIP_OK(c, rbt::launch_accumulate(*c, yy, (int)s, (int)d, ptok, pw, nr, out));
+  return RBT_OK;
+}
+
+}  // namespace
+
+// ================================================================================================
+// C ABI
+// ================================================================================================
+extern "C" {
+
+const char *rbt_version(void) { return "rabbit_amd 0.1.0 (gfx950)"; }
+
+int rbt_init(rbt_ctx **out, int device) {
+  if (!out) return RBT_E_INVALID;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    return RBT_E_HIP;
+  }
+  if (device < 0 || device >= n) return RBT_E_INVALID;
+  if (hipSetDevice(device) != hipSuccess) return RBT_E_HIP;
+  rbt_ctx *c = new rbt_ctx();
+  c->device = device;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
+    c->num_cu = prop.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int)) != hipSuccess ||
+      hipMemset(c->d_flags, 0, FLAG_N * sizeof(int)) != hipSuccess) {
+    (void)hipGetLastError();
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+    return RBT_E_HIP;
+  }
+  *out = c;
+  return RBT_OK;
+}
+
+void rbt_destroy(rbt_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  for (auto &kv : c->layers) free_layer(kv.second);
+  for (auto &kv : c->pool)
+    if (kv.second.alloc) (void)hipFree(kv.second.alloc);
+  for (int i = 0; i < SC_N; i++)
+    if (c->scratch[i]) (void)hipFree(c->scratch[i]);
+  if (c->d_flags) (void)hipFree(c->d_flags);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+const char *rbt_last_error(const rbt_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+int rbt_sync(rbt_ctx *c) {
+  if (!c) return RBT_E_INVALID;
+  return sync_and_check(c);
+}
+
+void *rbt_stream(rbt_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+size_t rbt_qt_resident_bytes(const rbt_qt *w) {
+  if (!w) return 0;
+  // quant.rs:214-228
+  switch (w->kind) {
+    case RBT_QT_F32: return w->rows * w->cols * 4;
+    case RBT_QT_I4_GROUPED:
+      return w->group_size ? w->rows * div_ceil(w->cols, 2) + w->rows * div_ceil(w->cols, w->group_size) * 4 : 0;
+    case RBT_QT_MXFP4: return w->rows * div_ceil(w->cols, 2) + w->rows * div_ceil(w->cols, 32);
+    default: return 0;
+  }
+}
+
+int rbt_dequant_rows_d(rbt_ctx *c, const rbt_qt *w, size_t row0, size_t nrows, float *out) {
+  if (!c) return RBT_E_INVALID;
+  RBT_TRY(check_qt(c, w, "dequant"));
+  if (row0 + nrows > w->rows) return fail(c, RBT_E_INVALID, "rows [%zu, %zu) out of range", row0, row0 + nrows);
+  if (!out) return fail(c, RBT_E_INVALID, "null out");
+  HIP_OK(c, rbt::launch_dequant(*c, out, w->kind, w->data, w->scale, w->cols, w->group_size, row0, nrows));
+  return RBT_OK;
+}
+
+int rbt_dequant_rows(rbt_ctx *c, const rbt_qt *w, size_t row0, size_t nrows, float *out) {
+  if (!c) return RBT_E_INVALID;
+  RBT_TRY(check_qt(c, w, "dequant"));
+  if (row0 + nrows > w->rows) return fail(c, RBT_E_INVALID, "rows [%zu, %zu) out of range", row0, row0 + nrows);
+  if (!out) return fail(c, RBT_E_INVALID, "null out");
+  void *base;
+  size_t nd = qt_data_bytes(*w), ns = qt_scale_bytes(*w);
+  RBT_TRY(scratch(c, SC_STAGE, align256(nd) + align256(ns), &base));
+  size_t cur = 0;
+  rbt_qt d;
+  RBT_TRY(upload_qt(c, *w, (uint8_t *)base, &cur, &d));
+  float *o;
+  RBT_TRY(scratch_t(c, SC_OUT, nrows * w->cols, &o));
+  HIP_OK(c, rbt::launch_dequant(*c, o, d.kind, d.data, d.scale, d.cols, d.group_size, row0, nrows));
+  HIP_OK(c, hipMemcpyAsync(out, o, nrows * w->cols * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
+}
+
+int rbt_matmul_qt_d(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) {
+  if (!c) return RBT_E_INVALID;
+  if (!y || !x) return fail(c, RBT_E_INVALID, "null y or x");
+  return matmul_dev(c, y, x, w, s);
+}
+
+int rbt_matmul_qt(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) {
+  if (!c) return RBT_E_INVALID;
+  RBT_TRY(check_qt(c, w, "matmul_qt"));
+  if (!y || !x) return fail(c, RBT_E_INVALID, "null y or x");
+  if (s == 0) return RBT_OK;
+  void *base;
+  size_t nd = qt_data_bytes(*w), ns = qt_scale_bytes(*w);
+  RBT_TRY(scratch(c, SC_STAGE, align256(nd) + align256(ns), &base));
+  size_t cur = 0;
+  rbt_qt d;
+  RBT_TRY(upload_qt(c, *w, (uint8_t *)base, &cur, &d));
+  void *dx;
+  float *dy;
+  RBT_TRY(stage_in(c, SC_X, x, s * w->cols * 4, &dx));
+  RBT_TRY(scratch_t(c, SC_Y, s * w->rows, &dy));
+  RBT_TRY(matmul_dev(c, dy, (const float *)dx, &d, s));
+  HIP_OK(c, hipMemcpyAsync(y, dy, s * w->rows * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
+}
+
+static rbt_qt make_qt(int kind, size_t rows, size_t cols, const void *data, const void *scale, size_t gs) {
+  rbt_qt q;
+  q.rows = rows;
+  q.cols = cols;
+  q.kind = kind;
+  q.data = data;
+  q.scale = scale;
+  q.group_size = gs;
+  return q;
+}
+
+int rbt_matmul(rbt_ctx *c, float *y, const float *x, const float *w, size_t s, size_t i, size_t o) {
+  rbt_qt q = make_qt(RBT_QT_F32, o, i, w, nullptr, 0);
+  return rbt_matmul_qt(c, y, x, &q, s);
+}
+int rbt_matmul_d(rbt_ctx *c, float *y, const float *x, const float *w, size_t s, size_t i, size_t o) {
+  rbt_qt q = make_qt(RBT_QT_F32, o, i, w, nullptr, 0);
+  return rbt_matmul_qt_d(c, y, x, &q, s);
+}
+int rbt_matmul_mxfp4(rbt_ctx *c, float *y, const float *x, const uint8_t *data, const uint8_t *bs, size_t s, size_t i,
+                     size_t o) {
+  rbt_qt q = make_qt(RBT_QT_MXFP4, o, i, data, bs, 32);
+  return rbt_matmul_qt(c, y, x, &q, s);
+}
+int rbt_matmul_mxfp4_d(rbt_ctx *c, float *y, const float *x, const uint8_t *data, const uint8_t *bs, size_t s,
+                       size_t i, size_t o) {
+  rbt_qt q = make_qt(RBT_QT_MXFP4, o, i, data, bs, 32);
+  return rbt_matmul_qt_d(c, y, x, &q, s);
+}
+int rbt_matmul_i4_grouped(rbt_ctx *c, float *y, const float *x, const uint8_t *q4, const float *scale, size_t gs,
+                          size_t s, size_t i, size_t o) {
+  rbt_qt q = make_qt(RBT_QT_I4_GROUPED, o, i, q4, scale, gs);
+  return rbt_matmul_qt(c, y, x, &q, s);
+}
+int rbt_matmul_i4_grouped_d(rbt_ctx *c, float *y, const float *x, const uint8_t *q4, const float *scale, size_t gs,
+                            size_t s, size_t i, size_t o) {
+  rbt_qt q = make_qt(RBT_QT_I4_GROUPED, o, i, q4, scale, gs);
+  return rbt_matmul_qt_d(c, y, x, &q, s);
+}
+
+int rbt_route_softmax_topk_d(rbt_ctx *c, const float *logits, size_t s, size_t n, size_t k, int32_t *ids, float *w) {
+  if (!c) return RBT_E_INVALID;
+  return route_dev(c, true, logits, nullptr, s, n, k, 0, 1.0f, 1, 1, ids, w);
+}
+
+int rbt_route_sigmoid_topk_d(rbt_ctx *c, const float *logits, const float *bias, size_t s, size_t n, size_t k,
+                             int32_t norm_topk, float routed_scale, size_t n_group, size_t topk_group, int32_t *ids,
+                             float *w) {
+  if (!c) return RBT_E_INVALID;
+  return route_dev(c, false, logits, bias, s, n, k, norm_topk, routed_scale, n_group, topk_group, ids, w);
+}
+
+static int route_host(rbt_ctx *c, bool softmax, const float *logits, const float *bias, size_t s, size_t n, size_t k,
+                      int32_t norm_topk, float routed_scale, size_t n_group, size_t topk_group, int32_t *ids,
+                      float *w) {
+  if (!c) return RBT_E_INVALID;
+  if (s == 0 || n == 0 || k == 0) return RBT_OK;
+  if (!logits || !ids || !w) return fail(c, RBT_E_INVALID, "null argument");
+  size_t kk = std::min(k, n);
+  void *dl, *db = nullptr;
+  int32_t *di;
+  float *dw;
+  RBT_TRY(stage_in(c, SC_X, logits, s * n * 4, &dl));
+  if (bias) RBT_TRY(stage_in(c, SC_S, bias, n * 4, &db));
+  RBT_TRY(scratch_t(c, SC_IDS_OUT, s * kk, &di));
+  RBT_TRY(scratch_t(c, SC_W_OUT, s * kk, &dw));
+  RBT_TRY(route_dev(c, softmax, (const float *)dl, (const float *)db, s, n, kk, norm_topk, routed_scale, n_group,
+                    topk_group, di, dw));
+  HIP_OK(c, hipMemcpyAsync(ids, di, s * kk * 4, hipMemcpyDeviceToHost, c->stream));
+  HIP_OK(c, hipMemcpyAsync(w, dw, s * kk * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
+}
+
+int rbt_route_softmax_topk(rbt_ctx *c, const float *logits, size_t s, size_t n, size_t k, int32_t *ids, float *w) {
+  return route_host(c, true, logits, nullptr, s, n, k, 0, 1.0f, 1, 1, ids, w);
+}
+
+int rbt_route_sigmoid_topk(rbt_ctx *c, const float *logits, const float *bias, size_t s, size_t n, size_t k,
+                           int32_t norm_topk, float routed_scale, size_t n_group, size_t topk_group, int32_t *ids,
+                           float *w) {
+  return route_host(c, false, logits, bias, s, n, k, norm_topk, routed_scale, n_group, topk_group, ids, w);
+}
+
+int rbt_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq) {
+  if ((!ids || !uniq) && s * k) return RBT_E_INVALID;
+  // glm52/moe.rs:333-344 (host-side; the device pipeline computes the same order in k_group)
+  std::vector<int32_t> seen;
+  int n = 0;
+  for (size_t t = 0; t < s * k; t++) {
+    if (std::find(seen.begin(), seen.end(), ids[t]) == seen.end()) {
+      seen.push_back(ids[t]);
+      uniq[n++] = ids[t];
+    }
+  }
+  return n;
+}
+
+int rbt_apply_single_expert_d(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s,
+                              size_t k, const float *x, size_t d, size_t i, int32_t act, float *out) {
+  if (!c) return RBT_E_INVALID;
+  return apply_single_dev(c, slot, ids, w, s, k, x, d, i, act, out);
+}
+
+int rbt_apply_single_expert(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s,
+                            size_t k, const float *x, size_t d, size_t i, int32_t act, float *out) {
+  if (!c) return RBT_E_INVALID;
+  if (!slot || !ids || !w || !x || !out) return fail(c, RBT_E_INVALID, "null argument");
+  if (s == 0 || k == 0) return RBT_OK;
+  rbt_expert_slot dslot;
+  const rbt_expert_slot *use = slot;
+  if (!find_pool_slot(c, slot)) {
+    RbtExpertDev v;
+    int kind;
+    size_t gs;
+    RBT_TRY(slot_view(c, slot, d, i, &v, &kind, &gs));  // validates before any copy
+    void *base;
+    RBT_TRY(scratch(c, SC_STAGE, slot_bytes(slot), &base));
+    RBT_TRY(upload_slot(c, slot, (uint8_t *)base, &dslot));
+    use = &dslot;
+  }
+  void *dx, *dids, *dw;
+  float *dout;
+  RBT_TRY(stage_in(c, SC_X, x, s * d * 4, &dx));
+  RBT_TRY(stage_in(c, SC_IDS_OUT, ids, s * k * 4, &dids));
+  RBT_TRY(stage_in(c, SC_W_OUT, w, s * k * 4, &dw));
+  RBT_TRY(scratch_t(c, SC_OUT, s * d, &dout));
+  HIP_OK(c, hipMemcpyAsync(dout, out, s * d * 4, hipMemcpyHostToDevice, c->stream));
+  RBT_TRY(apply_single_dev(c, use, (const int32_t *)dids, (const float *)dw, s, k, (const float *)dx, d, i, act,
+                           dout));
+  HIP_OK(c, hipMemcpyAsync(out, dout, s * d * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
+}
+
+int rbt_pool_put(rbt_ctx *c, uint32_t layer, const rbt_expert_slot *h) {
+  if (!c) return RBT_E_INVALID;
+  if (!h) return fail(c, RBT_E_INVALID, "null slot");
+  size_t d, i;
+  slot_dims(h, &d, &i);
+  RbtExpertDev v;
+  int kind;
+  size_t gs;
+  RBT_TRY(slot_view(c, h, d, i, &v, &kind, &gs));  // byte-length / shape validation
+  size_t nb = slot_bytes(h);
+  void *p;
+  if (hipMalloc(&p, nb) != hipSuccess) {
+    (void)hipGetLastError();
+    return fail(c, RBT_E_NOMEM, "hipMalloc(%zu) for expert %u failed", nb, h->eid);
+  }
+  rbt_expert_slot ds;
+  int rc = upload_slot(c, h, (uint8_t *)p, &ds);
+  if (rc == RBT_OK) rc = hipStreamSynchronize(c->stream) == hipSuccess ? RBT_OK : RBT_E_HIP;
+  if (rc != RBT_OK) {
+    (void)hipFree(p);
+    return rc;
+  }
+  return pool_insert(c, layer, ds, p, nb);
+}
+
+int rbt_pool_put_device(rbt_ctx *c, uint32_t layer, const rbt_expert_slot *s) {
+  if (!c) return RBT_E_INVALID;
+  if (!s) return fail(c, RBT_E_INVALID, "null slot");
+  size_t d, i;
+  slot_dims(s, &d, &i);
+  RbtExpertDev v;
+  int kind;
+  size_t gs;
+  RBT_TRY(slot_view(c, s, d, i, &v, &kind, &gs));
+  for (const void *p : {(const void *)v.gd, (const void *)v.ud, (const void *)v.dd})
+    if ((uintptr_t)p % 16) return fail(c, RBT_E_INVALID, "device slot data must be 16-byte aligned");
+  return pool_insert(c, layer, *s, nullptr, 0);
+}
+
+const rbt_expert_slot *rbt_pool_alloc(rbt_ctx *c, uint32_t layer, uint32_t eid, int32_t kind, size_t d, size_t i,
+                                      size_t gs) {
+  if (!c) return nullptr;
+  if ((kind != RBT_QT_MXFP4 && kind != RBT_QT_I4_GROUPED) || d == 0 || i == 0 ||
+      (kind == RBT_QT_I4_GROUPED && gs == 0)) {
+    fail(c, RBT_E_INVALID, "rbt_pool_alloc: bad kind or shape");
+    return nullptr;
+  }
+  rbt_expert_slot s{};
+  s.eid = eid;
+  s.fused = 0;
+  s.gate = make_qt(kind, i, d, nullptr, nullptr, kind == RBT_QT_I4_GROUPED ? gs : 0);
+  s.up = s.gate;
+  s.down = make_qt(kind, d, i, nullptr, nullptr, kind == RBT_QT_I4_GROUPED ? gs : 0);
+  size_t nb = slot_bytes(&s);
+  void *p;
+  if (hipMalloc(&p, nb) != hipSuccess) {
+    (void)hipGetLastError();
+    fail(c, RBT_E_NOMEM, "hipMalloc(%zu) for expert %u failed", nb, eid);
+    return nullptr;
+  }
+  uint8_t *b = (uint8_t *)p;
+  size_t cur = 0;
+  for (rbt_qt *q : {&s.gate, &s.up, &s.down}) {
+    q->data = b + cur;
+    cur += align256(qt_data_bytes(*q));
+    q->scale = b + cur;
+    cur += align256(qt_scale_bytes(*q));
+  }
+  if (pool_insert(c, layer, s, p, nb) != RBT_OK) {
+    (void)hipFree(p);
+    return nullptr;
+  }
+  return &c->pool[((uint64_t)layer << 32) | eid].slot;
+}
+
+const rbt_expert_slot *rbt_pool_get(rbt_ctx *c, uint32_t layer, uint32_t eid) {
+  if (!c) return nullptr;
+  auto it = c->pool.find(((uint64_t)layer << 32) | eid);
+  return it == c->pool.end() ? nullptr : &it->second.slot;
+}
+
+size_t rbt_pool_resident_bytes(rbt_ctx *c) {
+  if (!c) return 0;
+  size_t n = 0;
+  for (auto &kv : c->pool) {
+    const rbt_expert_slot &s = kv.second.slot;
+    if (s.fused) n += rbt_qt_resident_bytes(&s.gate_up);
+    else n += rbt_qt_resident_bytes(&s.gate) + rbt_qt_resident_bytes(&s.up);
+    n += rbt_qt_resident_bytes(&s.down);
+  }
+  return n;
+}
+
+int rbt_moe_layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
+  if (!c) return RBT_E_INVALID;
+  return layer_set(c, layer, d, false);
+}
+
+int rbt_moe_layer_set_device(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
+  if (!c) return RBT_E_INVALID;
+  return layer_set(c, layer, d, true);
+}
+
+int rbt_moe_forward_d(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
+                      float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  return moe_forward_dev(c, layer, x, s, out, ids_out, w_out);
+}
+
+int rbt_moe_forward(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
+                    float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  auto lit = c->layers.find(layer);
+  if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
+  if (s == 0) return RBT_OK;
+  if (!x || !out) return fail(c, RBT_E_INVALID, "null x or out");
+  const rbt_moe_layer_desc &D = lit->second.desc;
+  size_t H = D.hidden, k = std::min(D.topk, D.n_experts);
+  void *dx;
+  float *dout, *dw;
+  int32_t *di;
+  RBT_TRY(stage_in(c, SC_X, x, s * H * 4, &dx));
+  RBT_TRY(scratch_t(c, SC_OUT, s * H, &dout));
+  RBT_TRY(scratch_t(c, SC_IDS_OUT, s * k, &di));
+  RBT_TRY(scratch_t(c, SC_W_OUT, s * k, &dw));
+  RBT_TRY(moe_forward_dev(c, layer, (const float *)dx, s, dout, di, dw));
+  HIP_OK(c, hipMemcpyAsync(out, dout, s * H * 4, hipMemcpyDeviceToHost, c->stream));
+  if (ids_out) HIP_OK(c, hipMemcpyAsync(ids_out, di, s * k * 4, hipMemcpyDeviceToHost, c->stream));
+  if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, dw, s * k * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
+}
+
+int rbt_synth_mxfp4_d(rbt_ctx *c, uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,
+                      uint32_t lo, uint32_t hi) {
+  if (!c) return RBT_E_INVALID;
+  if (!data || !scale || lo > hi || hi > 255) return fail(c, RBT_E_INVALID, "bad synth arguments");
+  HIP_OK(c, rbt::launch_synth_mxfp4(*c, data, scale, rows, cols, seed, lo, hi));
+  return RBT_OK;
+}
+
+int rbt_synth_i4g_d(rbt_ctx *c, uint8_t *data, float *scale, size_t rows, size_t cols, size_t gs, uint64_t seed,
+                    float lo, float hi) {
+  if (!c) return RBT_E_INVALID;
+  if (!data || !scale || gs == 0) return fail(c, RBT_E_INVALID, "bad synth arguments");
+  HIP_OK(c, rbt::launch_synth_i4g(*c, data, scale, rows, cols, gs, seed, lo, hi));
+  return RBT_OK;
+}
+
+}  // extern "C"

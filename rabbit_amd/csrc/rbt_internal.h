@@ -1,0 +1,67 @@
+// rbt_internal.h -- host-side declarations shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/rabbit_amd.h"
+#include "rbt_device.h"
+
+namespace rbt {
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int num_cu = 256;
+};
+
+struct RouterArgs {
+  int family, E, erows, k, H, S;
+  const float *logit_bias, *router_bias;
+  int norm_topk;
+  float routed_scale;
+  int n_group, topk_group;
+  const float *x, *W;
+};
+
+// gemv.hip
+hipError_t launch_generic(const Ctx &c, int kind, float *y, const float *x, const void *data, const void *scale,
+                          size_t gs, size_t s, size_t i, size_t o);
+hipError_t launch_dequant(const Ctx &c, float *out, int kind, const void *data, const void *scale, size_t cols,
+                          size_t gs, size_t row0, size_t nrows);
+bool decode_shape_ok(size_t cols, int kind, size_t gs);
+// Decode GEMV over a job table (see gemv.hip). jobs == nullptr uses `single` for every job.
+// njobs_dev (optional) caps the job count from device memory.
+hipError_t launch_decode(const Ctx &c, bool gateup, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
+                         int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
+                         int rows, float *y, long y_stride);
+hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,
+                               const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
+                               const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride);
+
+// router.hip
+hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
+                                double *mid, double *bnd);
+hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
+                                float *wts, float *sh_scale, int *stats);
+hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);
+hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,
+                        int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq);
+hipError_t launch_combine(const Ctx &c, const float *y, int S, int k, int H, const int *tok_pair, const float *tok_w,
+                          const float *sh_scale, int has_shared, int gated, float *out);
+
+// moe.hip
+hipError_t launch_single_rows(const Ctx &c, const int32_t *ids, const float *w, int S, int k, int eid, int *pair_tok,
+                              float *pair_w, int *nr);
+hipError_t launch_accumulate(const Ctx &c, const float *y, int S, int H, const int *pair_tok, const float *pair_w,
+                             const int *nr, float *out);
+
+// synth.hip
+hipError_t launch_synth_mxfp4(const Ctx &c, uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,
+                              uint32_t lo, uint32_t hi);
+hipError_t launch_synth_i4g(const Ctx &c, uint8_t *data, float *scale, size_t rows, size_t cols, size_t gs,
+                            uint64_t seed, float lo, float hi);
+
+}  // namespace rbt

@@ -1,0 +1,573 @@
+// router.hip -- router logits, top-k selection and token -> expert grouping for gfx950.
+//
+// The reference computes every router logit as a left-to-right fp32 fold of rounded products
+// (kernels.rs:113-124, Iterator::sum) and selects on it; a tree reduction on the GPU would round
+// differently and could flip a near-tie at the k / k+1 boundary. Selection here is exact anyway:
+//
+//  1. k_router_logits: one workgroup per router row. It forms the products p_k = fl32(x_k w_k)
+//     exactly as the reference does, sums them in fp64 (S), and computes a rigorous bound B on
+//     |L_ref - S|, where L_ref is the reference's sequential fp32 result. With S_j the exact prefix
+//     sums, u = 2^-24, u' = u/(1-u) and T = sum_j |S_j|, the fold's error obeys
+//     |L_ref - S| <= u' T / (1 - n u'). T needs every prefix sum, so the workgroup runs a parallel
+//     fp64 scan. Extra slack covers the fp64 arithmetic itself.
+//  2. k_router_select: one wave per token. The fp32 interval [lo, hi] that must contain L_ref is
+//     pushed through the monotone key map (logit bias, sigmoid, selection bias), top-k is taken on
+//     the midpoints with the reference's tie rule (higher key first, lower expert id on ties), and
+//     then certified: every expert whose key interval could reach the selected set and overlaps
+//     another such interval gets its exact sequential fp32 fold recomputed (one lane each, same
+//     operation order as the reference). After that, every relevant comparison is either strict or
+//     an exact tie, so the ids are the reference's ids.
+//  3. k_group (several tokens): unique_experts order (glm52/moe.rs:333-344), per-expert token
+//     lists in token order, and per-token pick lists ordered by first occurrence.
+#include "rbt_device.h"
+#include "rbt_internal.h"
+
+namespace rbt {
+
+// ------------------------------------------------------------------------------------------------
+// 1. logits with certified error bound
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ double block_excl_scan_256(double v, double *sh, double *total) {
+  // inclusive wave scan
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  double inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    double o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) sh[wid] = inc;
+  __syncthreads();
+  double off = 0.0, tot = 0.0;
+  for (int w = 0; w < 4; w++) {
+    if (w < wid) off += sh[w];
+    tot += sh[w];
+  }
+  __syncthreads();
+  *total = tot;
+  return off + inc - v;
+}
+
+__device__ __forceinline__ double block_sum_256(double v, double *sh) {
+  v = rbt_wave_sum_d(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) sh[wid] = v;
+  __syncthreads();
+  double t = sh[0] + sh[1] + sh[2] + sh[3];
+  __syncthreads();
+  return t;
+}
+
+constexpr int ROUTER_MAXC = 32;  // cached products per thread (H <= 8192 keeps them in registers)
+
+// Rows 0..E-1 are router rows; row E (when sgate != nullptr) is the shared-expert gate vector.
+__global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__ x, int S, int H,
+                                                       const float *__restrict__ W, int E,
+                                                       const float *__restrict__ sgate, double *__restrict__ mid,
+                                                       double *__restrict__ bnd, int erows) {
+  __shared__ double sh[4];
+  const int e = blockIdx.x;
+  const float *w = e < E ? W + (size_t)e * H : sgate;
+  const int t = threadIdx.x;
+  const int c = (H + 255) / 256;
+  const int k0 = t * c;
+  const int k1 = min(k0 + c, H);
+  const double u1 = 5.9604648328104515e-08;  // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16; // 2^-53
+  for (int s = 0; s < S; s++) {
+    const float *xs = x + (size_t)s * H;
+    float pc[ROUTER_MAXC];
+    double run = 0.0, pabs = 0.0;
+    if (c <= ROUTER_MAXC) {
+#pragma unroll
+      for (int j = 0; j < ROUTER_MAXC; j++) {
+        int k = k0 + j;
+        float p = (j < c && k < k1) ? __fmul_rn(xs[k], w[k]) : 0.0f;
+        pc[j] = p;
+        run += (double)p;
+        pabs += fabs((double)p);
+      }
+    } else {
+      for (int k = k0; k < k1; k++) {
+        float p = __fmul_rn(xs[k], w[k]);
+        run += (double)p;
+        pabs += fabs((double)p);
+      }
+    }
+    double total;
+    double pre = block_excl_scan_256(run, sh, &total);
+    double T = 0.0;
+    if (c <= ROUTER_MAXC) {
+#pragma unroll
+      for (int j = 0; j < ROUTER_MAXC; j++) {
+        if (j < c && k0 + j < k1) {
+          pre += (double)pc[j];
+          T += fabs(pre);
+        }
+      }
+    } else {
+      for (int k = k0; k < k1; k++) {
+        pre += (double)__fmul_rn(xs[k], w[k]);
+        T += fabs(pre);
+      }
+    }
+    T = block_sum_256(T, sh);
+    double P = block_sum_256(pabs, sh);
+    if (t == 0) {
+      double n = (double)H;
+      double slack = 4.0 * n * e64 * (P + T) + n * n * e64 * P;
+      double Tu = T * (1.0 + 4.0 * n * e64) + slack;
+      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
+      B = B * (1.0 + 1e-9) + 1e-300;
+      mid[(size_t)s * erows + e] = total;
+      bnd[(size_t)s * erows + e] = B;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// 2. per-token selection
+// ------------------------------------------------------------------------------------------------
+// sigmoid as the reference writes it, 1/(1 + exp(-v)), with exp correctly rounded to f32 (the
+// reference calls the platform libm's expf).
+__device__ __forceinline__ float sigmoid_ref(float v) {
+  float e = (float)exp(-(double)v);
+  return __fdiv_rn(1.0f, __fadd_rn(1.0f, e));
+}
+
+struct SelParams {
+  int family;  // RBT_FAMILY_*
+  int E, erows, k, H, S;
+  const float *logit_bias;   // may be null
+  const float *router_bias;  // may be null
+  int norm_topk;
+  float routed_scale;
+  int n_group, topk_group;
+  const float *x;  // [S, H] for exact recomputation
+  const float *W;  // [E, H]
+};
+
+// Selection key of one logit value for the family (monotone non-decreasing in the logit).
+__device__ __forceinline__ float sel_key(const SelParams &P, int e, float l) {
+  if (P.logit_bias) l = __fadd_rn(l, P.logit_bias[e]);
+  if (P.family == RBT_FAMILY_QWEN38) return l;
+  float p = sigmoid_ref(l);
+  return P.router_bias ? __fadd_rn(p, P.router_bias[e]) : p;
+}
+
+// (key desc, id asc) ordering: true if (ka, a) ranks before (kb, b).
+__device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
+  return ka > kb || (ka == kb && a < b);
+}
+
+constexpr int SEL_MAXE = 2048;
+constexpr int SEL_MAXK = 64;
+
+// Top-k over keys[] restricted to allowed (nullptr = all); writes out[0..k). One wave.
+__device__ void wave_topk(const float *keys, const unsigned char *allowed, int E, int k, int *out) {
+  const int lane = threadIdx.x & 63;
+  __shared__ unsigned char taken[SEL_MAXE];
+  for (int e = lane; e < E; e += 64) taken[e] = 0;
+  __syncthreads();
+  for (int r = 0; r < k; r++) {
+    float bk = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int e = lane; e < E; e += 64) {
+      if (taken[e] || (allowed && !allowed[e])) continue;
+      if (bi == 0x7fffffff || ranks_before(keys[e], e, bk, bi)) { bk = keys[e]; bi = e; }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      float ok = __shfl_xor(bk, m, 64);
+      int oi = __shfl_xor(bi, m, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || ranks_before(ok, oi, bk, bi))) { bk = ok; bi = oi; }
+    }
+    if (lane == 0) {
+      out[r] = bi;
+      if (bi != 0x7fffffff) taken[bi] = 1;
+    }
+    __syncthreads();
+  }
+}
+
+// The reference's sequential logit: fold(-0.0, +) of fl32(x_k * w_k), k ascending.
+__device__ float exact_logit(const float *xs, const float *w, int H) {
+  float a = -0.0f;
+  for (int k = 0; k < H; k++) a = __fadd_rn(a, __fmul_rn(xs[k], w[k]));
+  return a;
+}
+
+__global__ __launch_bounds__(64) void k_router_select(SelParams P, const double *__restrict__ mid,
+                                                      const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                      float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                      int *__restrict__ stats) {
+  __shared__ float klo[SEL_MAXE], khi[SEL_MAXE], kmid[SEL_MAXE], lmid[SEL_MAXE];
+  __shared__ unsigned char exact[SEL_MAXE], allowed[SEL_MAXE];
+  __shared__ int sel[SEL_MAXK];
+  __shared__ int amb_list[SEL_MAXE];
+  __shared__ int namb;
+  __shared__ float kth_lo;
+  const int lane = threadIdx.x;
+  const int s = blockIdx.x;
+  const int E = P.E, k = P.k;
+  const double *ms = mid + (size_t)s * P.erows;
+  const double *bs = bnd + (size_t)s * P.erows;
+
+  for (int e = lane; e < E; e += 64) {
+    double m = ms[e], b = bs[e];
+    float lo = __double2float_rd(m - b * (1.0 + 1e-12));
+    float hi = __double2float_ru(m + b * (1.0 + 1e-12));
+    float md = __double2float_rn(m);
+    if (md < lo) md = lo;
+    if (md > hi) md = hi;
+    lmid[e] = md;
+    klo[e] = sel_key(P, e, lo);
+    khi[e] = sel_key(P, e, hi);
+    kmid[e] = sel_key(P, e, md);
+    exact[e] = (lo == hi);
+  }
+  if (lane == 0) namb = 0;
+  __syncthreads();
+
+  // Group restriction (rank_top_grouped, glm52/moe.rs:214-229) needs group scores from the keys;
+  // for n_group > 1 every group's top-2 sum must itself be certain, so its experts are made exact.
+  const bool grouped = P.family != RBT_FAMILY_QWEN38 && P.n_group > 1;
+  if (grouped) {
+    for (int e = lane; e < E; e += 64) {
+      if (!exact[e]) {
+        float l = exact_logit(P.x + (size_t)s * P.H, P.W + (size_t)e * P.H, P.H);
+        lmid[e] = l;
+        klo[e] = khi[e] = kmid[e] = sel_key(P, e, l);
+        exact[e] = 1;
+      }
+    }
+    __syncthreads();
+    if (lane == 0) {
+      int gsz = E / P.n_group;
+      float gs[64];
+      int ord[64];
+      for (int g = 0; g < P.n_group; g++) {
+        float t1 = -INFINITY, t2 = -INFINITY;
+        for (int e = g * gsz; e < (g + 1) * gsz; e++) {
+          float v = kmid[e];
+          if (v > t1) { t2 = t1; t1 = v; }
+          else if (v > t2) { t2 = v; }
+        }
+        gs[g] = isfinite(t2) ? __fadd_rn(t1, t2) : t1;
+        ord[g] = g;
+      }
+      for (int a = 1; a < P.n_group; a++) {
+        int cur = ord[a], b = a;
+        while (b > 0 && (gs[ord[b - 1]] < gs[cur] || (gs[ord[b - 1]] == gs[cur] && ord[b - 1] > cur))) {
+          ord[b] = ord[b - 1];
+          b--;
+        }
+        ord[b] = cur;
+      }
+      for (int e = 0; e < E; e++) allowed[e] = 0;
+      for (int t = 0; t < P.topk_group && t < P.n_group; t++)
+        for (int e = ord[t] * gsz; e < (ord[t] + 1) * gsz; e++) allowed[e] = 1;
+    }
+    __syncthreads();
+  }
+  int kk = k;
+  if (grouped) {
+    int na = 0;
+    for (int e = 0; e < E; e++) na += allowed[e];
+    if (kk > na) kk = na;
+  }
+
+  wave_topk(kmid, grouped ? allowed : nullptr, E, kk, sel);
+
+  // Certify: R = experts whose upper key reaches the lowest selected lower key.
+  if (lane == 0) {
+    float m = INFINITY;
+    for (int r = 0; r < kk; r++) m = fminf(m, klo[sel[r]]);
+    kth_lo = m;
+  }
+  // R as a list (set semantics: its order does not matter).
+  __shared__ int rlist[SEL_MAXE];
+  __shared__ int nr;
+  if (lane == 0) nr = 0;
+  __syncthreads();
+  for (int e = lane; e < E; e += 64) {
+    if ((grouped && !allowed[e]) || khi[e] < kth_lo) continue;
+    rlist[atomicAdd(&nr, 1)] = e;
+  }
+  __syncthreads();
+  const int nR = nr;
+  for (int j = lane; j < nR; j += 64) {
+    const int e = rlist[j];
+    if (exact[e]) continue;
+    // e is in R and not exact: ambiguous if its interval overlaps any other member of R.
+    bool a = false;
+    for (int m = 0; m < nR && !a; m++) {
+      const int f = rlist[m];
+      if (f != e && klo[e] <= khi[f] && klo[f] <= khi[e]) a = true;
+    }
+    if (a) amb_list[atomicAdd(&namb, 1)] = e;
+  }
+  __syncthreads();
+  const int na = namb;
+  if (na > 0) {
+    for (int j = lane; j < na; j += 64) {
+      int e = amb_list[j];
+      float l = exact_logit(P.x + (size_t)s * P.H, P.W + (size_t)e * P.H, P.H);
+      lmid[e] = l;
+      klo[e] = khi[e] = kmid[e] = sel_key(P, e, l);
+      exact[e] = 1;
+    }
+    __syncthreads();
+    wave_topk(kmid, grouped ? allowed : nullptr, E, kk, sel);
+  }
+  if (lane == 0 && stats) atomicAdd(stats, na);
+
+  // Weights.
+  if (lane == 0) {
+    int32_t *io = ids + (size_t)s * k;
+    float *wo = wts + (size_t)s * k;
+    if (P.family == RBT_FAMILY_QWEN38) {
+      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
+      float lv[SEL_MAXK];
+      for (int r = 0; r < kk; r++) {
+        int e = sel[r];
+        lv[r] = P.logit_bias ? __fadd_rn(lmid[e], P.logit_bias[e]) : lmid[e];
+      }
+      float mx = lv[0], sum = 0.0f;
+      for (int r = 0; r < kk; r++) {
+        lv[r] = (float)exp((double)__fsub_rn(lv[r], mx));
+        sum = __fadd_rn(sum, lv[r]);
+      }
+      for (int r = 0; r < kk; r++) {
+        io[r] = sel[r];
+        wo[r] = __fdiv_rn(lv[r], sum);
+      }
+    } else {
+      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
+      float wv[SEL_MAXK];
+      for (int r = 0; r < kk; r++) {
+        int e = sel[r];
+        float l = P.logit_bias ? __fadd_rn(lmid[e], P.logit_bias[e]) : lmid[e];
+        wv[r] = sigmoid_ref(l);
+      }
+      if (P.norm_topk) {
+        float sum = -0.0f;
+        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, wv[r]);
+        sum = __fadd_rn(sum, 1e-20f);
+        for (int r = 0; r < kk; r++) wv[r] = __fdiv_rn(wv[r], sum);
+      }
+      for (int r = 0; r < kk; r++) {
+        io[r] = sel[r];
+        wo[r] = __fmul_rn(wv[r], P.routed_scale);
+      }
+    }
+    for (int r = kk; r < k; r++) {
+      io[r] = -1;
+      wo[r] = 0.0f;
+    }
+    if (sh_scale) {
+      float gl = (P.erows > E) ? __double2float_rn(ms[E]) : 0.0f;
+      sh_scale[s] = (P.erows > E) ? sigmoid_ref(gl) : 1.0f;
+    }
+  }
+}
+
+// Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
+// interval is a point (bound 0) and the same selection code applies.
+__global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
+                                double *__restrict__ bnd) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    mid[i] = (double)logits[i];
+    bnd[i] = 0.0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// 3. grouping: pairs (token, slot) ordered by (unique_experts position, token).
+//   pair_job[p]   -> expert device view (table lookup), or the shared expert for p >= S*k
+//   pair_tok[p]   -> token index
+//   tok_pair[t*k + j] -> the t-th token's pairs sorted by unique_experts position
+//   tok_w[t*k + j]    -> matching routing weight
+// One workgroup; thread e handles expert e.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids, const float *__restrict__ wts, int S,
+                                                int k, int E, const RbtExpertDev *__restrict__ table,
+                                                const RbtExpertDev *__restrict__ shared_dev, RbtExpertDev *pair_job,
+                                                int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
+  extern __shared__ int smem[];
+  int *first = smem;       // [E]
+  int *cnt = smem + E;     // [E]
+  int *off = smem + 2 * E; // [E]
+  const int P = S * k;
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    first[e] = 0x7fffffff;
+    cnt[e] = 0;
+  }
+  __syncthreads();
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    int e = ids[p];
+    if (e >= 0 && e < E) {
+      atomicMin(&first[e], p);
+      atomicAdd(&cnt[e], 1);
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int o = 0;
+    if (cnt[e] > 0)
+      for (int f = 0; f < E; f++)
+        if (cnt[f] > 0 && first[f] < first[e]) o += cnt[f];
+    off[e] = o;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && nuniq) {
+    int u = 0;
+    for (int e = 0; e < E; e++) u += cnt[e] > 0;
+    *nuniq = u;
+  }
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    if (cnt[e] == 0) continue;
+    int c = 0;
+    RbtExpertDev J = table[e];
+    if (J.gd == nullptr || J.dd == nullptr) atomicOr(err, 1);
+    for (int t = 0; t < S; t++) {
+      for (int j = 0; j < k; j++) {
+        if (ids[t * k + j] == e) {
+          int p = off[e] + c++;
+          pair_job[p] = J;
+          pair_tok[p] = t;
+          tok_pair[t * k + j] = p;  // unsorted for now
+          tok_w[t * k + j] = wts[t * k + j];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // shared-expert pairs, and per-token sort of the picks by pair index (= first-occurrence order)
+  for (int t = threadIdx.x; t < S; t += blockDim.x) {
+    pair_job[P + t] = *shared_dev;
+    pair_tok[P + t] = t;
+    int *tp = tok_pair + t * k;
+    float *tw = tok_w + t * k;
+    for (int a = 1; a < k; a++) {
+      int cp = tp[a];
+      float cw = tw[a];
+      int b = a;
+      while (b > 0 && (unsigned)tp[b - 1] > (unsigned)cp) {
+        tp[b] = tp[b - 1];
+        tw[b] = tw[b - 1];
+        b--;
+      }
+      tp[b] = cp;
+      tw[b] = cw;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// combine: out[t, d] = sum over t's picks (unique_experts order) of w * y[pair, d], accumulated in
+// fp32 with separate roundings (glm52/moe.rs:508-512), then + shared (qwen38/generate.rs:346-349)
+// scaled by the token's shared gate (qwen38/generate.rs:316-322) when gated.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, int S, int k, int H,
+                                                 const int *__restrict__ tok_pair, const float *__restrict__ tok_w,
+                                                 const float *__restrict__ sh_scale, int has_shared, int gated,
+                                                 float *__restrict__ out) {
+  size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)S * H) return;
+  int t = (int)(idx / H), d = (int)(idx % H);
+  float acc = 0.0f;
+  for (int j = 0; j < k; j++) {
+    int p = tok_pair[t * k + j];
+    if (p < 0) continue;
+    acc = __fadd_rn(acc, __fmul_rn(tok_w[t * k + j], y[(size_t)p * H + d]));
+  }
+  if (has_shared) {
+    float sh = y[((size_t)S * k + t) * H + d];
+    if (gated) sh = __fmul_rn(sh, sh_scale[t]);
+    acc = __fadd_rn(acc, sh);
+  }
+  out[idx] = acc;
+}
+
+// Single-token routing writes the grouping directly: pair j = slot j.
+__global__ void k_group_s1(const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
+                           const RbtExpertDev *__restrict__ table, const RbtExpertDev *__restrict__ shared_dev,
+                           RbtExpertDev *pair_job, int *pair_tok, int *tok_pair, float *tok_w, int *err) {
+  int j = threadIdx.x;
+  if (j < k) {
+    int e = ids[j];
+    RbtExpertDev J = {};
+    if (e >= 0 && e < E) J = table[e];
+    if (e >= 0 && (J.gd == nullptr || J.dd == nullptr)) atomicOr(err, 1);
+    pair_job[j] = J;
+    pair_tok[j] = 0;
+    tok_pair[j] = e >= 0 ? j : -1;
+    tok_w[j] = wts[j];
+  } else if (j == k) {
+    pair_job[k] = *shared_dev;
+    pair_tok[k] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// launchers
+// ------------------------------------------------------------------------------------------------
+hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
+                                double *mid, double *bnd) {
+  int erows = E + (sgate ? 1 : 0);
+  hipLaunchKernelGGL(k_router_logits, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
+                                float *wts, float *sh_scale, int *stats) {
+  SelParams P;
+  P.family = a.family;
+  P.E = a.E;
+  P.erows = a.erows;
+  P.k = a.k;
+  P.H = a.H;
+  P.S = a.S;
+  P.logit_bias = a.logit_bias;
+  P.router_bias = a.router_bias;
+  P.norm_topk = a.norm_topk;
+  P.routed_scale = a.routed_scale;
+  P.n_group = a.n_group;
+  P.topk_group = a.topk_group;
+  P.x = a.x;
+  P.W = a.W;
+  hipLaunchKernelGGL(k_router_select, dim3(a.S), dim3(64), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+  return hipGetLastError();
+}
+
+hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_logits_to_mid, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c.stream, logits, n, mid, bnd);
+  return hipGetLastError();
+}
+
+hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,
+                        int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
+  if (S == 1) {
+    hipLaunchKernelGGL(k_group_s1, dim3(1), dim3(((k + 1 + 63) / 64) * 64), 0, c.stream, ids, wts, k, E, table,
+                       shared_dev, pair_job, pair_tok, tok_pair, tok_w, err);
+  } else {
+    size_t smem = (size_t)3 * E * sizeof(int);
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), smem, c.stream, ids, wts, S, k, E, table, shared_dev, pair_job,
+                       pair_tok, tok_pair, tok_w, err, nuniq);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const Ctx &c, const float *y, int S, int k, int H, const int *tok_pair, const float *tok_w,
+                          const float *sh_scale, int has_shared, int gated, float *out) {
+  size_t n = (size_t)S * H;
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c.stream, y, S, k, H, tok_pair, tok_w,
+                     sh_scale, has_shared, gated, out);
+  return hipGetLastError();
+}
+
+}  // namespace rbt

@@ -1,0 +1,34 @@
+"""Shared helpers for the tests: seeded inputs, tolerances, reference-style PRNG."""
+import numpy as np
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+def xorshift_vec(n: int, seed: int) -> np.ndarray:
+    """The reference tests' PRNG (kernels.rs:1311-1321): xorshift32 mapped to ~U(-1, 1) in f32."""
+    s = seed & 0xFFFFFFFF
+    out = np.empty(n, np.float32)
+    for i in range(n):
+        s ^= (s << 13) & 0xFFFFFFFF
+        s ^= s >> 17
+        s ^= (s << 5) & 0xFFFFFFFF
+        out[i] = (np.float32(s) / np.float32(4294967295.0) - np.float32(0.5)) * np.float32(2.0)
+    return out
+
+
+def normal(shape, seed, std=1.0) -> np.ndarray:
+    return (np.random.default_rng(seed).standard_normal(shape) * std).astype(np.float32)
+
+
+def bits_equal(a, b) -> bool:
+    """Bitwise equality of f32 arrays, treating any two NaNs as equal."""
+    a = np.ascontiguousarray(a, np.float32).ravel()
+    b = np.ascontiguousarray(b, np.float32).ravel()
+    same = a.view(np.uint32) == b.view(np.uint32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(same | both_nan))

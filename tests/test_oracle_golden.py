@@ -1,0 +1,332 @@
+"""Pins the CPU oracle: the reference's own known-answer tests (tests/golden/kats.json), closed forms,
+and brute force on small inputs. Each check is chosen so that a plausible restatement mistake (a
+dropped term, a wrong sign or index, a fused multiply-add, a transposed operand) fails it."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from helpers import bits_equal, rel_l2, xorshift_vec
+
+KATS = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "kats.json")))
+
+
+def f32(v):
+    return np.float32(v)
+
+
+# ---- quant.rs ---------------------------------------------------------------------------------
+def test_e2m1_table_kat(orc):
+    k = KATS["e2m1_table"]
+    got = np.array([orc.e2m1_decode(c) for c in k["codes"]], np.float32)
+    assert bits_equal(got, np.array(k["values"], np.float32))  # includes -0.0 for code 8
+
+
+def test_e8m0_points_and_exhaustive_powers_of_two(orc):
+    k = KATS["e8m0_points"]
+    for b, v in zip(k["bytes"], k["values"]):
+        assert orc.e8m0_decode(b) == v
+    # quant.rs:895-905: every byte 0..254 equals 2^(b-127) exactly (byte 0 is the subnormal 2^-127)
+    for b in range(255):
+        assert orc.e8m0_decode(b) == math.ldexp(1.0, b - 127), b
+    assert orc.e8m0_decode_bits(255) == 0x7F800000  # quant.rs:391-396: +inf bits, not NaN
+    assert orc.e8m0_decode_bits(0) == 1 << 22
+
+
+def test_row_f32_disk_bytes_kat(orc):
+    k = KATS["disk_bytes"]
+    q = orc.QT.mxfp4(np.array(k["data"], np.uint8), np.array(k["scale"], np.uint8), 1, k["cols"])
+    assert bits_equal(q.row_f32(0), np.array(k["row0"], np.float32))
+
+
+def test_row_f32_mxfp4_closed_form_every_byte_and_scale(orc):
+    # Every data byte with every scale byte: w = e2m1(n) * 2^(b-127) exactly (quant.rs:325-339).
+    mags = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0]
+    data = np.arange(256, dtype=np.uint8)  # one row of 512 elements = 16 blocks
+    for sb in list(range(0, 256, 7)) + [0, 1, 254, 255]:
+        scale = np.full(16, sb, np.uint8)
+        got = orc.QT.mxfp4(data, scale, 1, 512).row_f32(0)
+        sc = math.ldexp(1.0, sb - 127) if sb < 255 else math.inf
+        exp = []
+        for byte in range(256):
+            for nib in (byte & 0xF, byte >> 4):
+                m = mags[nib & 7]
+                v = np.float32(m) * np.float32(sc) if not (m == 0.0 and sc == math.inf) else np.float32(np.nan)
+                exp.append(-v if nib & 8 else v)
+        assert bits_equal(got, np.array(exp, np.float32)), sb
+
+
+def test_row_f32_i4g_closed_form(orc):
+    rows, cols, gs = 3, 37, 8  # partial trailing group (quant.rs:606-623 fixture shape)
+    rng = np.random.default_rng(0)
+    nib = rng.integers(0, 16, (rows, cols))
+    data = np.zeros((rows, (cols + 1) // 2), np.uint8)
+    for r in range(rows):
+        for k in range(cols):
+            data[r, k // 2] |= nib[r, k] << (4 * (k % 2))
+    ng = (cols + gs - 1) // gs
+    scale = rng.uniform(0.005, 0.02, (rows, ng)).astype(np.float32)
+    q = orc.QT.i4g(data, scale, rows, cols, gs)
+    for r in range(rows):
+        exp = np.array([np.float32(nib[r, k] - 8) * scale[r, k // gs] for k in range(cols)], np.float32)
+        assert bits_equal(q.row_f32(r), exp)
+
+
+def test_resident_bytes(orc):
+    # quant.rs:1011-1017 (resident_bytes_matches_format) plus the MXFP4/grouped formulas
+    assert orc.QT.mxfp4(np.zeros(10 * 50, np.uint8), np.zeros(10 * 4, np.uint8), 10, 100).resident_bytes() == \
+        10 * 50 + 10 * 4
+    assert orc.QT.i4g(np.zeros(10 * 50, np.uint8), np.zeros(10 * 4, np.float32), 10, 100, 25).resident_bytes() == \
+        10 * 50 + 10 * 4 * 4
+
+
+# ---- kernels.rs --------------------------------------------------------------------------------
+def test_matmul_kat(orc):
+    k = KATS["matmul"]
+    y = orc.matmul(np.array(k["x"], np.float32), np.array(k["w"], np.float32), k["s"], k["i"], k["o"])
+    assert list(y) == k["y"]
+
+
+def seq_dot_f32(x, w):
+    """Left-to-right fold of rounded f32 products, one rounding per operation (pure Python)."""
+    a = np.float32(-0.0)
+    for xv, wv in zip(x.astype(np.float32), w.astype(np.float32)):
+        a = np.float32(a + np.float32(xv * wv))
+    return a
+
+
+def test_matmul_sequential_order_brute_force(orc):
+    s, i, o = 2, 301, 5
+    x = xorshift_vec(s * i, 7) * 3
+    w = xorshift_vec(o * i, 8)
+    y = orc.matmul(x, w, s, i, o).reshape(s, o)
+    for si in range(s):
+        for oi in range(o):
+            assert y[si, oi] == seq_dot_f32(x[si * i:(si + 1) * i], w[oi * i:(oi + 1) * i])
+
+
+def test_mxfp4_two_block_kat(orc):
+    k = KATS["mxfp4_two_block"]
+    args = (np.array(k["x"], np.float32), np.array(k["data"], np.uint8), np.array(k["block_scale"], np.uint8), 1,
+            k["cols"], 1)
+    assert list(orc.matmul_mxfp4_scalar(*args)) == k["y"]
+    assert list(orc.matmul_mxfp4_tier(*args)) == k["y"]
+
+
+def test_i4g_two_group_kat(orc):
+    k = KATS["i4g_two_group"]
+    y = orc.matmul_i4_grouped(np.array(k["x"], np.float32), np.array(k["q4"], np.uint8),
+                              np.array(k["scale"], np.float32), k["gs"], 1, k["cols"], 1)
+    assert list(y) == k["y"]
+
+
+def test_mxfp4_scalar_brute_force_sequential(orc):
+    # a += (x*e2m1)*e8m0, sequential, no FMA (kernels.rs:247-267); odd cols and a partial block
+    rows, cols, s = 4, 77, 2
+    q = orc.synth_mxfp4(rows, cols, seed=5, exp_lo=100, exp_hi=140)
+    x = xorshift_vec(s * cols, 3)
+    y = orc.matmul_mxfp4_scalar(x, q.data, q.scale, s, cols, rows).reshape(s, rows)
+    dense = q.dense()
+    for si in range(s):
+        for r in range(rows):
+            a = np.float32(0.0)
+            for k in range(cols):
+                e = dense[r, k]
+                sc = np.float32(math.ldexp(1.0, int(q.scale[r * 3 + k // 32]) - 127))
+                m = np.float32(e / sc)  # exact: e2m1 value
+                a = np.float32(a + np.float32(np.float32(x[si * cols + k] * m) * sc))
+            assert y[si, r] == a
+
+
+def test_i4g_brute_force_sequential(orc):
+    rows, cols, gs, s = 3, 70, 16, 2
+    q = orc.synth_i4g(rows, cols, gs, seed=9)
+    x = xorshift_vec(s * cols, 4)
+    y = orc.matmul_i4_grouped(x, q.data, q.scale, gs, s, cols, rows).reshape(s, rows)
+    ng = (cols + gs - 1) // gs
+    for si in range(s):
+        for r in range(rows):
+            a = np.float32(0.0)
+            for k in range(cols):
+                byte = q.data[r * ((cols + 1) // 2) + k // 2]
+                n = (byte >> (4 * (k % 2))) & 0xF
+                a = np.float32(a + np.float32(np.float32(x[si * cols + k] * np.float32(int(n) - 8)) *
+                                              q.scale[r * ng + k // gs]))
+            assert y[si, r] == a
+
+
+def test_matmul_qt_mxfp4_matches_dequant_dot(orc):
+    # kernels.rs:1570-1596: within 1e-3 of row_f32 dotted sequentially
+    rows, cols, s = 5, 96, 2
+    q = orc.synth_mxfp4(rows, cols, seed=31)
+    x = xorshift_vec(s * cols, 32)
+    dense = q.dense().astype(np.float64)
+    exp = (x.reshape(s, cols).astype(np.float64) @ dense.T)
+    for simd in (False, True):
+        y = orc.matmul_qt(x, q, s, simd=simd).reshape(s, rows)
+        assert np.max(np.abs(y - exp)) < 1e-3
+
+
+@pytest.mark.parametrize("tier", ["avx2", "avx512"])
+def test_simd_tiers_within_tolerance_of_scalar(orc, tier):
+    k = KATS["tier_cols"]
+    if tier == "avx512" and not orc.lib().orc_cpu_has_avx512():
+        pytest.skip("no AVX-512F/BW")
+    if tier == "avx2" and not orc.lib().orc_cpu_has_avx2():
+        pytest.skip("no AVX2")
+    for cols in k["cols"]:
+        q = orc.synth_mxfp4(k["rows"], cols, seed=cols * 3 + 9, exp_lo=120, exp_hi=134)
+        x = xorshift_vec(cols, cols * 7 + 10)
+        ys = orc.matmul_mxfp4_scalar(x, q.data, q.scale, 1, cols, k["rows"])
+        yt = orc.matmul_mxfp4_tier(x, q.data, q.scale, 1, cols, k["rows"], tier=tier)
+        assert np.max(np.abs(ys - yt)) < k["tol"], cols
+
+
+def test_simd_tier_large_rel_l2(orc):
+    q = orc.synth_mxfp4(64, 8192, seed=1)
+    x = np.random.default_rng(1).standard_normal(8192).astype(np.float32)
+    ys = orc.matmul_mxfp4_scalar(x, q.data, q.scale, 1, 8192, 64)
+    yt = orc.matmul_mxfp4_tier(x, q.data, q.scale, 1, 8192, 64)
+    assert rel_l2(yt, ys) < 1e-5
+
+
+# ---- routers -----------------------------------------------------------------------------------
+def test_route_select_kat(orc):
+    k = KATS["route_select"]
+    ids, w = orc.route_softmax(np.array(k["logits"], np.float32), k["k"])
+    assert list(ids) == k["ids"]
+    assert w[0] > w[1] > w[2]
+
+
+def test_route_ties_and_k_ge_n(orc):
+    for c in KATS["route_ties"]["cases"]:
+        ids, _ = orc.route_softmax(np.array(c["logits"], np.float32), c["k"])
+        assert list(ids) == c["ids"]
+    k = KATS["route_k_ge_n"]
+    ids, w = orc.route_softmax(np.array(k["logits"], np.float32), k["k"])
+    assert list(ids) == k["ids"] and abs(float(w.sum()) - 1.0) < 1e-6
+    ids, w = orc.route_softmax(np.array(k["logits"], np.float32), 0)
+    assert len(ids) == 0
+
+
+def test_route_matches_hf_transcription(orc):
+    from golden.make_golden import lcg_logits
+    k = KATS["route_hf"]
+    for c in k["cases"]:
+        ids, w = orc.route_softmax(lcg_logits(k["n"], c["seed"]), k["k"])
+        assert list(ids) == c["ids"]
+        assert np.max(np.abs(w - np.array(c["weights"], np.float32))) < k["tol"]
+
+
+def test_route_shift_invariance(orc):
+    from golden.make_golden import lcg_logits
+    l = lcg_logits(128, 11)
+    a_ids, a_w = orc.route_softmax(l, 10)
+    b_ids, b_w = orc.route_softmax((l + np.float32(17.5)).astype(np.float32), 10)
+    assert list(a_ids) == list(b_ids) and np.max(np.abs(a_w - b_w)) < 1e-6
+
+
+def test_glm_selection_uses_biased_score_weight_uses_plain_sigmoid(orc):
+    k = KATS["glm_select_vs_weight"]
+    logits = orc.matmul(np.array(k["x"], np.float32), np.array(k["router"], np.float32), 1, 2, 2)
+    ids, w = orc.route_sigmoid(logits, k["k"], bias=np.array(k["bias"], np.float32), norm_topk=False)
+    assert list(ids) == k["ids"] and abs(w[0] - k["weight"]) < k["tol"]
+
+
+def test_glm_norm_topk_sums_to_routed_scale(orc):
+    k = KATS["glm_norm_topk"]
+    logits = xorshift_vec(5, 3)
+    ids, w = orc.route_sigmoid(logits, 3, bias=xorshift_vec(5, 4), norm_topk=True, routed_scale=k["routed_scale"])
+    assert abs(float(w.sum()) - k["routed_scale"]) < k["tol"]
+
+
+def test_glm_grouped_kats(orc):
+    for c in KATS["glm_grouped"]["cases"]:
+        # The KATs rank raw choice values; sigmoid is strictly monotone on them, so feeding the
+        # logit = choice through route_sigmoid must give the same ids.
+        ids, _ = orc.route_sigmoid(np.array(c["choice"], np.float32), c["k"], norm_topk=False,
+                                   n_group=c["n_group"], topk_group=c["topk_group"])
+        assert list(ids) == c["ids"]
+
+
+def test_unique_experts_first_occurrence_order(orc):
+    ids = np.array([[5, 2, 9], [2, 7, 5], [1, 9, 3]], np.int32)
+    assert list(orc.unique_experts(ids)) == [5, 2, 9, 7, 1, 3]
+
+
+# ---- experts and layers ------------------------------------------------------------------------
+def test_fused_gate_up_matches_separate_bit_exact(orc):
+    k = KATS["fused_separate"]
+    d, i = k["d"], k["i"]
+    gate = xorshift_vec(i * d, 7)
+    up = xorshift_vec(i * d, 8)
+    down = xorshift_vec(d * i, 9)
+    sep = orc.Slot(0, orc.QT.f32(down, d, i), gate=orc.QT.f32(gate, i, d), up=orc.QT.f32(up, i, d))
+    fus = orc.Slot(0, orc.QT.f32(down, d, i), gate_up=orc.QT.f32(np.concatenate([gate, up]), 2 * i, d))
+    x = xorshift_vec(3 * d, 10)
+    ids = np.zeros((3, 1), np.int32)
+    w = np.array(k["weights"], np.float32).reshape(3, 1)
+    a = orc.apply_single_expert(sep, ids, w, x, d, i, np.zeros(3 * d, np.float32))
+    b = orc.apply_single_expert(fus, ids, w, x, d, i, np.zeros(3 * d, np.float32))
+    assert bits_equal(a, b)
+
+
+def _np_expert(x, g, u, dn):
+    gg = x @ g.T
+    uu = x @ u.T
+    h = gg / (1.0 + np.exp(-gg)) * uu
+    return h @ dn.T
+
+
+def test_moe_forward_matches_independent_sum(orc):
+    # glm52/moe.rs:1037-1136 pattern: an independent full sum (fp64 numpy) over every routed expert
+    d, i, E, s = 64, 32, 6, 3
+    experts = {}
+    dense = {}
+    for e in range(E):
+        g = orc.synth_mxfp4(i, d, seed=100 + 3 * e)
+        u = orc.synth_mxfp4(i, d, seed=101 + 3 * e)
+        dn = orc.synth_mxfp4(d, i, seed=102 + 3 * e)
+        experts[e] = orc.Slot(e, dn, gate=g, up=u)
+        dense[e] = (g.dense(), u.dense(), dn.dense())
+    sg, su, sd = orc.synth_mxfp4(i, d, seed=7), orc.synth_mxfp4(i, d, seed=8), orc.synth_mxfp4(d, i, seed=9)
+    shared = orc.Slot(0, sd, gate=sg, up=su)
+    rng = np.random.default_rng(3)
+    router = (rng.standard_normal((E, d)) * 0.3).astype(np.float32)
+    gvec = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    x = rng.standard_normal((s, d)).astype(np.float32)
+    for fam in (orc.FAMILY_QWEN38, orc.FAMILY_GLM52):
+        L = orc.MoeLayer(fam, d, i, E, 3, router, experts, shared=shared,
+                         shared_gate=gvec if fam == orc.FAMILY_QWEN38 else None)
+        out, ids, w = L.forward(x, s)
+        exp = np.zeros((s, d))
+        x64 = x.astype(np.float64)
+        for t in range(s):
+            for j in range(3):
+                g, u, dn = dense[int(ids[t, j])]
+                exp[t] += w[t, j] * _np_expert(x64[t:t + 1], g, u, dn)[0]
+            sh = _np_expert(x64[t:t + 1], sg.dense(), su.dense(), sd.dense())[0]
+            if fam == orc.FAMILY_QWEN38:
+                sh = sh / (1.0 + np.exp(-(x64[t] @ gvec)))
+            exp[t] += sh
+        assert rel_l2(out, exp) < 1e-5
+        # routing itself: logits by the sequential fold, then the family's router
+        lg = L.router_logits(x, s)
+        for t in range(s):
+            if fam == orc.FAMILY_QWEN38:
+                rid, rw = orc.route_softmax(lg[t], 3)
+            else:
+                rid, rw = orc.route_sigmoid(lg[t], 3)
+            assert list(rid) == list(ids[t]) and bits_equal(rw, w[t])
+
+
+def test_synth_generator_distribution(orc):
+    q = orc.synth_mxfp4(256, 1024, seed=42)
+    nib = np.concatenate([q.data & 0xF, q.data >> 4])
+    hist = np.bincount(nib, minlength=16)
+    assert hist.min() > 0.9 * hist.mean() and hist.max() < 1.1 * hist.mean()
+    assert q.scale.min() == 119 and q.scale.max() == 123
+    g = orc.synth_i4g(64, 256, 32, seed=1)
+    assert g.scale.min() >= 0.005 and g.scale.max() < 0.02
