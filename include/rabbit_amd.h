@@ -196,6 +196,20 @@ int rbt_moe_forward(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, floa
 int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
                       int32_t *ids_out, float *w_out);
 
+/* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
+typedef struct {
+    double router_ms;    /* router logits + top-k selection + grouping */
+    double gateup_ms;    /* gate/up dequant-GEMV with SiLU (all experts of the call) */
+    double down_ms;      /* down dequant-GEMV */
+    double combine_ms;   /* weighted combine + shared expert */
+    uint64_t calls;      /* rbt_moe_forward_d calls recorded */
+    uint64_t ambiguous;  /* router logits recomputed exactly because of a near-tie */
+} rbt_profile;
+/* When on, rbt_moe_forward_d records HIP events on the context stream around each phase. */
+int rbt_profile_enable(rbt_ctx *ctx, int32_t on);
+/* Synchronises the stream and returns the accumulated phase times; reset != 0 clears them. */
+int rbt_profile_read(rbt_ctx *ctx, rbt_profile *out, int32_t reset);
+
 /* ---- synthetic workload generator (benchmarks and tests; bit-identical to oracle/) ------------ */
 /* Fills an MXFP4 [rows, cols] matrix in device memory: nibbles uniform over 0..15, E8M0 bytes
  * uniform over exp_lo..exp_hi, from a counter-based hash of `seed`. */

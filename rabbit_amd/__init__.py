@@ -113,7 +113,7 @@ class Context:
         h = C.c_void_p()
         rc = self.lib.rbt_init(C.byref(h), device)
         if rc != 0:
-            raise RbtError(rc, f"rbt_init(device={device}) failed")
+            raise RbtError(rc, (self.lib.rbt_last_error(None) or b"rbt_init failed").decode())
         self.h = h
         self._keep = []  # host arrays referenced by device-layer descriptors
 
@@ -257,6 +257,15 @@ class Context:
 
     def synth_i4g(self, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo=0.005, s_hi=0.02):
         self.check(self.lib.rbt_synth_i4g_d(self.h, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo, s_hi))
+
+    # -- instrumentation --------------------------------------------------------------------
+    def profile_enable(self, on: bool = True):
+        self.check(self.lib.rbt_profile_enable(self.h, int(on)))
+
+    def profile_read(self, reset: bool = True) -> dict:
+        p = abi.RbtProfile()
+        self.check(self.lib.rbt_profile_read(self.h, C.byref(p), int(reset)))
+        return {f: getattr(p, f) for f, _ in abi.RbtProfile._fields_}
 
     # -- MoE layer ----------------------------------------------------------------------------
     def moe_layer_set(self, layer, family, hidden, moe_inter, n_experts, topk, router, shared: Slot | None = None,

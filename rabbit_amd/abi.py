@@ -46,6 +46,11 @@ class RbtMoeLayerDesc(C.Structure):
                 ("has_shared", C.c_int32), ("shared", RbtExpertSlot), ("shared_gate", C.c_void_p)]
 
 
+class RbtProfile(C.Structure):
+    _fields_ = [("router_ms", C.c_double), ("gateup_ms", C.c_double), ("down_ms", C.c_double),
+                ("combine_ms", C.c_double), ("calls", C.c_uint64), ("ambiguous", C.c_uint64)]
+
+
 _P, _S, _I, _F, _U32, _U64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_float, C.c_uint32, C.c_uint64
 _CTX = C.c_void_p
 
@@ -84,6 +89,8 @@ SIGNATURES = {
     "rbt_moe_layer_set_device": (_I, [_CTX, _U32, C.POINTER(RbtMoeLayerDesc)]),
     "rbt_moe_forward": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
     "rbt_moe_forward_d": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
+    "rbt_profile_enable": (_I, [_CTX, _I]),
+    "rbt_profile_read": (_I, [_CTX, C.POINTER(RbtProfile), _I]),
     "rbt_synth_mxfp4_d": (_I, [_CTX, _P, _P, _S, _S, _U64, _U32, _U32]),
     "rbt_synth_i4g_d": (_I, [_CTX, _P, _P, _S, _S, _S, _U64, _F, _F]),
 }
@@ -106,6 +113,13 @@ def load(path: str = LIB_PATH):
     if not os.path.exists(path):
         raise RuntimeError(f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
                            "or `python rabbit_amd/build.py` (there is no CPU fallback)")
+    # One HIP runtime per process: PyTorch-ROCm ships its own libamdhip64 (SONAME libamdhip64.so.7).
+    # Importing torch first makes this library bind to that already-loaded runtime; loading ours
+    # first would pull /opt/rocm's copy in beside torch's, and the second runtime finds no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = C.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)  # AttributeError = the build lacks a declared symbol

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cstdarg>
 #include <initializer_list>
 #include <cstdio>
@@ -75,6 +76,11 @@ struct rbt_ctx : rbt::Ctx {
   std::map<uint32_t, Layer> layers;
   int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts
   int h_flags[8] = {};
+  // profiling: one row of 5 events per recorded moe_forward_d call
+  bool prof = false;
+  std::vector<hipEvent_t> ev_free;
+  std::vector<std::array<hipEvent_t, 5>> ev_rows;
+  rbt_profile acc{};
 };
 
 namespace {
@@ -289,7 +295,8 @@ int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) 
 // Runs gate/up (+SiLU) then down for `njobs` (expert, token) pairs.
 //   x: [tokens, d], x_index[p] = token of pair p; h: [njobs, i]; y: [njobs, d].
 int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
-                 const int *njobs_dev, const float *x, const int *x_index, size_t d, size_t i, float *h, float *y) {
+                 const int *njobs_dev, const float *x, const int *x_index, size_t d, size_t i, float *h, float *y,
+                 hipEvent_t *mark = nullptr) {
   bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
   bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
   if (fast_gu)
@@ -298,6 +305,7 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
   else
     HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
                                        (int)i, h, (long)i));
+  if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
   if (fast_dn)
     HIP_OK(c, rbt::launch_decode(*c, false, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i, (int)i, (int)d,
                                  y, (long)d));
@@ -438,6 +446,20 @@ int pool_insert(rbt_ctx *c, uint32_t layer, const rbt_expert_slot &slot, void *a
   return RBT_OK;
 }
 
+hipEvent_t take_event(rbt_ctx *c) {
+  if (!c->ev_free.empty()) {
+    hipEvent_t e = c->ev_free.back();
+    c->ev_free.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return e;
+}
+
 int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
                     float *w_out) {
   auto lit = c->layers.find(layer);
@@ -467,8 +489,9 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
   RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
   RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
-  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)npairs, &pjob));
-  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)npairs, &ptok));
+  // k_group always writes the S shared-expert pair slots after the P routed ones.
+  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)(P + S), &pjob));
+  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)(P + S), &ptok));
   RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
   RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
   size_t hi = std::max((size_t)I, L.shared_inter);
@@ -476,6 +499,13 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RBT_TRY(scratch_t(c, SC_YY, (size_t)npairs * H, &yy));
   int *dflags = c->d_flags;
 
+  std::array<hipEvent_t, 5> ev{};
+  if (c->prof) {
+    for (auto &e : ev) e = take_event(c);
+    for (auto &e : ev)
+      if (!e) return fail(c, RBT_E_HIP, "hipEventCreate failed");
+    HIP_OK(c, hipEventRecord(ev[0], c->stream));
+  }
   HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
   rbt::RouterArgs ra{D.family, E,          erows,          k,     H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
@@ -486,16 +516,24 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
                      L.shared_inter == (size_t)I;
   RbtExpertDev none{};
+  hipEvent_t *mark = c->prof ? &ev[2] : nullptr;
+  if (c->prof) HIP_OK(c, hipEventRecord(ev[1], c->stream));
   if (merge || !D.has_shared) {
-    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy));
+    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy, mark));
   } else {
-    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, P, nullptr, x, ptok, H, I, h, yy));
+    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, P, nullptr, x, ptok, H, I, h, yy, nullptr));
     // shared pairs [P, P+S): h rows at stride shared_inter after the routed block
     float *hs = h + (size_t)P * I;
     RBT_TRY(expert_pairs(c, L.shared_kind, L.shared_gs, pjob + P, none, S, nullptr, x, ptok + P, H, L.shared_inter, hs,
-                         yy + (size_t)P * H));
+                         yy + (size_t)P * H, nullptr));
+    if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
   }
+  if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
   HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
+  if (c->prof) {
+    HIP_OK(c, hipEventRecord(ev[4], c->stream));
+    c->ev_rows.push_back(ev);
+  }
   if (ids_out)
     HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
   if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, wts, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
@@ -551,28 +589,40 @@ extern "C" {
 
 const char *rbt_version(void) { return "rabbit_amd 0.1.0 (gfx950)"; }
 
+// rbt_init has no context to hold its error message; rbt_last_error(NULL) returns this one.
+static thread_local std::string g_init_err;
+
+static int init_fail(int code, const char *what, hipError_t e) {
+  char buf[256];
+  snprintf(buf, sizeof buf, "rbt_init: %s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+  g_init_err = buf;
+  (void)hipGetLastError();
+  return code;
+}
+
 int rbt_init(rbt_ctx **out, int device) {
   if (!out) return RBT_E_INVALID;
   *out = nullptr;
   int n = 0;
-  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
-    (void)hipGetLastError();
-    return RBT_E_HIP;
-  }
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return init_fail(RBT_E_HIP, "hipGetDeviceCount", e);
+  if (n == 0) return init_fail(RBT_E_HIP, "hipGetDeviceCount (no device)", hipSuccess);
   if (device < 0 || device >= n) return RBT_E_INVALID;
-  if (hipSetDevice(device) != hipSuccess) return RBT_E_HIP;
+  if ((e = hipSetDevice(device)) != hipSuccess) return init_fail(RBT_E_HIP, "hipSetDevice", e);
   rbt_ctx *c = new rbt_ctx();
   c->device = device;
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, device) == hipSuccess && prop.multiProcessorCount > 0)
     c->num_cu = prop.multiProcessorCount;
-  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int)) != hipSuccess ||
-      hipMemset(c->d_flags, 0, FLAG_N * sizeof(int)) != hipSuccess) {
-    (void)hipGetLastError();
+  const char *what = nullptr;
+  if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) what = "hipStreamCreateWithFlags";
+  else if ((e = hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMalloc";
+  else if ((e = hipMemset(c->d_flags, 0, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMemset";
+  if (what) {
+    int rc = init_fail(RBT_E_HIP, what, e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
-    return RBT_E_HIP;
+    return rc;
   }
   *out = c;
   return RBT_OK;
@@ -588,11 +638,14 @@ void rbt_destroy(rbt_ctx *c) {
   for (int i = 0; i < SC_N; i++)
     if (c->scratch[i]) (void)hipFree(c->scratch[i]);
   if (c->d_flags) (void)hipFree(c->d_flags);
+  for (auto &r : c->ev_rows)
+    for (auto e : r) c->ev_free.push_back(e);
+  for (auto e : c->ev_free) (void)hipEventDestroy(e);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
 
-const char *rbt_last_error(const rbt_ctx *c) { return c ? c->err.c_str() : "null context"; }
+const char *rbt_last_error(const rbt_ctx *c) { return c ? c->err.c_str() : g_init_err.c_str(); }
 
 int rbt_sync(rbt_ctx *c) {
   if (!c) return RBT_E_INVALID;
@@ -929,6 +982,36 @@ int rbt_moe_forward(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   if (ids_out) HIP_OK(c, hipMemcpyAsync(ids_out, di, s * k * 4, hipMemcpyDeviceToHost, c->stream));
   if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, dw, s * k * 4, hipMemcpyDeviceToHost, c->stream));
   return sync_and_check(c);
+}
+
+int rbt_profile_enable(rbt_ctx *c, int32_t on) {
+  if (!c) return RBT_E_INVALID;
+  c->prof = on != 0;
+  return RBT_OK;
+}
+
+int rbt_profile_read(rbt_ctx *c, rbt_profile *out, int32_t reset) {
+  if (!c || !out) return RBT_E_INVALID;
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  for (auto &r : c->ev_rows) {
+    float t[4];
+    for (int j = 0; j < 4; j++) HIP_OK(c, hipEventElapsedTime(&t[j], r[j], r[j + 1]));
+    c->acc.router_ms += t[0];
+    c->acc.gateup_ms += t[1];
+    c->acc.down_ms += t[2];
+    c->acc.combine_ms += t[3];
+    c->acc.calls += 1;
+    for (auto e : r) c->ev_free.push_back(e);
+  }
+  c->ev_rows.clear();
+  HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
+  c->acc.ambiguous = (uint64_t)c->h_flags[FLAG_AMB];
+  *out = c->acc;
+  if (reset) {
+    c->acc = rbt_profile{};
+    HIP_OK(c, hipMemset(c->d_flags + FLAG_AMB, 0, sizeof(int)));
+  }
+  return RBT_OK;
 }
 
 int rbt_synth_mxfp4_d(rbt_ctx *c, uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,

@@ -404,6 +404,13 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     first[e] = 0x7fffffff;
     cnt[e] = 0;
   }
+  // Slots without a pick (grouped routing can select fewer than k) stay empty: null job, no pair.
+  for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    pair_job[p] = RbtExpertDev{};
+    pair_tok[p] = 0;
+    tok_pair[p] = -1;
+    tok_w[p] = 0.0f;
+  }
   __syncthreads();
   for (int p = threadIdx.x; p < P; p += blockDim.x) {
     int e = ids[p];

@@ -40,6 +40,7 @@ def ctx(rbt_lib):
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU")
+    torch.zeros(1, device="cuda")  # initialise the device through torch first (one HIP runtime)
     import rabbit_amd
     c = rabbit_amd.Context(0)
     yield c
