@@ -42,6 +42,7 @@ enum ScratchSlot {
   SC_OUT,
   SC_IDS_OUT,
   SC_W_OUT,
+  SC_GU,
   SC_N
 };
 
@@ -284,7 +285,7 @@ int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) 
     RbtExpertDev one{};
     one.dd = (const uint8_t *)w->data;
     one.ds = w->scale;
-    HIP_OK(c, rbt::launch_decode(*c, false, w->kind, nullptr, one, (int)s, nullptr, x, nullptr, (long)i, (int)i,
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, w->kind, nullptr, one, (int)s, nullptr, x, nullptr, (long)i, (int)i,
                                  (int)o, y, (long)o));
     return RBT_OK;
   }
@@ -293,22 +294,35 @@ int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) 
 }
 
 // Runs gate/up (+SiLU) then down for `njobs` (expert, token) pairs.
-//   x: [tokens, d], x_index[p] = token of pair p; h: [njobs, i]; y: [njobs, d].
+//   x: [tokens, d], x_index[p] = token of pair p; y: [njobs, d].
+//   h: scratch of njobs * 2i floats. The fast path writes the stacked gate|up dot products there
+//   and the down kernel applies silu(g) * u while loading its activations; the generic path writes
+//   the activated [njobs, i] directly.
 int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                  const int *njobs_dev, const float *x, const int *x_index, size_t d, size_t i, float *h, float *y,
                  hipEvent_t *mark = nullptr) {
-  bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
-  bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
-  if (fast_gu)
-    HIP_OK(c, rbt::launch_decode(*c, true, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d, (int)i,
-                                 h, (long)i));
-  else
-    HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
-                                       (int)i, h, (long)i));
+  const bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
+  const bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
+  if (fast_gu && fast_dn) {
+    // stacked gate|up dot products (column parts) into gu, silu(g) * u into h, down from h.
+    const int parts = rbt::decode_parts((int)d);
+    const long gs_stride = (long)(2 * parts * i);
+    float *gu;
+    RBT_TRY(scratch_t(c, SC_GU, (size_t)njobs * gs_stride, &gu));
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_STACKED, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d,
+                                 (int)d, (int)(2 * i), gu, gs_stride, parts));
+    HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h));
+    if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
+                                 (int)i, (int)d, y, (long)d));
+    return RBT_OK;
+  }
+  HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
+                                     (int)i, h, (long)i));
   if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
   if (fast_dn)
-    HIP_OK(c, rbt::launch_decode(*c, false, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i, (int)i, (int)d,
-                                 y, (long)d));
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
+                                 (int)i, (int)d, y, (long)d));
   else
     HIP_OK(c, rbt::launch_pair_generic(*c, false, kind, gs, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
                                        (int)i, (int)d, y, (long)d));

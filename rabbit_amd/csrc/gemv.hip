@@ -15,6 +15,8 @@
 //
 // Accumulation is fp32 with fused multiply-add; the reference's sequential sum is reassociated
 // (within the 1e-5 relative-L2 contract), the dequantized weight itself is exact.
+#include <algorithm>
+
 #include "rbt_device.h"
 #include "rbt_internal.h"
 
@@ -81,139 +83,252 @@ __device__ __forceinline__ void load_x_slice(float (&xr)[NB][32], float (&xs)[NB
   }
 }
 
-// Partial dot of one MXFP4 row over this lane's blocks.
-template <int NB, int LPR>
-__device__ __forceinline__ float row_dot_mxfp4(const uint8_t *__restrict__ rowd, const uint8_t *__restrict__ rows,
-                                               int q, int nblk, const float (&xr)[NB][32]) {
-  rbt_u4 w[NB];
-  uint32_t sb[NB];
+
+
+// ------------------------------------------------------------------------------------------------
+// Decode kernel over a job table. Each job u is one expert (or one plain matrix); MODE selects the
+// matrix and the activation:
+//   MODE_DOWN   : y[u*y_stride + r] = down_u[r] . x_u                         (r < rows)
+//   MODE_STACKED: gate_u and up_u as one [2*half, cols] matrix: rows [0, half) are gate's, rows
+//                 [half, 2*half) up's; y[u*y_stride + r] = that row . x_u     (r < rows = 2*half)
+//   MODE_ACT    : like MODE_DOWN, but the activation is built on the fly from a stacked gate/up
+//                 result g|u (2*cols floats): x_k = silu(g_k) * u_k (glm52/moe.rs:33-80).
+// x_u = x + tok(u)*x_stride with tok(u) = x_index[u] (or u when x_index is null).
+// The flattened (job, row) range is split into equal contiguous runs, one per wave. An iteration
+// covers U * (64/LPR) consecutive rows; the next iteration's blocks are loaded before the current
+// one is reduced (double buffering), so a wave keeps two iterations of weight bytes in flight. With
+// U > 1 the host guarantees rows % (U * 64/LPR) == 0 (an iteration never straddles two jobs). A
+// job whose weights are absent (null pointers) yields zeros.
+// ------------------------------------------------------------------------------------------------
+enum { MODE_DOWN = 0, MODE_STACKED = 1, MODE_ACT = 2 };
+
+template <int NB, int U>
+struct DecodeFrag {
+  rbt_u4 w[U][NB];
+  uint32_t sb[U][NB];  // E8M0 byte (MXFP4) or f32 bits (I4G)
+};
+
+// Loads the blocks of IPI = U * (64/LPR) consecutive rows starting at `row` (a row pointer into
+// `d`, rows rb bytes apart; scales `sc`, nblk per row). Lane (sub, q) takes rows row + u*RPI + sub.
+template <int NB, int LPR, int U, bool I4G>
+__device__ __forceinline__ void frag_load(DecodeFrag<NB, U> &f, const uint8_t *__restrict__ d,
+                                          const uint8_t *__restrict__ sc, int row, int q, int sub, int nblk,
+                                          unsigned rb, int sstride) {
+  constexpr int RPI = RBT_WAVE / LPR;
 #pragma unroll
-  for (int j = 0; j < NB; j++) {
-    int b = q + LPR * j;
-    if (b < nblk) {
-      w[j] = __builtin_nontemporal_load(reinterpret_cast<const rbt_u4 *>(rowd) + b);
-      sb[j] = rows[b];
-    } else {
-      w[j] = rbt_u4{0u, 0u, 0u, 0u};
-      sb[j] = 127;
+  for (int u = 0; u < U; u++) {
+    const unsigned r = (unsigned)(row + u * RPI + sub);
+    const rbt_u4 *rp = reinterpret_cast<const rbt_u4 *>(d + (size_t)r * rb);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int b = q + LPR * j;
+      if (NB * LPR == nblk || b < nblk) {
+        f.w[u][j] = __builtin_nontemporal_load(rp + b);
+        if (I4G)
+          f.sb[u][j] = reinterpret_cast<const uint32_t *>(sc)[(size_t)r * sstride + b];
+        else
+          f.sb[u][j] = sc[(size_t)r * sstride + b];
+      } else {
+        f.w[u][j] = I4G ? rbt_u4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u} : rbt_u4{0u, 0u, 0u, 0u};
+        f.sb[u][j] = I4G ? 0u : 127u;
+      }
     }
   }
-  float acc[NB];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    float sc = rbt_e8m0(sb[j]);
-    float a = 0.0f;
-    a = fp4_dword_dot(w[j].x, sc, &xr[j][0], a);
-    a = fp4_dword_dot(w[j].y, sc, &xr[j][8], a);
-    a = fp4_dword_dot(w[j].z, sc, &xr[j][16], a);
-    a = fp4_dword_dot(w[j].w, sc, &xr[j][24], a);
-    acc[j] = a;
-  }
+}
+
+template <int NB, bool I4G>
+__device__ __forceinline__ float block_dots(const rbt_u4 (&w)[NB], const uint32_t (&sb)[NB], const float (&xr)[NB][32],
+                                            const float (&xs)[NB]) {
   float r = 0.0f;
 #pragma unroll
-  for (int j = 0; j < NB; j++) r += acc[j];
+  for (int j = 0; j < NB; j++) {
+    float a = 0.0f;
+    if (I4G) {
+      a = i4_dword_dot(w[j].x, &xr[j][0], a);
+      a = i4_dword_dot(w[j].y, &xr[j][8], a);
+      a = i4_dword_dot(w[j].z, &xr[j][16], a);
+      a = i4_dword_dot(w[j].w, &xr[j][24], a);
+      // sum_k x_k (n_k - 8) = sum_k x_k n_k - 8 sum_k x_k, then the group scale.
+      r = __builtin_fmaf(__builtin_fmaf(-8.0f, xs[j], a), __uint_as_float(sb[j]), r);
+    } else {
+      const float sc = rbt_e8m0(sb[j]);
+      a = fp4_dword_dot(w[j].x, sc, &xr[j][0], a);
+      a = fp4_dword_dot(w[j].y, sc, &xr[j][8], a);
+      a = fp4_dword_dot(w[j].z, sc, &xr[j][16], a);
+      a = fp4_dword_dot(w[j].w, sc, &xr[j][24], a);
+      r += a;
+    }
+  }
   return r;
 }
 
-// Partial dot of one grouped-int4 row (group_size 32) over this lane's blocks.
-template <int NB, int LPR>
-__device__ __forceinline__ float row_dot_i4g(const uint8_t *__restrict__ rowd, const float *__restrict__ rows, int q,
-                                             int nblk, const float (&xr)[NB][32], const float (&xs)[NB]) {
-  rbt_u4 w[NB];
-  float sc[NB];
+// x slice for MODE_ACT: x_k = silu(g_k) * u_k from a stacked gate/up result. The producer may have
+// split its rows into PARTS column ranges: gu holds PARTS partial gate vectors, then PARTS partial
+// up vectors (cols floats each), summed here.
+template <int PARTS>
+__device__ __forceinline__ float4 sum_parts(const float *__restrict__ p, int cols, int off) {
+  float4 v = *reinterpret_cast<const float4 *>(p + off);
 #pragma unroll
-  for (int j = 0; j < NB; j++) {
-    int b = q + LPR * j;
-    if (b < nblk) {
-      w[j] = __builtin_nontemporal_load(reinterpret_cast<const rbt_u4 *>(rowd) + b);
-      sc[j] = rows[b];
-    } else {
-      w[j] = rbt_u4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-      sc[j] = 0.0f;
-    }
+  for (int h = 1; h < PARTS; h++) {
+    const float4 w = *reinterpret_cast<const float4 *>(p + h * cols + off);
+    v.x += w.x;
+    v.y += w.y;
+    v.z += w.z;
+    v.w += w.w;
   }
-  float r = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    float a = 0.0f;
-    a = i4_dword_dot(w[j].x, &xr[j][0], a);
-    a = i4_dword_dot(w[j].y, &xr[j][8], a);
-    a = i4_dword_dot(w[j].z, &xr[j][16], a);
-    a = i4_dword_dot(w[j].w, &xr[j][24], a);
-    // sum_k x_k (n_k - 8) = sum_k x_k n_k - 8 sum_k x_k, then the group scale.
-    r = __builtin_fmaf(__builtin_fmaf(-8.0f, xs[j], a), sc[j], r);
-  }
-  return r;
+  return v;
 }
 
-// ------------------------------------------------------------------------------------------------
-// Decode kernel over a job table. Each job u is one expert (or one plain matrix):
-//   GATEUP: y[u*y_stride + r] = silu(gate_u[r] . x_u) * (up_u[r] . x_u), r < rows
-//   else:   y[u*y_stride + r] = down_u[r] . x_u
-// with x_u = x + tok(u)*x_stride, tok(u) = x_index[u] (or u when x_index is null). The flattened
-// (job, row) range is split into equal contiguous runs, one per wave, so a wave reloads its x slice
-// only when the token changes. A job whose weights are absent (null pointers) yields zeros.
-// ------------------------------------------------------------------------------------------------
-template <int NB, int LPR, bool GATEUP, bool I4G>
+template <int NB, int LPR, int PARTS>
+__device__ __forceinline__ void load_act_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ gu,
+                                               int q, int nblk, int cols) {
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int b = q + LPR * j;
+    float s = 0.0f;
+    if (b < nblk) {
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float4 g = sum_parts<PARTS>(gu, cols, 32 * b + 4 * t);
+        const float4 u = sum_parts<PARTS>(gu + PARTS * cols, cols, 32 * b + 4 * t);
+        xr[j][4 * t + 0] = rbt_silu(g.x) * u.x;
+        xr[j][4 * t + 1] = rbt_silu(g.y) * u.y;
+        xr[j][4 * t + 2] = rbt_silu(g.z) * u.z;
+        xr[j][4 * t + 3] = rbt_silu(g.w) * u.w;
+      }
+#pragma unroll
+      for (int t = 0; t < 32; t++) s += xr[j][t];
+    } else {
+#pragma unroll
+      for (int t = 0; t < 32; t++) xr[j][t] = 0.0f;
+    }
+    xs[j] = s;
+  }
+}
+
+template <int NB, int LPR, int U, bool I4G>
+__device__ __forceinline__ void frag_reduce_store(const DecodeFrag<NB, U> &f, const float (&xr)[NB][32],
+                                                  const float (&xs)[NB], float *__restrict__ yrow, int q, int sub) {
+  constexpr int RPI = RBT_WAVE / LPR;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    float a = block_dots<NB, I4G>(f.w[u], f.sb[u], xr, xs);
+    a = rbt_group_sum<LPR>(a);
+    if (q == 0) yrow[u * RPI + sub] = a;
+    // one row at a time: keeps the scheduler from decoding every row's nibbles up front, which
+    // would cost 32 registers per block and halve the waves per SIMD.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int NB, int LPR, int U, int MODE, bool I4G, int CS, int PARTS>
 __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restrict__ jobs, RbtExpertDev single,
                                                      int njobs, const int *__restrict__ njobs_dev,
                                                      const float *__restrict__ x, const int *__restrict__ x_index,
                                                      long x_stride, int cols, int rows, float *__restrict__ y,
                                                      long y_stride) {
-  constexpr int RPI = RBT_WAVE / LPR;  // rows per wave iteration
+  constexpr int RPI = RBT_WAVE / LPR;  // rows side by side in one wave
+  constexpr int IPI = U * RPI;         // rows per iteration
   const int lane = threadIdx.x & (RBT_WAVE - 1);
   const int q = lane % LPR, sub = lane / LPR;
-  const long nwaves = (long)gridDim.x * (blockDim.x / RBT_WAVE);
-  const long wave = (long)blockIdx.x * (blockDim.x / RBT_WAVE) + threadIdx.x / RBT_WAVE;
+  const int nwaves = gridDim.x * (blockDim.x / RBT_WAVE);
+  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / RBT_WAVE) + threadIdx.x / RBT_WAVE);
   int nj = njobs;
   if (njobs_dev) nj = min(nj, *njobs_dev);
-  const long total = (long)nj * rows;
-  long per = (total + nwaves - 1) / nwaves;
-  per = ((per + RPI - 1) / RPI) * RPI;
-  const long begin = wave * per;
-  if (begin >= total) return;
-  const long end = min(begin + per, total);
+  // Each logical row of `cols` columns is processed as CS column ranges ("parts"), so a lane's x
+  // slice covers cols/CS columns. A segment is a run of rows of one matrix and one part: per job,
+  // MODE_STACKED has 2*CS segments (gate parts, then up parts), the other modes CS. `rows` counts
+  // logical rows per job (2*half for MODE_STACKED); segment lengths are multiples of IPI.
+  const int seg = MODE == MODE_STACKED ? rows / 2 : rows;
+  const int nseg_job = (rows / seg) * CS;
+  const int total = nj * seg * nseg_job;
+  int per = (total + nwaves - 1) / nwaves;
+  per = ((per + IPI - 1) / IPI) * IPI;
+  int pos = wave * per;
+  if (pos >= total) return;
+  const int end = min(pos + per, total);
 
-  const int nblk = cols / 32;
-  const size_t rb = (size_t)cols / 2;
-  const size_t sstride = (size_t)nblk;  // scale elements per row (u8 for MXFP4, f32 for I4G)
+  const int pcols = cols / CS;  // columns of one part
+  const int nblk = pcols / 32;
+  const unsigned rb = (unsigned)cols / 2;
 
   float xr[NB][32];
   float xs[NB];
   long cur = -1;
+  DecodeFrag<NB, U> f0, f1;
 
-  for (long base = begin; base < end; base += RPI) {
-    const long item = base + sub;
-    const bool valid = item < end;
-    const int u = valid ? (int)(item / rows) : (int)((end - 1) / rows);
-    const int r = valid ? (int)(item % rows) : 0;
-    const long tok = x_stride == 0 ? 0 : (x_index ? (long)x_index[u] : (long)u);
-    if (tok != cur) {
-      load_x_slice<NB, LPR>(xr, xs, x + tok * x_stride, q, nblk);
-      cur = tok;
+  while (pos < end) {
+    // one segment: rows [r, r1) of matrix (job, part)
+    const int sidx = pos / seg;
+    const int job = sidx / nseg_job, sj = sidx - job * nseg_job;
+    const int mat = sj / CS, h = sj - mat * CS;  // matrix (gate/up for MODE_STACKED), column part
+    int r = pos - sidx * seg;
+    const int r1 = min(seg, r + (end - pos));
+    pos += r1 - r;
+    const RbtExpertDev J = jobs ? jobs[job] : single;
+    const uint8_t *d = MODE == MODE_STACKED ? (mat ? J.ud : J.gd) : J.dd;
+    const uint8_t *sc = reinterpret_cast<const uint8_t *>(MODE == MODE_STACKED ? (mat ? J.us : J.gs) : J.ds);
+    float *yrow = y + (long)job * y_stride + (long)sj * seg;
+    if (d == nullptr) {
+      for (int rr = r + lane; rr < r1; rr += RBT_WAVE) yrow[rr] = 0.0f;
+      continue;
     }
-    const RbtExpertDev J = jobs ? jobs[u] : single;
-    float a = 0.0f, b = 0.0f;
-    if (GATEUP) {
-      if (J.gd && J.ud) {
-        if (I4G) {
-          a = row_dot_i4g<NB, LPR>(J.gd + r * rb, reinterpret_cast<const float *>(J.gs) + r * sstride, q, nblk, xr, xs);
-          b = row_dot_i4g<NB, LPR>(J.ud + r * rb, reinterpret_cast<const float *>(J.us) + r * sstride, q, nblk, xr, xs);
-        } else {
-          a = row_dot_mxfp4<NB, LPR>(J.gd + r * rb, reinterpret_cast<const uint8_t *>(J.gs) + r * sstride, q, nblk, xr);
-          b = row_dot_mxfp4<NB, LPR>(J.ud + r * rb, reinterpret_cast<const uint8_t *>(J.us) + r * sstride, q, nblk, xr);
-        }
-      }
-      b = rbt_group_sum<LPR>(b);
-    } else if (J.dd) {
-      if (I4G)
-        a = row_dot_i4g<NB, LPR>(J.dd + r * rb, reinterpret_cast<const float *>(J.ds) + r * sstride, q, nblk, xr, xs);
+    d += (size_t)h * (pcols / 2);                         // part h of every row
+    sc += (size_t)h * nblk * (I4G ? 4 : 1);
+    // ping-pong over iterations of IPI rows: the next iteration's blocks are in flight while the
+    // current one is reduced. The first weight loads go out before the activation slice is read.
+    frag_load<NB, LPR, U, I4G>(f0, d, sc, r, q, sub, nblk, rb, CS * nblk);
+    const long tok = x_stride == 0 ? 0 : (x_index ? (long)x_index[job] : (long)job);
+    if (tok * CS + h != cur) {
+      if (MODE == MODE_ACT)
+        load_act_slice<NB, LPR, PARTS>(xr, xs, x + tok * x_stride, q, nblk, cols);
       else
-        a = row_dot_mxfp4<NB, LPR>(J.dd + r * rb, reinterpret_cast<const uint8_t *>(J.ds) + r * sstride, q, nblk, xr);
+        load_x_slice<NB, LPR>(xr, xs, x + tok * x_stride + (long)h * pcols, q, nblk);
+      cur = tok * CS + h;
     }
-    a = rbt_group_sum<LPR>(a);
-    if (valid && q == 0) y[(long)u * y_stride + r] = GATEUP ? rbt_silu(a) * b : a;
+    for (; r < r1; r += 2 * IPI) {
+      const bool has1 = r + IPI < r1;
+      if (has1) frag_load<NB, LPR, U, I4G>(f1, d, sc, r + IPI, q, sub, nblk, rb, CS * nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f0, xr, xs, yrow + r, q, sub);
+      if (!has1) break;
+      if (r + 2 * IPI < r1) frag_load<NB, LPR, U, I4G>(f0, d, sc, r + 2 * IPI, q, sub, nblk, rb, CS * nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f1, xr, xs, yrow + r + IPI, q, sub);
+    }
   }
+}
+
+// Activation between the stacked gate/up GEMV and the down GEMV: h[p, k] = silu(g) * u with g and
+// u summed over the producer's column parts (gu per pair: PARTS gate vectors, then PARTS up vectors
+// of `half` floats each). silu(g) * u rounds as the reference writes it (glm52/moe.rs:33-35, :58).
+template <int PARTS>
+__global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, long gu_stride, int half, int npairs,
+                                                const int *__restrict__ npairs_dev, float *__restrict__ h) {
+  int np = npairs;
+  if (npairs_dev) np = min(np, *npairs_dev);
+  const long n = (long)np * half;
+  for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (long)gridDim.x * blockDim.x) {
+    const long p = idx / half, k = idx - p * half;
+    const float *g = gu + p * gu_stride;
+    float gv = g[k], uv = g[PARTS * half + k];
+#pragma unroll
+    for (int j = 1; j < PARTS; j++) {
+      gv += g[j * half + k];
+      uv += g[(PARTS + j) * half + k];
+    }
+    h[idx] = rbt_silu(gv) * uv;
+  }
+}
+
+hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
+                         int parts, float *h) {
+  const long n = (long)npairs * half;
+  if (n <= 0) return hipSuccess;
+  const int blocks = (int)std::min<long>((n + 255) / 256, (long)c.num_cu * 4);
+  if (parts == 2)
+    hipLaunchKernelGGL(k_swiglu<2>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev, h);
+  else
+    hipLaunchKernelGGL(k_swiglu<1>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev, h);
+  return hipGetLastError();
 }
 
 // Same contract as k_decode_gemv for any shape (odd columns, partial blocks, any group size):
@@ -389,51 +504,78 @@ bool decode_shape_ok(size_t cols, int kind, size_t gs) {
   return cols / 32 <= 256;  // up to 8192 columns
 }
 
-template <int NB, int LPR, bool GATEUP, bool I4G>
+template <int NB, int LPR, int U, int MODE, bool I4G, int CS, int PARTS>
 static hipError_t launch_decode_t(const Ctx &c, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                                   const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
                                   int rows, float *y, long y_stride) {
-  constexpr int RPI = RBT_WAVE / LPR;
-  long total = (long)njobs * rows;
-  // About 8 waves per CU; each wave takes an equal contiguous run of rows (computed in-kernel from
-  // the actual job count).
+  constexpr int IPI = U * (RBT_WAVE / LPR);
+  const long total = (long)njobs * rows * CS;
+  if (total >= (1L << 31)) return hipErrorInvalidValue;
+  // ~8 waves per CU; each wave takes an equal contiguous run of rows (recomputed in-kernel from the
+  // actual job count).
   long waves = (long)c.num_cu * 8;
-  long iters = (total + RPI - 1) / RPI;
+  long iters = (total + IPI - 1) / IPI;
   if (waves > iters) waves = iters;
   if (waves < 1) waves = 1;
   int blocks = (int)((waves + 3) / 4);
-  hipLaunchKernelGGL((k_decode_gemv<NB, LPR, GATEUP, I4G>), dim3(blocks), dim3(256), 0, c.stream, jobs, single, njobs,
-                     njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride);
+  hipLaunchKernelGGL((k_decode_gemv<NB, LPR, U, MODE, I4G, CS, PARTS>), dim3(blocks), dim3(256), 0, c.stream, jobs,
+                     single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride);
   return hipGetLastError();
 }
 
-template <bool GATEUP, bool I4G>
+// Kernel shape per row length. Long rows (hidden = 6144..8192 columns) are split into two column
+// parts of a whole wave each (x slice <= 128 floats per lane before the split, <= 64 after); short
+// rows (moe_inter = 2048) take 32 lanes, two rows side by side and two unrolled.
+// The stacked gate/up producer's split count is what the MODE_ACT consumer sums (parts_of()).
+static int long_split(int cols) { return cols >= 4096 && cols % 64 == 0 && (cols / 64) % 32 == 0 ? 2 : 1; }
+
+template <int MODE, bool I4G, int PARTS>
 static hipError_t launch_decode_k(const Ctx &c, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                                   const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
                                   int rows, float *y, long y_stride) {
-#define RBT_DEC(NB, LPR) \
-  return launch_decode_t<NB, LPR, GATEUP, I4G>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride)
-  int nblk = cols / 32;
-  if (nblk <= 16) RBT_DEC(1, 16);
-  if (nblk <= 32) RBT_DEC(2, 16);
-  if (nblk <= 48) RBT_DEC(3, 16);
-  if (nblk <= 64) RBT_DEC(4, 16);
-  if (nblk <= 96) RBT_DEC(3, 32);
-  if (nblk <= 128) RBT_DEC(4, 32);
-  if (nblk <= 192) RBT_DEC(3, 64);
-  RBT_DEC(4, 64);
+#define RBT_DEC(NB, LPR, U, CS)                                                                                    \
+  return launch_decode_t<NB, LPR, U, MODE, I4G, CS, PARTS>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, \
+                                                           cols, rows, y, y_stride)
+  const int seg = MODE == MODE_STACKED ? rows / 2 : rows;  // rows of one matrix
+  if (MODE == MODE_STACKED && long_split(cols) == 2 && seg % 2 == 0) {  // parts summed by MODE_ACT
+    const int nblk = cols / 64;  // blocks per part
+    if (nblk <= 64) RBT_DEC(1, 64, 2, 2);
+    if (nblk <= 128) RBT_DEC(2, 64, 2, 2);
+  }
+  const int nblk = cols / 32;
+  if (nblk <= 64 && nblk > 32 && seg % 4 == 0) RBT_DEC(1, 64, 4, 1);  // one x copy per wave
+  if (nblk <= 64 && seg % 4 == 0) {
+    if (nblk <= 16) RBT_DEC(1, 16, 1, 1);
+    if (nblk <= 32) RBT_DEC(2, 16, 1, 1);
+  }
+  if (nblk <= 64) RBT_DEC(1, 64, 1, 1);
+  if (nblk <= 128) RBT_DEC(2, 64, 1, 1);
+  if (nblk <= 192) RBT_DEC(3, 64, 1, 1);
+  RBT_DEC(4, 64, 1, 1);
 #undef RBT_DEC
 }
 
-hipError_t launch_decode(const Ctx &c, bool gateup, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
+int decode_parts(int cols) { return long_split(cols); }
+
+// mode: 0 = plain rows (down / single matrix), 1 = stacked gate|up rows, 2 = plain rows with the
+// SiLU-gated activation built from a stacked g|u input produced with `parts` column parts.
+hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                         int rows, float *y, long y_stride) {
+                         int rows, float *y, long y_stride, int parts) {
   if (njobs <= 0 || rows <= 0) return hipSuccess;
-  if (kind == RBT_QT_I4_GROUPED)
-    return gateup ? launch_decode_k<true, true>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride)
-                  : launch_decode_k<false, true>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride);
-  return gateup ? launch_decode_k<true, false>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride)
-                : launch_decode_k<false, false>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride);
+  const bool i4 = kind == RBT_QT_I4_GROUPED;
+#define RBT_MODE(M, P)                                                                                              \
+  return i4 ? launch_decode_k<M, true, P>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y,   \
+                                          y_stride)                                                                 \
+            : launch_decode_k<M, false, P>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y,  \
+                                           y_stride)
+  if (mode == MODE_STACKED) RBT_MODE(MODE_STACKED, 1);
+  if (mode == MODE_ACT) {
+    if (parts == 2) RBT_MODE(MODE_ACT, 2);
+    RBT_MODE(MODE_ACT, 1);
+  }
+  RBT_MODE(MODE_DOWN, 1);
+#undef RBT_MODE
 }
 
 hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,

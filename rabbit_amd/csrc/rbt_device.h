@@ -34,11 +34,23 @@ __device__ __forceinline__ float rbt_e2m1(uint32_t n) {
 __device__ __forceinline__ float rbt_silu(float g) { return g / (1.0f + expf(-g)); }
 __device__ __forceinline__ float rbt_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
-// Butterfly sum over groups of `width` lanes (width a power of two <= 64).
+// v + (v from another lane of the same 16-lane DPP row), one v_add_f32_dpp.
+template <int CTRL>
+__device__ __forceinline__ float rbt_dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of WIDTH lanes (WIDTH a power of two <= 64). Within a 16-lane row the
+// butterfly runs on DPP (quad_perm xor 1, xor 2, row_half_mirror, row_mirror); every lane of the
+// group ends with the sum for WIDTH <= 32. For WIDTH = 64 the total is valid in lanes 0..31.
 template <int WIDTH>
 __device__ __forceinline__ float rbt_group_sum(float v) {
-#pragma unroll
-  for (int m = WIDTH / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, RBT_WAVE);
+  if (WIDTH >= 2) v = rbt_dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (WIDTH >= 4) v = rbt_dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (WIDTH >= 8) v = rbt_dpp_add<0x141>(v);  // row_half_mirror
+  if (WIDTH >= 16) v = rbt_dpp_add<0x140>(v); // row_mirror
+  if (WIDTH >= 32) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));  // xor 16
+  if (WIDTH >= 64) v += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   return v;
 }
 

@@ -33,9 +33,19 @@ hipError_t launch_dequant(const Ctx &c, float *out, int kind, const void *data, 
 bool decode_shape_ok(size_t cols, int kind, size_t gs);
 // Decode GEMV over a job table (see gemv.hip). jobs == nullptr uses `single` for every job.
 // njobs_dev (optional) caps the job count from device memory.
-hipError_t launch_decode(const Ctx &c, bool gateup, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
+// mode: 0 = plain rows, 1 = stacked gate|up rows (raw dots), 2 = plain rows whose activation is
+// silu(g) * u built from a stacked g|u input.
+enum { DECODE_DOWN = 0, DECODE_STACKED = 1, DECODE_ACT = 2 };
+// parts: for DECODE_ACT, the column-part count the stacked producer used (decode_parts(hidden)).
+hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                         int rows, float *y, long y_stride);
+                         int rows, float *y, long y_stride, int parts = 1);
+// h[p, k] = silu(sum of gate parts) * (sum of up parts) for the stacked producer's output.
+hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
+                         int parts, float *h);
+// Column parts the stacked gate/up kernel splits a row of `cols` columns into; its output per job
+// is 2 * parts vectors of `half` floats (gate parts, then up parts).
+int decode_parts(int cols);
 hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,
                                const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
                                const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride);

@@ -125,6 +125,143 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
   }
 }
 
+// Fast path (H % 256 == 0): one wave per router row. The row is walked in chunks of 256 elements,
+// lane l taking the 4 consecutive elements [4l, 4l+4) of each chunk with one 16-byte load (so each
+// load instruction reads 1 KB contiguous); a wave-wide fp64 exclusive scan per chunk gives every
+// prefix sum S_j for the bound term T.
+__device__ __forceinline__ double wave_incl_scan_d(double v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    double o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(256) void k_router_logits_w(const float *__restrict__ x, int S, int H,
+                                                         const float *__restrict__ W, int E,
+                                                         const float *__restrict__ sgate, double *__restrict__ mid,
+                                                         double *__restrict__ bnd, int erows) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= erows) return;
+  const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
+  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16;  // 2^-53
+  const int nch = H / 256;
+  for (int s = 0; s < S; s++) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)s * H);
+    double base = 0.0, T = 0.0, Pa = 0.0;
+    for (int c = 0; c < nch; c++) {
+      const float4 xv = x4[c * 64 + lane], wv = w4[c * 64 + lane];
+      const double p0 = (double)__fmul_rn(xv.x, wv.x), p1 = (double)__fmul_rn(xv.y, wv.y);
+      const double p2 = (double)__fmul_rn(xv.z, wv.z), p3 = (double)__fmul_rn(xv.w, wv.w);
+      const double l1 = p0 + p1, l2 = l1 + p2, l3 = l2 + p3;
+      const double inc = wave_incl_scan_d(l3);
+      const double pre = base + (inc - l3);
+      T += fabs(pre + p0) + fabs(pre + l1) + fabs(pre + l2) + fabs(pre + l3);
+      Pa += fabs(p0) + fabs(p1) + fabs(p2) + fabs(p3);
+      base += __shfl(inc, 63, 64);
+    }
+    T = rbt_wave_sum_d(T);
+    Pa = rbt_wave_sum_d(Pa);
+    if (lane == 0) {
+      const double n = (double)H;
+      const double slack = 8.0 * n * e64 * (Pa + T) + n * n * e64 * Pa;
+      const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
+      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
+      B = B * (1.0 + 1e-9) + 1e-300;
+      mid[(size_t)s * erows + row] = base;
+      bnd[(size_t)s * erows + row] = B;
+    }
+  }
+}
+
+// Transposed variant (H % 256 == 0, H <= 8192): one 64-thread workgroup per router row. The wave
+// loads the row and x with coalesced 16-byte loads, forms the products and stores them to LDS so
+// that lane l then owns the contiguous segment [l*H/64, (l+1)*H/64): one sequential fp64 prefix per
+// lane and a single wave scan give every prefix sum S_j. The segment stride is padded by 4 floats
+// so the 16-byte LDS reads of neighbouring lanes fall in different banks.
+constexpr int RT_MAXH = 8192;
+
+__global__ __launch_bounds__(64) void k_router_logits_t(const float *__restrict__ x, int S, int H,
+                                                        const float *__restrict__ W, int E,
+                                                        const float *__restrict__ sgate, double *__restrict__ mid,
+                                                        double *__restrict__ bnd, int erows) {
+  __shared__ float lp[RT_MAXH + 4 * 64];
+  const int lane = threadIdx.x;
+  const int row = blockIdx.x;
+  const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
+  const int seg = H / 64;      // elements per lane segment
+  const int segp = seg + 4;    // padded segment stride in LDS
+  const int nch = H / 256;     // coalesced chunks (one float4 per lane)
+  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16;  // 2^-53
+  constexpr int MAXCH = RT_MAXH / 256;
+  float4 wv[MAXCH];
+#pragma unroll
+  for (int c = 0; c < MAXCH; c++)
+    if (c < nch) wv[c] = w4[c * 64 + lane];
+  for (int s = 0; s < S; s++) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)s * H);
+    float4 xv[MAXCH];
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++)
+      if (c < nch) xv[c] = x4[c * 64 + lane];
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) {
+      if (c < nch) {
+        const int j = c * 256 + 4 * lane;            // first of this lane's 4 elements
+        const int dst = (j / seg) * segp + (j % seg); // 4 consecutive elements stay in one segment
+        float4 p;
+        p.x = __fmul_rn(xv[c].x, wv[c].x);
+        p.y = __fmul_rn(xv[c].y, wv[c].y);
+        p.z = __fmul_rn(xv[c].z, wv[c].z);
+        p.w = __fmul_rn(xv[c].w, wv[c].w);
+        *reinterpret_cast<float4 *>(&lp[dst]) = p;
+      }
+    }
+    __syncthreads();
+    const float *mine = lp + lane * segp;
+    double loc = 0.0, pa = 0.0;
+    for (int t = 0; t < seg; t += 4) {
+      const float4 p = *reinterpret_cast<const float4 *>(mine + t);
+      loc += (double)p.x;
+      loc += (double)p.y;
+      loc += (double)p.z;
+      loc += (double)p.w;
+      pa += fabs((double)p.x) + fabs((double)p.y) + fabs((double)p.z) + fabs((double)p.w);
+    }
+    const double inc = wave_incl_scan_d(loc);
+    double pre = inc - loc, T = 0.0;
+    for (int t = 0; t < seg; t += 4) {
+      const float4 p = *reinterpret_cast<const float4 *>(mine + t);
+      pre += (double)p.x;
+      T += fabs(pre);
+      pre += (double)p.y;
+      T += fabs(pre);
+      pre += (double)p.z;
+      T += fabs(pre);
+      pre += (double)p.w;
+      T += fabs(pre);
+    }
+    T = rbt_wave_sum_d(T);
+    pa = rbt_wave_sum_d(pa);
+    const double total = __shfl(inc, 63, 64);
+    if (lane == 0) {
+      const double n = (double)H;
+      const double slack = 8.0 * n * e64 * (pa + T) + n * n * e64 * pa;
+      const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
+      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
+      B = B * (1.0 + 1e-9) + 1e-300;
+      mid[(size_t)s * erows + row] = total;
+      bnd[(size_t)s * erows + row] = B;
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // 2. per-token selection
 // ------------------------------------------------------------------------------------------------
@@ -153,6 +290,14 @@ __device__ __forceinline__ float sel_key(const SelParams &P, int e, float l) {
   if (P.family == RBT_FAMILY_QWEN38) return l;
   float p = sigmoid_ref(l);
   return P.router_bias ? __fadd_rn(p, P.router_bias[e]) : p;
+}
+
+// Same map with the expert's bias values already loaded (lb/rb ignored when the pointer is null).
+__device__ __forceinline__ float sel_key_v(const SelParams &P, float lb, float rb, float l) {
+  if (P.logit_bias) l = __fadd_rn(l, lb);
+  if (P.family == RBT_FAMILY_QWEN38) return l;
+  const float p = sigmoid_ref(l);
+  return P.router_bias ? __fadd_rn(p, rb) : p;
 }
 
 // (key desc, id asc) ordering: true if (ka, a) ranks before (kb, b).
@@ -197,7 +342,7 @@ __device__ float exact_logit(const float *xs, const float *w, int H) {
   return a;
 }
 
-__global__ __launch_bounds__(64) void k_router_select(SelParams P, const double *__restrict__ mid,
+__global__ __launch_bounds__(64) void k_router_select_grouped(SelParams P, const double *__restrict__ mid,
                                                       const double *__restrict__ bnd, int32_t *__restrict__ ids,
                                                       float *__restrict__ wts, float *__restrict__ sh_scale,
                                                       int *__restrict__ stats) {
@@ -372,6 +517,241 @@ __global__ __launch_bounds__(64) void k_router_select(SelParams P, const double 
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Fast selection (n_group <= 1): 256 threads per token. Wave 0 holds lane-strided expert keys in
+// registers (expert e = lane + 64 m), takes the top-k with wave-wide argmax rounds and certifies
+// it; all four waves then recompute the ambiguous experts' logits exactly.
+// ------------------------------------------------------------------------------------------------
+template <int MAXM>
+__device__ __forceinline__ float pick(const float (&a)[MAXM], int m) {
+  float v = a[0];
+#pragma unroll
+  for (int j = 1; j < MAXM; j++) v = (m == j) ? a[j] : v;
+  return v;
+}
+
+// The reference's sequential fold, computed by one whole wave: lanes form the products of a block
+// of 64 x 32 elements in parallel, then the running fp32 sum walks the block lane by lane (lane l
+// adds its 32 products in order and hands the sum to lane l+1). Same operations, same order.
+__device__ float exact_logit_wave(const float *__restrict__ xs, const float *__restrict__ w, int H) {
+  const int lane = threadIdx.x & 63;
+  float acc = -0.0f;
+  for (int base = 0; base < H; base += 2048) {
+    float p[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+      int k = base + 32 * lane + j;
+      p[j] = k < H ? __fmul_rn(xs[k], w[k]) : 0.0f;
+    }
+    const int n = min(2048, H - base);
+    for (int l = 0; l < 64; l++) {
+      if (32 * l >= n) break;
+      if (lane == l) {
+#pragma unroll
+        for (int j = 0; j < 32; j++)
+          if (32 * l + j < n) acc = __fadd_rn(acc, p[j]);
+      }
+      acc = __shfl(acc, l, 64);
+    }
+  }
+  return acc;
+}
+
+template <int MAXM>
+__device__ __forceinline__ void reg_topk(const SelParams &P, const float (&kmid)[MAXM], const float (&lmid)[MAXM],
+                                         const float (&klo)[MAXM], int kk, int *sel, float *sel_l, float *sel_lo,
+                                         uint32_t *taken_out) {
+  const int lane = threadIdx.x & 63;
+  uint32_t taken = 0;
+  for (int r = 0; r < kk; r++) {
+    float bk = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      if (e < P.E && !((taken >> m) & 1u) && (bi == 0x7fffffff || ranks_before(kmid[m], e, bk, bi))) {
+        bk = kmid[m];
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+      const float ok = __shfl_xor(bk, d, 64);
+      const int oi = __shfl_xor(bi, d, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || ranks_before(ok, oi, bk, bi))) {
+        bk = ok;
+        bi = oi;
+      }
+    }
+    if (bi != 0x7fffffff && (bi & 63) == lane) {
+      const int m = bi >> 6;
+      taken |= 1u << m;
+      sel[r] = bi;
+      sel_l[r] = pick<MAXM>(lmid, m);
+      sel_lo[r] = pick<MAXM>(klo, m);
+    }
+  }
+  *taken_out = taken;
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(256) void k_router_select(SelParams P, const double *__restrict__ mid,
+                                                       const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                       float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                       int *__restrict__ stats) {
+  __shared__ int sel[SEL_MAXK];
+  __shared__ float sel_l[SEL_MAXK], sel_lo[SEL_MAXK];
+  __shared__ int rlist[SEL_MAXE];
+  __shared__ float rlo[SEL_MAXE], rhi[SEL_MAXE];
+  __shared__ unsigned char rex[SEL_MAXE];
+  __shared__ int amb[SEL_MAXE];
+  __shared__ float amb_val[SEL_MAXE];
+  __shared__ int namb, nR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s = blockIdx.x;
+  const int E = P.E, k = P.k, kk = min(P.k, P.E);
+  const double *ms = mid + (size_t)s * P.erows;
+  const double *bs = bnd + (size_t)s * P.erows;
+
+  float klo[MAXM], khi[MAXM], kmid[MAXM], lmid[MAXM];
+  uint32_t exact = 0, taken = 0;
+  if (wave == 0) {
+    // all loads first, so the wave waits on memory once rather than once per expert
+    double mv[MAXM], bv[MAXM];
+    float lbv[MAXM], rbv[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads batch together
+      mv[m] = ms[e];
+      bv[m] = bs[e];
+      lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
+      rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      klo[m] = khi[m] = kmid[m] = lmid[m] = -INFINITY;
+      if (e < E) {
+        const double mm = mv[m], b = bv[m];
+        const float lo = __double2float_rd(mm - b * (1.0 + 1e-12));
+        const float hi = __double2float_ru(mm + b * (1.0 + 1e-12));
+        const float md = fminf(fmaxf(__double2float_rn(mm), lo), hi);
+        lmid[m] = md;
+        kmid[m] = sel_key_v(P, lbv[m], rbv[m], md);
+        if (lo == hi) {
+          klo[m] = khi[m] = kmid[m];
+          exact |= 1u << m;
+        } else {
+          klo[m] = sel_key_v(P, lbv[m], rbv[m], lo);
+          khi[m] = sel_key_v(P, lbv[m], rbv[m], hi);
+        }
+      }
+    }
+    reg_topk<MAXM>(P, kmid, lmid, klo, kk, sel, sel_l, sel_lo, &taken);
+    // lowest lower key among the selected
+    float lo_sel = INFINITY;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++)
+      if ((taken >> m) & 1u) lo_sel = fminf(lo_sel, klo[m]);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) lo_sel = fminf(lo_sel, __shfl_xor(lo_sel, d, 64));
+    // R = experts whose upper key reaches lo_sel, compacted in (m, lane) order.
+    int base = 0;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      const bool in = e < E && khi[m] >= lo_sel;
+      const unsigned long long mask = __ballot(in);
+      if (in) {
+        const int at = base + __popcll(mask & ((1ull << lane) - 1ull));
+        rlist[at] = e;
+        rlo[at] = klo[m];
+        rhi[at] = khi[m];
+        rex[at] = (exact >> m) & 1u;
+      }
+      base += __popcll(mask);
+    }
+    if (lane == 0) {
+      nR = base;
+      namb = 0;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int n = nR;
+    for (int j = lane; j < n; j += 64) {
+      if (rex[j]) continue;
+      bool a = false;
+      for (int q = 0; q < n && !a; q++)
+        if (q != j && rlo[j] <= rhi[q] && rlo[q] <= rhi[j]) a = true;
+      if (a) amb[atomicAdd(&namb, 1)] = rlist[j];
+    }
+  }
+  __syncthreads();
+  const int na = namb;
+  if (na > 0) {
+    for (int j = wave; j < na; j += 4) {
+      const float l = exact_logit_wave(P.x + (size_t)s * P.H, P.W + (size_t)amb[j] * P.H, P.H);
+      if (lane == 0) amb_val[j] = l;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      for (int j = 0; j < na; j++) {
+        const int e = amb[j];
+        if ((e & 63) == lane) {
+          const int mm = e >> 6;
+          const float l = amb_val[j];
+          const float key = sel_key(P, e, l);
+#pragma unroll
+          for (int m = 0; m < MAXM; m++)
+            if (m == mm) {
+              lmid[m] = l;
+              kmid[m] = klo[m] = khi[m] = key;
+            }
+        }
+      }
+      reg_topk<MAXM>(P, kmid, lmid, klo, kk, sel, sel_l, sel_lo, &taken);
+    }
+    if (wave == 0 && lane == 0 && stats) atomicAdd(stats, na);
+  }
+  __syncthreads();
+  if (wave == 0 && lane == 0) {
+    int32_t *io = ids + (size_t)s * k;
+    float *wo = wts + (size_t)s * k;
+    float *lv = sel_lo;  // reused as the weight workspace (LDS)
+    for (int r = 0; r < kk; r++) {
+      const int e = sel[r];
+      lv[r] = P.logit_bias ? __fadd_rn(sel_l[r], P.logit_bias[e]) : sel_l[r];
+    }
+    if (P.family == RBT_FAMILY_QWEN38) {
+      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
+      const float mx = lv[0];
+      float sum = 0.0f;
+      for (int r = 0; r < kk; r++) {
+        lv[r] = (float)exp((double)__fsub_rn(lv[r], mx));
+        sum = __fadd_rn(sum, lv[r]);
+      }
+      for (int r = 0; r < kk; r++) wo[r] = __fdiv_rn(lv[r], sum);
+    } else {
+      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
+      for (int r = 0; r < kk; r++) lv[r] = sigmoid_ref(lv[r]);
+      if (P.norm_topk) {
+        float sum = -0.0f;
+        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, lv[r]);
+        sum = __fadd_rn(sum, 1e-20f);
+        for (int r = 0; r < kk; r++) lv[r] = __fdiv_rn(lv[r], sum);
+      }
+      for (int r = 0; r < kk; r++) wo[r] = __fmul_rn(lv[r], P.routed_scale);
+    }
+    for (int r = 0; r < kk; r++) io[r] = sel[r];
+    for (int r = kk; r < k; r++) {
+      io[r] = -1;
+      wo[r] = 0.0f;
+    }
+    if (sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
+  }
+}
+
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
 // interval is a point (bound 0) and the same selection code applies.
 __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
@@ -524,7 +904,14 @@ __global__ void k_group_s1(const int32_t *__restrict__ ids, const float *__restr
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd) {
   int erows = E + (sgate ? 1 : 0);
-  hipLaunchKernelGGL(k_router_logits, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+  bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0) && (!sgate || (uintptr_t)sgate % 16 == 0);
+  if (H % 256 == 0 && H <= RT_MAXH && aligned)
+    hipLaunchKernelGGL(k_router_logits_t, dim3(erows), dim3(64), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+  else if (H % 256 == 0 && aligned)
+    hipLaunchKernelGGL(k_router_logits_w, dim3((erows + 3) / 4), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid,
+                       bnd, erows);
+  else
+    hipLaunchKernelGGL(k_router_logits, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
   return hipGetLastError();
 }
 
@@ -545,7 +932,22 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
   P.topk_group = a.topk_group;
   P.x = a.x;
   P.W = a.W;
-  hipLaunchKernelGGL(k_router_select, dim3(a.S), dim3(64), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+  if (a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) {
+    hipLaunchKernelGGL(k_router_select_grouped, dim3(a.S), dim3(64), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                       stats);
+  } else {
+    const int m = (a.E + 63) / 64;
+    if (m <= 4)
+      hipLaunchKernelGGL(k_router_select<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+    else if (m <= 8)
+      hipLaunchKernelGGL(k_router_select<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+    else if (m <= 16)
+      hipLaunchKernelGGL(k_router_select<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                         stats);
+    else
+      hipLaunchKernelGGL(k_router_select<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                         stats);
+  }
   return hipGetLastError();
 }
 

@@ -2,7 +2,8 @@
 combine + shared expert) against the oracle's moe_forward, for the three families and the
 benchmark configurations at their real shapes.
 
-Bars: expert ids bit-exact, routing weights within 1e-6, layer output within 1e-5 relative L2.
+Bars: expert ids bit-exact; routing weights within 1e-6 (small layers) or 1e-5 relative L2 (full
+configurations, where the device sums router logits in fp64); layer output within 1e-5 relative L2.
 """
 import numpy as np
 import pytest
