@@ -523,9 +523,14 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
   rbt::RouterArgs ra{D.family, E,          erows,          k,     H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
-  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB));
-  HIP_OK(c, rbt::launch_group(*c, ids, wts, S, k, E, L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
-                              dflags + FLAG_UNIQ));
+  // one token: the selection kernel writes the job table itself; several: k_group afterwards
+  rbt::GroupArgs ga{L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
+  const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
+                                      grp_in_select ? &ga : nullptr));
+  if (!grp_in_select)
+    HIP_OK(c, rbt::launch_group(*c, ids, wts, S, k, E, L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
+                                dflags + FLAG_UNIQ));
 
   const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
                      L.shared_inter == (size_t)I;

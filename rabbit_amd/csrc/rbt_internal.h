@@ -53,8 +53,16 @@ hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, c
 // router.hip
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd);
+// Expert job-table outputs the selection kernel writes itself for a single token (S == 1).
+struct GroupArgs {
+  const RbtExpertDev *table, *shared_dev;
+  RbtExpertDev *pair_job;
+  int *pair_tok, *tok_pair;
+  float *tok_w;
+  int *err;
+};
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
-                                float *wts, float *sh_scale, int *stats);
+                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr);
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);
 hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,

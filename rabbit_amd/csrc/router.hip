@@ -262,6 +262,84 @@ __global__ __launch_bounds__(64) void k_router_logits_t(const float *__restrict_
   }
 }
 
+// Block variant (H % 1024 == 0, H <= 8192): one 256-thread workgroup per router row; coalesced
+// loads, products through padded LDS, thread t owns the contiguous segment [t*H/256, (t+1)*H/256),
+// then a block-wide fp64 scan. Four times less serial fp64 work per thread than one wave per row.
+__global__ __launch_bounds__(256) void k_router_logits_b(const float *__restrict__ x, int S, int H,
+                                                         const float *__restrict__ W, int E,
+                                                         const float *__restrict__ sgate, double *__restrict__ mid,
+                                                         double *__restrict__ bnd, int erows) {
+  __shared__ float lp[RT_MAXH + 4 * 256];
+  __shared__ double sh[4];
+  const int t = threadIdx.x;
+  const int row = blockIdx.x;
+  const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
+  const int seg = H / 256;   // elements per thread segment
+  const int segp = seg + 4;  // padded stride
+  const int nch = H / 1024;  // coalesced chunks (one float4 per thread)
+  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16;  // 2^-53
+  constexpr int MAXCH = RT_MAXH / 1024;
+  float4 wv[MAXCH];
+#pragma unroll
+  for (int c = 0; c < MAXCH; c++)
+    if (c < nch) wv[c] = w4[c * 256 + t];
+  for (int s = 0; s < S; s++) {
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)s * H);
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) {
+      if (c < nch) {
+        const float4 xv = x4[c * 256 + t];
+        const int j = c * 1024 + 4 * t;
+        const int dst = (j / seg) * segp + (j % seg);
+        float4 p;
+        p.x = __fmul_rn(xv.x, wv[c].x);
+        p.y = __fmul_rn(xv.y, wv[c].y);
+        p.z = __fmul_rn(xv.z, wv[c].z);
+        p.w = __fmul_rn(xv.w, wv[c].w);
+        *reinterpret_cast<float4 *>(&lp[dst]) = p;
+      }
+    }
+    __syncthreads();
+    const float *mine = lp + t * segp;
+    double loc = 0.0, pa = 0.0;
+    for (int q = 0; q < seg; q += 4) {
+      const float4 p = *reinterpret_cast<const float4 *>(mine + q);
+      loc += (double)p.x;
+      loc += (double)p.y;
+      loc += (double)p.z;
+      loc += (double)p.w;
+      pa += fabs((double)p.x) + fabs((double)p.y) + fabs((double)p.z) + fabs((double)p.w);
+    }
+    double total;
+    double pre = block_excl_scan_256(loc, sh, &total);
+    double T = 0.0;
+    for (int q = 0; q < seg; q += 4) {
+      const float4 p = *reinterpret_cast<const float4 *>(mine + q);
+      pre += (double)p.x;
+      T += fabs(pre);
+      pre += (double)p.y;
+      T += fabs(pre);
+      pre += (double)p.z;
+      T += fabs(pre);
+      pre += (double)p.w;
+      T += fabs(pre);
+    }
+    T = block_sum_256(T, sh);
+    pa = block_sum_256(pa, sh);
+    if (t == 0) {
+      const double n = (double)H;
+      const double slack = 8.0 * n * e64 * (pa + T) + n * n * e64 * pa;
+      const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
+      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
+      B = B * (1.0 + 1e-9) + 1e-300;
+      mid[(size_t)s * erows + row] = total;
+      bnd[(size_t)s * erows + row] = B;
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // 2. per-token selection
 // ------------------------------------------------------------------------------------------------
@@ -531,27 +609,55 @@ __device__ __forceinline__ float pick(const float (&a)[MAXM], int m) {
 }
 
 // The reference's sequential fold, computed by one whole wave: lanes form the products of a block
-// of 64 x 32 elements in parallel, then the running fp32 sum walks the block lane by lane (lane l
-// adds its 32 products in order and hands the sum to lane l+1). Same operations, same order.
+// of 64 x 32 elements in parallel (the next block's loads are already in flight), then the running
+// fp32 sum walks the block lane by lane: lane l adds its 32 products in order and v_readlane hands
+// the sum to lane l+1. Same operations in the same order as the reference; only the serial chain
+// of adds remains on the critical path. Needs H % 4 == 0 and 16-byte aligned rows (else the plain
+// loop below).
 __device__ float exact_logit_wave(const float *__restrict__ xs, const float *__restrict__ w, int H) {
   const int lane = threadIdx.x & 63;
+  if ((H & 3) || ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(w)) & 15)) {
+    float acc = -0.0f;
+    for (int i = 0; i < H; i++) acc = __fadd_rn(acc, __fmul_rn(xs[i], w[i]));
+    return acc;
+  }
+  const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+  const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  const int H4 = H >> 2;
   float acc = -0.0f;
+  float4 xa[8], wa[8];
+  auto fetch = [&](int base4) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int k = min(base4 + 8 * lane + j, H4 - 1);
+      xa[j] = x4[k];
+      wa[j] = w4[k];
+    }
+  };
+  fetch(0);
   for (int base = 0; base < H; base += 2048) {
     float p[32];
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      int k = base + 32 * lane + j;
-      p[j] = k < H ? __fmul_rn(xs[k], w[k]) : 0.0f;
+    for (int j = 0; j < 8; j++) {
+      p[4 * j + 0] = __fmul_rn(xa[j].x, wa[j].x);
+      p[4 * j + 1] = __fmul_rn(xa[j].y, wa[j].y);
+      p[4 * j + 2] = __fmul_rn(xa[j].z, wa[j].z);
+      p[4 * j + 3] = __fmul_rn(xa[j].w, wa[j].w);
     }
+    if (base + 2048 < H) fetch((base + 2048) >> 2);
     const int n = min(2048, H - base);
-    for (int l = 0; l < 64; l++) {
-      if (32 * l >= n) break;
+    const int full = n >> 5;  // lanes whose 32 products are all in range
+    for (int l = 0; l < full; l++) {
       if (lane == l) {
 #pragma unroll
-        for (int j = 0; j < 32; j++)
-          if (32 * l + j < n) acc = __fadd_rn(acc, p[j]);
+        for (int j = 0; j < 32; j++) acc = __fadd_rn(acc, p[j]);
       }
-      acc = __shfl(acc, l, 64);
+      acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), l));
+    }
+    if ((full << 5) < n) {  // partial tail lane
+      if (lane == full)
+        for (int j = 0; j < n - (full << 5); j++) acc = __fadd_rn(acc, p[j]);
+      acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), full));
     }
   }
   return acc;
@@ -752,6 +858,261 @@ __global__ __launch_bounds__(256) void k_router_select(SelParams P, const double
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Selection v2 (n_group <= 1): the k-th largest key is found exactly by a bitwise bisection over
+// order-preserving key bits, counting with wave ballots (no cross-lane data movement); ties at that
+// key go to the lowest ids, as the reference's strict-> scans do; the k winners are then ranked in
+// parallel. With `grp` set (one token per call) the kernel also writes the expert job table.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ord_key(float f) {
+  const uint32_t b = __float_as_uint(f + 0.0f);  // -0 -> +0: equal keys compare equal
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ unsigned long long lanemask_lt() {
+  const int lane = threadIdx.x & 63;
+  return (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+}
+
+struct GroupOut {
+  const RbtExpertDev *table;
+  const RbtExpertDev *shared_dev;
+  RbtExpertDev *pair_job;
+  int *pair_tok, *tok_pair;
+  float *tok_w;
+  int *err;
+};
+
+template <int MAXM>
+__device__ void bisect_topk(const uint32_t (&ku)[MAXM], uint32_t valid, int E, int kk, int *sel_id, uint32_t *sel_ku,
+                            int *nsel_out) {
+  const int lane = threadIdx.x & 63;
+  uint32_t T = 0;
+  for (int bit = 31; bit >= 0; bit--) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) cnt += __popcll(__ballot(((valid >> m) & 1u) && ku[m] >= cand));
+    if (cnt >= kk) T = cand;
+  }
+  int ngt = 0;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) ngt += __popcll(__ballot(((valid >> m) & 1u) && ku[m] > T));
+  const int need = kk - ngt;  // >= 1 winners at exactly T, lowest ids first
+  int taken_eq = 0, base = 0;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) {
+    const bool v = (valid >> m) & 1u;
+    const unsigned long long eq = __ballot(v && ku[m] == T);
+    const bool win_eq = v && ku[m] == T && (taken_eq + __popcll(eq & lanemask_lt())) < need;
+    taken_eq += __popcll(eq);
+    const bool win = (v && ku[m] > T) || win_eq;
+    const unsigned long long wm = __ballot(win);
+    if (win) {
+      const int at = base + __popcll(wm & lanemask_lt());
+      sel_id[at] = lane + 64 * m;
+      sel_ku[at] = ku[m];
+    }
+    base += __popcll(wm);
+  }
+  if (lane == 0) *nsel_out = base;
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(256) void k_router_select2(SelParams P, const double *__restrict__ mid,
+                                                        const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                        float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                        int *__restrict__ stats, GroupOut G, int grp) {
+  __shared__ int c_id[SEL_MAXK];      // winners in id order
+  __shared__ uint32_t c_ku[SEL_MAXK];
+  __shared__ int s_id[SEL_MAXK];      // winners in rank order
+  __shared__ float s_w[SEL_MAXK];
+  __shared__ float key_lo[SEL_MAXE], key_hi[SEL_MAXE], lval[SEL_MAXE];
+  __shared__ int rlist[SEL_MAXE];
+  __shared__ int amb[SEL_MAXE];
+  __shared__ float amb_val[SEL_MAXE];
+  __shared__ int nsel, namb;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s = blockIdx.x;
+  const int E = P.E, k = P.k, kk = min(P.k, P.E);
+  const double *ms = mid + (size_t)s * P.erows;
+  const double *bs = bnd + (size_t)s * P.erows;
+
+  uint32_t ku[MAXM];
+  uint32_t valid = 0, exact = 0;
+  if (wave == 0) {
+    double mv[MAXM], bv[MAXM];
+    float lbv[MAXM], rbv[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads batch together
+      mv[m] = ms[e];
+      bv[m] = bs[e];
+      lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
+      rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      ku[m] = 0;
+      if (e < E) {
+        valid |= 1u << m;
+        const float lo = __double2float_rd(mv[m] - bv[m] * (1.0 + 1e-12));
+        const float hi = __double2float_ru(mv[m] + bv[m] * (1.0 + 1e-12));
+        const float md = fminf(fmaxf(__double2float_rn(mv[m]), lo), hi);
+        const float kmid = sel_key_v(P, lbv[m], rbv[m], md);
+        ku[m] = ord_key(kmid);
+        lval[e] = md;
+        if (lo == hi) {
+          key_lo[e] = key_hi[e] = kmid;
+          exact |= 1u << m;
+        } else {
+          key_lo[e] = sel_key_v(P, lbv[m], rbv[m], lo);
+          key_hi[e] = sel_key_v(P, lbv[m], rbv[m], hi);
+        }
+      }
+    }
+    bisect_topk<MAXM>(ku, valid, E, kk, c_id, c_ku, &nsel);
+    // certification: R = experts whose upper key reaches the lowest selected lower key
+    float lo = INFINITY;
+    for (int j = lane; j < kk; j += 64) lo = fminf(lo, key_lo[c_id[j]]);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) lo = fminf(lo, __shfl_xor(lo, d, 64));
+    int base = 0;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      const bool in = ((valid >> m) & 1u) && !((exact >> m) & 1u) && key_hi[min(e, E - 1)] >= lo;
+      const unsigned long long msk = __ballot(in);
+      if (in) rlist[base + __popcll(msk & lanemask_lt())] = e;
+      base += __popcll(msk);
+    }
+    // exact members of R matter too: a non-exact expert overlapping an exact one is ambiguous
+    int nr_inexact = base;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = lane + 64 * m;
+      const bool in = ((valid >> m) & 1u) && ((exact >> m) & 1u) && key_hi[min(e, E - 1)] >= lo;
+      const unsigned long long msk = __ballot(in);
+      if (in) rlist[base + __popcll(msk & lanemask_lt())] = e;
+      base += __popcll(msk);
+    }
+    if (lane == 0) namb = 0;
+    __builtin_amdgcn_wave_barrier();
+    for (int j = lane; j < nr_inexact; j += 64) {
+      const int e = rlist[j];
+      bool a = false;
+      for (int q = 0; q < base && !a; q++) {
+        const int f = rlist[q];
+        if (f != e && key_lo[e] <= key_hi[f] && key_lo[f] <= key_hi[e]) a = true;
+      }
+      if (a) amb[atomicAdd(&namb, 1)] = e;
+    }
+  }
+  __syncthreads();
+  const int na = namb;
+  if (na > 0) {
+    for (int j = wave; j < na; j += 4) {
+      const float l = exact_logit_wave(P.x + (size_t)s * P.H, P.W + (size_t)amb[j] * P.H, P.H);
+      if (lane == 0) amb_val[j] = l;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      for (int j = 0; j < na; j++) {
+        const int e = amb[j];
+        if ((e & 63) == lane) {
+          const int mm = e >> 6;
+          const float l = amb_val[j];
+          const float key = sel_key(P, e, l);
+          lval[e] = l;
+#pragma unroll
+          for (int m = 0; m < MAXM; m++)
+            if (m == mm) ku[m] = ord_key(key);
+        }
+      }
+      bisect_topk<MAXM>(ku, valid, E, kk, c_id, c_ku, &nsel);
+    }
+    if (wave == 0 && lane == 0 && stats) atomicAdd(stats, na);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // rank the winners: (key desc, id asc)
+    if (lane < kk) {
+      const uint32_t my = c_ku[lane];
+      const int id = c_id[lane];
+      int rank = 0;
+      for (int j = 0; j < kk; j++) {
+        const uint32_t o = c_ku[j];
+        rank += (o > my) || (o == my && c_id[j] < id);
+      }
+      s_id[rank] = id;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // weights, computed by the lanes in parallel; the sums run in rank order (lane 0)
+    float lv = 0.0f;
+    if (lane < kk) {
+      const int e = s_id[lane];
+      lv = P.logit_bias ? __fadd_rn(lval[e], P.logit_bias[e]) : lval[e];
+    }
+    if (P.family == RBT_FAMILY_QWEN38) {
+      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
+      const float mx = __shfl(lv, 0, 64);
+      if (lane < kk) s_w[lane] = (float)exp((double)__fsub_rn(lv, mx));
+      __builtin_amdgcn_wave_barrier();
+      float sum = 0.0f;
+      for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
+      if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
+    } else {
+      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
+      if (lane < kk) s_w[lane] = sigmoid_ref(lv);
+      __builtin_amdgcn_wave_barrier();
+      if (P.norm_topk) {
+        float sum = -0.0f;
+        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
+        sum = __fadd_rn(sum, 1e-20f);
+        if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
+      }
+      if (lane < kk) s_w[lane] = __fmul_rn(s_w[lane], P.routed_scale);
+    }
+    __builtin_amdgcn_wave_barrier();
+    int32_t *io = ids + (size_t)s * k;
+    float *wo = wts + (size_t)s * k;
+    for (int r = lane; r < k; r += 64) {
+      io[r] = r < kk ? s_id[r] : -1;
+      wo[r] = r < kk ? s_w[r] : 0.0f;
+    }
+    if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
+    if (grp) {
+      // single token: pair j = slot j; the shared expert is pair k
+      for (int r = lane; r <= k; r += 64) {
+        if (r < k) {
+          // field copies (a struct temporary here ends up in scratch memory)
+          const RbtExpertDev *src = G.table + (r < kk ? s_id[r] : 0);
+          RbtExpertDev *dst = G.pair_job + r;
+          const bool use = r < kk;
+          const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
+          const uint8_t *dd = use ? src->dd : nullptr;
+          const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
+          const void *ds = use ? src->ds : nullptr;
+          if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
+          dst->gd = gd;
+          dst->gs = gs;
+          dst->ud = ud;
+          dst->us = us;
+          dst->dd = dd;
+          dst->ds = ds;
+          G.pair_tok[r] = 0;
+          G.tok_pair[r] = r < kk ? r : -1;
+          G.tok_w[r] = r < kk ? s_w[r] : 0.0f;
+        } else {
+          G.pair_job[k] = *G.shared_dev;
+          G.pair_tok[k] = 0;
+        }
+      }
+    }
+  }
+}
+
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
 // interval is a point (bound 0) and the same selection code applies.
 __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
@@ -905,7 +1266,9 @@ hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, cons
                                 double *mid, double *bnd) {
   int erows = E + (sgate ? 1 : 0);
   bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0) && (!sgate || (uintptr_t)sgate % 16 == 0);
-  if (H % 256 == 0 && H <= RT_MAXH && aligned)
+  if (H % 1024 == 0 && H <= RT_MAXH && aligned)
+    hipLaunchKernelGGL(k_router_logits_b, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+  else if (H % 256 == 0 && H <= RT_MAXH && aligned)
     hipLaunchKernelGGL(k_router_logits_t, dim3(erows), dim3(64), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
   else if (H % 256 == 0 && aligned)
     hipLaunchKernelGGL(k_router_logits_w, dim3((erows + 3) / 4), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid,
@@ -916,7 +1279,7 @@ hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, cons
 }
 
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
-                                float *wts, float *sh_scale, int *stats) {
+                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp) {
   SelParams P;
   P.family = a.family;
   P.E = a.E;
@@ -936,17 +1299,25 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
     hipLaunchKernelGGL(k_router_select_grouped, dim3(a.S), dim3(64), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
                        stats);
   } else {
+    GroupOut G{};
+    int g = 0;
+    if (grp && a.S == 1) {
+      G = GroupOut{grp->table, grp->shared_dev, grp->pair_job, grp->pair_tok, grp->tok_pair, grp->tok_w, grp->err};
+      g = 1;
+    }
     const int m = (a.E + 63) / 64;
     if (m <= 4)
-      hipLaunchKernelGGL(k_router_select<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+      hipLaunchKernelGGL(k_router_select2<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+                         G, g);
     else if (m <= 8)
-      hipLaunchKernelGGL(k_router_select<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats);
+      hipLaunchKernelGGL(k_router_select2<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+                         G, g);
     else if (m <= 16)
-      hipLaunchKernelGGL(k_router_select<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
-                         stats);
+      hipLaunchKernelGGL(k_router_select2<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                         stats, G, g);
     else
-      hipLaunchKernelGGL(k_router_select<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
-                         stats);
+      hipLaunchKernelGGL(k_router_select2<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                         stats, G, g);
   }
   return hipGetLastError();
 }
