@@ -199,8 +199,8 @@ int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, fl
 /* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
 typedef struct {
     double router_ms;    /* router logits + top-k selection + grouping */
-    double gateup_ms;    /* gate/up dequant-GEMV with SiLU (all experts of the call) */
-    double down_ms;      /* down dequant-GEMV */
+    double gateup_ms;    /* gate/up dequant-GEMV (all experts of the call) */
+    double down_ms;      /* silu(g)*u and the down dequant-GEMV */
     double combine_ms;   /* weighted combine + shared expert */
     uint64_t calls;      /* rbt_moe_forward_d calls recorded */
     uint64_t ambiguous;  /* router logits recomputed exactly because of a near-tie */

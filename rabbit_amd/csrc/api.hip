@@ -311,8 +311,8 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
     RBT_TRY(scratch_t(c, SC_GU, (size_t)njobs * gs_stride, &gu));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_STACKED, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d,
                                  (int)d, (int)(2 * i), gu, gs_stride, parts));
-    HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h));
     if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
+    HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
                                  (int)i, (int)d, y, (long)d));
     return RBT_OK;
@@ -509,7 +509,8 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
   RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
   size_t hi = std::max((size_t)I, L.shared_inter);
-  RBT_TRY(scratch_t(c, SC_H, (size_t)npairs * hi, &h));
+  // 2 * hi floats per pair: fp32 h for the GEMV path, or three bf16 parts (1.5 * I) for the MFMA path
+  RBT_TRY(scratch_t(c, SC_H, (size_t)npairs * hi * 2, &h));
   RBT_TRY(scratch_t(c, SC_YY, (size_t)npairs * H, &yy));
   int *dflags = c->d_flags;
 
@@ -537,18 +538,31 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RbtExpertDev none{};
   hipEvent_t *mark = c->prof ? &ev[2] : nullptr;
   if (c->prof) HIP_OK(c, hipEventRecord(ev[1], c->stream));
-  if (merge || !D.has_shared) {
-    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy, mark));
-  } else {
-    RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, P, nullptr, x, ptok, H, I, h, yy, nullptr));
-    // shared pairs [P, P+S): h rows at stride shared_inter after the routed block
-    float *hs = h + (size_t)P * I;
-    RBT_TRY(expert_pairs(c, L.shared_kind, L.shared_gs, pjob + P, none, S, nullptr, x, ptok + P, H, L.shared_inter, hs,
-                         yy + (size_t)P * H, nullptr));
+  // MXFP4 decode shapes run on the matrix cores: gate/up with SiLU, then down with the ordered
+  // combine fused in (out written directly).
+  const bool mfma = (merge || !D.has_shared) && rbt::xgemm_ok(L.routed_kind, H, I, S, k, D.has_shared) &&
+                    ((uintptr_t)x % 16 == 0);
+  if (mfma) {
+    // h as three bf16 parts per pair (3 * I bf16 = 1.5 * I floats of the h scratch)
+    __bf16 *hp = reinterpret_cast<__bf16 *>(h);
+    HIP_OK(c, rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp));
     if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
+    HIP_OK(c, rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out));
+    if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+  } else {
+    if (merge || !D.has_shared) {
+      RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy, mark));
+    } else {
+      RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, P, nullptr, x, ptok, H, I, h, yy, nullptr));
+      // shared pairs [P, P+S): h rows at stride shared_inter after the routed block
+      float *hs = h + (size_t)P * I;
+      RBT_TRY(expert_pairs(c, L.shared_kind, L.shared_gs, pjob + P, none, S, nullptr, x, ptok + P, H, L.shared_inter,
+                           hs, yy + (size_t)P * H, nullptr));
+      if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
+    }
+    if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+    HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
   }
-  if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
-  HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
   if (c->prof) {
     HIP_OK(c, hipEventRecord(ev[4], c->stream));
     c->ev_rows.push_back(ev);

@@ -59,26 +59,28 @@ __device__ __forceinline__ float i4_dword_dot(uint32_t w, const float *xv, float
 template <int NB, int LPR>
 __device__ __forceinline__ void load_x_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ x,
                                              int q, int nblk) {
+  // unconditional loads from a clamped (in-bounds) block, then zeroed: no branches around loads,
+  // so the compiler can count outstanding loads instead of draining them.
+  const rbt_gf4 *xg = (const rbt_gf4 *)x;
 #pragma unroll
   for (int j = 0; j < NB; j++) {
-    int b = q + LPR * j;
-    float s = 0.0f;
-    if (b < nblk) {
-      const float4 *p = reinterpret_cast<const float4 *>(x + 32 * b);
+    const int b = q + LPR * j;
+    const bool ok = b < nblk;
+    const int bb = ok ? b : nblk - 1;
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        float4 v = p[t];
-        xr[j][4 * t + 0] = v.x;
-        xr[j][4 * t + 1] = v.y;
-        xr[j][4 * t + 2] = v.z;
-        xr[j][4 * t + 3] = v.w;
-      }
-#pragma unroll
-      for (int t = 0; t < 32; t++) s += xr[j][t];
-    } else {
-#pragma unroll
-      for (int t = 0; t < 32; t++) xr[j][t] = 0.0f;
+    for (int t = 0; t < 8; t++) {
+      const float4 v = xg[8 * bb + t];
+      xr[j][4 * t + 0] = ok ? v.x : 0.0f;
+      xr[j][4 * t + 1] = ok ? v.y : 0.0f;
+      xr[j][4 * t + 2] = ok ? v.z : 0.0f;
+      xr[j][4 * t + 3] = ok ? v.w : 0.0f;
     }
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 32; t++) s += xr[j][t];
     xs[j] = s;
   }
 }
@@ -110,6 +112,9 @@ struct DecodeFrag {
 
 // Loads the blocks of IPI = U * (64/LPR) consecutive rows starting at `row` (a row pointer into
 // `d`, rows rb bytes apart; scales `sc`, nblk per row). Lane (sub, q) takes rows row + u*RPI + sub.
+// Every load is unconditional (blocks past nblk re-read block nblk-1; block_dots drops them), so
+// the loop body is straight-line and the next iteration's loads stay in flight during this one's
+// arithmetic.
 template <int NB, int LPR, int U, bool I4G>
 __device__ __forceinline__ void frag_load(DecodeFrag<NB, U> &f, const uint8_t *__restrict__ d,
                                           const uint8_t *__restrict__ sc, int row, int q, int sub, int nblk,
@@ -118,27 +123,24 @@ __device__ __forceinline__ void frag_load(DecodeFrag<NB, U> &f, const uint8_t *_
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const unsigned r = (unsigned)(row + u * RPI + sub);
-    const rbt_u4 *rp = reinterpret_cast<const rbt_u4 *>(d + (size_t)r * rb);
+    const rbt_gu4 *rp = (const rbt_gu4 *)(d + (size_t)r * rb);
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int b = q + LPR * j;
-      if (NB * LPR == nblk || b < nblk) {
-        f.w[u][j] = __builtin_nontemporal_load(rp + b);
-        if (I4G)
-          f.sb[u][j] = reinterpret_cast<const uint32_t *>(sc)[(size_t)r * sstride + b];
-        else
-          f.sb[u][j] = sc[(size_t)r * sstride + b];
-      } else {
-        f.w[u][j] = I4G ? rbt_u4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u} : rbt_u4{0u, 0u, 0u, 0u};
-        f.sb[u][j] = I4G ? 0u : 127u;
-      }
+      const int bb = min(b, nblk - 1);
+      f.w[u][j] = __builtin_nontemporal_load(rp + bb);
+      if (I4G)
+        f.sb[u][j] = ((const rbt_gu32 *)sc)[(size_t)r * sstride + bb];
+      else
+        f.sb[u][j] = ((const rbt_gu8 *)sc)[(size_t)r * sstride + bb];
     }
   }
 }
 
-template <int NB, bool I4G>
+// Blocks b = q + LPR*j past nblk hold a re-read of block nblk-1 (frag_load) and contribute nothing.
+template <int NB, int LPR, bool I4G>
 __device__ __forceinline__ float block_dots(const rbt_u4 (&w)[NB], const uint32_t (&sb)[NB], const float (&xr)[NB][32],
-                                            const float (&xs)[NB]) {
+                                            const float (&xs)[NB], int q, int nblk) {
   float r = 0.0f;
 #pragma unroll
   for (int j = 0; j < NB; j++) {
@@ -149,14 +151,15 @@ __device__ __forceinline__ float block_dots(const rbt_u4 (&w)[NB], const uint32_
       a = i4_dword_dot(w[j].z, &xr[j][16], a);
       a = i4_dword_dot(w[j].w, &xr[j][24], a);
       // sum_k x_k (n_k - 8) = sum_k x_k n_k - 8 sum_k x_k, then the group scale.
-      r = __builtin_fmaf(__builtin_fmaf(-8.0f, xs[j], a), __uint_as_float(sb[j]), r);
+      const float t = __builtin_fmaf(__builtin_fmaf(-8.0f, xs[j], a), __uint_as_float(sb[j]), r);
+      r = (q + LPR * j < nblk) ? t : r;
     } else {
       const float sc = rbt_e8m0(sb[j]);
       a = fp4_dword_dot(w[j].x, sc, &xr[j][0], a);
       a = fp4_dword_dot(w[j].y, sc, &xr[j][8], a);
       a = fp4_dword_dot(w[j].z, sc, &xr[j][16], a);
       a = fp4_dword_dot(w[j].w, sc, &xr[j][24], a);
-      r += a;
+      r += (q + LPR * j < nblk) ? a : 0.0f;
     }
   }
   return r;
@@ -208,11 +211,12 @@ __device__ __forceinline__ void load_act_slice(float (&xr)[NB][32], float (&xs)[
 
 template <int NB, int LPR, int U, bool I4G>
 __device__ __forceinline__ void frag_reduce_store(const DecodeFrag<NB, U> &f, const float (&xr)[NB][32],
-                                                  const float (&xs)[NB], float *__restrict__ yrow, int q, int sub) {
+                                                  const float (&xs)[NB], float *__restrict__ yrow, int q, int sub,
+                                                  int nblk) {
   constexpr int RPI = RBT_WAVE / LPR;
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    float a = block_dots<NB, I4G>(f.w[u], f.sb[u], xr, xs);
+    float a = block_dots<NB, LPR, I4G>(f.w[u], f.sb[u], xr, xs, q, nblk);
     a = rbt_group_sum<LPR>(a);
     if (q == 0) yrow[u * RPI + sub] = a;
     // one row at a time: keeps the scheduler from decoding every row's nibbles up front, which
@@ -286,13 +290,17 @@ __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restr
         load_x_slice<NB, LPR>(xr, xs, x + tok * x_stride + (long)h * pcols, q, nblk);
       cur = tok * CS + h;
     }
-    for (; r < r1; r += 2 * IPI) {
-      const bool has1 = r + IPI < r1;
-      if (has1) frag_load<NB, LPR, U, I4G>(f1, d, sc, r + IPI, q, sub, nblk, rb, CS * nblk);
-      frag_reduce_store<NB, LPR, U, I4G>(f0, xr, xs, yrow + r, q, sub);
-      if (!has1) break;
-      if (r + 2 * IPI < r1) frag_load<NB, LPR, U, I4G>(f0, d, sc, r + 2 * IPI, q, sub, nblk, rb, CS * nblk);
-      frag_reduce_store<NB, LPR, U, I4G>(f1, xr, xs, yrow + r + IPI, q, sub);
+    // The prefetch is unconditional: past the segment's last iteration it re-reads that iteration
+    // (rlast), so every load sits in straight-line code.
+    const int rlast = r1 - IPI;
+    while (true) {
+      frag_load<NB, LPR, U, I4G>(f1, d, sc, min(r + IPI, rlast), q, sub, nblk, rb, CS * nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f0, xr, xs, yrow + r, q, sub, nblk);
+      if (r + IPI >= r1) break;
+      frag_load<NB, LPR, U, I4G>(f0, d, sc, min(r + 2 * IPI, rlast), q, sub, nblk, rb, CS * nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f1, xr, xs, yrow + r + IPI, q, sub, nblk);
+      r += 2 * IPI;
+      if (r >= r1) break;
     }
   }
 }

@@ -12,6 +12,19 @@
 
 typedef float rbt_f2 __attribute__((ext_vector_type(2)));
 typedef unsigned int rbt_u4 __attribute__((ext_vector_type(4)));
+// Global-address-space views (addrspace 1): loads through them are global_load_* rather than
+// flat_load_*, which count only in vmcnt and let the compiler keep several loads in flight.
+// The host compilation pass only parses device functions, and HIP's float4 class has no
+// address-space-qualified constructors there, so it sees plain types.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define RBT_GLOBAL __attribute__((address_space(1)))
+#else
+#define RBT_GLOBAL
+#endif
+typedef RBT_GLOBAL const rbt_u4 rbt_gu4;
+typedef RBT_GLOBAL const float4 rbt_gf4;
+typedef RBT_GLOBAL const uint32_t rbt_gu32;
+typedef RBT_GLOBAL const uint8_t rbt_gu8;
 
 // e8m0_decode (quant.rs:391-396): byte 0 is the subnormal 2^-127, every other byte is the f32
 // biased exponent field (255 -> +inf).

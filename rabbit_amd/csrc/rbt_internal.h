@@ -50,6 +50,15 @@ hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, c
                                const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
                                const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride);
 
+// xgemm.hip: MXFP4 expert products on the matrix cores (decode shapes).
+bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared);
+hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok, int npairs, const float *x,
+                          long x_stride, int K, int I, __bf16 *hp);
+// hp: h as three bf16 parts per pair, hp[(p*3 + part)*I + k].
+hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
+                        int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
+                        int has_shared, int gated, float *out);
+
 // router.hip
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd);

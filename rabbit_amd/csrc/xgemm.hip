@@ -1,0 +1,396 @@
+// xgemm.hip -- MXFP4 expert products on the matrix cores (gfx950 MFMA), decode shapes.
+//
+// Weights: each lane loads 16 bytes (32 E2M1 codes, one 32-element block) of one weight row and
+// turns them into bf16 with v_cvt_scalef32_pk_bf16_fp4, which applies the block's E8M0 scale in the
+// same instruction. e2m1 * 2^(s-127) has at most two significant bits, so the bf16 weight equals
+// the reference's dequantized weight (quant.rs:325-339) for every scale the weights use in
+// practice: normal values are exact, only blocks whose scaled codes fall below 2^-126 (scale bytes
+// 0..2) reach the matrix core as bf16 subnormals.
+//
+// Activations: x (fp32) is split exactly into three bf16 parts hi + mid + lo (each the bf16
+// rounding of what the previous parts leave), and the parts are three columns of the MFMA's B
+// operand. Products of bf16 values are exact in fp32 and the matrix core accumulates in fp32, so the
+// result has fp32-accumulation accuracy (the 1e-5 relative-L2 contract), like an FMA chain with a
+// different association.
+//
+// Tile shape: v_mfma_f32_16x16x32_bf16 multiplies a 16x32 A tile by a 32x16 B tile. Lane l
+// supplies A[l%16][8*(l/16) + 0..7] and B[8*(l/16) + 0..7][l%16] and receives D[4*(l/16) + i][l%16],
+// i = 0..3. The 16 A rows here are "virtual rows" v = 4*rho + kappa: weight row rho (0..3) of a
+// 4-row tile, restricted to column quarter kappa, where a 512-column step is cut into four
+// 128-column quarters. Lane l (rho = (l%16)/4, kappa = l%4, g = l/16) loads 16 bytes = 32 codes of
+// its row at columns 512*c + 128*kappa + 32*g, so one load instruction reads 4 rows x 256
+// contiguous bytes (streams of 16 rows x 64 bytes run at two thirds of the bandwidth on this part).
+// B column j = 4*kappa' + p holds activation part p (< 3; p = 3 is zero) at quarter kappa'. Only
+// the D entries with kappa' == kappa are used: lane l's useful value is acc[(l%16)/4] for weight
+// row l/16, and the 12 useful lanes of a 16-lane row group sum to that row's dot product.
+//
+// Work split:
+//   k_xgateup : a wave owns 16 gate and 16 up rows (four 4-row tiles each) of one (expert, token)
+//               pair over all columns; the four waves of a workgroup share the pair's activation
+//               parts in LDS. Output h = silu(g) * u (glm52/moe.rs:33-80) as three bf16 parts.
+//   k_xdown   : a wave owns one 4-row tile of the output for every pair of the call, one pair after
+//               the other (the pair's h parts in LDS), and accumulates the ordered combine of
+//               qwen38/generate.rs:303-349 / glm52/moe.rs:508-512 in place -> out.
+#include "rbt_device.h"
+#include "rbt_internal.h"
+
+namespace rbt {
+
+typedef __bf16 xb8 __attribute__((ext_vector_type(8)));
+typedef __bf16 xb2 __attribute__((ext_vector_type(2)));
+typedef float xf4 __attribute__((ext_vector_type(4)));
+
+constexpr int XG_PAD = 8;        // bf16 padding between the LDS part rows (bank spread)
+constexpr int XD_MAXP = 80;      // pairs per down launch (partial tiles kept in LDS)
+
+// 8 E2M1 codes (one dword) -> 8 bf16, scaled by the block's E8M0 value.
+__device__ __forceinline__ xb8 fp4x8_bf16(uint32_t w, float sc) {
+  const xb2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+  const xb2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+  const xb2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+  const xb2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
+  return xb8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// x = hi + mid + lo, each part the bf16 rounding of the remainder (the remainders are exact in
+// fp32: x and hi agree to within one bf16 ulp).
+__device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l) {
+  h = (__bf16)x;
+  const float r1 = x - (float)h;
+  m = (__bf16)r1;
+  const float r2 = r1 - (float)m;
+  l = (__bf16)r2;
+}
+
+struct XChunk {
+  rbt_u4 w;    // 32 E2M1 codes of this lane's row at its 32 columns of the step
+  uint32_t s;  // the row's four E8M0 bytes of this lane's quarter (blocks 16*step + 4*kappa .. +3)
+};
+
+// One 512-column step of a lane's row: `row` points at the lane's 16 bytes of step 0 (row start +
+// 64*kappa + 16*g), `srow` at its quarter's scale dword of step 0 (scale row + 4*kappa, 4-byte
+// aligned). A step is 256 bytes of codes and 16 scale bytes.
+__device__ __forceinline__ void xload(XChunk &c, const uint8_t *row, const uint8_t *srow, int step) {
+  c.w = __builtin_nontemporal_load((const rbt_gu4 *)(row + 256 * step));
+  c.s = *(const rbt_gu32 *)(srow + 16 * step);
+}
+
+// The four B operands of one step: lane l (column j = l%16: quarter j/4, part j%4) reads 8 values
+// of its part per MFMA; lanes of part 3 read a 64-byte zero block (their pointer does not move).
+struct XB {
+  xb8 b[4];
+};
+__device__ __forceinline__ XB xb_read(const char *bp) {
+  XB r;
+#pragma unroll
+  for (int m = 0; m < 4; m++) r.b[m] = *reinterpret_cast<const xb8 *>(bp + 16 * m);
+  return r;
+}
+
+// acc0/acc1 += A(chunk) . B: even and odd MFMAs go to separate accumulators (two independent
+// dependency chains); the caller adds them in a fixed order.
+// E8M0 byte -> f32 scale, max(b << 23, 2^-127 bits): byte 0 is 2^-127, 255 the +inf bits
+// (e8m0_decode, quant.rs:391-396). Written as volatile asm so it stays in the step that multiplies
+// the chunk: as plain code, instruction selection places the byte test right after the byte's
+// load, four steps early, and the compiler then waits for that load there.
+// `sh` = 8 * (lane's block within the dword).
+__device__ __forceinline__ float e8m0_inplace(uint32_t sw, uint32_t sh) {
+  uint32_t r;
+  asm volatile("v_bfe_u32 %0, %1, %2, 8\n\tv_lshlrev_b32 %0, 23, %0\n\tv_max_u32 %0, 0x400000, %0"
+               : "=&v"(r)
+               : "v"(sw), "v"(sh));
+  return __uint_as_float(r);
+}
+
+// acc += A(step) . B: the four MFMAs of the lane's 32 codes (8 per MFMA).
+__device__ __forceinline__ void xmma1(const XChunk &c, uint32_t sh, const XB &B, xf4 &acc) {
+  const float sc = e8m0_inplace(c.s, sh);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(c.w.x, sc), B.b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(c.w.y, sc), B.b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(c.w.z, sc), B.b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(c.w.w, sc), B.b[3], acc, 0, 0, 0);
+}
+
+// Dot product of weight row l/16 of the tile from the accumulator (see the tile-shape notes): the
+// lane's useful entry is acc[(l%16)/4] unless its part is 3; the 16 lanes of the row group sum
+// them (every lane of the group ends with the same value).
+__device__ __forceinline__ float row_dot(const xf4 &acc, int col) {
+  const int kq = col >> 2;
+  float v = kq == 0 ? acc[0] : kq == 1 ? acc[1] : kq == 2 ? acc[2] : acc[3];
+  v = (col & 3) == 3 ? 0.0f : v;
+  return rbt_group_sum<16>(v);
+}
+
+// ------------------------------------------------------------------------------------------------
+// gate/up: grid (I/64, npairs), 256 threads. Wave w owns rows 16*(4*blockIdx.x + w) .. +15 of gate
+// and of up for pair p = blockIdx.y, as four 4-row tiles, over all K = 512*NCH columns. The step
+// loop is fully unrolled: the loads of step c + XG_DEPTH are issued while step c multiplies.
+// h = silu(gate . x) * (up . x) goes out as three bf16 parts hp[(p*3 + part)*I + r].
+// ------------------------------------------------------------------------------------------------
+constexpr int XG_DEPTH = 2;  // steps in flight per wave (8 KB of codes each)
+
+template <int NCH>
+__global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict__ jobs, const int *__restrict__ tok,
+                                                 const float *__restrict__ x, long x_stride, int I,
+                                                 __bf16 *__restrict__ hp) {
+  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024;
+  __shared__ __attribute__((aligned(16))) __bf16 xs[3 * stride];
+  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  const int p = blockIdx.y;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int rho = col >> 2, kap = col & 3;
+  const uint32_t sh = 8u * (uint32_t)g;
+  const RbtExpertDev J = jobs[p];
+  const long r0 = 16L * (4 * blockIdx.x + w);  // first row of the wave
+  if (J.gd == nullptr || J.ud == nullptr) {
+    for (int e = threadIdx.x; e < 3 * 64; e += 256)
+      hp[((long)p * 3 + e / 64) * I + 64 * blockIdx.x + (e & 63)] = (__bf16)0.0f;
+    return;
+  }
+  // activation first (the oldest loads in flight), then the weight ring
+  float4 xv[XV];
+  {
+    const rbt_gf4 *s4 = (const rbt_gf4 *)(x + (long)tok[p] * x_stride);
+#pragma unroll
+    for (int j = 0; j < XV; j++) xv[j] = s4[threadIdx.x + 256 * j];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // lane pointers: tile t, matrix m (0 gate, 1 up)
+  const uint8_t *wrow[2][4], *srow[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; m++)
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const long rr = r0 + 4 * t + rho;
+      wrow[m][t] = (m ? J.ud : J.gd) + rr * (K >> 1) + 64 * kap + 16 * g;
+      srow[m][t] = (const uint8_t *)(m ? J.us : J.gs) + rr * (K >> 5) + 4 * kap;
+    }
+  XChunk ring[XG_DEPTH][2][4];
+#pragma unroll
+  for (int d = 0; d < XG_DEPTH; d++) {
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) xload(ring[d][m][t], wrow[m][t], srow[m][t], d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
+#pragma unroll
+  for (int j = 0; j < XV; j++) {
+    const int q = threadIdx.x + 256 * j;
+    const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      __bf16 hh, mm, ll;
+      split3(e4[e], hh, mm, ll);
+      xs[4 * q + e] = hh;
+      xs[stride + 4 * q + e] = mm;
+      xs[2 * stride + 4 * q + e] = ll;
+    }
+  }
+  __syncthreads();
+
+  const int bq = col >> 2, bpart = col & 3;
+  const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
+                             : reinterpret_cast<const char *>(zb);
+  const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
+  xf4 acc[2][4];
+#pragma unroll
+  for (int m = 0; m < 2; m++)
+#pragma unroll
+    for (int t = 0; t < 4; t++) acc[m][t] = xf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NCH; c++) {
+    const int d = c % XG_DEPTH;
+    const XB B = xb_read(bp + binc * c);
+#pragma unroll
+    for (int m = 0; m < 2; m++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        xmma1(ring[d][m][t], sh, B, acc[m][t]);
+      }
+    if (c + XG_DEPTH < NCH) {
+#pragma unroll
+      for (int m = 0; m < 2; m++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) xload(ring[d][m][t], wrow[m][t], srow[m][t], c + XG_DEPTH);
+    }
+    // keep each step's work in its step (see e8m0_inplace)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    const float gv = row_dot(acc[0][t], col), uv = row_dot(acc[1][t], col);
+    if (col == 0) {  // lane 16*g: row r0 + 4t + g
+      const float hv = rbt_silu(gv) * uv;
+      __bf16 hh, mm, ll;
+      split3(hv, hh, mm, ll);
+      const long rr = r0 + 4 * t + g;
+      hp[((long)p * 3 + 0) * I + rr] = hh;
+      hp[((long)p * 3 + 1) * I + rr] = mm;
+      hp[((long)p * 3 + 2) * I + rr] = ll;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// down + combine: grid (H/16), 256 threads. Wave w owns output rows 16*blockIdx.x + 4w .. +3 (one
+// tile) over all I = 512*NCH columns, for every pair of the call in pair order, with each pair's h
+// parts (hp, bf16) staged in LDS by the whole workgroup. The ordered combine of
+//   out[t, r] = sum_j w[t,j] * y_{pair(t,j)}[r]   (pairs in tok_pair order, separate roundings)
+//             + shared_t[r] * sh_scale[t]         (has_shared; the scale only when gated)
+// is accumulated per (token, row) in LDS as the pairs arrive: pairs are grouped in the order
+// tok_pair lists them (first occurrence), so each token's terms come in its own order, and the
+// shared pairs [S*k, S*k + S) come last. Requires npairs <= XD_MAXP, S <= 16.
+// ------------------------------------------------------------------------------------------------
+constexpr int XD_DEPTH = 8;  // (pair, step) chunks in flight per wave: two pairs of NCH = 4 steps
+
+template <int NCH>
+__global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ jobs, int npairs,
+                                               const __bf16 *__restrict__ hp, int I, int H, int S, int k,
+                                               const int *__restrict__ tok, const int *__restrict__ tok_pair,
+                                               const float *__restrict__ tok_w, const float *__restrict__ sh_scale,
+                                               int has_shared, int gated, float *__restrict__ out) {
+  constexpr int KD = NCH * 512, stride = KD + XG_PAD;
+  constexpr int HV = 3 * KD / 8 / 256;  // 16-byte pieces of a pair's parts per thread
+  __shared__ __attribute__((aligned(16))) __bf16 hs[2][3 * stride];
+  __shared__ float oacc[16][16];        // [token][row of the workgroup]
+  __shared__ float pw[XD_MAXP];         // weight of each pair (routing weight or shared scale)
+  __shared__ int ptok[XD_MAXP];
+  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int rho = col >> 2, kap = col & 3;
+  const uint32_t sh = 8u * (uint32_t)g;
+  const int P = S * k;
+  if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
+  oacc[threadIdx.x >> 4][threadIdx.x & 15] = 0.0f;
+  for (int pp = threadIdx.x; pp < npairs; pp += 256) {
+    float wv = 0.0f;
+    int tt = pp < P ? tok[pp] : pp - P;
+    if (pp < P) {
+      for (int j = 0; j < k; j++)
+        if (tok_pair[tt * k + j] == pp) wv = tok_w[tt * k + j];
+    } else {
+      wv = gated ? sh_scale[tt] : 1.0f;
+    }
+    pw[pp] = wv;
+    ptok[pp] = (pp < P || has_shared) ? tt : -1;
+  }
+  // Pairs with a null job load the rows of the first live pair (valid memory) and add nothing.
+  int live0 = -1;
+  for (int pp = 0; pp < npairs && live0 < 0; pp++)
+    if (jobs[pp].dd != nullptr) live0 = pp;
+  __syncthreads();
+  const int tile_r0 = 16 * blockIdx.x + 4 * w;
+  if (live0 >= 0) {
+    const uint8_t *fd = jobs[live0].dd, *fs = (const uint8_t *)jobs[live0].ds;
+    auto lane_rows = [&](int pp, const uint8_t *&wr, const uint8_t *&sr) {
+      const RbtExpertDev J = jobs[pp];
+      const uint8_t *d = J.dd ? J.dd : fd;
+      const uint8_t *scl = J.dd ? (const uint8_t *)J.ds : fs;
+      const long rr = tile_r0 + rho;
+      wr = d + rr * (KD >> 1) + 64 * kap + 16 * g;
+      sr = scl + rr * (KD >> 5) + 4 * kap;
+    };
+    rbt_u4 hv[HV];
+    auto load_h = [&](int pp) {
+      const rbt_gu4 *s4 = (const rbt_gu4 *)(hp + (long)pp * 3 * KD);
+#pragma unroll
+      for (int j = 0; j < HV; j++) hv[j] = s4[threadIdx.x + 256 * j];
+    };
+    auto store_h = [&](int buf) {
+#pragma unroll
+      for (int j = 0; j < HV; j++) {
+        const int e = 8 * (threadIdx.x + 256 * j);  // element in [0, 3*KD)
+        const int part = e / KD, kk = e - part * KD;
+        *reinterpret_cast<rbt_u4 *>(&hs[buf][part * stride + kk]) = hv[j];
+      }
+    };
+    // chunk q = (pair q / NCH, step q % NCH); ring slot q % XD_DEPTH
+    const int total = npairs * NCH;
+    static_assert(XD_DEPTH == 2 * NCH, "the ring holds two pairs");
+    XChunk ring[XD_DEPTH];
+    load_h(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < XD_DEPTH; i++) {
+      const int q = min(i, total - 1);
+      const uint8_t *wr, *sr;
+      lane_rows(q / NCH, wr, sr);
+      xload(ring[i], wr, sr, q % NCH);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    store_h(0);
+    __syncthreads();
+    const int bq = col >> 2, bpart = col & 3;
+    const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
+    const int binc = bpart < 3 ? 1024 : 0;
+    // Pairs two at a time so ring slots are compile-time (slot = half*NCH + step); with an odd
+    // pair count the last half is a dummy (clamped, in-bounds loads; nothing accumulated).
+    for (int pp = 0; pp < npairs; pp += 2) {
+#pragma unroll
+      for (int half = 0; half < 2; half++) {
+        const int cp = pp + half;
+        load_h(min(cp + 1, npairs - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[half]) + boff : reinterpret_cast<const char *>(zb);
+        xf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+          const int slot = half * NCH + c;
+          const XB B = xb_read(bp + binc * c);
+          xmma1(ring[slot], sh, B, acc);
+          const int qn = min((cp + 2) * NCH + c, total - 1);
+          const uint8_t *wr, *sr;
+          lane_rows(qn / NCH, wr, sr);
+          xload(ring[slot], wr, sr, qn % NCH);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        const float y = row_dot(acc, col);
+        if (cp < npairs) {
+          const int tt = ptok[cp];
+          if (col == 0 && tt >= 0 && jobs[cp].dd != nullptr) {  // lane 16*g: row tile_r0 + g
+            float &o = oacc[tt][4 * w + g];
+            o = __fadd_rn(o, __fmul_rn(pw[cp], y));
+          }
+        }
+        store_h(half ^ 1);
+        __syncthreads();
+      }
+    }
+  }
+  const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
+  if (t < S) out[(long)t * H + 16 * blockIdx.x + rr] = oacc[t][rr];
+}
+
+bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared) {
+  if (kind != RBT_QT_MXFP4) return false;
+  if ((d != 8192 && d != 7168) || i % 64 != 0) return false;  // gate/up: K = 512 * NCH
+  if (i != 2048 || d % 16 != 0) return false;                 // down: K = 2048
+  const long np = (long)S * k + (has_shared ? S : 0);
+  return np <= XD_MAXP && S <= 16;
+}
+
+hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok, int npairs, const float *x,
+                          long x_stride, int K, int I, __bf16 *hp) {
+  if (npairs <= 0) return hipSuccess;
+  const dim3 grid(I / 64, npairs);
+  if (K == 8192)
+    hipLaunchKernelGGL(k_xgateup<16>, grid, dim3(256), 0, c.stream, jobs, tok, x, x_stride, I, hp);
+  else if (K == 7168)
+    hipLaunchKernelGGL(k_xgateup<14>, grid, dim3(256), 0, c.stream, jobs, tok, x, x_stride, I, hp);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
+                        int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
+                        int has_shared, int gated, float *out) {
+  if (npairs <= 0 || npairs > XD_MAXP || I != 2048 || S > 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_xdown<4>, dim3(H / 16), dim3(256), 0, c.stream, jobs, npairs, hp, I, H, S, k, tok, tok_pair,
+                     tok_w, sh_scale, has_shared, gated, out);
+  return hipGetLastError();
+}
+
+}  // namespace rbt
