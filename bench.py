@@ -280,7 +280,7 @@ def main():
                    "topk": cfg.topk, "shared_expert": cfg.shared, "weights": "mxfp4" if cfg.kind == R.QT_MXFP4
                    else "int4-grouped", "tokens_per_step": 1, "resident_pool_gb": round(pool_gb, 2),
                    "graph_tokens": G},
-        "roofline": {"bound": "hbm", "kernel": "k_decode_gemv stacked gate/up, all 11 experts",
+        "roofline": {"bound": "hbm", "kernel": "k_xgateup (gate/up + SiLU, MFMA on fp4->bf16 weights), all 11 experts",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": gu_bytes,
                      "launch_us": round(gu_us, 2), "traffic": traffic},
