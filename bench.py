@@ -30,6 +30,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer decode µs/token + expert GEMV HBM GB/s (% of 8 TB/s), MXFP4"
 HBM_PEAK_GBPS = 8000.0
+# the gate/up kernel the MXFP4 decode path launches (its FETCH/WRITE counters: profiles/traffic_<cfg>.json)
+ROOFLINE_KERNEL = "rbt::k_xgateup<16>"
 
 
 def log(*a):
@@ -253,7 +255,9 @@ def main():
     tf = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
     if os.path.exists(tf):
         try:
-            traffic = json.load(open(tf)).get("gateup_bytes_per_launch")
+            t = json.load(open(tf))
+            # only a measurement of the kernel this build launches counts
+            traffic = t.get("gateup_bytes_per_launch") if t.get("kernel") == ROOFLINE_KERNEL else None
         except (OSError, ValueError):
             traffic = None
 
