@@ -141,6 +141,80 @@ def cpu_baseline(cfg, seed, x_tokens, budget_s, gpu_out=None):
     return res
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def bench_prefill(args, ctx, cfg, pool_gb):
+    """C4: one MoE-layer call over cfg.tokens tokens (512) per step. value = us per layer call;
+    roofline = the grouped gate/up GEMM (HBM: weights of every unique expert + shared; also its
+    MFMA utilisation); the down GEMM is reported beside it."""
+    import torch
+    import rabbit_amd.workloads as W
+    S, H, I, k = cfg.tokens, cfg.hidden, cfg.inter, cfg.topk
+    steps = max(1, min(args.steps, 64))
+    warm = max(1, min(args.warmup, 8))
+    nb = steps + warm
+    xs = [torch.from_numpy(W.tokens(cfg, S, args.seed + 5 + b)).cuda() for b in range(nb)]
+    out = torch.empty(S * H, dtype=torch.float32, device="cuda")
+    ids = torch.empty(S * k, dtype=torch.int32, device="cuda")
+    uniq = []
+    for b in range(warm):
+        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
+    ctx.sync()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for b in range(warm, nb):
+        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    us_call = wall / steps * 1e6
+    log(f"[bench] prefill: {steps} calls of {S} tokens, {us_call:.1f} us/call")
+    ctx.profile_read(reset=True)
+    ctx.profile_enable(True)
+    for b in range(warm, nb):
+        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
+        ctx.sync()
+        uniq.append(len(np.unique(ids.cpu().numpy())))
+    prof = ctx.profile_read(reset=True)
+    ctx.profile_enable(False)
+    n = max(1, prof["calls"])
+    gu_us = prof["gateup_ms"] / n * 1e3
+    dn_us = prof["down_ms"] / n * 1e3
+    rt_us = prof["router_ms"] / n * 1e3
+    cb_us = prof["combine_ms"] / n * 1e3
+    U = float(np.mean(uniq))
+    nexp = U + 1  # + shared
+    gu_bytes = nexp * 2 * I * (H // 2 + H // 32)
+    dn_bytes = nexp * H * (I // 2 + I // 32)
+    pairs = S * k + S
+    gu_flops = 2.0 * pairs * 2 * I * H
+    dn_flops = 2.0 * pairs * H * I
+    gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
+    res = {
+        "metric": "MoE-layer prefill us/call (512 tokens) + grouped-GEMM HBM GB/s and MFMA utilisation, MXFP4",
+        "value": round(us_call, 1), "unit": "us/call", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(us_call / 1e3, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16-mfma/f32-acc", "data": "synthetic",
+        "config": {"workload": cfg.name, "tokens_per_step": S, "hidden": H, "moe_inter": I,
+                   "n_experts": cfg.n_experts, "topk": k, "shared_expert": cfg.shared, "weights": "mxfp4",
+                   "resident_pool_gb": round(pool_gb, 2), "unique_experts_mean": round(U, 1)},
+        "us_per_token": round(us_call / S, 3),
+        "roofline": {"bound": "hbm", "kernel": "k_pgateup (grouped gate/up GEMM + SiLU)",
+                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": int(gu_bytes),
+                     "launch_us": round(gu_us, 2), "traffic": None,
+                     "mfma_tflops": round(gu_flops / (gu_us * 1e-6) / 1e12, 1),
+                     "mfma_util": round(gu_flops / (gu_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "down": {"bytes": int(dn_bytes), "us": round(dn_us, 2), "gbps": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
+                 "mfma_util": round(dn_flops / (dn_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+        "phase_us": {"router+group": round(rt_us, 2), "gateup": round(gu_us, 2), "down": round(dn_us, 2),
+                     "combine": round(cb_us, 2)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,8 +240,9 @@ def main():
 
     torch.zeros(1, device="cuda")
     cfg = W.CONFIGS[args.config]
-    if cfg.tokens != 1:
-        raise SystemExit(f"bench.py times batch-1 decode; {args.config} is a parity-test configuration")
+    if cfg.tokens != 1 and args.config != "c4":
+        raise SystemExit(f"bench.py times batch-1 decode (c1) or the 512-token prefill (c4); {args.config} is a "
+                         "parity-test configuration")
     ctx = R.Context(0)
     hip = hip_runtime()
 
@@ -184,6 +259,8 @@ def main():
     W.build_layer(ctx, cfg, layer=0, seed=args.seed)
     pool_gb = ctx.pool_resident_bytes() / 1e9
     log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
+    if cfg.tokens != 1:
+        return bench_prefill(args, ctx, cfg, pool_gb)
 
     G = max(1, min(args.graph_tokens, args.steps))
     reps = (args.steps + G - 1) // G

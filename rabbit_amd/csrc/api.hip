@@ -43,6 +43,8 @@ enum ScratchSlot {
   SC_IDS_OUT,
   SC_W_OUT,
   SC_GU,
+  SC_XB,
+  SC_PGRP,
   SC_N
 };
 
@@ -474,6 +476,42 @@ hipEvent_t take_event(rbt_ctx *c) {
   return e;
 }
 
+// Prefill (several tokens, MXFP4): grouping into per-expert segments, x -> bf16, grouped gate/up
+// GEMM with SiLU, grouped down GEMM, ordered combine. ev (profiling) receives events 1..3.
+int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H, int I, const int32_t *ids,
+                const float *wts, const float *shs, int *ptok, int *tpair, float *tw, float *h, float *yy, bool gated,
+                float *out, hipEvent_t *ev) {
+  const rbt_moe_layer_desc &D = L.desc;
+  const int has_shared = D.has_shared ? 1 : 0;
+  const long W = (S + 31) / 32;
+  const long max_tiles = rbt::prefill_max_tiles(S, k, E, has_shared);
+  // one scratch block: bits [E*W], pc [E*W], segs [PG_MAXE], tiles [max_tiles], ntiles
+  const size_t off_pc = align256((size_t)E * W * 4), off_segs = off_pc + align256((size_t)E * W * 4);
+  const size_t off_tiles = off_segs + align256(sizeof(rbt::PSeg) * rbt::PG_MAXE);
+  const size_t off_nt = off_tiles + align256(sizeof(rbt::PTile) * (size_t)max_tiles);
+  void *blk;
+  RBT_TRY(scratch(c, SC_PGRP, off_nt + 256, &blk));
+  char *b = static_cast<char *>(blk);
+  uint32_t *bits = reinterpret_cast<uint32_t *>(b), *pc = reinterpret_cast<uint32_t *>(b + off_pc);
+  rbt::PSeg *segs = reinterpret_cast<rbt::PSeg *>(b + off_segs);
+  rbt::PTile *tiles = reinterpret_cast<rbt::PTile *>(b + off_tiles);
+  int *ntiles = reinterpret_cast<int *>(b + off_nt);
+  __bf16 *xb;
+  RBT_TRY(scratch_t(c, SC_XB, (size_t)S * H, &xb));
+  __bf16 *hb = reinterpret_cast<__bf16 *>(h);  // [S*k + S, I] bf16 fits the fp32 h scratch
+  int *dflags = c->d_flags;
+  HIP_OK(c, rbt::launch_pgroup(*c, ids, wts, S, k, E, has_shared, L.d_table, bits, pc, segs, tiles, ntiles, ptok,
+                               tpair, tw, dflags + FLAG_ERR, dflags + FLAG_UNIQ));
+  HIP_OK(c, rbt::launch_to_bf16(*c, x, (long)S * H, xb));
+  if (ev) HIP_OK(c, hipEventRecord(ev[1], c->stream));
+  HIP_OK(c, rbt::launch_pgateup(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, ptok, xb, S, H, I, hb));
+  if (ev) HIP_OK(c, hipEventRecord(ev[2], c->stream));
+  HIP_OK(c, rbt::launch_pdown(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, hb, I, H, yy));
+  if (ev) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+  HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, has_shared, gated ? 1 : 0, out));
+  return RBT_OK;
+}
+
 int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
                     float *w_out) {
   auto lit = c->layers.find(layer);
@@ -529,19 +567,27 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
   HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
                                       grp_in_select ? &ga : nullptr));
-  if (!grp_in_select)
-    HIP_OK(c, rbt::launch_group(*c, ids, wts, S, k, E, L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
-                                dflags + FLAG_UNIQ));
 
   const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
                      L.shared_inter == (size_t)I;
-  RbtExpertDev none{};
-  hipEvent_t *mark = c->prof ? &ev[2] : nullptr;
-  if (c->prof) HIP_OK(c, hipEventRecord(ev[1], c->stream));
   // MXFP4 decode shapes run on the matrix cores: gate/up with SiLU, then down with the ordered
   // combine fused in (out written directly).
   const bool mfma = (merge || !D.has_shared) && rbt::xgemm_ok(L.routed_kind, H, I, S, k, D.has_shared) &&
                     ((uintptr_t)x % 16 == 0);
+  // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores.
+  const bool grouped = !mfma && S > 1 && (merge || !D.has_shared) &&
+                       rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
+  if (grouped) {
+    RBT_TRY(prefill_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, out,
+                        c->prof ? ev.data() : nullptr));
+  } else {
+  if (!grp_in_select)
+    HIP_OK(c, rbt::launch_group(*c, ids, wts, S, k, E, L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
+                                dflags + FLAG_UNIQ));
+
+  RbtExpertDev none{};
+  hipEvent_t *mark = c->prof ? &ev[2] : nullptr;
+  if (c->prof) HIP_OK(c, hipEventRecord(ev[1], c->stream));
   if (mfma) {
     // h as three bf16 parts per pair (3 * I bf16 = 1.5 * I floats of the h scratch)
     __bf16 *hp = reinterpret_cast<__bf16 *>(h);
@@ -562,6 +608,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     }
     if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
     HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
+  }
   }
   if (c->prof) {
     HIP_OK(c, hipEventRecord(ev[4], c->stream));

@@ -1,0 +1,486 @@
+// prefill.hip -- MoE-layer prefill (many tokens per call) on the matrix cores, MXFP4 experts.
+//
+// The reference runs a prefill layer as apply_single_expert per unique expert (glm52/moe.rs:453-513,
+// called in unique_experts order by qwen38/generate.rs:327-342): gather the expert's tokens, three
+// matmul_mxfp4 calls with s = the expert's token count (kernels.rs:233), SiLU * up, and
+// out[t] += w * y. Here the same products run as grouped GEMMs over every expert of the call:
+//
+//   k_pgroup   token -> expert grouping: one segment per unique expert in first-occurrence order
+//              (unique_experts, glm52/moe.rs:333-344), its tokens in token order (the reference's
+//              gather order, glm52/moe.rs:465-470), the shared expert as the last segment (all S
+//              tokens); a tile table cuts segments into chunks of PF_TCH tokens.
+//   k_to_bf16  x (fp32) -> bf16, the MFMA operand.
+//   k_pgateup  per (tile, 64-row block): h = silu(gate . x) * (up . x) as bf16.
+//   k_pdown    per (tile, 64-row block): y = down . h, fp32, one row per (expert, token) pair.
+//   k_combine  (router.hip) out[t] = sum over t's picks in unique_experts order of w * y, then
+//              + the shared expert's y (gated for Qwen), each product and sum rounded separately.
+//
+// GEMM tiling (v_mfma_f32_16x16x32_bf16, D[16x16] += A[16x32] . B[32x16]): A rows are 16 weight
+// rows, B columns are 16 tokens. Lane l (r = l % 16, g = l / 16) loads 16 bytes = 32 E2M1 codes
+// of weight row r at columns 128 s + 32 g .. +31 of step s: exactly one 32-element MXFP4 block, so
+// one E8M0 byte scales them all. v_cvt_scalef32_pk_bf16_fp4 turns the codes into bf16 with the
+// block scale applied (e2m1 * 2^(b-127) has two significant bits, so the bf16 value is the
+// reference's dequantized weight, quant.rs:325-339, whenever it is a normal number). The four
+// MFMAs of a step use the codes' four dwords; MFMA m covers columns 128 s + 32 g + 8 m .. +7 in
+// lane group g, so the B lane (token r, group g) supplies the same 8 columns of its token's row.
+// Lane l receives D[4 g + i][r]: rows 4g..4g+3 of the wave's 16 for token r.
+//
+// Weights stream from HBM once per tile (non-temporal loads); the activations (x or h, bf16) are
+// small and stay in the caches across the row blocks of a tile.
+#include "rbt_device.h"
+#include "rbt_internal.h"
+
+namespace rbt {
+
+typedef __bf16 pb8 __attribute__((ext_vector_type(8)));
+typedef __bf16 pb4 __attribute__((ext_vector_type(4)));
+typedef __bf16 pb2 __attribute__((ext_vector_type(2)));
+typedef float pf4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------------------------------------
+// grouping
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ unsigned long long pg_lanemask_lt() {
+  const int lane = threadIdx.x & 63;
+  return (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+}
+
+// Exclusive prefix sum over the 1024 threads of the block; *total gets the sum. `ws` holds 17 ints.
+__device__ int pg_block_scan(int v, int *ws, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) ws[wave] = incl;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int i = 0; i < 16; i++) {
+      const int c = ws[i];
+      ws[i] = run;
+      run += c;
+    }
+    ws[16] = run;
+  }
+  __syncthreads();
+  const int r = ws[wave] + incl - v;
+  *total = ws[16];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ uint32_t pg_load(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One workgroup of 1024 threads. ids / wts are [S, k] (id -1 = no pick). bits / pc are scratch of
+// E * ceil(S/32) words each. Outputs:
+//   segs[u]     u < U: unique expert u (first-occurrence order), its pair offset and token count;
+//               u = U (has_shared): the shared expert, pairs [S*k, S*k + S), all tokens.
+//   tiles[i]    (segment, first token of the chunk), *ntiles = count.
+//   pair_tok[p] token of pair p; routed pairs are [0, n_routed) in segment order, tokens
+//               ascending within a segment; the shared pair of token t is S*k + t.
+//   tok_pair / tok_w [t*k + j]: token t's pairs and routing weights sorted by pair index, i.e. in
+//               unique_experts order (-1 / 0 for missing picks, placed last).
+__global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids, const float *__restrict__ wts, int S,
+                                                 int k, int E, int has_shared, const RbtExpertDev *__restrict__ table,
+                                                 uint32_t *__restrict__ bits, uint32_t *__restrict__ pc,
+                                                 PSeg *__restrict__ segs, PTile *__restrict__ tiles,
+                                                 int *__restrict__ ntiles, int *__restrict__ pair_tok,
+                                                 int *__restrict__ tok_pair, float *__restrict__ tok_w,
+                                                 int *__restrict__ err, int *__restrict__ nuniq) {
+  __shared__ int first[PG_MAXE], cnt[PG_MAXE], rank[PG_MAXE], byrank[PG_MAXE], segoff[PG_MAXE + 1];
+  __shared__ int ws[17];
+  __shared__ int carry_s;
+  const int tid = threadIdx.x;
+  const int W = (S + 31) >> 5;
+  const int P = S * k;
+  for (int e = tid; e < E; e += 1024) {
+    first[e] = 0x7fffffff;
+    cnt[e] = 0;
+  }
+  for (long i = tid; i < (long)E * W; i += 1024) bits[i] = 0u;
+  __threadfence();
+  __syncthreads();
+  // counts, first occurrences, token bitmaps
+  for (int p = tid; p < P; p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) {
+      const int t = p / k;
+      atomicAdd(&cnt[e], 1);
+      atomicMin(&first[e], p);
+      atomicOr(&bits[(long)e * W + (t >> 5)], 1u << (t & 31));
+      const RbtExpertDev J = table[e];
+      if (J.gd == nullptr || J.ud == nullptr || J.dd == nullptr) atomicOr(err, 1);
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  // rank of each used expert: the number of first occurrences before its own
+  if (tid == 0) carry_s = 0;
+  __syncthreads();
+  for (int base = 0; base < P; base += 1024) {
+    const int p = base + tid;
+    int e = -1;
+    bool fl = false;
+    if (p < P) {
+      e = ids[p];
+      fl = e >= 0 && e < E && first[e] == p;
+    }
+    int tot;
+    const int ex = pg_block_scan(fl ? 1 : 0, ws, &tot);
+    const int c0 = carry_s;
+    if (fl) {
+      rank[e] = c0 + ex;
+      byrank[c0 + ex] = e;
+    }
+    __syncthreads();
+    if (tid == 0) carry_s = c0 + tot;
+    __syncthreads();
+  }
+  const int U = carry_s;
+  // segment offsets in rank order (two ranks per thread)
+  {
+    const int u0 = 2 * tid, u1 = 2 * tid + 1;
+    const int c0 = u0 < U ? cnt[byrank[u0]] : 0, c1 = u1 < U ? cnt[byrank[u1]] : 0;
+    int tot;
+    const int ex = pg_block_scan(c0 + c1, ws, &tot);
+    if (u0 < U) segoff[u0] = ex;
+    if (u1 < U) segoff[u1] = ex + c0;
+    if (tid == 0) segoff[U] = tot;
+  }
+  __syncthreads();
+  // segments and tiles
+  {
+    const int nseg = U + (has_shared ? 1 : 0);
+    const int u0 = 2 * tid, u1 = 2 * tid + 1;
+    auto seg_cnt = [&](int u) { return u < U ? cnt[byrank[u]] : S; };
+    const int n0 = u0 < nseg ? (seg_cnt(u0) + PF_TCH - 1) / PF_TCH : 0;
+    const int n1 = u1 < nseg ? (seg_cnt(u1) + PF_TCH - 1) / PF_TCH : 0;
+    int tot;
+    const int ex = pg_block_scan(n0 + n1, ws, &tot);
+    if (u0 < nseg) {
+      segs[u0] = PSeg{u0 < U ? byrank[u0] : -1, u0 < U ? segoff[u0] : P, seg_cnt(u0), 0};
+      for (int c = 0; c < n0; c++) tiles[ex + c] = PTile{u0, c * PF_TCH};
+    }
+    if (u1 < nseg) {
+      segs[u1] = PSeg{u1 < U ? byrank[u1] : -1, u1 < U ? segoff[u1] : P, seg_cnt(u1), 0};
+      for (int c = 0; c < n1; c++) tiles[ex + n0 + c] = PTile{u1, c * PF_TCH};
+    }
+    if (tid == 0) {
+      *ntiles = tot;
+      if (nuniq) *nuniq = U;
+    }
+  }
+  // per-expert prefix counts of the token bitmap words
+  for (int e = tid; e < E; e += 1024) {
+    if (cnt[e] == 0) continue;
+    uint32_t run = 0;
+    for (int w = 0; w < W; w++) {
+      pc[(long)e * W + w] = run;
+      run += __popc(pg_load(&bits[(long)e * W + w]));
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  // Pairs, one thread per token. The slot of (t, e) within e's segment is the number of earlier
+  // tokens that picked e. Token t's picks are written in pair order, which is unique_experts order
+  // (segments are in rank order): pick j goes to position #{j' : key(j') < key(j)}, with
+  // key = rank of the expert, and missing picks after every real one in slot order.
+  for (int t = tid; t < S; t += 1024) {
+    const int32_t *ti = ids + (long)t * k;
+    for (int j = 0; j < k; j++) {
+      const int e = ti[j];
+      const bool v = e >= 0 && e < E;
+      const int kj = v ? rank[e] : E + j;
+      int pos = 0;
+      for (int j2 = 0; j2 < k; j2++) {
+        const int e2 = ti[j2];
+        pos += ((e2 >= 0 && e2 < E) ? rank[e2] : E + j2) < kj;
+      }
+      int pr = -1;
+      if (v) {
+        const long wi = (long)e * W + (t >> 5);
+        const int slot = (int)(pg_load(&pc[wi]) + __popc(pg_load(&bits[wi]) & ((1u << (t & 31)) - 1u)));
+        pr = segoff[rank[e]] + slot;
+        pair_tok[pr] = t;
+      }
+      tok_pair[(long)t * k + pos] = pr;
+      tok_w[(long)t * k + pos] = v ? wts[(long)t * k + j] : 0.0f;
+    }
+    if (has_shared) pair_tok[P + t] = t;
+  }
+}
+
+// x (fp32) -> bf16, round to nearest even. vec: x and xb allow 16- and 8-byte accesses.
+__global__ __launch_bounds__(256) void k_to_bf16(const float *__restrict__ x, long n, __bf16 *__restrict__ xb,
+                                                 int vec) {
+  const long i = 4 * ((long)blockIdx.x * 256 + threadIdx.x);
+  if (vec && i + 3 < n) {
+    const float4 v = *reinterpret_cast<const float4 *>(x + i);
+    *reinterpret_cast<pb4 *>(xb + i) = pb4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  } else {
+    for (long j = i; j < min(n, i + 4); j++) xb[j] = (__bf16)x[j];
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// grouped GEMMs
+// ------------------------------------------------------------------------------------------------
+// 8 E2M1 codes (one dword) -> 8 bf16 scaled by the block's E8M0 value.
+__device__ __forceinline__ pb8 pf_fp4x8(uint32_t w, float sc) {
+  const pb2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+  const pb2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+  const pb2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+  const pb2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
+  return pb8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// E8M0 byte -> f32 scale (e8m0_decode, quant.rs:391-396): byte 0 is 2^-127, 255 the +inf bits.
+__device__ __forceinline__ float pf_e8m0(uint32_t b) { return __uint_as_float(b == 0 ? (1u << 22) : (b << 23)); }
+
+// Tile decode shared by both GEMMs.
+struct PfTile {
+  RbtExpertDev J;
+  int pbase;  // first pair of the tile
+  int M;      // tokens in the tile (1..PF_TCH)
+  bool ok;
+};
+
+__device__ __forceinline__ PfTile pf_tile(int ti, const PTile *__restrict__ tiles, const PSeg *__restrict__ segs,
+                                          const RbtExpertDev *__restrict__ table,
+                                          const RbtExpertDev *__restrict__ shared_dev) {
+  PfTile r;
+  const PTile T = tiles[ti];
+  const PSeg G = segs[T.seg];
+  r.J = G.eid >= 0 ? table[G.eid] : *shared_dev;
+  r.pbase = G.off + T.c0;
+  r.M = min(PF_TCH, G.cnt - T.c0);
+  // a missing expert is reported by k_pgroup (error flag); its tiles compute nothing
+  r.ok = r.M > 0 && r.J.gd != nullptr && r.J.ud != nullptr && r.J.dd != nullptr;
+  return r;
+}
+
+// One K step (128 columns) of a wave's 16-row tile against NT column blocks of 16 tokens:
+// acc[q] += A(codes, scale) . B[q].
+template <int NT>
+__device__ __forceinline__ void pf_step(const rbt_u4 &a, float sc, const pb8 (&b)[NT][4], pf4 (&acc)[NT], int nt) {
+  const pb8 a0 = pf_fp4x8(a.x, sc), a1 = pf_fp4x8(a.y, sc), a2 = pf_fp4x8(a.z, sc), a3 = pf_fp4x8(a.w, sc);
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    if (q < nt) {
+      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[q][0], acc[q], 0, 0, 0);
+      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[q][1], acc[q], 0, 0, 0);
+      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[q][2], acc[q], 0, 0, 0);
+      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[q][3], acc[q], 0, 0, 0);
+    }
+  }
+}
+
+template <int NT>
+__device__ __forceinline__ void pf_load_b(pb8 (&b)[NT][4], const __bf16 *const (&bp)[NT], int s, int nt) {
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    if (q < nt) {
+      const rbt_gu4 *p = (const rbt_gu4 *)(bp[q] + 128 * s);
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const rbt_u4 v = p[m];
+        b[q][m] = __builtin_bit_cast(pb8, v);
+      }
+    }
+  }
+}
+
+// Gate/up: grid = ntiles_max * (I / 64) workgroups of 256 threads, row block fastest. Wave w of a
+// workgroup owns rows 64 * rb + 16 w .. +15 of gate and of up for the tile's tokens, over all
+// H columns. Output hb[pair, I] = bf16(silu(g) * u).
+__global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                                 const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
+                                                 const RbtExpertDev *__restrict__ shared_dev,
+                                                 const int *__restrict__ pair_tok, const __bf16 *__restrict__ xb,
+                                                 int S, int H, int I, __bf16 *__restrict__ hb) {
+  constexpr int NT = PF_NT;
+  const int nrb = I >> 6;
+  const int ti = blockIdx.x / nrb, rb = blockIdx.x - ti * nrb;
+  if (ti >= *ntiles) return;
+  const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
+  if (!T.ok) return;
+  const int nt = (T.M + 15) >> 4;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const long row = 64L * rb + 16 * w + r;
+  const long rowb = (long)(H >> 1), rows = (long)(H >> 5);
+  const uint8_t *ga = T.J.gd + row * rowb + 16 * g;
+  const uint8_t *ua = T.J.ud + row * rowb + 16 * g;
+  const uint8_t *gs = (const uint8_t *)T.J.gs + row * rows;
+  const uint8_t *us = (const uint8_t *)T.J.us + row * rows;
+  const __bf16 *bp[NT];
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    const int j = min(16 * q + r, T.M - 1);
+    const int tok = min(max(pair_tok[T.pbase + j], 0), S - 1);
+    bp[q] = xb + (long)tok * H + 32 * g;
+  }
+  pf4 ag[NT], au[NT];
+#pragma unroll
+  for (int q = 0; q < NT; q++) ag[q] = au[q] = pf4{0.f, 0.f, 0.f, 0.f};
+  const int nsteps = H >> 7;
+  rbt_u4 cg = __builtin_nontemporal_load((const rbt_gu4 *)(ga));
+  rbt_u4 cu = __builtin_nontemporal_load((const rbt_gu4 *)(ua));
+  rbt_u4 sg = *(const rbt_gu4 *)(gs);
+  rbt_u4 su = *(const rbt_gu4 *)(us);
+  pb8 b[NT][4];
+  pf_load_b<NT>(b, bp, 0, nt);
+  for (int s = 0; s < nsteps; s++) {
+    // scale bytes of this step: dword (s & 3) of the 16-byte group, byte g
+    const uint32_t swg = (s & 3) == 0 ? sg.x : (s & 3) == 1 ? sg.y : (s & 3) == 2 ? sg.z : sg.w;
+    const uint32_t swu = (s & 3) == 0 ? su.x : (s & 3) == 1 ? su.y : (s & 3) == 2 ? su.z : su.w;
+    const float scg = pf_e8m0((swg >> (8 * g)) & 0xffu), scu = pf_e8m0((swu >> (8 * g)) & 0xffu);
+    const rbt_u4 xg = cg, xu = cu;
+    pb8 bc[NT][4];
+#pragma unroll
+    for (int q = 0; q < NT; q++)
+#pragma unroll
+      for (int m = 0; m < 4; m++) bc[q][m] = b[q][m];
+    if (s + 1 < nsteps) {
+      cg = __builtin_nontemporal_load((const rbt_gu4 *)(ga + 64 * (s + 1)));
+      cu = __builtin_nontemporal_load((const rbt_gu4 *)(ua + 64 * (s + 1)));
+      if (((s + 1) & 3) == 0) {
+        sg = *(const rbt_gu4 *)(gs + 4 * (s + 1));
+        su = *(const rbt_gu4 *)(us + 4 * (s + 1));
+      }
+      pf_load_b<NT>(b, bp, s + 1, nt);
+    }
+    pf_step<NT>(xg, scg, bc, ag, nt);
+    pf_step<NT>(xu, scu, bc, au, nt);
+  }
+  const int orow = 64 * rb + 16 * w + 4 * g;
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    const int j = 16 * q + r;
+    if (q < nt && j < T.M) {
+      pb4 hv;
+#pragma unroll
+      for (int i = 0; i < 4; i++) hv[i] = (__bf16)(rbt_silu(ag[q][i]) * au[q][i]);
+      *reinterpret_cast<pb4 *>(hb + (long)(T.pbase + j) * I + orow) = hv;
+    }
+  }
+}
+
+// Down: grid = ntiles_max * (H / 64), 256 threads. Wave w owns down rows 64 * rb + 16 w .. +15
+// over all I columns for the tile's tokens; y[pair, H] fp32.
+__global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                               const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
+                                               const RbtExpertDev *__restrict__ shared_dev,
+                                               const __bf16 *__restrict__ hb, int I, int H, float *__restrict__ y) {
+  constexpr int NT = PF_NT;
+  const int nrb = H >> 6;
+  const int ti = blockIdx.x / nrb, rb = blockIdx.x - ti * nrb;
+  if (ti >= *ntiles) return;
+  const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
+  if (!T.ok) return;
+  const int nt = (T.M + 15) >> 4;
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const long row = 64L * rb + 16 * w + r;
+  const uint8_t *da = T.J.dd + row * (long)(I >> 1) + 16 * g;
+  const uint8_t *ds = (const uint8_t *)T.J.ds + row * (long)(I >> 5);
+  const __bf16 *bp[NT];
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    const int j = min(16 * q + r, T.M - 1);
+    bp[q] = hb + (long)(T.pbase + j) * I + 32 * g;
+  }
+  pf4 acc[NT];
+#pragma unroll
+  for (int q = 0; q < NT; q++) acc[q] = pf4{0.f, 0.f, 0.f, 0.f};
+  const int nsteps = I >> 7;
+  rbt_u4 cd = __builtin_nontemporal_load((const rbt_gu4 *)(da));
+  rbt_u4 sd = *(const rbt_gu4 *)(ds);
+  pb8 b[NT][4];
+  pf_load_b<NT>(b, bp, 0, nt);
+  for (int s = 0; s < nsteps; s++) {
+    const uint32_t sw = (s & 3) == 0 ? sd.x : (s & 3) == 1 ? sd.y : (s & 3) == 2 ? sd.z : sd.w;
+    const float sc = pf_e8m0((sw >> (8 * g)) & 0xffu);
+    const rbt_u4 xd = cd;
+    pb8 bc[NT][4];
+#pragma unroll
+    for (int q = 0; q < NT; q++)
+#pragma unroll
+      for (int m = 0; m < 4; m++) bc[q][m] = b[q][m];
+    if (s + 1 < nsteps) {
+      cd = __builtin_nontemporal_load((const rbt_gu4 *)(da + 64 * (s + 1)));
+      if (((s + 1) & 3) == 0) sd = *(const rbt_gu4 *)(ds + 4 * (s + 1));
+      pf_load_b<NT>(b, bp, s + 1, nt);
+    }
+    pf_step<NT>(xd, sc, bc, acc, nt);
+  }
+  const int orow = 64 * rb + 16 * w + 4 * g;
+#pragma unroll
+  for (int q = 0; q < NT; q++) {
+    const int j = 16 * q + r;
+    if (q < nt && j < T.M)
+      *reinterpret_cast<float4 *>(y + (long)(T.pbase + j) * H + orow) =
+          float4{acc[q][0], acc[q][1], acc[q][2], acc[q][3]};
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// launchers
+// ------------------------------------------------------------------------------------------------
+bool prefill_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k) {
+  if (kind != RBT_QT_MXFP4) return false;
+  // K steps of 128 columns with scale groups of 4 steps; 64-row blocks
+  if (d % 512 != 0 || i % 512 != 0 || d > (1u << 20) || i > (1u << 20)) return false;
+  // segments: every expert plus the shared one within PG_MAXE
+  return n_experts + 1 <= (size_t)PG_MAXE && k <= 64;
+}
+
+long prefill_max_tiles(int S, int k, int E, int has_shared) {
+  const long P = (long)S * k;
+  const long nseg = std::min<long>(E, P) + (has_shared ? 1 : 0);
+  return nseg + (P + (has_shared ? S : 0) + PF_TCH - 1) / PF_TCH;
+}
+
+hipError_t launch_pgroup(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E, int has_shared,
+                         const RbtExpertDev *table, uint32_t *bits, uint32_t *pc, PSeg *segs, PTile *tiles,
+                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
+  if (E > PG_MAXE) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pgroup, dim3(1), dim3(1024), 0, c.stream, ids, wts, S, k, E, has_shared, table, bits, pc, segs,
+                     tiles, ntiles, pair_tok, tok_pair, tok_w, err, nuniq);
+  return hipGetLastError();
+}
+
+hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb) {
+  if (n <= 0) return hipSuccess;
+  const long threads = (n + 3) / 4;
+  const int vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)xb % 8 == 0);
+  hipLaunchKernelGGL(k_to_bf16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, c.stream, x, n, xb, vec);
+  return hipGetLastError();
+}
+
+hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
+                          const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
+                          const __bf16 *xb, int S, int H, int I, __bf16 *hb) {
+  const long blocks = max_tiles * (I >> 6);
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffffL || H % 512 || I % 512) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pgateup, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table,
+                     shared_dev, pair_tok, xb, S, H, I, hb);
+  return hipGetLastError();
+}
+
+hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb, int I, int H,
+                        float *y) {
+  const long blocks = max_tiles * (H >> 6);
+  if (blocks <= 0) return hipSuccess;
+  if (blocks > 0x7fffffffL || H % 512 || I % 512) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pdown, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table, shared_dev,
+                     hb, I, H, y);
+  return hipGetLastError();
+}
+
+}  // namespace rbt

@@ -59,6 +59,33 @@ hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, cons
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);
 
+// prefill.hip: MXFP4 prefill as grouped GEMMs on the matrix cores.
+constexpr int PG_MAXE = 2048;  // segments (unique experts + shared) per call
+constexpr int PF_TCH = 64;     // tokens per GEMM tile
+constexpr int PF_NT = PF_TCH / 16;
+struct PSeg {
+  int eid;  // expert id, -1 for the shared expert
+  int off;  // first pair of the segment
+  int cnt;  // tokens (pairs) in the segment
+  int pad;
+};
+struct PTile {
+  int seg;  // segment index
+  int c0;   // first token of the tile within the segment
+};
+bool prefill_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k);
+long prefill_max_tiles(int S, int k, int E, int has_shared);
+hipError_t launch_pgroup(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E, int has_shared,
+                         const RbtExpertDev *table, uint32_t *bits, uint32_t *pc, PSeg *segs, PTile *tiles,
+                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq);
+hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb);
+hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
+                          const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
+                          const __bf16 *xb, int S, int H, int I, __bf16 *hb);
+hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb, int I, int H,
+                        float *y);
+
 // router.hip
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd);

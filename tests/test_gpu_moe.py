@@ -124,3 +124,61 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
         got.append(ids.cpu().numpy().copy())
     eids, _ = host.route(x)
     assert np.array_equal(np.stack(got), eids)
+
+
+# ---- prefill: grouped GEMMs on the matrix cores (bf16 operands, fp32 accumulation) -------------
+PREFILL_RTOL = 1e-2  # bf16-MFMA prefill outputs (x and h rounded to bf16)
+
+
+@pytest.mark.parametrize("family,gated,lb,S,E,k", [
+    (0, True, False, 2, 16, 4),      # smallest batch that takes the grouped path
+    (0, True, False, 130, 64, 6),    # ragged tiles, segments over 64 tokens (shared: 3 tiles)
+    (1, False, False, 97, 32, 8),    # GLM sigmoid routing, ungated shared expert
+    (2, False, True, 200, 48, 8),    # K3 routing with Zipf-skewed logits: hot experts span tiles
+])
+def test_moe_prefill_grouped(ctx, orc, family, gated, lb, S, E, k):
+    import rabbit_amd as R
+    H, I = 1024, 512
+    L = _small_layer(ctx, orc, family, R.QT_MXFP4, H, I, E, k, seed=77 + S, gated=gated, logit_bias=lb)
+    x = normal((S, H), 500 + S)
+    exp, eids, ew = L.forward(x, S, simd=True)
+    out = np.empty(S * H, np.float32)
+    ids = np.empty(S * k, np.int32)
+    w = np.empty(S * k, np.float32)
+    ctx.moe_forward(0, x, S, out, ids, w)
+    assert np.array_equal(ids.reshape(S, k), eids)
+    # weights come from the fp64-summed logits (the selection is certified separately)
+    assert rel_l2(w, ew) < RTOL
+    err = rel_l2(out, exp)
+    print(f"prefill S={S} family={family} rel_l2={err:.3e}")
+    assert err < PREFILL_RTOL
+    # each token's row on its own: no token's output may depend on the rest of the batch
+    for t in (0, S // 2, S - 1):
+        assert rel_l2(out.reshape(S, H)[t], exp[t]) < PREFILL_RTOL
+
+
+def test_moe_prefill_c4_full(ctx, orc):
+    """C4: 512-token prefill of the Qwen3.8-shaped layer, all 512 experts resident. Ids of every
+    token bit-exact against the oracle's sequential-fp32 router; outputs of a token sample (each
+    token's row depends only on its own picks) within the bf16 prefill tolerance."""
+    import rabbit_amd.workloads as W
+    from oracle.workload import HostLayer
+    import torch
+    cfg = W.CONFIGS["c4"]
+    S = cfg.tokens
+    W.build_layer(ctx, cfg, layer=0, seed=1000)
+    host = HostLayer(cfg, 1000)
+    x = W.tokens(cfg, S, 2024)
+    k = cfg.topk
+    out = torch.empty(S * cfg.hidden, dtype=torch.float32, device="cuda")
+    ids = torch.empty(S * k, dtype=torch.int32, device="cuda")
+    ctx.moe_forward(0, torch.from_numpy(x).cuda(), S, out, ids)
+    got_ids = ids.cpu().numpy().reshape(S, k)
+    eids, _ = host.route(x)
+    assert np.array_equal(got_ids, eids)
+    sample = np.array([0, 1, 137, 300, 511])
+    exp, _, _ = host.forward(x[sample], simd=True)
+    got = out.cpu().numpy().reshape(S, cfg.hidden)[sample]
+    err = rel_l2(got, exp)
+    print(f"c4 sample rel_l2={err:.3e}")
+    assert err < PREFILL_RTOL
