@@ -264,166 +264,284 @@ __device__ __forceinline__ PfTile pf_tile(int ti, const PTile *__restrict__ tile
   return r;
 }
 
-// One K step (128 columns) of a wave's 16-row tile against NT column blocks of 16 tokens:
-// acc[q] += A(codes, scale) . B[q].
-template <int NT>
-__device__ __forceinline__ void pf_step(const rbt_u4 &a, float sc, const pb8 (&b)[NT][4], pf4 (&acc)[NT], int nt) {
-  const pb8 a0 = pf_fp4x8(a.x, sc), a1 = pf_fp4x8(a.y, sc), a2 = pf_fp4x8(a.z, sc), a3 = pf_fp4x8(a.w, sc);
-#pragma unroll
-  for (int q = 0; q < NT; q++) {
-    if (q < nt) {
-      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b[q][0], acc[q], 0, 0, 0);
-      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b[q][1], acc[q], 0, 0, 0);
-      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, b[q][2], acc[q], 0, 0, 0);
-      acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, b[q][3], acc[q], 0, 0, 0);
-    }
-  }
+// A operand of one K step: the lane's 32 codes (16 bytes) and the scale dword holding its block's
+// E8M0 byte (byte g of the dword at 4 * step).
+struct PfA {
+  rbt_u4 w;
+  uint32_t s;
+};
+
+__device__ __forceinline__ void pf_load_a(PfA &a, const uint8_t *row, const uint8_t *srow, int s) {
+  a.w = __builtin_nontemporal_load((const rbt_gu4 *)(row + 64 * s));
+  a.s = *(const rbt_gu32 *)(srow + 4 * s);
 }
 
-template <int NT>
-__device__ __forceinline__ void pf_load_b(pb8 (&b)[NT][4], const __bf16 *const (&bp)[NT], int s, int nt) {
+__device__ __forceinline__ void pf_decode(const PfA &a, int g, pb8 (&A)[4]) {
+  const float sc = pf_e8m0((a.s >> (8 * g)) & 0xffu);
+  A[0] = pf_fp4x8(a.w.x, sc);
+  A[1] = pf_fp4x8(a.w.y, sc);
+  A[2] = pf_fp4x8(a.w.z, sc);
+  A[3] = pf_fp4x8(a.w.w, sc);
+}
+
+constexpr int PF_RBG = 8;         // workgroups per tile: each takes 1/8 of the rows (contiguous)
+constexpr int PB_STRIDE = 128 + 8;  // bf16 per LDS token row of a step (272 B: rows 4 banks apart)
+
+// The tile's activations for one K step (nt * 16 tokens x 128 columns, bf16) go through LDS: the
+// workgroup loads them with one coalesced 16-byte load per thread per 16 tokens (a token's 256
+// bytes are 16 consecutive lanes) and every wave reads its MFMA B operands from LDS. Thread t
+// stages token 16 q + t / 16, bytes 16 (t % 16) .. +15 of the step.
+//
+// Load order and the in-order memory counter: a wave waits for a global load by waiting until at
+// most N younger loads are outstanding, so every load it depends on must be as old as the weight
+// loads of the same step. Iteration `it` therefore issues the weight loads for it + D and the
+// activation loads for it + 1 + D together (register rings of depth D), and stores the activations
+// of it + 1 (issued D iterations earlier) to the LDS buffer the next iteration reads.
+template <int NTV>
+struct PfStage {
+  rbt_u4 v[NTV];
+};
+
+template <int NTV>
+__device__ __forceinline__ void pf_stage_load(PfStage<NTV> &st, const __bf16 *const (&src)[NTV], int s) {
 #pragma unroll
-  for (int q = 0; q < NT; q++) {
-    if (q < nt) {
-      const rbt_gu4 *p = (const rbt_gu4 *)(bp[q] + 128 * s);
+  for (int q = 0; q < NTV; q++) st.v[q] = *(const rbt_gu4 *)(src[q] + 128 * s);
+}
+
+template <int NTV>
+__device__ __forceinline__ void pf_stage_store(const PfStage<NTV> &st, __bf16 (*buf)[PB_STRIDE]) {
+  const int j = threadIdx.x >> 4, c = (threadIdx.x & 15) * 8;
 #pragma unroll
-      for (int m = 0; m < 4; m++) {
-        const rbt_u4 v = p[m];
-        b[q][m] = __builtin_bit_cast(pb8, v);
+  for (int q = 0; q < NTV; q++) *reinterpret_cast<rbt_u4 *>(&buf[16 * q + j][c]) = st.v[q];
+}
+
+// B operand of MFMA m for column block q: token 16 q + r, columns 32 g + 8 m .. +7 of the step.
+__device__ __forceinline__ pb8 pf_b(const __bf16 (*buf)[PB_STRIDE], int q, int m, int r, int g) {
+  return *reinterpret_cast<const pb8 *>(&buf[16 * q + r][32 * g + 8 * m]);
+}
+
+// One tile x row-block group. Wave w owns TILES 16-row tiles (16 TILES contiguous rows) of each
+// of NM matrices per row block (gate/up: NM = 2, down: NM = 1); a row block is 64 TILES rows, and
+// the workgroup walks `per` of them: blocks rb0, rb0 + PF_RBG, rb0 + 2 PF_RBG, ...
+//
+// The weights stream in groups of 4 K steps (512 columns): at the start of a group the wave issues
+// every load of the next group at once, the 16-byte codes of each step and, per 16-row tile, one
+// 16-byte load of its 4 steps' E8M0 bytes (byte 4 s + g of a row is the block of lane group g).
+// One scale load per 4 steps keeps the request count near one per 1 KB of codes, and the group in
+// flight (NM * TILES * 4 KB per wave) covers the memory latency while the current group computes.
+// NM = 2 writes hb = bf16(silu(g) * u), NM = 1 writes y (fp32).
+template <int NM, int NTV, int TILES>
+__device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&src)[NTV], const uint8_t *const (&a)[NM],
+                                        const uint8_t *const (&sc)[NM], long rowb, long rows, int rb0, int per,
+                                        int nsteps, int out_cols, __bf16 *__restrict__ hb, float *__restrict__ y,
+                                        __bf16 (*bs)[PF_TCH][PB_STRIDE]) {
+  constexpr int G = 4;  // K steps per group
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  constexpr int BR = 64 * TILES;                                                 // rows per row block
+  const long blk_a = (long)PF_RBG * BR * rowb, blk_s = (long)PF_RBG * BR * rows;  // between own blocks
+  const int total = per * nsteps;
+  if (total <= 0) return;  // no row block for this workgroup (uniform)
+  const uint8_t *pa[NM][TILES], *ps[NM][TILES];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int t = 0; t < TILES; t++) {
+      const long row = (long)rb0 * BR + 16 * TILES * w + 16 * t + r;
+      pa[m][t] = a[m] + row * rowb + 16 * g;
+      ps[m][t] = sc[m] + row * rows;
+    }
+  // next group to fetch (past the end: the last group again, never used)
+  int f_rb = 0, f_s = 0;
+  rbt_u4 nw[G][NM][TILES], ns[NM][TILES];
+  auto fetch_group = [&]() {
+    const int rb = min(f_rb, per - 1);
+    const int st = f_rb < per ? f_s : nsteps - G;
+    const long oa = (long)rb * blk_a + 64 * st, os = (long)rb * blk_s + 4 * st;
+#pragma unroll
+    for (int d = 0; d < G; d++)
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int t = 0; t < TILES; t++)
+          nw[d][m][t] = __builtin_nontemporal_load((const rbt_gu4 *)(pa[m][t] + oa + 64 * d));
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int t = 0; t < TILES; t++) ns[m][t] = *(const rbt_gu4 *)(ps[m][t] + os);
+    f_s += G;
+    if (f_s == nsteps) {
+      f_s = 0;
+      ++f_rb;
+    }
+  };
+  // activation stage ring: slot (it + 1) % G holds the activations of iteration it + 1, loaded in
+  // the same group batch as the weights it is used with
+  PfStage<NTV> st[G];
+  int a_s = 1 % nsteps;
+  int a_n = 1;
+  auto stage_next = [&](PfStage<NTV> &dst) {
+    pf_stage_load<NTV>(dst, src, a_n < total ? a_s : 0);
+    if (++a_s == nsteps) a_s = 0;
+    ++a_n;
+  };
+  {
+    PfStage<NTV> s0;
+    pf_stage_load<NTV>(s0, src, 0);
+#pragma unroll
+    for (int d = 0; d < G; d++) stage_next(st[(d + 1) % G]);
+    fetch_group();
+    pf_stage_store<NTV>(s0, bs[0]);
+  }
+  __syncthreads();
+  pf4 acc[NM][TILES][NTV];
+#pragma unroll
+  for (int m = 0; m < NM; m++)
+#pragma unroll
+    for (int t = 0; t < TILES; t++)
+#pragma unroll
+      for (int q = 0; q < NTV; q++) acc[m][t][q] = pf4{0.f, 0.f, 0.f, 0.f};
+  int c_rb = 0, c_s = 0;  // group being computed
+  for (int it0 = 0; it0 < total; it0 += G) {
+    rbt_u4 cw[G][NM][TILES], cs[NM][TILES];
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int t = 0; t < TILES; t++) {
+        cs[m][t] = ns[m][t];
+#pragma unroll
+        for (int d = 0; d < G; d++) cw[d][m][t] = nw[d][m][t];
       }
+    fetch_group();
+#pragma unroll
+    for (int d = 0; d < G; d++) {
+      const int buf = d & 1;  // iteration it reads LDS buffer it & 1 (nsteps even)
+      // activations of it + 1 (loaded a group ago) -> the other LDS buffer
+      pf_stage_store<NTV>(st[(d + 1) % G], bs[buf ^ 1]);
+      stage_next(st[(d + 1) % G]);
+#pragma unroll
+      for (int k4 = 0; k4 < 4; k4++) {
+        pb8 bv[NTV];
+#pragma unroll
+        for (int q = 0; q < NTV; q++) bv[q] = pf_b(bs[buf], q, k4, r, g);
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+          for (int t = 0; t < TILES; t++) {
+            const rbt_u4 sv = cs[m][t];
+            const uint32_t sw = d == 0 ? sv.x : d == 1 ? sv.y : d == 2 ? sv.z : sv.w;
+            const float scl = pf_e8m0((sw >> (8 * g)) & 0xffu);
+            const rbt_u4 c = cw[d][m][t];
+            const uint32_t code = k4 == 0 ? c.x : k4 == 1 ? c.y : k4 == 2 ? c.z : c.w;
+            const pb8 av = pf_fp4x8(code, scl);
+#pragma unroll
+            for (int q = 0; q < NTV; q++)
+              acc[m][t][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv[q], acc[m][t][q], 0, 0, 0);
+          }
+      }
+      __syncthreads();
+    }
+    c_s += G;
+    if (c_s == nsteps) {  // row block done (wave-uniform)
+#pragma unroll
+      for (int t = 0; t < TILES; t++) {
+        const int orow = (rb0 + PF_RBG * c_rb) * BR + 16 * TILES * w + 16 * t + 4 * g;
+#pragma unroll
+        for (int q = 0; q < NTV; q++) {
+          const int j = 16 * q + r;
+          if (j < T.M) {
+            if (NM == 2) {
+              pb4 hv;
+#pragma unroll
+              for (int i = 0; i < 4; i++) hv[i] = (__bf16)(rbt_silu(acc[0][t][q][i]) * acc[NM - 1][t][q][i]);
+              *reinterpret_cast<pb4 *>(hb + (long)(T.pbase + j) * out_cols + orow) = hv;
+            } else {
+              *reinterpret_cast<float4 *>(y + (long)(T.pbase + j) * out_cols + orow) =
+                  float4{acc[0][t][q][0], acc[0][t][q][1], acc[0][t][q][2], acc[0][t][q][3]};
+            }
+          }
+#pragma unroll
+          for (int m = 0; m < NM; m++) acc[m][t][q] = pf4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      c_s = 0;
+      ++c_rb;
     }
   }
 }
 
-// Gate/up: grid = ntiles_max * (I / 64) workgroups of 256 threads, row block fastest. Wave w of a
-// workgroup owns rows 64 * rb + 16 w .. +15 of gate and of up for the tile's tokens, over all
-// H columns. Output hb[pair, I] = bf16(silu(g) * u).
+// Gate/up: grid = ntiles_max * PF_RBG workgroups of 256 threads; workgroup (tile, gi) owns rows
+// [gi * I / PF_RBG, (gi + 1) * I / PF_RBG) of gate and of up for the tile's tokens, over all H
+// columns. Output hb[pair, I] = bf16(silu(g) * u) (glm52/moe.rs:33-80 Activation::Silu).
 __global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                  const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                  const RbtExpertDev *__restrict__ shared_dev,
                                                  const int *__restrict__ pair_tok, const __bf16 *__restrict__ xb,
                                                  int S, int H, int I, __bf16 *__restrict__ hb) {
-  constexpr int NT = PF_NT;
-  const int nrb = I >> 6;
-  const int ti = blockIdx.x / nrb, rb = blockIdx.x - ti * nrb;
+  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
+  const int ti = blockIdx.x / PF_RBG, gi = blockIdx.x - ti * PF_RBG;
   if (ti >= *ntiles) return;
   const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
   if (!T.ok) return;
   const int nt = (T.M + 15) >> 4;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const long row = 64L * rb + 16 * w + r;
-  const long rowb = (long)(H >> 1), rows = (long)(H >> 5);
-  const uint8_t *ga = T.J.gd + row * rowb + 16 * g;
-  const uint8_t *ua = T.J.ud + row * rowb + 16 * g;
-  const uint8_t *gs = (const uint8_t *)T.J.gs + row * rows;
-  const uint8_t *us = (const uint8_t *)T.J.us + row * rows;
-  const __bf16 *bp[NT];
-#pragma unroll
-  for (int q = 0; q < NT; q++) {
-    const int j = min(16 * q + r, T.M - 1);
-    const int tok = min(max(pair_tok[T.pbase + j], 0), S - 1);
-    bp[q] = xb + (long)tok * H + 32 * g;
-  }
-  pf4 ag[NT], au[NT];
-#pragma unroll
-  for (int q = 0; q < NT; q++) ag[q] = au[q] = pf4{0.f, 0.f, 0.f, 0.f};
   const int nsteps = H >> 7;
-  rbt_u4 cg = __builtin_nontemporal_load((const rbt_gu4 *)(ga));
-  rbt_u4 cu = __builtin_nontemporal_load((const rbt_gu4 *)(ua));
-  rbt_u4 sg = *(const rbt_gu4 *)(gs);
-  rbt_u4 su = *(const rbt_gu4 *)(us);
-  pb8 b[NT][4];
-  pf_load_b<NT>(b, bp, 0, nt);
-  for (int s = 0; s < nsteps; s++) {
-    // scale bytes of this step: dword (s & 3) of the 16-byte group, byte g
-    const uint32_t swg = (s & 3) == 0 ? sg.x : (s & 3) == 1 ? sg.y : (s & 3) == 2 ? sg.z : sg.w;
-    const uint32_t swu = (s & 3) == 0 ? su.x : (s & 3) == 1 ? su.y : (s & 3) == 2 ? su.z : su.w;
-    const float scg = pf_e8m0((swg >> (8 * g)) & 0xffu), scu = pf_e8m0((swu >> (8 * g)) & 0xffu);
-    const rbt_u4 xg = cg, xu = cu;
-    pb8 bc[NT][4];
-#pragma unroll
-    for (int q = 0; q < NT; q++)
-#pragma unroll
-      for (int m = 0; m < 4; m++) bc[q][m] = b[q][m];
-    if (s + 1 < nsteps) {
-      cg = __builtin_nontemporal_load((const rbt_gu4 *)(ga + 64 * (s + 1)));
-      cu = __builtin_nontemporal_load((const rbt_gu4 *)(ua + 64 * (s + 1)));
-      if (((s + 1) & 3) == 0) {
-        sg = *(const rbt_gu4 *)(gs + 4 * (s + 1));
-        su = *(const rbt_gu4 *)(us + 4 * (s + 1));
-      }
-      pf_load_b<NT>(b, bp, s + 1, nt);
-    }
-    pf_step<NT>(xg, scg, bc, ag, nt);
-    pf_step<NT>(xu, scu, bc, au, nt);
-  }
-  const int orow = 64 * rb + 16 * w + 4 * g;
-#pragma unroll
-  for (int q = 0; q < NT; q++) {
-    const int j = 16 * q + r;
-    if (q < nt && j < T.M) {
-      pb4 hv;
-#pragma unroll
-      for (int i = 0; i < 4; i++) hv[i] = (__bf16)(rbt_silu(ag[q][i]) * au[q][i]);
-      *reinterpret_cast<pb4 *>(hb + (long)(T.pbase + j) * I + orow) = hv;
-    }
+  // row blocks of BR rows, dealt round-robin to the PF_RBG workgroups of the tile
+  auto per_of = [&](int br) { return (I / br - gi + PF_RBG - 1) / PF_RBG; };
+  const long rowb = (long)(H >> 1), rows = (long)(H >> 5);
+  const uint8_t *const a[2] = {T.J.gd, T.J.ud};
+  const uint8_t *const sc[2] = {(const uint8_t *)T.J.gs, (const uint8_t *)T.J.us};
+  auto src_of = [&](int q) {
+    const int tok = min(max(pair_tok[T.pbase + min(16 * q + (int)(threadIdx.x >> 4), T.M - 1)], 0), S - 1);
+    return xb + (long)tok * H + (threadIdx.x & 15) * 8;
+  };
+  switch (nt) {
+    case 1: {
+      const __bf16 *src[1] = {src_of(0)};
+      pf_gemm<2, 1, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, I, hb, nullptr, bs);
+    } break;
+    case 2: {
+      const __bf16 *src[2] = {src_of(0), src_of(1)};
+      pf_gemm<2, 2, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, bs);
+    } break;
+    default: {
+      const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
+      pf_gemm<2, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, bs);
+    } break;
   }
 }
 
-// Down: grid = ntiles_max * (H / 64), 256 threads. Wave w owns down rows 64 * rb + 16 w .. +15
-// over all I columns for the tile's tokens; y[pair, H] fp32.
+// Down: grid = ntiles_max * PF_RBG, 256 threads; workgroup (tile, gi) owns down rows
+// [gi * H / PF_RBG, (gi + 1) * H / PF_RBG) over all I columns; y[pair, H] fp32.
 __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                const RbtExpertDev *__restrict__ shared_dev,
                                                const __bf16 *__restrict__ hb, int I, int H, float *__restrict__ y) {
-  constexpr int NT = PF_NT;
-  const int nrb = H >> 6;
-  const int ti = blockIdx.x / nrb, rb = blockIdx.x - ti * nrb;
+  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
+  const int ti = blockIdx.x / PF_RBG, gi = blockIdx.x - ti * PF_RBG;
   if (ti >= *ntiles) return;
   const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
   if (!T.ok) return;
   const int nt = (T.M + 15) >> 4;
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const long row = 64L * rb + 16 * w + r;
-  const uint8_t *da = T.J.dd + row * (long)(I >> 1) + 16 * g;
-  const uint8_t *ds = (const uint8_t *)T.J.ds + row * (long)(I >> 5);
-  const __bf16 *bp[NT];
-#pragma unroll
-  for (int q = 0; q < NT; q++) {
-    const int j = min(16 * q + r, T.M - 1);
-    bp[q] = hb + (long)(T.pbase + j) * I + 32 * g;
-  }
-  pf4 acc[NT];
-#pragma unroll
-  for (int q = 0; q < NT; q++) acc[q] = pf4{0.f, 0.f, 0.f, 0.f};
   const int nsteps = I >> 7;
-  rbt_u4 cd = __builtin_nontemporal_load((const rbt_gu4 *)(da));
-  rbt_u4 sd = *(const rbt_gu4 *)(ds);
-  pb8 b[NT][4];
-  pf_load_b<NT>(b, bp, 0, nt);
-  for (int s = 0; s < nsteps; s++) {
-    const uint32_t sw = (s & 3) == 0 ? sd.x : (s & 3) == 1 ? sd.y : (s & 3) == 2 ? sd.z : sd.w;
-    const float sc = pf_e8m0((sw >> (8 * g)) & 0xffu);
-    const rbt_u4 xd = cd;
-    pb8 bc[NT][4];
-#pragma unroll
-    for (int q = 0; q < NT; q++)
-#pragma unroll
-      for (int m = 0; m < 4; m++) bc[q][m] = b[q][m];
-    if (s + 1 < nsteps) {
-      cd = __builtin_nontemporal_load((const rbt_gu4 *)(da + 64 * (s + 1)));
-      if (((s + 1) & 3) == 0) sd = *(const rbt_gu4 *)(ds + 4 * (s + 1));
-      pf_load_b<NT>(b, bp, s + 1, nt);
-    }
-    pf_step<NT>(xd, sc, bc, acc, nt);
-  }
-  const int orow = 64 * rb + 16 * w + 4 * g;
-#pragma unroll
-  for (int q = 0; q < NT; q++) {
-    const int j = 16 * q + r;
-    if (q < nt && j < T.M)
-      *reinterpret_cast<float4 *>(y + (long)(T.pbase + j) * H + orow) =
-          float4{acc[q][0], acc[q][1], acc[q][2], acc[q][3]};
+  auto per_of = [&](int br) { return (H / br - gi + PF_RBG - 1) / PF_RBG; };
+  const long rowb = (long)(I >> 1), rows = (long)(I >> 5);
+  const uint8_t *const a[1] = {T.J.dd};
+  const uint8_t *const sc[1] = {(const uint8_t *)T.J.ds};
+  auto src_of = [&](int q) {
+    return hb + (long)(T.pbase + min(16 * q + (int)(threadIdx.x >> 4), T.M - 1)) * I + (threadIdx.x & 15) * 8;
+  };
+  switch (nt) {
+    case 1: {
+      const __bf16 *src[1] = {src_of(0)};
+      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, bs);
+    } break;
+    case 2: {
+      const __bf16 *src[2] = {src_of(0), src_of(1)};
+      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, bs);
+    } break;
+    default: {
+      const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
+      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, bs);
+    } break;
   }
 }
 
@@ -432,8 +550,8 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
 // ------------------------------------------------------------------------------------------------
 bool prefill_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k) {
   if (kind != RBT_QT_MXFP4) return false;
-  // K steps of 128 columns with scale groups of 4 steps; 64-row blocks
-  if (d % 512 != 0 || i % 512 != 0 || d > (1u << 20) || i > (1u << 20)) return false;
+  // K steps of 128 columns (gate/up: 4 in flight, down: 8), PF_RBG groups of 64-row blocks
+  if (d % 512 != 0 || i % 1024 != 0 || d > (1u << 20) || i > (1u << 20)) return false;
   // segments: every expert plus the shared one within PG_MAXE
   return n_experts + 1 <= (size_t)PG_MAXE && k <= 64;
 }
@@ -464,9 +582,9 @@ hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb) {
 hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                           const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
                           const __bf16 *xb, int S, int H, int I, __bf16 *hb) {
-  const long blocks = max_tiles * (I >> 6);
+  const long blocks = max_tiles * PF_RBG;
   if (blocks <= 0) return hipSuccess;
-  if (blocks > 0x7fffffffL || H % 512 || I % 512) return hipErrorInvalidValue;
+  if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pgateup, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table,
                      shared_dev, pair_tok, xb, S, H, I, hb);
   return hipGetLastError();
@@ -475,9 +593,9 @@ hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, l
 hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb, int I, int H,
                         float *y) {
-  const long blocks = max_tiles * (H >> 6);
+  const long blocks = max_tiles * PF_RBG;
   if (blocks <= 0) return hipSuccess;
-  if (blocks > 0x7fffffffL || H % 512 || I % 512) return hipErrorInvalidValue;
+  if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pdown, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table, shared_dev,
                      hb, I, H, y);
   return hipGetLastError();

@@ -138,7 +138,7 @@ PREFILL_RTOL = 1e-2  # bf16-MFMA prefill outputs (x and h rounded to bf16)
 ])
 def test_moe_prefill_grouped(ctx, orc, family, gated, lb, S, E, k):
     import rabbit_amd as R
-    H, I = 1024, 512
+    H, I = 1024, 1024  # the grouped path needs H % 512 == 0 and I % 1024 == 0
     L = _small_layer(ctx, orc, family, R.QT_MXFP4, H, I, E, k, seed=77 + S, gated=gated, logit_bias=lb)
     x = normal((S, H), 500 + S)
     exp, eids, ew = L.forward(x, S, simd=True)
@@ -152,6 +152,8 @@ def test_moe_prefill_grouped(ctx, orc, family, gated, lb, S, E, k):
     err = rel_l2(out, exp)
     print(f"prefill S={S} family={family} rel_l2={err:.3e}")
     assert err < PREFILL_RTOL
+    # bf16 operands leave an error of order 1e-3: far smaller means the fp32 GEMV path ran instead
+    assert err > 1e-4, "the grouped bf16 path did not run"
     # each token's row on its own: no token's output may depend on the rest of the batch
     for t in (0, S // 2, S - 1):
         assert rel_l2(out.reshape(S, H)[t], exp[t]) < PREFILL_RTOL
