@@ -45,6 +45,7 @@ enum ScratchSlot {
   SC_GU,
   SC_XB,
   SC_PGRP,
+  SC_RLOG,
   SC_N
 };
 
@@ -559,7 +560,15 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
       if (!e) return fail(c, RBT_E_HIP, "hipEventCreate failed");
     HIP_OK(c, hipEventRecord(ev[0], c->stream));
   }
-  HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
+  if (rbt::router_exact_ok(S, H) && (uintptr_t)x % 16 == 0) {
+    // batches: the reference's sequential fp32 logits themselves, then point intervals
+    float *lg;
+    RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * erows, &lg));
+    HIP_OK(c, rbt::launch_router_logits_exact(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, lg));
+    HIP_OK(c, rbt::launch_logits_to_mid(*c, lg, (size_t)S * erows, mid, bnd));
+  } else {
+    HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
+  }
   rbt::RouterArgs ra{D.family, E,          erows,          k,     H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
   // one token: the selection kernel writes the job table itself; several: k_group afterwards

@@ -89,6 +89,10 @@ hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, lon
 // router.hip
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd);
+// Batched path: the reference's sequential fp32 logits themselves, logits[S, E (+1 with sgate)].
+bool router_exact_ok(int S, int H);
+hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H, const float *W, int E,
+                                      const float *sgate, float *logits);
 // Expert job-table outputs the selection kernel writes itself for a single token (S == 1).
 struct GroupArgs {
   const RbtExpertDev *table, *shared_dev;

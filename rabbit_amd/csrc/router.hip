@@ -340,6 +340,90 @@ __global__ __launch_bounds__(256) void k_router_logits_b(const float *__restrict
   }
 }
 
+// Exact logits for a batch of tokens: logit[t, e] = fold(-0.0, +) of fl32(x[t, k] * w[e, k]) over
+// k ascending, the reference's own sequential sum (kernels.rs:113-124), so selection needs no
+// certification. Each lane carries four independent folds (2 tokens x 2 rows); a workgroup covers
+// 32 tokens x 32 router rows, with 256-column chunks of both operands staged through LDS (the
+// next chunk is loaded while the current one is folded). Rows E (when sgate is set) and beyond
+// read the shared-gate vector; rows past erows and tokens past S are computed on clamped inputs
+// and not written.
+constexpr int RX_T = 32, RX_E = 32, RX_KC = 256, RX_PAD = 4;
+constexpr int RX_EXACT_MIN_S = 64;  // from this batch size the exact folds beat the certified sums
+__global__ __launch_bounds__(256) void k_router_logits_exact(const float *__restrict__ x, int S, int H,
+                                                             const float *__restrict__ W, int E,
+                                                             const float *__restrict__ sgate, float *__restrict__ logits,
+                                                             int erows) {
+  __shared__ __attribute__((aligned(16))) float xs[2][RX_T][RX_KC + RX_PAD];
+  __shared__ __attribute__((aligned(16))) float ws[2][RX_E][RX_KC + RX_PAD];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int t0 = blockIdx.y * RX_T, e0 = blockIdx.x * RX_E;
+  // staging: thread tid moves row tid / 8, 32 consecutive floats (8 x float4) of each operand
+  const int sr = tid >> 3, sc = (tid & 7) * 32;
+  const float *xrow = x + (size_t)min(t0 + sr, S - 1) * H;
+  const int er = min(e0 + sr, erows - 1);
+  const float *wrow = er < E ? W + (size_t)er * H : sgate;
+  float4 stx[8], stw[8];
+  auto load_chunk = [&](int c) {
+    const float4 *px = reinterpret_cast<const float4 *>(xrow + c * RX_KC + sc);
+    const float4 *pw = reinterpret_cast<const float4 *>(wrow + c * RX_KC + sc);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      stx[i] = px[i];
+      stw[i] = pw[i];
+    }
+  };
+  auto store_chunk = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      *reinterpret_cast<float4 *>(&xs[b][sr][sc + 4 * i]) = stx[i];
+      *reinterpret_cast<float4 *>(&ws[b][sr][sc + 4 * i]) = stw[i];
+    }
+  };
+  // lane's folds: tokens 16 (wave >> 1) + 2 (lane & 7) + {0, 1}, rows 16 (wave & 1) + 2 (lane >> 3) + {0, 1}
+  const int lt = 16 * (wave >> 1) + 2 * (lane & 7), le = 16 * (wave & 1) + 2 * (lane >> 3);
+  float a00 = -0.0f, a01 = -0.0f, a10 = -0.0f, a11 = -0.0f;
+  const int nch = H / RX_KC;
+  load_chunk(0);
+  store_chunk(0);
+  if (nch > 1) load_chunk(1);
+  __syncthreads();
+  for (int c = 0; c < nch; c++) {
+    const int b = c & 1;
+    const float *x0 = xs[b][lt], *x1 = xs[b][lt + 1], *w0 = ws[b][le], *w1 = ws[b][le + 1];
+#pragma unroll 4
+    for (int k = 0; k < RX_KC; k += 4) {
+      const float4 xa = *reinterpret_cast<const float4 *>(x0 + k), xb = *reinterpret_cast<const float4 *>(x1 + k);
+      const float4 wa = *reinterpret_cast<const float4 *>(w0 + k), wb = *reinterpret_cast<const float4 *>(w1 + k);
+      a00 = __fadd_rn(a00, __fmul_rn(xa.x, wa.x));
+      a01 = __fadd_rn(a01, __fmul_rn(xa.x, wb.x));
+      a10 = __fadd_rn(a10, __fmul_rn(xb.x, wa.x));
+      a11 = __fadd_rn(a11, __fmul_rn(xb.x, wb.x));
+      a00 = __fadd_rn(a00, __fmul_rn(xa.y, wa.y));
+      a01 = __fadd_rn(a01, __fmul_rn(xa.y, wb.y));
+      a10 = __fadd_rn(a10, __fmul_rn(xb.y, wa.y));
+      a11 = __fadd_rn(a11, __fmul_rn(xb.y, wb.y));
+      a00 = __fadd_rn(a00, __fmul_rn(xa.z, wa.z));
+      a01 = __fadd_rn(a01, __fmul_rn(xa.z, wb.z));
+      a10 = __fadd_rn(a10, __fmul_rn(xb.z, wa.z));
+      a11 = __fadd_rn(a11, __fmul_rn(xb.z, wb.z));
+      a00 = __fadd_rn(a00, __fmul_rn(xa.w, wa.w));
+      a01 = __fadd_rn(a01, __fmul_rn(xa.w, wb.w));
+      a10 = __fadd_rn(a10, __fmul_rn(xb.w, wa.w));
+      a11 = __fadd_rn(a11, __fmul_rn(xb.w, wb.w));
+    }
+    if (c + 1 < nch) {
+      store_chunk(b ^ 1);
+      if (c + 2 < nch) load_chunk(c + 2);
+    }
+    __syncthreads();
+  }
+  const int ta = t0 + lt, ea = e0 + le;
+  if (ta < S && ea < erows) logits[(size_t)ta * erows + ea] = a00;
+  if (ta < S && ea + 1 < erows) logits[(size_t)ta * erows + ea + 1] = a01;
+  if (ta + 1 < S && ea < erows) logits[(size_t)(ta + 1) * erows + ea] = a10;
+  if (ta + 1 < S && ea + 1 < erows) logits[(size_t)(ta + 1) * erows + ea + 1] = a11;
+}
+
 // ------------------------------------------------------------------------------------------------
 // 2. per-token selection
 // ------------------------------------------------------------------------------------------------
@@ -1113,6 +1197,256 @@ __global__ __launch_bounds__(256) void k_router_select2(SelParams P, const doubl
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Selection v3 (n_group <= 1), one workgroup of 256 threads per token; wave 0 selects, all four
+// waves recompute ambiguous logits exactly.
+//  * Keys: expert e = lane + 64 m of wave 0 holds its key interval [klo, khi] (logit interval through
+//    the family's monotone key map) and the order-preserving bits of its midpoint key (0 = no
+//    expert, so no validity masks are needed in the hot loop).
+//  * Top-k: the k-th largest midpoint key by bisection over the 32 key bits, one compare and one
+//    ballot per key register per bit; ties at the threshold go to the lowest ids, as the
+//    reference's strict-> scans do (qwen38/moe.rs:48-58, glm52/moe.rs:170-186).
+//  * Certification, in registers: the set is certain when every inexact winner's lower key is
+//    above every loser's upper key and every inexact loser's upper key is below every winner's lower
+//    key (wave min / max); the order is certain when adjacent winners (sorted by midpoint) have
+//    disjoint intervals. Intervals that fail are recomputed as the reference computes them
+//    (exact_logit_wave) and become points; the selection then repeats until nothing is ambiguous.
+// ------------------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_min_f(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fminf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+template <int MAXM>
+__global__ __launch_bounds__(256) void k_router_select3(SelParams P, const double *__restrict__ mid,
+                                                        const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                        float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                        int *__restrict__ stats, GroupOut G, int grp) {
+  __shared__ int c_id[SEL_MAXK];  // winners in id order
+  __shared__ uint32_t c_ku[SEL_MAXK];
+  __shared__ float c_lo[SEL_MAXK], c_hi[SEL_MAXK], c_l[SEL_MAXK];
+  __shared__ int r_id[SEL_MAXK];  // winners in rank order
+  __shared__ float r_l[SEL_MAXK], r_lo[SEL_MAXK], r_hi[SEL_MAXK];
+  __shared__ float s_w[SEL_MAXK];
+  // every expert once for set membership, plus at most two per adjacent winner pair for order
+  __shared__ int amb[SEL_MAXE + 2 * SEL_MAXK];
+  __shared__ float amb_val[SEL_MAXE + 2 * SEL_MAXK];
+  __shared__ int namb;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int s = blockIdx.x;
+  const int E = P.E, k = P.k, kk = min(P.k, P.E);
+  const double *ms = mid + (size_t)s * P.erows;
+  const double *bs = bnd + (size_t)s * P.erows;
+
+  float klo[MAXM], khi[MAXM], lmid[MAXM], lbv[MAXM], rbv[MAXM];
+  uint32_t ku[MAXM];
+  if (wave == 0) {
+    double mv[MAXM], bv[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads batch together
+      mv[m] = ms[e];
+      bv[m] = bs[e];
+      lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
+      rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
+    }
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      ku[m] = 0;
+      klo[m] = khi[m] = lmid[m] = -INFINITY;
+      if (lane + 64 * m < E) {
+        const float lo = __double2float_rd(mv[m] - bv[m] * (1.0 + 1e-12));
+        const float hi = __double2float_ru(mv[m] + bv[m] * (1.0 + 1e-12));
+        const float md = fminf(fmaxf(__double2float_rn(mv[m]), lo), hi);
+        lmid[m] = md;
+        const float kmid = sel_key_v(P, lbv[m], rbv[m], md);
+        ku[m] = ord_key(kmid);
+        if (lo == hi) {
+          klo[m] = khi[m] = kmid;
+        } else {
+          klo[m] = sel_key_v(P, lbv[m], rbv[m], lo);
+          khi[m] = sel_key_v(P, lbv[m], rbv[m], hi);
+        }
+      }
+    }
+  }
+  int total_amb = 0;
+  for (;;) {
+    if (wave == 0) {
+      // k-th largest midpoint key
+      uint32_t T = 0;
+#pragma unroll 1
+      for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t cand = T | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int m = 0; m < MAXM; m++) cnt += __popcll(__ballot(ku[m] >= cand));
+        T = cnt >= kk ? cand : T;
+      }
+      int ngt = 0;
+#pragma unroll
+      for (int m = 0; m < MAXM; m++) ngt += __popcll(__ballot(ku[m] > T));
+      const int need = kk - ngt;
+      uint32_t win = 0;
+      int taken_eq = 0, base = 0;
+      float lo_sel = INFINITY, hi_uns = -INFINITY;
+#pragma unroll
+      for (int m = 0; m < MAXM; m++) {
+        const unsigned long long eq = __ballot(ku[m] == T);
+        const bool weq = ku[m] == T && (taken_eq + __popcll(eq & lanemask_lt())) < need;
+        taken_eq += __popcll(eq);
+        const bool w = ku[m] > T || weq;
+        const unsigned long long wm = __ballot(w);
+        if (w) {
+          const int at = base + __popcll(wm & lanemask_lt());
+          c_id[at] = lane + 64 * m;
+          c_ku[at] = ku[m];
+          c_lo[at] = klo[m];
+          c_hi[at] = khi[m];
+          c_l[at] = lmid[m];
+          win |= 1u << m;
+          lo_sel = fminf(lo_sel, klo[m]);
+        } else if (ku[m] != 0) {
+          hi_uns = fmaxf(hi_uns, khi[m]);
+        }
+        base += __popcll(wm);
+      }
+      lo_sel = wave_min_f(lo_sel);
+      hi_uns = wave_max_f(hi_uns);
+      if (lane == 0) namb = 0;
+      __builtin_amdgcn_wave_barrier();
+      // set membership: inexact experts on the wrong side of the other side's bound
+#pragma unroll
+      for (int m = 0; m < MAXM; m++) {
+        const bool inexact = ku[m] != 0 && klo[m] != khi[m];
+        const bool a = inexact && (((win >> m) & 1u) ? klo[m] <= hi_uns : khi[m] >= lo_sel);
+        if (a) amb[atomicAdd(&namb, 1)] = lane + 64 * m;
+      }
+      // order: rank the winners by midpoint (key desc, id asc), then check adjacent intervals
+      if (lane < kk) {
+        const uint32_t my = c_ku[lane];
+        const int id = c_id[lane];
+        int rank = 0;
+        for (int j = 0; j < kk; j++) {
+          const uint32_t o = c_ku[j];
+          rank += (o > my) || (o == my && c_id[j] < id);
+        }
+        r_id[rank] = id;
+        r_l[rank] = c_l[lane];
+        r_lo[rank] = c_lo[lane];
+        r_hi[rank] = c_hi[lane];
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (lane + 1 < kk) {
+        const bool ea = r_lo[lane] == r_hi[lane], eb = r_lo[lane + 1] == r_hi[lane + 1];
+        if (!(r_lo[lane] > r_hi[lane + 1]) && !(ea && eb)) {
+          // a winner already counted for set membership may be added twice: harmless
+          if (!ea) amb[atomicAdd(&namb, 1)] = r_id[lane];
+          if (!eb) amb[atomicAdd(&namb, 1)] = r_id[lane + 1];
+        }
+      }
+    }
+    __syncthreads();
+    const int na = namb;
+    if (na == 0) break;
+    total_amb += na;
+    for (int j = wave; j < na; j += 4) {
+      const float l = exact_logit_wave(P.x + (size_t)s * P.H, P.W + (size_t)amb[j] * P.H, P.H);
+      if (lane == 0) amb_val[j] = l;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      for (int j = 0; j < na; j++) {
+        const int e = amb[j];
+        if ((e & 63) == lane) {
+          const int mm = e >> 6;
+          const float l = amb_val[j];
+#pragma unroll
+          for (int m = 0; m < MAXM; m++)
+            if (m == mm) {
+              const float key = sel_key_v(P, lbv[m], rbv[m], l);
+              lmid[m] = l;
+              klo[m] = khi[m] = key;
+              ku[m] = ord_key(key);
+            }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (wave == 0) {
+    if (lane == 0 && stats && total_amb) atomicAdd(stats, total_amb);
+    // weights, computed by the lanes in parallel; the sums run in rank order (lane 0)
+    float lv = 0.0f;
+    if (lane < kk) {
+      const int e = r_id[lane];
+      lv = P.logit_bias ? __fadd_rn(r_l[lane], P.logit_bias[e]) : r_l[lane];
+    }
+    if (P.family == RBT_FAMILY_QWEN38) {
+      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
+      const float mx = __shfl(lv, 0, 64);
+      if (lane < kk) s_w[lane] = (float)exp((double)__fsub_rn(lv, mx));
+      __builtin_amdgcn_wave_barrier();
+      float sum = 0.0f;
+      for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
+      if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
+    } else {
+      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
+      if (lane < kk) s_w[lane] = sigmoid_ref(lv);
+      __builtin_amdgcn_wave_barrier();
+      if (P.norm_topk) {
+        float sum = -0.0f;
+        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
+        sum = __fadd_rn(sum, 1e-20f);
+        if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
+      }
+      if (lane < kk) s_w[lane] = __fmul_rn(s_w[lane], P.routed_scale);
+    }
+    __builtin_amdgcn_wave_barrier();
+    int32_t *io = ids + (size_t)s * k;
+    float *wo = wts + (size_t)s * k;
+    for (int r = lane; r < k; r += 64) {
+      io[r] = r < kk ? r_id[r] : -1;
+      wo[r] = r < kk ? s_w[r] : 0.0f;
+    }
+    if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
+    if (grp) {
+      // single token: pair j = slot j; the shared expert is pair k
+      for (int r = lane; r <= k; r += 64) {
+        if (r < k) {
+          // field copies (a struct temporary here ends up in scratch memory)
+          const RbtExpertDev *src = G.table + (r < kk ? r_id[r] : 0);
+          RbtExpertDev *dst = G.pair_job + r;
+          const bool use = r < kk;
+          const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
+          const uint8_t *dd = use ? src->dd : nullptr;
+          const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
+          const void *ds = use ? src->ds : nullptr;
+          if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
+          dst->gd = gd;
+          dst->gs = gs;
+          dst->ud = ud;
+          dst->us = us;
+          dst->dd = dd;
+          dst->ds = ds;
+          G.pair_tok[r] = 0;
+          G.tok_pair[r] = r < kk ? r : -1;
+          G.tok_w[r] = r < kk ? s_w[r] : 0.0f;
+        } else {
+          G.pair_job[k] = *G.shared_dev;
+          G.pair_tok[k] = 0;
+        }
+      }
+    }
+  }
+}
+
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
 // interval is a point (bound 0) and the same selection code applies.
 __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
@@ -1278,6 +1612,18 @@ hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, cons
   return hipGetLastError();
 }
 
+bool router_exact_ok(int S, int H) { return S >= RX_EXACT_MIN_S && H % RX_KC == 0; }
+
+hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H, const float *W, int E,
+                                      const float *sgate, float *logits) {
+  const int erows = E + (sgate ? 1 : 0);
+  if (H % RX_KC != 0 || ((uintptr_t)x | (uintptr_t)W | (uintptr_t)(sgate ? sgate : W)) % 16 != 0)
+    return hipErrorInvalidValue;
+  const dim3 grid((erows + RX_E - 1) / RX_E, (S + RX_T - 1) / RX_T);
+  hipLaunchKernelGGL(k_router_logits_exact, grid, dim3(256), 0, c.stream, x, S, H, W, E, sgate, logits, erows);
+  return hipGetLastError();
+}
+
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp) {
   SelParams P;
@@ -1307,16 +1653,16 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
     }
     const int m = (a.E + 63) / 64;
     if (m <= 4)
-      hipLaunchKernelGGL(k_router_select2<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+      hipLaunchKernelGGL(k_router_select3<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
                          G, g);
     else if (m <= 8)
-      hipLaunchKernelGGL(k_router_select2<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+      hipLaunchKernelGGL(k_router_select3<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
                          G, g);
     else if (m <= 16)
-      hipLaunchKernelGGL(k_router_select2<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+      hipLaunchKernelGGL(k_router_select3<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
                          stats, G, g);
     else
-      hipLaunchKernelGGL(k_router_select2<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+      hipLaunchKernelGGL(k_router_select3<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
                          stats, G, g);
   }
   return hipGetLastError();
