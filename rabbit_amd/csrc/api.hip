@@ -600,7 +600,10 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   if (mfma) {
     // h as three bf16 parts per pair (3 * I bf16 = 1.5 * I floats of the h scratch)
     __bf16 *hp = reinterpret_cast<__bf16 *>(h);
-    HIP_OK(c, rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp));
+    if (S == 1 && (long)npairs * (I / 4) >= 4L * c->num_cu)  // every wave of the balanced grid has work
+      HIP_OK(c, rbt::launch_xgateup1(*c, pjob, npairs, x, H, I, hp));
+    else
+      HIP_OK(c, rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp));
     if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
     HIP_OK(c, rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out));
     if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));

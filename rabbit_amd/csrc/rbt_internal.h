@@ -54,6 +54,9 @@ hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, c
 bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared);
 hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok, int npairs, const float *x,
                           long x_stride, int K, int I, __bf16 *hp);
+// One token (every pair reads x): the same products balanced over num_cu workgroups.
+hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const float *x, int K, int I,
+                           __bf16 *hp);
 // hp: h as three bf16 parts per pair, hp[(p*3 + part)*I + k].
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,

@@ -129,17 +129,44 @@ __device__ __forceinline__ float row_dot(const xf4 &acc, int col) {
 // ------------------------------------------------------------------------------------------------
 constexpr int XG_DEPTH = 2;  // steps in flight per wave (8 KB of codes each)
 
+// acc += A(codes, scale) . B: the four MFMAs of one 16-byte chunk.
+__device__ __forceinline__ void xmma_s(const rbt_u4 &w, float sc, const XB &B, xf4 &acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.x, sc), B.b[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.y, sc), B.b[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.z, sc), B.b[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.w, sc), B.b[3], acc, 0, 0, 0);
+}
+
+// E8M0 byte -> f32 (e8m0_decode, quant.rs:391-396): 0 -> 2^-127, 255 -> the +inf bits.
+__device__ __forceinline__ float xe8m0(uint32_t b) { return __uint_as_float(max(b << 23, 0x400000u)); }
+
+// Block scales of a wave's rows go through a wave-private LDS window. A group of 4 steps needs
+// 64 scale bytes per row (blocks 64 G .. 64 G + 63); the wave's 32 rows (16 gate, 16 up) are
+// 128 pieces of 16 bytes, two per lane, loaded one group ahead and stored after the current group
+// has read its window. A lane then reads the one byte of each chunk from LDS instead of issuing a
+// 4-byte global load per chunk and step (16x fewer scale requests to the memory pipeline).
+struct XScale {
+  const uint8_t *p[2];  // piece i: matrix i (gate, up), row lane/4 of the wave, bytes 16 (lane % 4)
+  int last;             // last valid 16-byte offset of a row's scale bytes
+  rbt_u4 v[2];
+  __device__ __forceinline__ void load(int G) {
+    const int off = min(64 * G, last);  // past the row end: a valid address, never read back
+#pragma unroll
+    for (int i = 0; i < 2; i++) v[i] = *(const rbt_gu4 *)(p[i] + off);
+  }
+};
+
 template <int NCH>
 __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict__ jobs, const int *__restrict__ tok,
                                                  const float *__restrict__ x, long x_stride, int I,
                                                  __bf16 *__restrict__ hp) {
-  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024;
+  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024, SR = K >> 5;
   __shared__ __attribute__((aligned(16))) __bf16 xs[3 * stride];
   __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  __shared__ __attribute__((aligned(16))) uint8_t sw[4][2][32][64];  // [wave][buffer][row][byte]
   const int p = blockIdx.y;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int rho = col >> 2, kap = col & 3;
-  const uint32_t sh = 8u * (uint32_t)g;
   const RbtExpertDev J = jobs[p];
   const long r0 = 16L * (4 * blockIdx.x + w);  // first row of the wave
   if (J.gd == nullptr || J.ud == nullptr) {
@@ -147,31 +174,33 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
       hp[((long)p * 3 + e / 64) * I + 64 * blockIdx.x + (e & 63)] = (__bf16)0.0f;
     return;
   }
-  // activation first (the oldest loads in flight), then the weight ring
+  // activation first (the oldest loads in flight), then the scale window and the weight ring
   float4 xv[XV];
   {
     const rbt_gf4 *s4 = (const rbt_gf4 *)(x + (long)tok[p] * x_stride);
 #pragma unroll
     for (int j = 0; j < XV; j++) xv[j] = s4[threadIdx.x + 256 * j];
   }
+  XScale S;
+  S.last = SR - 16 * ((lane & 3) + 1);
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    S.p[i] = (const uint8_t *)(i ? J.us : J.gs) + (r0 + (lane >> 2)) * SR + 16 * (lane & 3);
+  S.load(0);
   __builtin_amdgcn_sched_barrier(0);
   // lane pointers: tile t, matrix m (0 gate, 1 up)
-  const uint8_t *wrow[2][4], *srow[2][4];
+  const uint8_t *wrow[2][4];
 #pragma unroll
   for (int m = 0; m < 2; m++)
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      const long rr = r0 + 4 * t + rho;
-      wrow[m][t] = (m ? J.ud : J.gd) + rr * (K >> 1) + 64 * kap + 16 * g;
-      srow[m][t] = (const uint8_t *)(m ? J.us : J.gs) + rr * (K >> 5) + 4 * kap;
-    }
-  XChunk ring[XG_DEPTH][2][4];
+    for (int t = 0; t < 4; t++) wrow[m][t] = (m ? J.ud : J.gd) + (r0 + 4 * t + rho) * (K >> 1) + 64 * kap + 16 * g;
+  rbt_u4 ring[XG_DEPTH][2][4];
 #pragma unroll
   for (int d = 0; d < XG_DEPTH; d++) {
 #pragma unroll
     for (int m = 0; m < 2; m++)
 #pragma unroll
-      for (int t = 0; t < 4; t++) xload(ring[d][m][t], wrow[m][t], srow[m][t], d);
+      for (int t = 0; t < 4; t++) ring[d][m][t] = __builtin_nontemporal_load((const rbt_gu4 *)(wrow[m][t] + 256 * d));
     __builtin_amdgcn_sched_barrier(0);
   }
   if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
@@ -188,6 +217,10 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
       xs[2 * stride + 4 * q + e] = ll;
     }
   }
+  // scale window of group 0, and group 1 in flight
+#pragma unroll
+  for (int i = 0; i < 2; i++) *reinterpret_cast<rbt_u4 *>(&sw[w][0][(lane >> 2) + 16 * i][16 * (lane & 3)]) = S.v[i];
+  if (NCH > 4) S.load(1);
   __syncthreads();
 
   const int bq = col >> 2, bpart = col & 3;
@@ -203,19 +236,27 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
   for (int c = 0; c < NCH; c++) {
     const int d = c % XG_DEPTH;
     const XB B = xb_read(bp + binc * c);
+    const uint8_t(*win)[64] = sw[w][(c >> 2) & 1];
+    const int sb = 16 * (c & 3) + 4 * kap + g;
 #pragma unroll
     for (int m = 0; m < 2; m++)
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        xmma1(ring[d][m][t], sh, B, acc[m][t]);
-      }
+      for (int t = 0; t < 4; t++) xmma_s(ring[d][m][t], xe8m0(win[16 * m + 4 * t + rho][sb]), B, acc[m][t]);
     if (c + XG_DEPTH < NCH) {
 #pragma unroll
       for (int m = 0; m < 2; m++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) xload(ring[d][m][t], wrow[m][t], srow[m][t], c + XG_DEPTH);
+        for (int t = 0; t < 4; t++)
+          ring[d][m][t] = __builtin_nontemporal_load((const rbt_gu4 *)(wrow[m][t] + 256 * (c + XG_DEPTH)));
     }
-    // keep each step's work in its step (see e8m0_inplace)
+    if ((c & 3) == 3 && c + 1 < NCH) {
+      // group (c + 1) / 4 -> its window (this wave read the other buffer's last bytes just above)
+      const int G = (c + 1) >> 2;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        *reinterpret_cast<rbt_u4 *>(&sw[w][G & 1][(lane >> 2) + 16 * i][16 * (lane & 3)]) = S.v[i];
+      if (4 * (G + 1) < NCH) S.load(G + 1);
+    }
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
@@ -230,6 +271,147 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
       hp[((long)p * 3 + 1) * I + rr] = mm;
       hp[((long)p * 3 + 2) * I + rr] = ll;
     }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// gate/up for one token (every pair reads the same x): balanced over the whole chip. The work is
+// U = npairs * I/4 units, unit u = (pair u / (I/4), 4-row tile u % (I/4)) of gate and of up; wave i
+// of the grid takes units [i U / NW, (i+1) U / NW), so every CU streams the same number of bytes
+// (a workgroup per CU; per-pair grids leave a third of the CUs with twice the work at small pair
+// counts). A wave runs its units as one stream of (unit, step) iterations, XG1_D of them in flight
+// (2 chunks of 16 bytes per lane each), and keeps each unit's scale bytes (4 rows x K/32 bytes of
+// gate and of up) in a private LDS window loaded one unit ahead.
+// ------------------------------------------------------------------------------------------------
+template <int NCH>
+__global__ __launch_bounds__(256) void k_xgateup1(const RbtExpertDev *__restrict__ jobs, int npairs,
+                                                  const float *__restrict__ x, int I, __bf16 *__restrict__ hp) {
+  // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
+  // the first half of the next unit (slots and the unit epilogue are compile-time positions)
+  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024, SR = K >> 5, D = NCH / 2;
+  static_assert(NCH % 2 == 0, "even step count");
+  __shared__ __attribute__((aligned(16))) __bf16 xs[3 * stride];
+  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  __shared__ __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
+  const int rho = col >> 2, kap = col & 3;
+  const int tpp = I >> 2;  // 4-row tiles per pair
+  const long U = (long)npairs * tpp, NW = 4L * gridDim.x, wi = 4L * blockIdx.x + w;
+  const int u0 = (int)(wi * U / NW), u1 = (int)((wi + 1) * U / NW);
+  // activation: the token's three bf16 parts to LDS (every workgroup)
+  float4 xv[XV];
+  {
+    const rbt_gf4 *s4 = (const rbt_gf4 *)x;
+#pragma unroll
+    for (int j = 0; j < XV; j++) xv[j] = s4[threadIdx.x + 256 * j];
+  }
+  // the wave's units span at most two pairs (U / NW < I / 4)
+  const int pa = u0 / tpp, pb = min(pa + 1, npairs - 1);
+  const RbtExpertDev JA = jobs[pa], JB = jobs[pb];
+  const bool live = u1 > u0 && JA.gd != nullptr && JA.ud != nullptr && JB.gd != nullptr && JB.ud != nullptr;
+  // lane pointers of unit u (clamped to the wave's last unit): codes of gate / up at step 0, and the
+  // lane's scale piece (16 bytes of row (lane >> 4) & 3, clamped at the row end)
+  const int s_row = (lane >> 4) & 3, s_off = min(16 * (lane & 15), SR - 16);
+  struct UPtr {
+    const uint8_t *g, *u, *gs, *us;
+  };
+  auto uptr = [&](int u) {
+    u = min(u, u1 - 1);
+    const int pp = u / tpp;
+    const RbtExpertDev &J = pp == pa ? JA : JB;
+    const long row0 = 4L * (u - pp * tpp);
+    UPtr r;
+    r.g = J.gd + (row0 + rho) * (K >> 1) + 64 * kap + 16 * g;
+    r.u = J.ud + (row0 + rho) * (K >> 1) + 64 * kap + 16 * g;
+    r.gs = (const uint8_t *)J.gs + (row0 + s_row) * SR + s_off;
+    r.us = (const uint8_t *)J.us + (row0 + s_row) * SR + s_off;
+    return r;
+  };
+  rbt_u4 ring[D][2], sv[2];
+  UPtr cur{}, nxt{};
+  if (live) {
+    cur = uptr(u0);
+    nxt = uptr(u0 + 1);
+    sv[0] = *(const rbt_gu4 *)cur.gs;
+    sv[1] = *(const rbt_gu4 *)cur.us;
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+      ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.g + 256 * d));
+      ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * d));
+    }
+  }
+  if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
+#pragma unroll
+  for (int j = 0; j < XV; j++) {
+    const int q = threadIdx.x + 256 * j;
+    const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      __bf16 hh, mm, ll;
+      split3(e4[e], hh, mm, ll);
+      xs[4 * q + e] = hh;
+      xs[stride + 4 * q + e] = mm;
+      xs[2 * stride + 4 * q + e] = ll;
+    }
+  }
+  auto sstore = [&](int buf) {
+    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][0][s_row][16 * (lane & 15)]) = sv[0];
+    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][1][s_row][16 * (lane & 15)]) = sv[1];
+  };
+  if (live) {
+    sstore(0);
+    sv[0] = *(const rbt_gu4 *)nxt.gs;  // scales of the next unit (the last unit's own, if none)
+    sv[1] = *(const rbt_gu4 *)nxt.us;
+  }
+  __syncthreads();
+  if (!live) {
+    // a missing expert is reported by the grouping (error flag); zero this wave's rows of h
+    for (int u = u0; u < u1; u++) {
+      const int pp = u / tpp;
+      if (lane < 12) hp[((long)pp * 3 + lane / 4) * I + 4L * (u - pp * tpp) + (lane & 3)] = (__bf16)0.0f;
+    }
+    return;
+  }
+  const int bq = col >> 2, bpart = col & 3;
+  const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
+                             : reinterpret_cast<const char *>(zb);
+  const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
+  for (int u = u0; u < u1; u++) {
+    const uint8_t(*win)[4][256] = sw[w][(u - u0) & 1];
+    xf4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+      const int d = c % D;
+      const XB B = xb_read(bp + binc * c);
+      const int sb = 16 * c + 4 * kap + g;
+      const rbt_u4 cg = ring[d][0], cu = ring[d][1];
+      // refill: step c + D of this unit, or step c - D of the next one
+      const uint8_t *rg = c < D ? cur.g + 256 * (c + D) : nxt.g + 256 * (c - D);
+      const uint8_t *ru = c < D ? cur.u + 256 * (c + D) : nxt.u + 256 * (c - D);
+      ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)rg);
+      ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)ru);
+      xmma_s(cg, xe8m0(win[0][rho][sb]), B, ag);
+      xmma_s(cu, xe8m0(win[1][rho][sb]), B, au);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // unit done: h for its 4 rows
+    const float gv = row_dot(ag, col), uv = row_dot(au, col);
+    const int pp = u / tpp;
+    if (col == 0) {  // lane 16*g: row 4 t + g of the unit's pair
+      const float hv = rbt_silu(gv) * uv;
+      __bf16 hh, mm, ll;
+      split3(hv, hh, mm, ll);
+      const long rr = 4L * (u - pp * tpp) + g;
+      hp[((long)pp * 3 + 0) * I + rr] = hh;
+      hp[((long)pp * 3 + 1) * I + rr] = mm;
+      hp[((long)pp * 3 + 2) * I + rr] = ll;
+    }
+    // next unit's scales into the other window, then look one unit further ahead
+    sstore((u + 1 - u0) & 1);
+    cur = nxt;
+    nxt = uptr(u + 2);
+    sv[0] = *(const rbt_gu4 *)nxt.gs;
+    sv[1] = *(const rbt_gu4 *)nxt.us;
   }
 }
 
@@ -369,6 +551,20 @@ bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared) {
   if (i != 2048 || d % 16 != 0) return false;                 // down: K = 2048
   const long np = (long)S * k + (has_shared ? S : 0);
   return np <= XD_MAXP && S <= 16;
+}
+
+hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const float *x, int K, int I,
+                           __bf16 *hp) {
+  if (npairs <= 0) return hipSuccess;
+  if (I % 4 != 0 || (long)npairs * (I / 4) < 4L * c.num_cu) return hipErrorInvalidValue;
+  const dim3 grid(c.num_cu);
+  if (K == 8192)
+    hipLaunchKernelGGL(k_xgateup1<16>, grid, dim3(256), 0, c.stream, jobs, npairs, x, I, hp);
+  else if (K == 7168)
+    hipLaunchKernelGGL(k_xgateup1<14>, grid, dim3(256), 0, c.stream, jobs, npairs, x, I, hp);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok, int npairs, const float *x,
