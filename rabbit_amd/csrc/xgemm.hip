@@ -433,16 +433,20 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
                                                const int *__restrict__ tok, const int *__restrict__ tok_pair,
                                                const float *__restrict__ tok_w, const float *__restrict__ sh_scale,
                                                int has_shared, int gated, float *__restrict__ out) {
-  constexpr int KD = NCH * 512, stride = KD + XG_PAD;
+  constexpr int KD = NCH * 512, stride = KD + XG_PAD, SRD = KD >> 5;
   constexpr int HV = 3 * KD / 8 / 256;  // 16-byte pieces of a pair's parts per thread
+  static_assert(SRD == 64, "a row's scale bytes are four 16-byte pieces");
   __shared__ __attribute__((aligned(16))) __bf16 hs[2][3 * stride];
-  __shared__ float oacc[16][16];        // [token][row of the workgroup]
-  __shared__ float pw[XD_MAXP];         // weight of each pair (routing weight or shared scale)
-  __shared__ int ptok[XD_MAXP];
+  __shared__ float oacc[16][16];  // [token][row of the workgroup]
+  __shared__ float pw[XD_MAXP];   // weight of each pair (routing weight or shared scale)
+  __shared__ int ptok[XD_MAXP];   // token of each pair (-1: adds nothing)
+  __shared__ const uint8_t *pd[XD_MAXP];  // down codes / scales of each pair (a live pair's for null jobs)
+  __shared__ const uint8_t *ps[XD_MAXP];
+  __shared__ int plive[XD_MAXP];
+  __shared__ __attribute__((aligned(16))) uint8_t sw[4][2][4][4][64];  // [wave][buffer][pair of group][row][byte]
   __shared__ __attribute__((aligned(16))) __bf16 zb[32];
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int rho = col >> 2, kap = col & 3;
-  const uint32_t sh = 8u * (uint32_t)g;
   const int P = S * k;
   if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
   oacc[threadIdx.x >> 4][threadIdx.x & 15] = 0.0f;
@@ -455,91 +459,106 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
     } else {
       wv = gated ? sh_scale[tt] : 1.0f;
     }
+    const RbtExpertDev J = jobs[pp];
+    plive[pp] = J.dd != nullptr && J.ds != nullptr;
+    pd[pp] = J.dd;
+    ps[pp] = (const uint8_t *)J.ds;
     pw[pp] = wv;
     ptok[pp] = (pp < P || has_shared) ? tt : -1;
   }
-  // Pairs with a null job load the rows of the first live pair (valid memory) and add nothing.
+  __syncthreads();
+  // Pairs with a null job read the rows of the first live pair (valid memory) and add nothing.
   int live0 = -1;
   for (int pp = 0; pp < npairs && live0 < 0; pp++)
-    if (jobs[pp].dd != nullptr) live0 = pp;
+    if (plive[pp]) live0 = pp;
+  if (live0 < 0) {
+    const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
+    if (t < S) out[(long)t * H + 16 * blockIdx.x + rr] = 0.0f;
+    return;
+  }
+  __syncthreads();
+  for (int pp = threadIdx.x; pp < npairs; pp += 256)
+    if (!plive[pp]) {
+      pd[pp] = pd[live0];
+      ps[pp] = ps[live0];
+      ptok[pp] = -1;
+    }
   __syncthreads();
   const int tile_r0 = 16 * blockIdx.x + 4 * w;
-  if (live0 >= 0) {
-    const uint8_t *fd = jobs[live0].dd, *fs = (const uint8_t *)jobs[live0].ds;
-    auto lane_rows = [&](int pp, const uint8_t *&wr, const uint8_t *&sr) {
-      const RbtExpertDev J = jobs[pp];
-      const uint8_t *d = J.dd ? J.dd : fd;
-      const uint8_t *scl = J.dd ? (const uint8_t *)J.ds : fs;
-      const long rr = tile_r0 + rho;
-      wr = d + rr * (KD >> 1) + 64 * kap + 16 * g;
-      sr = scl + rr * (KD >> 5) + 4 * kap;
-    };
-    rbt_u4 hv[HV];
-    auto load_h = [&](int pp) {
-      const rbt_gu4 *s4 = (const rbt_gu4 *)(hp + (long)pp * 3 * KD);
+  const long wrow = (long)(tile_r0 + rho) * (KD >> 1) + 64 * kap + 16 * g;  // lane's code offset in a matrix
+  // chunk (pair q, step c) of the lane (pairs past the end read the last pair again)
+  auto chunk = [&](int q, int c) {
+    return __builtin_nontemporal_load((const rbt_gu4 *)(pd[min(q, npairs - 1)] + wrow + 256 * c));
+  };
+  // scale window of pair group G (4 pairs): lane l holds pair 4G + l/16, row (l/4) % 4, bytes 16 (l % 4)
+  const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
+  auto sload = [&](int G) {
+    return *(const rbt_gu4 *)(ps[min(4 * G + s_q, npairs - 1)] + (long)(tile_r0 + s_row) * SRD + 16 * s_seg);
+  };
+  auto sstore = [&](int buf, const rbt_u4 &v) {
+    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][s_q][s_row][16 * s_seg]) = v;
+  };
+  rbt_u4 hv[2][HV];
+  auto load_h = [&](int q, rbt_u4 (&dst)[HV]) {
+    const rbt_gu4 *s4 = (const rbt_gu4 *)(hp + (long)min(q, npairs - 1) * 3 * KD);
 #pragma unroll
-      for (int j = 0; j < HV; j++) hv[j] = s4[threadIdx.x + 256 * j];
-    };
-    auto store_h = [&](int buf) {
+    for (int j = 0; j < HV; j++) dst[j] = s4[threadIdx.x + 256 * j];
+  };
+  auto store_h = [&](int buf, const rbt_u4 (&src)[HV]) {
 #pragma unroll
-      for (int j = 0; j < HV; j++) {
-        const int e = 8 * (threadIdx.x + 256 * j);  // element in [0, 3*KD)
-        const int part = e / KD, kk = e - part * KD;
-        *reinterpret_cast<rbt_u4 *>(&hs[buf][part * stride + kk]) = hv[j];
-      }
-    };
-    // chunk q = (pair q / NCH, step q % NCH); ring slot q % XD_DEPTH
-    const int total = npairs * NCH;
-    static_assert(XD_DEPTH == 2 * NCH, "the ring holds two pairs");
-    XChunk ring[XD_DEPTH];
-    load_h(0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < XD_DEPTH; i++) {
-      const int q = min(i, total - 1);
-      const uint8_t *wr, *sr;
-      lane_rows(q / NCH, wr, sr);
-      xload(ring[i], wr, sr, q % NCH);
-      __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < HV; j++) {
+      const int e = 8 * (threadIdx.x + 256 * j);  // element in [0, 3*KD)
+      const int part = e / KD, kk = e - part * KD;
+      *reinterpret_cast<rbt_u4 *>(&hs[buf][part * stride + kk]) = src[j];
     }
-    store_h(0);
-    __syncthreads();
-    const int bq = col >> 2, bpart = col & 3;
-    const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
-    const int binc = bpart < 3 ? 1024 : 0;
-    // Pairs two at a time so ring slots are compile-time (slot = half*NCH + step); with an odd
-    // pair count the last half is a dummy (clamped, in-bounds loads; nothing accumulated).
-    for (int pp = 0; pp < npairs; pp += 2) {
+  };
+  // prologue: h of pairs 0 and 1, scale windows of groups 0 (stored) and 1 (in flight), codes of
+  // pairs 0 and 1 in the ring
+  load_h(0, hv[0]);
+  load_h(1, hv[1]);
+  rbt_u4 sv = sload(0);
+  rbt_u4 ring[2 * NCH];
 #pragma unroll
-      for (int half = 0; half < 2; half++) {
-        const int cp = pp + half;
-        load_h(min(cp + 1, npairs - 1));
+  for (int i = 0; i < 2 * NCH; i++) ring[i] = chunk(i / NCH, i % NCH);
+  store_h(0, hv[0]);
+  sstore(0, sv);
+  sv = sload(1);
+  __syncthreads();
+  const int bq = col >> 2, bpart = col & 3;
+  const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
+  const int binc = bpart < 3 ? 1024 : 0;
+  const int ngroups = (npairs + 3) / 4;
+  for (int G = 0; G < ngroups; G++) {
+#pragma unroll
+    for (int h4 = 0; h4 < 4; h4++) {
+      const int cp = 4 * G + h4, hb = h4 & 1;
+      // h of pair cp + 2 (stored to LDS at the end of pair cp + 1)
+      load_h(cp + 2, hv[hb]);
+      const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[hb]) + boff : reinterpret_cast<const char *>(zb);
+      const uint8_t(*win)[64] = sw[w][G & 1][h4];
+      xf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NCH; c++) {
+        const int slot = hb * NCH + c;
+        const XB B = xb_read(bp + binc * c);
+        const rbt_u4 cw = ring[slot];
+        ring[slot] = chunk(cp + 2, c);
+        xmma_s(cw, xe8m0(win[rho][16 * c + 4 * kap + g]), B, acc);
         __builtin_amdgcn_sched_barrier(0);
-        const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[half]) + boff : reinterpret_cast<const char *>(zb);
-        xf4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-          const int slot = half * NCH + c;
-          const XB B = xb_read(bp + binc * c);
-          xmma1(ring[slot], sh, B, acc);
-          const int qn = min((cp + 2) * NCH + c, total - 1);
-          const uint8_t *wr, *sr;
-          lane_rows(qn / NCH, wr, sr);
-          xload(ring[slot], wr, sr, qn % NCH);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        const float y = row_dot(acc, col);
-        if (cp < npairs) {
-          const int tt = ptok[cp];
-          if (col == 0 && tt >= 0 && jobs[cp].dd != nullptr) {  // lane 16*g: row tile_r0 + g
-            float &o = oacc[tt][4 * w + g];
-            o = __fadd_rn(o, __fmul_rn(pw[cp], y));
-          }
-        }
-        store_h(half ^ 1);
-        __syncthreads();
       }
+      const float y = row_dot(acc, col);
+      if (cp < npairs) {
+        const int tt = ptok[cp];
+        if (col == 0 && tt >= 0) {  // lane 16*g: row tile_r0 + g
+          float &o = oacc[tt][4 * w + g];
+          o = __fadd_rn(o, __fmul_rn(pw[cp], y));
+        }
+      }
+      store_h(hb ^ 1, hv[hb ^ 1]);  // h of pair cp + 1 (loaded during pair cp - 1)
+      __syncthreads();
     }
+    sstore((G + 1) & 1, sv);
+    sv = sload(G + 2);
   }
   const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
   if (t < S) out[(long)t * H + 16 * blockIdx.x + rr] = oacc[t][rr];
