@@ -8,7 +8,8 @@ rotate over the whole pool and the 256 MB Infinity Cache cannot serve them.
 value    = microseconds per token (whole layer), timed over --steps tokens replayed through a HIP
            graph of --graph-tokens consecutive layer calls (the way a decode step would run).
 roofline = the dominant kernel, the gate/up dequant-GEMV: algorithmic bytes per launch / its mean
-           duration, measured live with HIP events on the library's stream (second pass).
+           duration, measured live with HIP events on the library's stream (second pass; the events
+           are recorded by the kernel dispatch itself, at its start and end).
 cpu_baseline = the reference's AVX-512 (or AVX2) MXFP4 tier, restated in oracle/, timed on this
            host's cores over a bounded sample of the same tokens.
 
@@ -323,10 +324,18 @@ def main():
     cb_us = prof["combine_ms"] / n * 1e3
 
     nexp = cfg.topk + (1 if cfg.shared else 0)
-    gu_bytes = nexp * 2 * cfg.inter * (H // 2 + H // 32)
-    dn_bytes = nexp * H * (cfg.inter // 2 + cfg.inter // 32)
+    per_gu = 2 * cfg.inter * (H // 2 + H // 32)  # gate + up bytes of one expert
+    per_dn = H * (cfg.inter // 2 + cfg.inter // 32)
+    # experts each kernel actually streamed per call (the shared expert's gate/up may run inside the
+    # router's selection launch, on the CUs it leaves idle)
+    gu_exp = prof["gateup_experts"] / n if prof["gateup_experts"] else nexp
+    dn_exp = prof["down_experts"] / n if prof["down_experts"] else nexp
+    gu_bytes = int(round(gu_exp * per_gu))
+    dn_bytes = int(round(dn_exp * per_dn))
     gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
-    ex_gbps = (gu_bytes + dn_bytes) / ((gu_us + dn_us) * 1e-6) / 1e9
+    # every expert's bytes over the time the layer spends in its expert kernels
+    ex_bytes = nexp * (per_gu + per_dn)
+    ex_gbps = ex_bytes / ((gu_us + dn_us) * 1e-6) / 1e9
 
     traffic = None
     tf = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
@@ -361,12 +370,15 @@ def main():
                    "topk": cfg.topk, "shared_expert": cfg.shared, "weights": "mxfp4" if cfg.kind == R.QT_MXFP4
                    else "int4-grouped", "tokens_per_step": 1, "resident_pool_gb": round(pool_gb, 2),
                    "graph_tokens": G},
-        "roofline": {"bound": "hbm", "kernel": "k_xgateup1 (gate/up + SiLU, MFMA on fp4->bf16 weights, balanced over all CUs), all 11 experts",
+        "roofline": {"bound": "hbm", "kernel": "k_xgateup1 (gate/up + SiLU, MFMA on fp4->bf16 weights, balanced over all CUs)",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": gu_bytes,
                      "launch_us": round(gu_us, 2), "traffic": traffic},
-        "expert_gemv": {"bytes_per_token": gu_bytes + dn_bytes, "us": round(gu_us + dn_us, 2),
-                        "gbps": round(ex_gbps, 1), "frac": round(ex_gbps / HBM_PEAK_GBPS, 4)},
+        "expert_gemv": {"bytes_per_token": ex_bytes, "us": round(gu_us + dn_us, 2),
+                        "gbps": round(ex_gbps, 1), "frac": round(ex_gbps / HBM_PEAK_GBPS, 4),
+                        "experts": nexp, "gateup_kernel_experts": gu_exp, "down_kernel_experts": dn_exp,
+                        "note": "all experts' bytes over the gate/up + down kernel times; experts the gate/up "
+                                "kernel does not stream ran inside the router phase"},
         "phase_us": {"router": round(rt_us, 2), "gateup": round(gu_us, 2), "down": round(dn_us, 2),
                      "combine": round(cb_us, 2)},
         "eager_us_per_token": round(eager_us, 2),

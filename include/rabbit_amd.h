@@ -204,6 +204,9 @@ typedef struct {
     double combine_ms;   /* weighted combine + shared expert */
     uint64_t calls;      /* rbt_moe_forward_d calls recorded */
     uint64_t ambiguous;  /* router logits recomputed exactly because of a near-tie */
+    uint64_t gateup_experts; /* one-token calls: experts whose gate/up the gate/up phase streamed (a shared
+                                expert whose gate/up ran inside the router phase is not counted) */
+    uint64_t down_experts;   /* one-token calls: experts whose down the down phase streamed */
 } rbt_profile;
 /* When on, rbt_moe_forward_d records HIP events on the context stream around each phase. */
 int rbt_profile_enable(rbt_ctx *ctx, int32_t on);

@@ -48,7 +48,8 @@ class RbtMoeLayerDesc(C.Structure):
 
 class RbtProfile(C.Structure):
     _fields_ = [("router_ms", C.c_double), ("gateup_ms", C.c_double), ("down_ms", C.c_double),
-                ("combine_ms", C.c_double), ("calls", C.c_uint64), ("ambiguous", C.c_uint64)]
+                ("combine_ms", C.c_double), ("calls", C.c_uint64), ("ambiguous", C.c_uint64),
+                ("gateup_experts", C.c_uint64), ("down_experts", C.c_uint64)]
 
 
 _P, _S, _I, _F, _U32, _U64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_float, C.c_uint32, C.c_uint64

@@ -83,7 +83,8 @@ struct rbt_ctx : rbt::Ctx {
   // profiling: one row of 5 events per recorded moe_forward_d call
   bool prof = false;
   std::vector<hipEvent_t> ev_free;
-  std::vector<std::array<hipEvent_t, 5>> ev_rows;
+  std::vector<std::array<hipEvent_t, 7>> ev_rows;
+  std::vector<std::array<uint64_t, 2>> ev_experts;  // per recorded call: gate/up and down experts
   rbt_profile acc{};
 };
 
@@ -314,7 +315,10 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
     RBT_TRY(scratch_t(c, SC_GU, (size_t)njobs * gs_stride, &gu));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_STACKED, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d,
                                  (int)d, (int)(2 * i), gu, gs_stride, parts));
-    if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
+    if (mark) {
+      HIP_OK(c, hipEventRecord(mark[0], c->stream));
+      HIP_OK(c, hipEventRecord(mark[1], c->stream));
+    }
     HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
                                  (int)i, (int)d, y, (long)d));
@@ -322,7 +326,10 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
   }
   HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
                                      (int)i, h, (long)i));
-  if (mark) HIP_OK(c, hipEventRecord(*mark, c->stream));
+  if (mark) {
+    HIP_OK(c, hipEventRecord(mark[0], c->stream));
+    HIP_OK(c, hipEventRecord(mark[1], c->stream));
+  }
   if (fast_dn)
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
                                  (int)i, (int)d, y, (long)d));
@@ -478,7 +485,8 @@ hipEvent_t take_event(rbt_ctx *c) {
 }
 
 // Prefill (several tokens, MXFP4): grouping into per-expert segments, x -> bf16, grouped gate/up
-// GEMM with SiLU, grouped down GEMM, ordered combine. ev (profiling) receives events 1..3.
+// GEMM with SiLU, grouped down GEMM, ordered combine. ev (profiling): event 1 after the grouping,
+// 2..5 recorded by the two GEMM dispatches (start, end each).
 int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H, int I, const int32_t *ids,
                 const float *wts, const float *shs, int *ptok, int *tpair, float *tw, float *h, float *yy, bool gated,
                 float *out, hipEvent_t *ev) {
@@ -505,10 +513,15 @@ int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H
                                tpair, tw, dflags + FLAG_ERR, dflags + FLAG_UNIQ));
   HIP_OK(c, rbt::launch_to_bf16(*c, x, (long)S * H, xb));
   if (ev) HIP_OK(c, hipEventRecord(ev[1], c->stream));
-  HIP_OK(c, rbt::launch_pgateup(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, ptok, xb, S, H, I, hb));
-  if (ev) HIP_OK(c, hipEventRecord(ev[2], c->stream));
-  HIP_OK(c, rbt::launch_pdown(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, hb, I, H, yy));
-  if (ev) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+  if (ev) c->t_start = ev[2], c->t_stop = ev[3];
+  const hipError_t e1 = rbt::launch_pgateup(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, ptok, xb, S, H,
+                                            I, hb);
+  c->t_start = c->t_stop = nullptr;
+  HIP_OK(c, e1);
+  if (ev) c->t_start = ev[4], c->t_stop = ev[5];
+  const hipError_t e2 = rbt::launch_pdown(*c, tiles, ntiles, max_tiles, segs, L.d_table, L.d_shared, hb, I, H, yy);
+  c->t_start = c->t_stop = nullptr;
+  HIP_OK(c, e2);
   HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, has_shared, gated ? 1 : 0, out));
   return RBT_OK;
 }
@@ -553,7 +566,9 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RBT_TRY(scratch_t(c, SC_YY, (size_t)npairs * H, &yy));
   int *dflags = c->d_flags;
 
-  std::array<hipEvent_t, 5> ev{};
+  // profiling events: [0] start, [1] routing done, [2, 3] gate/up kernel, [4, 5] down kernel,
+  // [6] end (the MFMA kernels record their own start and end)
+  std::array<hipEvent_t, 7> ev{};
   if (c->prof) {
     for (auto &e : ev) e = take_event(c);
     for (auto &e : ev)
@@ -574,15 +589,19 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   // one token: the selection kernel writes the job table itself; several: k_group afterwards
   rbt::GroupArgs ga{L.d_table, L.d_shared, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
   const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
-  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
-                                      grp_in_select ? &ga : nullptr));
-
   const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
                      L.shared_inter == (size_t)I;
   // MXFP4 decode shapes run on the matrix cores: gate/up with SiLU, then down with the ordered
   // combine fused in (out written directly).
   const bool mfma = (merge || !D.has_shared) && rbt::xgemm_ok(L.routed_kind, H, I, S, k, D.has_shared) &&
                     ((uintptr_t)x % 16 == 0);
+  // One token: the balanced gate/up covers the routed pairs, and the shared expert's gate/up runs in
+  // the selection launch (it does not depend on the routing).
+  const bool gu1 = mfma && S == 1 && (long)k * (I / 4) >= 4L * c->num_cu;
+  const bool sh_in_select = gu1 && D.has_shared && grp_in_select;
+  rbt::SharedGateUp sgu{L.d_shared, x, H, I, reinterpret_cast<__bf16 *>(h) + (size_t)k * 3 * I};
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
+                                      grp_in_select ? &ga : nullptr, sh_in_select ? &sgu : nullptr));
   // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores.
   const bool grouped = !mfma && S > 1 && (merge || !D.has_shared) &&
                        rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
@@ -595,19 +614,24 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
                                 dflags + FLAG_UNIQ));
 
   RbtExpertDev none{};
-  hipEvent_t *mark = c->prof ? &ev[2] : nullptr;
+  hipEvent_t *mark = c->prof ? &ev[3] : nullptr;
   if (c->prof) HIP_OK(c, hipEventRecord(ev[1], c->stream));
   if (mfma) {
     // h as three bf16 parts per pair (3 * I bf16 = 1.5 * I floats of the h scratch)
     __bf16 *hp = reinterpret_cast<__bf16 *>(h);
-    if (S == 1 && (long)npairs * (I / 4) >= 4L * c->num_cu)  // every wave of the balanced grid has work
-      HIP_OK(c, rbt::launch_xgateup1(*c, pjob, npairs, x, H, I, hp));
-    else
-      HIP_OK(c, rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp));
-    if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
-    HIP_OK(c, rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out));
-    if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+    if (c->prof) c->t_start = ev[2], c->t_stop = ev[3];
+    // every wave of the balanced grid has work; the shared pair is done when it ran in selection
+    const hipError_t e2 = gu1 ? rbt::launch_xgateup1(*c, pjob, sh_in_select ? k : npairs, x, H, I, hp)
+                              : rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp);
+    c->t_start = c->t_stop = nullptr;
+    HIP_OK(c, e2);
+    if (c->prof) c->t_start = ev[4], c->t_stop = ev[5];
+    const hipError_t e3 =
+        rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out);
+    c->t_start = c->t_stop = nullptr;
+    HIP_OK(c, e3);
   } else {
+    if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
     if (merge || !D.has_shared) {
       RBT_TRY(expert_pairs(c, L.routed_kind, L.routed_gs, pjob, none, npairs, nullptr, x, ptok, H, I, h, yy, mark));
     } else {
@@ -616,15 +640,21 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
       float *hs = h + (size_t)P * I;
       RBT_TRY(expert_pairs(c, L.shared_kind, L.shared_gs, pjob + P, none, S, nullptr, x, ptok + P, H, L.shared_inter,
                            hs, yy + (size_t)P * H, nullptr));
-      if (c->prof) HIP_OK(c, hipEventRecord(ev[2], c->stream));
+      if (c->prof) {
+        HIP_OK(c, hipEventRecord(ev[3], c->stream));  // the two expert sets as one gate/up+down phase
+        HIP_OK(c, hipEventRecord(ev[4], c->stream));
+      }
     }
-    if (c->prof) HIP_OK(c, hipEventRecord(ev[3], c->stream));
+    if (c->prof) HIP_OK(c, hipEventRecord(ev[5], c->stream));
     HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
   }
   }
   if (c->prof) {
-    HIP_OK(c, hipEventRecord(ev[4], c->stream));
+    HIP_OK(c, hipEventRecord(ev[6], c->stream));
     c->ev_rows.push_back(ev);
+    // one-token decode: the experts each phase streamed (prefill: 0, unknown on the host)
+    const uint64_t ne = S == 1 ? (uint64_t)npairs : 0;
+    c->ev_experts.push_back({S == 1 ? ne - (sh_in_select ? 1 : 0) : 0, ne});
   }
   if (ids_out)
     HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
@@ -1085,17 +1115,24 @@ int rbt_profile_enable(rbt_ctx *c, int32_t on) {
 int rbt_profile_read(rbt_ctx *c, rbt_profile *out, int32_t reset) {
   if (!c || !out) return RBT_E_INVALID;
   HIP_OK(c, hipStreamSynchronize(c->stream));
-  for (auto &r : c->ev_rows) {
+  for (size_t i = 0; i < c->ev_rows.size(); i++) {
+    auto &r = c->ev_rows[i];
     float t[4];
-    for (int j = 0; j < 4; j++) HIP_OK(c, hipEventElapsedTime(&t[j], r[j], r[j + 1]));
+    HIP_OK(c, hipEventElapsedTime(&t[0], r[0], r[1]));
+    HIP_OK(c, hipEventElapsedTime(&t[1], r[2], r[3]));
+    HIP_OK(c, hipEventElapsedTime(&t[2], r[4], r[5]));
+    HIP_OK(c, hipEventElapsedTime(&t[3], r[5], r[6]));
     c->acc.router_ms += t[0];
     c->acc.gateup_ms += t[1];
     c->acc.down_ms += t[2];
     c->acc.combine_ms += t[3];
     c->acc.calls += 1;
+    c->acc.gateup_experts += c->ev_experts[i][0];
+    c->acc.down_experts += c->ev_experts[i][1];
     for (auto e : r) c->ev_free.push_back(e);
   }
   c->ev_rows.clear();
+  c->ev_experts.clear();
   HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
   c->acc.ambiguous = (uint64_t)c->h_flags[FLAG_AMB];
   *out = c->acc;

@@ -585,7 +585,7 @@ hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, l
   const long blocks = max_tiles * PF_RBG;
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_pgateup, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table,
+  launch_k(c, k_pgateup, dim3((unsigned)blocks), dim3(256), tiles, ntiles, segs, table,
                      shared_dev, pair_tok, xb, S, H, I, hb);
   return hipGetLastError();
 }
@@ -596,7 +596,7 @@ hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, lon
   const long blocks = max_tiles * PF_RBG;
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_pdown, dim3((unsigned)blocks), dim3(256), 0, c.stream, tiles, ntiles, segs, table, shared_dev,
+  launch_k(c, k_pdown, dim3((unsigned)blocks), dim3(256), tiles, ntiles, segs, table, shared_dev,
                      hb, I, H, y);
   return hipGetLastError();
 }

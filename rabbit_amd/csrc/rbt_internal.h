@@ -1,6 +1,7 @@
 // rbt_internal.h -- host-side declarations shared by the library's translation units.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -14,7 +15,19 @@ struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
   int num_cu = 256;
+  // Profiling: when set, the next timed launch records these events itself at the kernel's start
+  // and end (hipExtLaunchKernelGGL), so the interval excludes dispatch gaps.
+  hipEvent_t t_start = nullptr, t_stop = nullptr;
 };
+
+// Launch on the context's stream; timed by the dispatch when the context holds kernel events.
+template <typename K, typename... A>
+inline void launch_k(const Ctx &c, K kernel, dim3 grid, dim3 block, A... args) {
+  if (c.t_start)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, c.stream, c.t_start, c.t_stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, c.stream, args...);
+}
 
 struct RouterArgs {
   int family, E, erows, k, H, S;
@@ -104,8 +117,17 @@ struct GroupArgs {
   float *tok_w;
   int *err;
 };
+// The shared expert's gate/up for a one-token call (balanced body of xgemm), run by the selection
+// launch on the CUs its one selecting workgroup leaves idle. hp: the shared pair's output parts.
+struct SharedGateUp {
+  const RbtExpertDev *dev;
+  const float *x;
+  int K, I;
+  __bf16 *hp;
+};
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
-                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr);
+                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr,
+                                const SharedGateUp *sgu = nullptr);
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);
 hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,

@@ -21,6 +21,7 @@
 //     lists in token order, and per-token pick lists ordered by first occurrence.
 #include "rbt_device.h"
 #include "rbt_internal.h"
+#include "rbt_xmfma.h"
 
 namespace rbt {
 
@@ -1224,10 +1225,10 @@ __device__ __forceinline__ float wave_max_f(float v) {
 }
 
 template <int MAXM>
-__global__ __launch_bounds__(256) void k_router_select3(SelParams P, const double *__restrict__ mid,
-                                                        const double *__restrict__ bnd, int32_t *__restrict__ ids,
-                                                        float *__restrict__ wts, float *__restrict__ sh_scale,
-                                                        int *__restrict__ stats, GroupOut G, int grp) {
+__device__ __forceinline__ void select3_body(const SelParams &P, const double *__restrict__ mid,
+                                             const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                             float *__restrict__ wts, float *__restrict__ sh_scale,
+                                             int *__restrict__ stats, const GroupOut &G, int grp, int s) {
   __shared__ int c_id[SEL_MAXK];  // winners in id order
   __shared__ uint32_t c_ku[SEL_MAXK];
   __shared__ float c_lo[SEL_MAXK], c_hi[SEL_MAXK], c_l[SEL_MAXK];
@@ -1239,7 +1240,6 @@ __global__ __launch_bounds__(256) void k_router_select3(SelParams P, const doubl
   __shared__ float amb_val[SEL_MAXE + 2 * SEL_MAXK];
   __shared__ int namb;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int s = blockIdx.x;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
   const double *ms = mid + (size_t)s * P.erows;
   const double *bs = bnd + (size_t)s * P.erows;
@@ -1447,6 +1447,30 @@ __global__ __launch_bounds__(256) void k_router_select3(SelParams P, const doubl
   }
 }
 
+template <int MAXM>
+__global__ __launch_bounds__(256) void k_router_select3(SelParams P, const double *__restrict__ mid,
+                                                        const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                        float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                        int *__restrict__ stats, GroupOut G, int grp) {
+  select3_body<MAXM>(P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x);
+}
+
+// One token with a shared expert: workgroup 0 selects; the other workgroups stream the shared
+// expert's gate/up (it does not depend on the routing) on the CUs the selection leaves idle.
+template <int MAXM, int NCH>
+__global__ __launch_bounds__(256) void k_router_select3_sh(SelParams P, const double *__restrict__ mid,
+                                                           const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                           float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                           int *__restrict__ stats, GroupOut G, int grp,
+                                                           const RbtExpertDev *__restrict__ shared_dev,
+                                                           const float *__restrict__ x, int I,
+                                                           __bf16 *__restrict__ hp_shared) {
+  if (blockIdx.x == 0)
+    select3_body<MAXM>(P, mid, bnd, ids, wts, sh_scale, stats, G, grp, 0);
+  else
+    xgateup1_body<NCH>(shared_dev, 1, x, I, hp_shared, blockIdx.x - 1, gridDim.x - 1);
+}
+
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
 // interval is a point (bound 0) and the same selection code applies.
 __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
@@ -1625,7 +1649,7 @@ hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H
 }
 
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
-                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp) {
+                                float *wts, float *sh_scale, int *stats, const GroupArgs *grp, const SharedGateUp *sgu) {
   SelParams P;
   P.family = a.family;
   P.E = a.E;
@@ -1652,6 +1676,26 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
       g = 1;
     }
     const int m = (a.E + 63) / 64;
+    if (sgu && a.S == 1 && m <= 8 && (sgu->K == 8192 || sgu->K == 7168)) {
+      const dim3 grid(max(2, c.num_cu));
+      if (m <= 4) {
+        if (sgu->K == 8192)
+          hipLaunchKernelGGL((k_router_select3_sh<4, 16>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                             stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
+        else
+          hipLaunchKernelGGL((k_router_select3_sh<4, 14>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                             stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
+      } else {
+        if (sgu->K == 8192)
+          hipLaunchKernelGGL((k_router_select3_sh<8, 16>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                             stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
+        else
+          hipLaunchKernelGGL((k_router_select3_sh<8, 14>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+                             stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
+      }
+      return hipGetLastError();
+    }
+    if (sgu) return hipErrorInvalidValue;
     if (m <= 4)
       hipLaunchKernelGGL(k_router_select3<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
                          G, g);

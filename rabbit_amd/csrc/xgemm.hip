@@ -33,34 +33,11 @@
 //               qwen38/generate.rs:303-349 / glm52/moe.rs:508-512 in place -> out.
 #include "rbt_device.h"
 #include "rbt_internal.h"
+#include "rbt_xmfma.h"
 
 namespace rbt {
 
-typedef __bf16 xb8 __attribute__((ext_vector_type(8)));
-typedef __bf16 xb2 __attribute__((ext_vector_type(2)));
-typedef float xf4 __attribute__((ext_vector_type(4)));
-
-constexpr int XG_PAD = 8;        // bf16 padding between the LDS part rows (bank spread)
-constexpr int XD_MAXP = 80;      // pairs per down launch (partial tiles kept in LDS)
-
-// 8 E2M1 codes (one dword) -> 8 bf16, scaled by the block's E8M0 value.
-__device__ __forceinline__ xb8 fp4x8_bf16(uint32_t w, float sc) {
-  const xb2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
-  const xb2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
-  const xb2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
-  const xb2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
-  return xb8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// x = hi + mid + lo, each part the bf16 rounding of the remainder (the remainders are exact in
-// fp32: x and hi agree to within one bf16 ulp).
-__device__ __forceinline__ void split3(float x, __bf16 &h, __bf16 &m, __bf16 &l) {
-  h = (__bf16)x;
-  const float r1 = x - (float)h;
-  m = (__bf16)r1;
-  const float r2 = r1 - (float)m;
-  l = (__bf16)r2;
-}
+constexpr int XD_MAXP = 80;  // pairs per down launch (partial tiles kept in LDS)
 
 struct XChunk {
   rbt_u4 w;    // 32 E2M1 codes of this lane's row at its 32 columns of the step
@@ -73,18 +50,6 @@ struct XChunk {
 __device__ __forceinline__ void xload(XChunk &c, const uint8_t *row, const uint8_t *srow, int step) {
   c.w = __builtin_nontemporal_load((const rbt_gu4 *)(row + 256 * step));
   c.s = *(const rbt_gu32 *)(srow + 16 * step);
-}
-
-// The four B operands of one step: lane l (column j = l%16: quarter j/4, part j%4) reads 8 values
-// of its part per MFMA; lanes of part 3 read a 64-byte zero block (their pointer does not move).
-struct XB {
-  xb8 b[4];
-};
-__device__ __forceinline__ XB xb_read(const char *bp) {
-  XB r;
-#pragma unroll
-  for (int m = 0; m < 4; m++) r.b[m] = *reinterpret_cast<const xb8 *>(bp + 16 * m);
-  return r;
 }
 
 // acc0/acc1 += A(chunk) . B: even and odd MFMAs go to separate accumulators (two independent
@@ -111,16 +76,6 @@ __device__ __forceinline__ void xmma1(const XChunk &c, uint32_t sh, const XB &B,
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(c.w.w, sc), B.b[3], acc, 0, 0, 0);
 }
 
-// Dot product of weight row l/16 of the tile from the accumulator (see the tile-shape notes): the
-// lane's useful entry is acc[(l%16)/4] unless its part is 3; the 16 lanes of the row group sum
-// them (every lane of the group ends with the same value).
-__device__ __forceinline__ float row_dot(const xf4 &acc, int col) {
-  const int kq = col >> 2;
-  float v = kq == 0 ? acc[0] : kq == 1 ? acc[1] : kq == 2 ? acc[2] : acc[3];
-  v = (col & 3) == 3 ? 0.0f : v;
-  return rbt_group_sum<16>(v);
-}
-
 // ------------------------------------------------------------------------------------------------
 // gate/up: grid (I/64, npairs), 256 threads. Wave w owns rows 16*(4*blockIdx.x + w) .. +15 of gate
 // and of up for pair p = blockIdx.y, as four 4-row tiles, over all K = 512*NCH columns. The step
@@ -128,17 +83,6 @@ __device__ __forceinline__ float row_dot(const xf4 &acc, int col) {
 // h = silu(gate . x) * (up . x) goes out as three bf16 parts hp[(p*3 + part)*I + r].
 // ------------------------------------------------------------------------------------------------
 constexpr int XG_DEPTH = 2;  // steps in flight per wave (8 KB of codes each)
-
-// acc += A(codes, scale) . B: the four MFMAs of one 16-byte chunk.
-__device__ __forceinline__ void xmma_s(const rbt_u4 &w, float sc, const XB &B, xf4 &acc) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.x, sc), B.b[0], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.y, sc), B.b[1], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.z, sc), B.b[2], acc, 0, 0, 0);
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fp4x8_bf16(w.w, sc), B.b[3], acc, 0, 0, 0);
-}
-
-// E8M0 byte -> f32 (e8m0_decode, quant.rs:391-396): 0 -> 2^-127, 255 -> the +inf bits.
-__device__ __forceinline__ float xe8m0(uint32_t b) { return __uint_as_float(max(b << 23, 0x400000u)); }
 
 // Block scales of a wave's rows go through a wave-private LDS window. A group of 4 steps needs
 // 64 scale bytes per row (blocks 64 G .. 64 G + 63); the wave's 32 rows (16 gate, 16 up) are
@@ -274,145 +218,11 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
   }
 }
 
-// ------------------------------------------------------------------------------------------------
-// gate/up for one token (every pair reads the same x): balanced over the whole chip. The work is
-// U = npairs * I/4 units, unit u = (pair u / (I/4), 4-row tile u % (I/4)) of gate and of up; wave i
-// of the grid takes units [i U / NW, (i+1) U / NW), so every CU streams the same number of bytes
-// (a workgroup per CU; per-pair grids leave a third of the CUs with twice the work at small pair
-// counts). A wave runs its units as one stream of (unit, step) iterations, XG1_D of them in flight
-// (2 chunks of 16 bytes per lane each), and keeps each unit's scale bytes (4 rows x K/32 bytes of
-// gate and of up) in a private LDS window loaded one unit ahead.
-// ------------------------------------------------------------------------------------------------
+// gate/up for one token: the balanced body (rbt_xmfma.h) over the whole grid.
 template <int NCH>
 __global__ __launch_bounds__(256) void k_xgateup1(const RbtExpertDev *__restrict__ jobs, int npairs,
                                                   const float *__restrict__ x, int I, __bf16 *__restrict__ hp) {
-  // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
-  // the first half of the next unit (slots and the unit epilogue are compile-time positions)
-  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024, SR = K >> 5, D = NCH / 2;
-  static_assert(NCH % 2 == 0, "even step count");
-  __shared__ __attribute__((aligned(16))) __bf16 xs[3 * stride];
-  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
-  __shared__ __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
-  const int rho = col >> 2, kap = col & 3;
-  const int tpp = I >> 2;  // 4-row tiles per pair
-  const long U = (long)npairs * tpp, NW = 4L * gridDim.x, wi = 4L * blockIdx.x + w;
-  const int u0 = (int)(wi * U / NW), u1 = (int)((wi + 1) * U / NW);
-  // activation: the token's three bf16 parts to LDS (every workgroup)
-  float4 xv[XV];
-  {
-    const rbt_gf4 *s4 = (const rbt_gf4 *)x;
-#pragma unroll
-    for (int j = 0; j < XV; j++) xv[j] = s4[threadIdx.x + 256 * j];
-  }
-  // the wave's units span at most two pairs (U / NW < I / 4)
-  const int pa = u0 / tpp, pb = min(pa + 1, npairs - 1);
-  const RbtExpertDev JA = jobs[pa], JB = jobs[pb];
-  const bool live = u1 > u0 && JA.gd != nullptr && JA.ud != nullptr && JB.gd != nullptr && JB.ud != nullptr;
-  // lane pointers of unit u (clamped to the wave's last unit): codes of gate / up at step 0, and the
-  // lane's scale piece (16 bytes of row (lane >> 4) & 3, clamped at the row end)
-  const int s_row = (lane >> 4) & 3, s_off = min(16 * (lane & 15), SR - 16);
-  struct UPtr {
-    const uint8_t *g, *u, *gs, *us;
-  };
-  auto uptr = [&](int u) {
-    u = min(u, u1 - 1);
-    const int pp = u / tpp;
-    const RbtExpertDev &J = pp == pa ? JA : JB;
-    const long row0 = 4L * (u - pp * tpp);
-    UPtr r;
-    r.g = J.gd + (row0 + rho) * (K >> 1) + 64 * kap + 16 * g;
-    r.u = J.ud + (row0 + rho) * (K >> 1) + 64 * kap + 16 * g;
-    r.gs = (const uint8_t *)J.gs + (row0 + s_row) * SR + s_off;
-    r.us = (const uint8_t *)J.us + (row0 + s_row) * SR + s_off;
-    return r;
-  };
-  rbt_u4 ring[D][2], sv[2];
-  UPtr cur{}, nxt{};
-  if (live) {
-    cur = uptr(u0);
-    nxt = uptr(u0 + 1);
-    sv[0] = *(const rbt_gu4 *)cur.gs;
-    sv[1] = *(const rbt_gu4 *)cur.us;
-#pragma unroll
-    for (int d = 0; d < D; d++) {
-      ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.g + 256 * d));
-      ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * d));
-    }
-  }
-  if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
-#pragma unroll
-  for (int j = 0; j < XV; j++) {
-    const int q = threadIdx.x + 256 * j;
-    const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      __bf16 hh, mm, ll;
-      split3(e4[e], hh, mm, ll);
-      xs[4 * q + e] = hh;
-      xs[stride + 4 * q + e] = mm;
-      xs[2 * stride + 4 * q + e] = ll;
-    }
-  }
-  auto sstore = [&](int buf) {
-    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][0][s_row][16 * (lane & 15)]) = sv[0];
-    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][1][s_row][16 * (lane & 15)]) = sv[1];
-  };
-  if (live) {
-    sstore(0);
-    sv[0] = *(const rbt_gu4 *)nxt.gs;  // scales of the next unit (the last unit's own, if none)
-    sv[1] = *(const rbt_gu4 *)nxt.us;
-  }
-  __syncthreads();
-  if (!live) {
-    // a missing expert is reported by the grouping (error flag); zero this wave's rows of h
-    for (int u = u0; u < u1; u++) {
-      const int pp = u / tpp;
-      if (lane < 12) hp[((long)pp * 3 + lane / 4) * I + 4L * (u - pp * tpp) + (lane & 3)] = (__bf16)0.0f;
-    }
-    return;
-  }
-  const int bq = col >> 2, bpart = col & 3;
-  const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
-                             : reinterpret_cast<const char *>(zb);
-  const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
-  for (int u = u0; u < u1; u++) {
-    const uint8_t(*win)[4][256] = sw[w][(u - u0) & 1];
-    xf4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-      const int d = c % D;
-      const XB B = xb_read(bp + binc * c);
-      const int sb = 16 * c + 4 * kap + g;
-      const rbt_u4 cg = ring[d][0], cu = ring[d][1];
-      // refill: step c + D of this unit, or step c - D of the next one
-      const uint8_t *rg = c < D ? cur.g + 256 * (c + D) : nxt.g + 256 * (c - D);
-      const uint8_t *ru = c < D ? cur.u + 256 * (c + D) : nxt.u + 256 * (c - D);
-      ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)rg);
-      ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)ru);
-      xmma_s(cg, xe8m0(win[0][rho][sb]), B, ag);
-      xmma_s(cu, xe8m0(win[1][rho][sb]), B, au);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    // unit done: h for its 4 rows
-    const float gv = row_dot(ag, col), uv = row_dot(au, col);
-    const int pp = u / tpp;
-    if (col == 0) {  // lane 16*g: row 4 t + g of the unit's pair
-      const float hv = rbt_silu(gv) * uv;
-      __bf16 hh, mm, ll;
-      split3(hv, hh, mm, ll);
-      const long rr = 4L * (u - pp * tpp) + g;
-      hp[((long)pp * 3 + 0) * I + rr] = hh;
-      hp[((long)pp * 3 + 1) * I + rr] = mm;
-      hp[((long)pp * 3 + 2) * I + rr] = ll;
-    }
-    // next unit's scales into the other window, then look one unit further ahead
-    sstore((u + 1 - u0) & 1);
-    cur = nxt;
-    nxt = uptr(u + 2);
-    sv[0] = *(const rbt_gu4 *)nxt.gs;
-    sv[1] = *(const rbt_gu4 *)nxt.us;
-  }
+  xgateup1_body<NCH>(jobs, npairs, x, I, hp, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -486,9 +296,12 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
   __syncthreads();
   const int tile_r0 = 16 * blockIdx.x + 4 * w;
   const long wrow = (long)(tile_r0 + rho) * (KD >> 1) + 64 * kap + 16 * g;  // lane's code offset in a matrix
-  // chunk (pair q, step c) of the lane (pairs past the end read the last pair again)
+  // chunk (pair q, step c) of the lane; past the last pair the loads read the cached activation
+  // parts instead (never used)
+  const uint8_t *dummy = reinterpret_cast<const uint8_t *>(hp) + 64 * kap + 16 * g;
   auto chunk = [&](int q, int c) {
-    return __builtin_nontemporal_load((const rbt_gu4 *)(pd[min(q, npairs - 1)] + wrow + 256 * c));
+    const uint8_t *a = q < npairs ? pd[min(q, npairs - 1)] + wrow : dummy;
+    return __builtin_nontemporal_load((const rbt_gu4 *)(a + 256 * c));
   };
   // scale window of pair group G (4 pairs): lane l holds pair 4G + l/16, row (l/4) % 4, bytes 16 (l % 4)
   const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
@@ -578,9 +391,9 @@ hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, c
   if (I % 4 != 0 || (long)npairs * (I / 4) < 4L * c.num_cu) return hipErrorInvalidValue;
   const dim3 grid(c.num_cu);
   if (K == 8192)
-    hipLaunchKernelGGL(k_xgateup1<16>, grid, dim3(256), 0, c.stream, jobs, npairs, x, I, hp);
+    launch_k(c, k_xgateup1<16>, grid, dim3(256), jobs, npairs, x, I, hp);
   else if (K == 7168)
-    hipLaunchKernelGGL(k_xgateup1<14>, grid, dim3(256), 0, c.stream, jobs, npairs, x, I, hp);
+    launch_k(c, k_xgateup1<14>, grid, dim3(256), jobs, npairs, x, I, hp);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -591,9 +404,9 @@ hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok
   if (npairs <= 0) return hipSuccess;
   const dim3 grid(I / 64, npairs);
   if (K == 8192)
-    hipLaunchKernelGGL(k_xgateup<16>, grid, dim3(256), 0, c.stream, jobs, tok, x, x_stride, I, hp);
+    launch_k(c, k_xgateup<16>, grid, dim3(256), jobs, tok, x, x_stride, I, hp);
   else if (K == 7168)
-    hipLaunchKernelGGL(k_xgateup<14>, grid, dim3(256), 0, c.stream, jobs, tok, x, x_stride, I, hp);
+    launch_k(c, k_xgateup<14>, grid, dim3(256), jobs, tok, x, x_stride, I, hp);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -603,7 +416,7 @@ hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, cons
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out) {
   if (npairs <= 0 || npairs > XD_MAXP || I != 2048 || S > 16) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_xdown<4>, dim3(H / 16), dim3(256), 0, c.stream, jobs, npairs, hp, I, H, S, k, tok, tok_pair,
+  launch_k(c, k_xdown<4>, dim3(H / 16), dim3(256), jobs, npairs, hp, I, H, S, k, tok, tok_pair,
                      tok_w, sh_scale, has_shared, gated, out);
   return hipGetLastError();
 }
