@@ -626,8 +626,11 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e2);
     if (c->prof) c->t_start = ev[4], c->t_stop = ev[5];
+    // one token: the balanced down (all pairs' h in LDS); batches: a grid of row blocks
     const hipError_t e3 =
-        rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out);
+        S == 1 && rbt::xdown1_ok(npairs, I)
+            ? rbt::launch_xdown1(*c, pjob, npairs, hp, I, H, k, tpair, tw, shs, D.has_shared, gated, out)
+            : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e3);
   } else {

@@ -71,6 +71,11 @@ hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok
 hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const float *x, int K, int I,
                            __bf16 *hp);
 // hp: h as three bf16 parts per pair, hp[(p*3 + part)*I + k].
+// One token: down + ordered combine balanced over num_cu workgroups, every pair's h in LDS.
+bool xdown1_ok(int npairs, size_t i);
+hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int k,
+                         const int *tok_pair, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+                         float *out);
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);

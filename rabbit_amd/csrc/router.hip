@@ -470,6 +470,7 @@ __device__ __forceinline__ bool ranks_before(float ka, int a, float kb, int b) {
 
 constexpr int SEL_MAXE = 2048;
 constexpr int SEL_MAXK = 64;
+constexpr int SEL_NC = 64;  // most candidates the fast selection ranks (one per lane)
 
 // Top-k over keys[] restricted to allowed (nullptr = all); writes out[0..k). One wave.
 __device__ void wave_topk(const float *keys, const unsigned char *allowed, int E, int k, int *out) {
@@ -1204,14 +1205,20 @@ __global__ __launch_bounds__(256) void k_router_select2(SelParams P, const doubl
 //  * Keys: expert e = lane + 64 m of wave 0 holds its key interval [klo, khi] (logit interval through
 //    the family's monotone key map) and the order-preserving bits of its midpoint key (0 = no
 //    expert, so no validity masks are needed in the hot loop).
-//  * Top-k: the k-th largest midpoint key by bisection over the 32 key bits, one compare and one
-//    ballot per key register per bit; ties at the threshold go to the lowest ids, as the
-//    reference's strict-> scans do (qwen38/moe.rs:48-58, glm52/moe.rs:170-186).
+//  * Top-k: the candidates are the keys at or above the kk-th largest of the 64 lane maxima (found
+//    by bisection over 32 key bits with one ballot per bit); at least kk keys reach it, so every
+//    winner is a candidate. The candidates (usually a few more than kk) are ranked by midpoint key
+//    desc, id asc, as the reference's strict-> scans order them (qwen38/moe.rs:48-58,
+//    glm52/moe.rs:170-186), and the first kk win. More than 64 candidates (many equal keys) fall
+//    back to a bisection for the kk-th largest key over all keys with the same tie rule.
 //  * Certification, in registers: the set is certain when every inexact winner's lower key is
 //    above every loser's upper key and every inexact loser's upper key is below every winner's lower
-//    key (wave min / max); the order is certain when adjacent winners (sorted by midpoint) have
-//    disjoint intervals. Intervals that fail are recomputed as the reference computes them
-//    (exact_logit_wave) and become points; the selection then repeats until nothing is ambiguous.
+//    key (wave min / max); the order is certain when every pair of winners has disjoint intervals
+//    or is a pair of exact values. Intervals that fail are recomputed as the reference computes
+//    them (exact_logit_wave) and become points; the selection then repeats until nothing is
+//    ambiguous (checking every pair makes one recomputation pass enough in practice).
+//  * The winners' job-table entries are loaded by their candidate lanes while the selection is
+//    certified and written in rank order at the end.
 // ------------------------------------------------------------------------------------------------
 __device__ __forceinline__ float wave_min_f(float v) {
 #pragma unroll
@@ -1239,6 +1246,9 @@ __device__ __forceinline__ void select3_body(const SelParams &P, const double *_
   __shared__ int amb[SEL_MAXE + 2 * SEL_MAXK];
   __shared__ float amb_val[SEL_MAXE + 2 * SEL_MAXK];
   __shared__ int namb;
+  __shared__ int q_id[SEL_NC];  // candidates (fast path)
+  __shared__ uint32_t q_ku[SEL_NC];
+  __shared__ float q_lo[SEL_NC], q_hi[SEL_NC], q_l[SEL_NC];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
   const double *ms = mid + (size_t)s * P.erows;
@@ -1277,78 +1287,177 @@ __device__ __forceinline__ void select3_body(const SelParams &P, const double *_
     }
   }
   int total_amb = 0;
+  // fast path state of the last pass: the lane's candidate, its rank and its job-table entry
+  bool fast = false;
+  int my_rank = -1, my_id = 0;
+  const uint8_t *pf_gd = nullptr, *pf_ud = nullptr, *pf_dd = nullptr;
+  const void *pf_gs = nullptr, *pf_us = nullptr, *pf_ds = nullptr;
   for (;;) {
     if (wave == 0) {
-      // k-th largest midpoint key
-      uint32_t T = 0;
+      // Candidates: the keys at or above M, the kk-th largest of the 64 lane maxima. The maxima of
+      // kk lanes reach M, so at least kk keys do and the kk winners are all candidates; usually
+      // only a few more than kk keys qualify.
+      uint32_t lmax = 0;
+#pragma unroll
+      for (int m = 0; m < MAXM; m++) lmax = max(lmax, ku[m]);
+      uint32_t M = 0;
 #pragma unroll 1
       for (int bit = 31; bit >= 0; bit--) {
-        const uint32_t cand = T | (1u << bit);
-        int cnt = 0;
-#pragma unroll
-        for (int m = 0; m < MAXM; m++) cnt += __popcll(__ballot(ku[m] >= cand));
-        T = cnt >= kk ? cand : T;
+        const uint32_t cand = M | (1u << bit);
+        M = __popcll(__ballot(lmax >= cand)) >= kk ? cand : M;
       }
-      int ngt = 0;
+      int nc = 0;
 #pragma unroll
-      for (int m = 0; m < MAXM; m++) ngt += __popcll(__ballot(ku[m] > T));
-      const int need = kk - ngt;
-      uint32_t win = 0;
-      int taken_eq = 0, base = 0;
-      float lo_sel = INFINITY, hi_uns = -INFINITY;
+      for (int m = 0; m < MAXM; m++) nc += __popcll(__ballot(ku[m] >= M));
+      fast = nc <= SEL_NC && M != 0;  // M = 0 only if some key maps to 0 (a NaN): bisection path
+      if (fast) {
+        uint32_t cm = 0;
+        int base = 0;
 #pragma unroll
-      for (int m = 0; m < MAXM; m++) {
-        const unsigned long long eq = __ballot(ku[m] == T);
-        const bool weq = ku[m] == T && (taken_eq + __popcll(eq & lanemask_lt())) < need;
-        taken_eq += __popcll(eq);
-        const bool w = ku[m] > T || weq;
-        const unsigned long long wm = __ballot(w);
-        if (w) {
-          const int at = base + __popcll(wm & lanemask_lt());
-          c_id[at] = lane + 64 * m;
-          c_ku[at] = ku[m];
-          c_lo[at] = klo[m];
-          c_hi[at] = khi[m];
-          c_l[at] = lmid[m];
-          win |= 1u << m;
-          lo_sel = fminf(lo_sel, klo[m]);
-        } else if (ku[m] != 0) {
-          hi_uns = fmaxf(hi_uns, khi[m]);
+        for (int m = 0; m < MAXM; m++) {
+          const bool c = ku[m] >= M;
+          const unsigned long long cb = __ballot(c);
+          if (c) {
+            const int at = base + __popcll(cb & lanemask_lt());
+            q_id[at] = lane + 64 * m;
+            q_ku[at] = ku[m];
+            q_lo[at] = klo[m];
+            q_hi[at] = khi[m];
+            q_l[at] = lmid[m];
+            cm |= 1u << m;
+          }
+          base += __popcll(cb);
         }
-        base += __popcll(wm);
-      }
-      lo_sel = wave_min_f(lo_sel);
-      hi_uns = wave_max_f(hi_uns);
-      if (lane == 0) namb = 0;
-      __builtin_amdgcn_wave_barrier();
-      // set membership: inexact experts on the wrong side of the other side's bound
+        float hi_out = -INFINITY;  // upper keys of the non-candidates (never winners)
 #pragma unroll
-      for (int m = 0; m < MAXM; m++) {
-        const bool inexact = ku[m] != 0 && klo[m] != khi[m];
-        const bool a = inexact && (((win >> m) & 1u) ? klo[m] <= hi_uns : khi[m] >= lo_sel);
-        if (a) amb[atomicAdd(&namb, 1)] = lane + 64 * m;
-      }
-      // order: rank the winners by midpoint (key desc, id asc), then check adjacent intervals
-      if (lane < kk) {
-        const uint32_t my = c_ku[lane];
-        const int id = c_id[lane];
-        int rank = 0;
-        for (int j = 0; j < kk; j++) {
-          const uint32_t o = c_ku[j];
-          rank += (o > my) || (o == my && c_id[j] < id);
+        for (int m = 0; m < MAXM; m++)
+          if (!((cm >> m) & 1u) && ku[m] != 0) hi_out = fmaxf(hi_out, khi[m]);
+        __builtin_amdgcn_wave_barrier();
+        // rank of candidate `lane` among the candidates: key desc, id asc
+        float clo = INFINITY, chi = -INFINITY, cl = 0.0f;
+        my_rank = -1;
+        if (lane < nc) {
+          const uint32_t my = q_ku[lane];
+          my_id = q_id[lane];
+          clo = q_lo[lane];
+          chi = q_hi[lane];
+          cl = q_l[lane];
+          int rank = 0;
+          for (int j = 0; j < nc; j++) {
+            const uint32_t o = q_ku[j];
+            rank += (o > my) || (o == my && q_id[j] < my_id);
+          }
+          my_rank = rank;
+          if (grp) {  // the job-table entry, in flight while the selection is certified
+            const RbtExpertDev *src = G.table + my_id;
+            pf_gd = src->gd;
+            pf_gs = src->gs;
+            pf_ud = src->ud;
+            pf_us = src->us;
+            pf_dd = src->dd;
+            pf_ds = src->ds;
+          }
         }
-        r_id[rank] = id;
-        r_l[rank] = c_l[lane];
-        r_lo[rank] = c_lo[lane];
-        r_hi[rank] = c_hi[lane];
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (lane + 1 < kk) {
-        const bool ea = r_lo[lane] == r_hi[lane], eb = r_lo[lane + 1] == r_hi[lane + 1];
-        if (!(r_lo[lane] > r_hi[lane + 1]) && !(ea && eb)) {
-          // a winner already counted for set membership may be added twice: harmless
-          if (!ea) amb[atomicAdd(&namb, 1)] = r_id[lane];
-          if (!eb) amb[atomicAdd(&namb, 1)] = r_id[lane + 1];
+        const bool iw = my_rank >= 0 && my_rank < kk;
+        const float lo_sel = wave_min_f(iw ? clo : INFINITY);
+        const float hi_uns = wave_max_f(fmaxf(hi_out, (lane < nc && !iw) ? chi : -INFINITY));
+        if (iw) {
+          r_id[my_rank] = my_id;
+          r_l[my_rank] = cl;
+          r_lo[my_rank] = clo;
+          r_hi[my_rank] = chi;
+        }
+        if (lane == 0) namb = 0;
+        __builtin_amdgcn_wave_barrier();
+        // set membership: inexact experts on the wrong side of the other side's bound
+#pragma unroll
+        for (int m = 0; m < MAXM; m++)
+          if (!((cm >> m) & 1u) && ku[m] != 0 && klo[m] != khi[m] && khi[m] >= lo_sel)
+            amb[atomicAdd(&namb, 1)] = lane + 64 * m;
+        const bool cexact = clo == chi;
+        bool amb_me = lane < nc && !cexact && (iw ? clo <= hi_uns : chi >= lo_sel);
+        // order: every pair of winners must be strictly ordered or an exact tie-broken pair (checking
+        // all pairs, not only neighbours, keeps one recomputation pass enough)
+        if (iw && !cexact) {
+          for (int q = 0; q < kk; q++) {
+            const float ql = r_lo[q], qh = r_hi[q];
+            const bool sure = q < my_rank ? ql > chi : (q > my_rank ? clo > qh : true);
+            amb_me |= !sure;
+          }
+        }
+        if (amb_me) amb[atomicAdd(&namb, 1)] = my_id;
+      } else {
+        // k-th largest midpoint key
+        uint32_t T = 0;
+  #pragma unroll 1
+        for (int bit = 31; bit >= 0; bit--) {
+          const uint32_t cand = T | (1u << bit);
+          int cnt = 0;
+#pragma unroll
+          for (int m = 0; m < MAXM; m++) cnt += __popcll(__ballot(ku[m] >= cand));
+          T = cnt >= kk ? cand : T;
+        }
+        int ngt = 0;
+#pragma unroll
+        for (int m = 0; m < MAXM; m++) ngt += __popcll(__ballot(ku[m] > T));
+        const int need = kk - ngt;
+        uint32_t win = 0;
+        int taken_eq = 0, base = 0;
+        float lo_sel = INFINITY, hi_uns = -INFINITY;
+#pragma unroll
+        for (int m = 0; m < MAXM; m++) {
+          const unsigned long long eq = __ballot(ku[m] == T);
+          const bool weq = ku[m] == T && (taken_eq + __popcll(eq & lanemask_lt())) < need;
+          taken_eq += __popcll(eq);
+          const bool w = ku[m] > T || weq;
+          const unsigned long long wm = __ballot(w);
+          if (w) {
+            const int at = base + __popcll(wm & lanemask_lt());
+            c_id[at] = lane + 64 * m;
+            c_ku[at] = ku[m];
+            c_lo[at] = klo[m];
+            c_hi[at] = khi[m];
+            c_l[at] = lmid[m];
+            win |= 1u << m;
+            lo_sel = fminf(lo_sel, klo[m]);
+          } else if (ku[m] != 0) {
+            hi_uns = fmaxf(hi_uns, khi[m]);
+          }
+          base += __popcll(wm);
+        }
+        lo_sel = wave_min_f(lo_sel);
+        hi_uns = wave_max_f(hi_uns);
+        if (lane == 0) namb = 0;
+        __builtin_amdgcn_wave_barrier();
+        // set membership: inexact experts on the wrong side of the other side's bound
+#pragma unroll
+        for (int m = 0; m < MAXM; m++) {
+          const bool inexact = ku[m] != 0 && klo[m] != khi[m];
+          const bool a = inexact && (((win >> m) & 1u) ? klo[m] <= hi_uns : khi[m] >= lo_sel);
+          if (a) amb[atomicAdd(&namb, 1)] = lane + 64 * m;
+        }
+        // order: rank the winners by midpoint (key desc, id asc), then check adjacent intervals
+        if (lane < kk) {
+          const uint32_t my = c_ku[lane];
+          const int id = c_id[lane];
+          int rank = 0;
+          for (int j = 0; j < kk; j++) {
+            const uint32_t o = c_ku[j];
+            rank += (o > my) || (o == my && c_id[j] < id);
+          }
+          r_id[rank] = id;
+          r_l[rank] = c_l[lane];
+          r_lo[rank] = c_lo[lane];
+          r_hi[rank] = c_hi[lane];
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane + 1 < kk) {
+          const bool ea = r_lo[lane] == r_hi[lane], eb = r_lo[lane + 1] == r_hi[lane + 1];
+          if (!(r_lo[lane] > r_hi[lane + 1]) && !(ea && eb)) {
+            // a winner already counted for set membership may be added twice: harmless
+            if (!ea) amb[atomicAdd(&namb, 1)] = r_id[lane];
+            if (!eb) amb[atomicAdd(&namb, 1)] = r_id[lane + 1];
+          }
         }
       }
     }
@@ -1418,23 +1527,36 @@ __device__ __forceinline__ void select3_body(const SelParams &P, const double *_
     if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
     if (grp) {
       // single token: pair j = slot j; the shared expert is pair k
+      if (fast && my_rank >= 0 && my_rank < kk) {
+        // winners of the fast path: the entries their candidate lanes loaded during certification
+        RbtExpertDev *dst = G.pair_job + my_rank;
+        if (pf_gd == nullptr || pf_dd == nullptr) atomicOr(G.err, 1);
+        dst->gd = pf_gd;
+        dst->gs = pf_gs;
+        dst->ud = pf_ud;
+        dst->us = pf_us;
+        dst->dd = pf_dd;
+        dst->ds = pf_ds;
+      }
       for (int r = lane; r <= k; r += 64) {
         if (r < k) {
-          // field copies (a struct temporary here ends up in scratch memory)
-          const RbtExpertDev *src = G.table + (r < kk ? r_id[r] : 0);
-          RbtExpertDev *dst = G.pair_job + r;
-          const bool use = r < kk;
-          const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
-          const uint8_t *dd = use ? src->dd : nullptr;
-          const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
-          const void *ds = use ? src->ds : nullptr;
-          if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
-          dst->gd = gd;
-          dst->gs = gs;
-          dst->ud = ud;
-          dst->us = us;
-          dst->dd = dd;
-          dst->ds = ds;
+          if (!fast || r >= kk) {
+            // field copies (a struct temporary here ends up in scratch memory)
+            const RbtExpertDev *src = G.table + (r < kk ? r_id[r] : 0);
+            RbtExpertDev *dst = G.pair_job + r;
+            const bool use = r < kk;
+            const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
+            const uint8_t *dd = use ? src->dd : nullptr;
+            const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
+            const void *ds = use ? src->ds : nullptr;
+            if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
+            dst->gd = gd;
+            dst->gs = gs;
+            dst->ud = ud;
+            dst->us = us;
+            dst->dd = dd;
+            dst->ds = ds;
+          }
           G.pair_tok[r] = 0;
           G.tok_pair[r] = r < kk ? r : -1;
           G.tok_w[r] = r < kk ? s_w[r] : 0.0f;

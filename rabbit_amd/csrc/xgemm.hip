@@ -377,6 +377,177 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
   if (t < S) out[(long)t * H + 16 * blockIdx.x + rr] = oacc[t][rr];
 }
 
+// ------------------------------------------------------------------------------------------------
+// down + combine for one token, balanced over the whole chip: one workgroup of XD1_NW waves per CU.
+// Workgroup b owns the 4-row output tiles [T0, T1) (an equal share of H/4) and the units
+// (tile, pair) over them, u = tile * npairs + pair, dealt evenly over its waves. Every pair's h
+// parts are staged in LDS once (no per-pair barriers); a wave streams its units' 16-byte code chunks
+// with four units (16 chunks) in flight, block scales for four units at a time through a
+// wave-private LDS window (one 16-byte load per lane), and leaves each unit's four row sums in LDS.
+// The ordered combine then runs per output row, in pair order with the shared pair last:
+//   out[r] = (...(w_0 y_0[r] + w_1 y_1[r]) + ...) + w_s y_s[r]   (separate roundings)
+// the same order as the grid-per-row-block kernel above.
+// ------------------------------------------------------------------------------------------------
+constexpr int XD1_NP = 11;   // pairs whose h fits in LDS (top-10 + shared at I = 2048)
+constexpr int XD1_NW = 8;    // waves per workgroup
+constexpr int XD1_TPW = 16;  // most 4-row tiles per workgroup
+
+// Barrier for LDS hand-offs only: global loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <int NCH>
+__global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__restrict__ jobs, int npairs,
+                                                        const __bf16 *__restrict__ hp, int H, int k,
+                                                        const int *__restrict__ tok_pair,
+                                                        const float *__restrict__ tok_w,
+                                                        const float *__restrict__ sh_scale, int has_shared,
+                                                        int gated, float *__restrict__ out) {
+  constexpr int KD = NCH * 512, stride = KD + XG_PAD, SRD = KD >> 5;
+  constexpr int PPP = 3 * KD / 8;                                  // 16-byte pieces of one pair's parts
+  constexpr int HI = (XD1_NP * PPP + 64 * XD1_NW - 1) / (64 * XD1_NW);  // pieces per thread
+  static_assert(NCH == 4 && SRD == 64, "a unit is 4 rows x 4 chunks with 64 scale bytes per row");
+  __shared__ __attribute__((aligned(16))) __bf16 hs[XD1_NP][3 * stride];
+  __shared__ __attribute__((aligned(16))) uint8_t sw[XD1_NW][2][4][4][64];  // [wave][buffer][unit][row][byte]
+  __shared__ float yb[XD1_TPW][XD1_NP][4];  // row sums per (tile, pair)
+  __shared__ float pw[XD1_NP];
+  __shared__ const uint8_t *pd[XD1_NP];
+  __shared__ const uint8_t *ps[XD1_NP];
+  __shared__ int plive[XD1_NP], padd[XD1_NP];
+  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rho = col >> 2, kap = col & 3;
+  const int ntile = H >> 2;
+  const int T0 = (int)((long)blockIdx.x * ntile / gridDim.x), T1 = (int)((long)(blockIdx.x + 1) * ntile / gridDim.x);
+  const int nt = T1 - T0;
+  if (tid < 32) zb[tid] = (__bf16)0.0f;
+  if (tid < npairs) {
+    const int pp = tid;
+    float wv = 0.0f;
+    if (pp < k) {
+      for (int j = 0; j < k; j++)
+        if (tok_pair[j] == pp) wv = tok_w[j];
+    } else {
+      wv = gated ? sh_scale[0] : 1.0f;
+    }
+    const RbtExpertDev J = jobs[pp];
+    const int live = J.dd != nullptr && J.ds != nullptr;
+    plive[pp] = live;
+    padd[pp] = live && (pp < k || has_shared);
+    pd[pp] = J.dd;
+    ps[pp] = (const uint8_t *)J.ds;
+    pw[pp] = wv;
+  }
+  // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside hp)
+  const int npc = npairs * PPP;
+  rbt_u4 hr[HI];
+#pragma unroll
+  for (int i = 0; i < HI; i++) hr[i] = *(const rbt_gu4 *)(hp + 8L * min(tid + 64 * XD1_NW * i, npc - 1));
+  lds_barrier();  // tables
+  const int NU = nt * npairs;
+  const int u0 = w * NU / XD1_NW, u1 = (w + 1) * NU / XD1_NW;
+  const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
+  const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
+  // lane pointer of unit u (chunk 0); past the wave's units or for a null job: cached dummy bytes
+  auto uptr = [&](int u) -> const uint8_t * {
+    if (u >= u1) return dummy;
+    const int tl = u / npairs, pp = u - tl * npairs;
+    return plive[pp] ? pd[pp] + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
+  };
+  // scale window of units ub .. ub+3: lane l holds unit ub + l/16, row (l/4) % 4, bytes 16 (l % 4)
+  const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
+  auto sload = [&](int ub) {
+    const int u = ub + s_q;
+    const uint8_t *p = hb8 + 16 * s_seg;
+    if (u < u1) {
+      const int tl = u / npairs, pp = u - tl * npairs;
+      if (plive[pp]) p = ps[pp] + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
+    }
+    return *(const rbt_gu4 *)p;
+  };
+  auto sstore = [&](int buf, const rbt_u4 &v) {
+    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][s_q][s_row][16 * s_seg]) = v;
+  };
+  rbt_u4 sv = sload(u0);
+  rbt_u4 ring[4][NCH];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint8_t *p = uptr(u0 + j);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(p + 256 * c));
+  }
+#pragma unroll
+  for (int i = 0; i < HI; i++) {
+    const int e = tid + 64 * XD1_NW * i;
+    if (e < npc) {
+      const int pp = e / PPP, q = e - pp * PPP;
+      *reinterpret_cast<rbt_u4 *>(&hs[pp][(q / (KD / 8)) * stride + 8 * (q % (KD / 8))]) = hr[i];
+    }
+  }
+  sstore(0, sv);
+  sv = sload(u0 + 4);
+  lds_barrier();  // h parts
+  const int bq = col >> 2, bpart = col & 3;
+  const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
+  const int binc = bpart < 3 ? 1024 : 0;
+  int buf = 0;
+  for (int ub = u0; ub < u1; ub += 4) {
+    const uint8_t(*win)[4][64] = sw[w][buf];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int u = ub + j;
+      const uint8_t *np = uptr(u + 4);
+      rbt_u4 cw[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; c++) {
+        cw[c] = ring[j][c];
+        ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(np + 256 * c));
+      }
+      if (u < u1) {
+        const int tl = u / npairs, pp = u - tl * npairs;
+        const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[pp]) + boff : reinterpret_cast<const char *>(zb);
+        xf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+          const XB B = xb_read(bp + binc * c);
+          xmma_s(cw[c], xe8m0(win[j][rho][16 * c + 4 * kap + g]), B, acc);
+        }
+        const float y = row_dot(acc, col);
+        if (col == 0) yb[tl][pp][g] = y;  // lane 16 g: row 4 (T0 + tl) + g
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    buf ^= 1;
+    sstore(buf, sv);
+    sv = sload(ub + 8);
+  }
+  __syncthreads();
+  if (tid < 4 * nt) {
+    const int tl = tid >> 2, r = tid & 3;
+    float o = 0.0f;
+    for (int pp = 0; pp < npairs; pp++)
+      if (padd[pp]) o = __fadd_rn(o, __fmul_rn(pw[pp], yb[tl][pp][r]));
+    out[4 * (T0 + tl) + r] = o;
+  }
+}
+
+bool xdown1_ok(int npairs, size_t i) { return i == 2048 && npairs >= 1 && npairs <= XD1_NP; }
+
+hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int k,
+                         const int *tok_pair, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+                         float *out) {
+  const int grid = c.num_cu;
+  if (!xdown1_ok(npairs, I) || H % 4 != 0 || grid <= 0 || (H / 4 + grid - 1) / grid > XD1_TPW)
+    return hipErrorInvalidValue;
+  launch_k(c, k_xdown1<4>, dim3(grid), dim3(64 * XD1_NW), jobs, npairs, hp, H, k, tok_pair, tok_w, sh_scale,
+           has_shared, gated, out);
+  return hipGetLastError();
+}
+
 bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared) {
   if (kind != RBT_QT_MXFP4) return false;
   if ((d != 8192 && d != 7168) || i % 64 != 0) return false;  // gate/up: K = 512 * NCH

@@ -92,9 +92,11 @@ def _full_config(ctx, name, ntok, seed=1000):
     return cfg, host, x, out.cpu().numpy(), ids.cpu().numpy().reshape(ntok, k), w.cpu().numpy().reshape(ntok, k)
 
 
-@pytest.mark.parametrize("name,ntok", [("c1", 2), ("c2", 2), ("c3", 8)])
+@pytest.mark.parametrize("name,ntok", [("c0", 1), ("c1", 1), ("c1", 2), ("c2", 1), ("c2", 2), ("c3", 1), ("c3", 8)])
 def test_moe_forward_full_config(ctx, orc, name, ntok):
-    """The benchmark configurations at full size (every routed expert resident in HBM)."""
+    """The benchmark configurations at full size (every routed expert resident in HBM). One token
+    takes the decode kernels (chip-balanced gate/up and down, the shared expert's gate/up inside
+    the selection launch); several take the per-pair kernels."""
     cfg, host, x, out, ids, w = _full_config(ctx, name, ntok)
     exp, eids, ew = host.forward(x)
     assert np.array_equal(ids, eids)
