@@ -46,6 +46,7 @@ enum ScratchSlot {
   SC_XB,
   SC_PGRP,
   SC_RLOG,
+  SC_RREC,
   SC_N
 };
 
@@ -80,6 +81,7 @@ struct rbt_ctx : rbt::Ctx {
   std::map<uint32_t, Layer> layers;
   int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts
   int h_flags[8] = {};
+  unsigned *d_sync = nullptr;  // device: epoch and flags of the one-launch router
   // profiling: one row of 5 events per recorded moe_forward_d call
   bool prof = false;
   std::vector<hipEvent_t> ev_free;
@@ -90,7 +92,7 @@ struct rbt_ctx : rbt::Ctx {
 
 namespace {
 
-constexpr int FLAG_ERR = 0, FLAG_AMB = 1, FLAG_UNIQ = 2, FLAG_NR = 3, FLAG_N = 8;
+constexpr int FLAG_ERR = 0, FLAG_AMB = 1, FLAG_UNIQ = 2, FLAG_NR = 3, FLAG_SYNC = 4, FLAG_N = 8;
 
 int fail(rbt_ctx *c, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(rbt_ctx *c, int code, const char *fmt, ...) {
@@ -217,6 +219,12 @@ void slot_dims(const rbt_expert_slot *s, size_t *d, size_t *i) {
 int sync_and_check(rbt_ctx *c) {
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
+  if (c->h_flags[FLAG_SYNC]) {
+    // a cross-workgroup wait timed out: clear its flag and the sync area for the next call
+    HIP_OK(c, hipMemset(c->d_flags + FLAG_SYNC, 0, sizeof(int)));
+    HIP_OK(c, hipMemset(c->d_sync, 0, rbt::router1_sync_bytes()));
+    return fail(c, RBT_E_HIP, "a cross-workgroup wait on the device timed out");
+  }
   if (c->h_flags[FLAG_ERR]) {
     HIP_OK(c, hipMemset(c->d_flags, 0, sizeof(int)));
     return fail(c, RBT_E_NOT_RESIDENT, "a routed expert is not resident in the pool");
@@ -575,15 +583,6 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
       if (!e) return fail(c, RBT_E_HIP, "hipEventCreate failed");
     HIP_OK(c, hipEventRecord(ev[0], c->stream));
   }
-  if (rbt::router_exact_ok(S, H) && (uintptr_t)x % 16 == 0) {
-    // batches: the reference's sequential fp32 logits themselves, then point intervals
-    float *lg;
-    RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * erows, &lg));
-    HIP_OK(c, rbt::launch_router_logits_exact(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, lg));
-    HIP_OK(c, rbt::launch_logits_to_mid(*c, lg, (size_t)S * erows, mid, bnd));
-  } else {
-    HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, gated ? D.shared_gate : nullptr, mid, bnd));
-  }
   rbt::RouterArgs ra{D.family, E,          erows,          k,     H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
   // one token: the selection kernel writes the job table itself; several: k_group afterwards
@@ -596,12 +595,32 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool mfma = (merge || !D.has_shared) && rbt::xgemm_ok(L.routed_kind, H, I, S, k, D.has_shared) &&
                     ((uintptr_t)x % 16 == 0);
   // One token: the balanced gate/up covers the routed pairs, and the shared expert's gate/up runs in
-  // the selection launch (it does not depend on the routing).
+  // the router launch (it does not depend on the routing).
   const bool gu1 = mfma && S == 1 && (long)k * (I / 4) >= 4L * c->num_cu;
   const bool sh_in_select = gu1 && D.has_shared && grp_in_select;
   rbt::SharedGateUp sgu{L.d_shared, x, H, I, reinterpret_cast<__bf16 *>(h) + (size_t)k * 3 * I};
-  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
-                                      grp_in_select ? &ga : nullptr, sh_in_select ? &sgu : nullptr));
+  const float *sgate = gated ? D.shared_gate : nullptr;
+  const bool r1 = grp_in_select && rbt::router1_ok(ra, c->num_cu, sh_in_select ? &sgu : nullptr) &&
+                  (uintptr_t)(sgate ? sgate : x) % 16 == 0;
+  if (r1) {
+    // one token: logits, selection and the shared expert's gate/up in one launch
+    float *rec;
+    RBT_TRY(scratch_t(c, SC_RREC, (size_t)E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
+    HIP_OK(c, rbt::launch_router1(*c, ra, sgate, mid, bnd, ids, wts, shs, dflags + FLAG_AMB, &ga,
+                                  sh_in_select ? &sgu : nullptr, c->d_sync, dflags + FLAG_SYNC, rec));
+  } else {
+    if (rbt::router_exact_ok(S, H) && (uintptr_t)x % 16 == 0) {
+      // batches: the reference's sequential fp32 logits themselves, then point intervals
+      float *lg;
+      RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * erows, &lg));
+      HIP_OK(c, rbt::launch_router_logits_exact(*c, x, S, H, D.router, E, sgate, lg));
+      HIP_OK(c, rbt::launch_logits_to_mid(*c, lg, (size_t)S * erows, mid, bnd));
+    } else {
+      HIP_OK(c, rbt::launch_router_logits(*c, x, S, H, D.router, E, sgate, mid, bnd));
+    }
+    HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
+                                        grp_in_select ? &ga : nullptr, sh_in_select ? &sgu : nullptr));
+  }
   // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores.
   const bool grouped = !mfma && S > 1 && (merge || !D.has_shared) &&
                        rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
@@ -743,8 +762,12 @@ int rbt_init(rbt_ctx **out, int device) {
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) what = "hipStreamCreateWithFlags";
   else if ((e = hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMalloc";
   else if ((e = hipMemset(c->d_flags, 0, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMemset";
+  else if ((e = hipMalloc((void **)&c->d_sync, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMalloc";
+  else if ((e = hipMemset(c->d_sync, 0, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMemset";
   if (what) {
     int rc = init_fail(RBT_E_HIP, what, e);
+    if (c->d_sync) (void)hipFree(c->d_sync);
+    if (c->d_flags) (void)hipFree(c->d_flags);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
     return rc;
@@ -763,6 +786,7 @@ void rbt_destroy(rbt_ctx *c) {
   for (int i = 0; i < SC_N; i++)
     if (c->scratch[i]) (void)hipFree(c->scratch[i]);
   if (c->d_flags) (void)hipFree(c->d_flags);
+  if (c->d_sync) (void)hipFree(c->d_sync);
   for (auto &r : c->ev_rows)
     for (auto e : r) c->ev_free.push_back(e);
   for (auto e : c->ev_free) (void)hipEventDestroy(e);

@@ -73,6 +73,76 @@ __device__ __forceinline__ double rbt_wave_sum_d(double v) {
   return v;
 }
 
+// fp64 DPP move (both halves) with 0.0 in lanes whose source is outside the row or masked.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ double rbt_dpp0_d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, ROW_MASK, BANK_MASK, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, ROW_MASK, BANK_MASK, false);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+// Inclusive wave scan (sum) with DPP: row_shr 1, 2, 4, 8 scan each row of 16 lanes, then
+// row_bcast:15 adds row 0's total into row 1 (and row 2's into row 3) and row_bcast:31 adds
+// rows 0-1 into rows 2-3. No LDS traffic (cross-lane shuffles go through it).
+__device__ __forceinline__ double rbt_wave_scan_d(double v) {
+  v += rbt_dpp0_d<0x111, 0xf, 0xf>(v);
+  v += rbt_dpp0_d<0x112, 0xf, 0xf>(v);
+  v += rbt_dpp0_d<0x114, 0xf, 0xf>(v);
+  v += rbt_dpp0_d<0x118, 0xf, 0xf>(v);
+  v += rbt_dpp0_d<0x142, 0xa, 0xf>(v);
+  v += rbt_dpp0_d<0x143, 0xc, 0xf>(v);
+  return v;
+}
+
+// 32-bit DPP moves with a given fill for lanes whose source is outside the row or masked.
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ uint32_t rbt_dpp_u(uint32_t fill, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+template <int CTRL, int ROW_MASK, int BANK_MASK>
+__device__ __forceinline__ float rbt_dpp_f(float fill, float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), CTRL, ROW_MASK, BANK_MASK, false));
+}
+
+// Wave maximum / minimum over the DPP scan pattern (as rbt_wave_scan_d); every lane gets the result.
+__device__ __forceinline__ uint32_t rbt_wave_max_u(uint32_t v) {
+  v = max(v, rbt_dpp_u<0x111, 0xf, 0xf>(0u, v));
+  v = max(v, rbt_dpp_u<0x112, 0xf, 0xf>(0u, v));
+  v = max(v, rbt_dpp_u<0x114, 0xf, 0xf>(0u, v));
+  v = max(v, rbt_dpp_u<0x118, 0xf, 0xf>(0u, v));
+  v = max(v, rbt_dpp_u<0x142, 0xa, 0xf>(0u, v));
+  v = max(v, rbt_dpp_u<0x143, 0xc, 0xf>(0u, v));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+__device__ __forceinline__ float rbt_wave_min_f(float v) {
+  v = fminf(v, rbt_dpp_f<0x111, 0xf, 0xf>(INFINITY, v));
+  v = fminf(v, rbt_dpp_f<0x112, 0xf, 0xf>(INFINITY, v));
+  v = fminf(v, rbt_dpp_f<0x114, 0xf, 0xf>(INFINITY, v));
+  v = fminf(v, rbt_dpp_f<0x118, 0xf, 0xf>(INFINITY, v));
+  v = fminf(v, rbt_dpp_f<0x142, 0xa, 0xf>(INFINITY, v));
+  v = fminf(v, rbt_dpp_f<0x143, 0xc, 0xf>(INFINITY, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float rbt_wave_max_f(float v) {
+  v = fmaxf(v, rbt_dpp_f<0x111, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, rbt_dpp_f<0x112, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, rbt_dpp_f<0x114, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, rbt_dpp_f<0x118, 0xf, 0xf>(-INFINITY, v));
+  v = fmaxf(v, rbt_dpp_f<0x142, 0xa, 0xf>(-INFINITY, v));
+  v = fmaxf(v, rbt_dpp_f<0x143, 0xc, 0xf>(-INFINITY, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Wave total through the DPP scan (the value of lane 63, in every lane).
+__device__ __forceinline__ double rbt_wave_total_d(double v) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(rbt_wave_scan_d(v));
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, 63);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), 63);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // Device view of one expert: gate/up/down as separate (data, scale) pointers. A fused gate_up
 // tensor is presented as two views into the same allocation.
 struct RbtExpertDev {

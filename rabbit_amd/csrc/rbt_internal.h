@@ -133,6 +133,18 @@ struct SharedGateUp {
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr,
                                 const SharedGateUp *sgu = nullptr);
+// One token: logits, selection and the shared expert's gate/up in one launch (num_cu workgroups; rec
+// holds E * ROUTER1_REC_BYTES of scratch
+// that synchronise through `sync`, router1_sync_bytes() of device memory that must hold zeros
+// before the first call and is left consistent by every normal call; a wait that times out sets
+// *err, and the caller must zero `sync` again before the next call).
+size_t router1_sync_bytes();
+bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
+hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
+                          int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs *grp,
+                          const SharedGateUp *sgu, unsigned *sync, int *err, void *rec);
+// Device bytes of the key records launch_router1 writes (per router row).
+constexpr size_t ROUTER1_REC_BYTES = 16;
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);
 hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,

@@ -82,17 +82,25 @@ __device__ __forceinline__ float row_dot(const xf4 &acc, int col) {
 // ------------------------------------------------------------------------------------------------
 // Workgroup wg of nwg (the caller's grid, or its part of one) runs the body; hp points at pair 0's
 // output parts.
+// LDS of the one-token gate/up (sized for K = 8192).
+struct GuLds {
+  __attribute__((aligned(16))) __bf16 xs[3 * (8192 + XG_PAD)];
+  __attribute__((aligned(16))) __bf16 zb[32];
+  __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
+};
+
 template <int NCH>
-__device__ __forceinline__ void xgateup1_body(const RbtExpertDev *__restrict__ jobs, int npairs,
+__device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
                                               const float *__restrict__ x, int I, __bf16 *__restrict__ hp, int wg,
                                               int nwg) {
   // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
   // the first half of the next unit (slots and the unit epilogue are compile-time positions)
   constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024, SR = K >> 5, D = NCH / 2;
   static_assert(NCH % 2 == 0, "even step count");
-  __shared__ __attribute__((aligned(16))) __bf16 xs[3 * stride];
-  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
-  __shared__ __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
+  static_assert(K <= 8192, "GuLds holds K <= 8192");
+  __bf16 *xs = L.xs;
+  __bf16 *zb = L.zb;
+  uint8_t(&sw)[4][2][2][4][256] = L.sw;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15;
   const int rho = col >> 2, kap = col & 3;
   const int tpp = I >> 2;  // 4-row tiles per pair

@@ -1231,24 +1231,72 @@ __device__ __forceinline__ float wave_max_f(float v) {
   return v;
 }
 
+// LDS of the selection (one token per workgroup).
+struct SelLds {
+  int c_id[SEL_MAXK];  // winners in id order (bisection path)
+  uint32_t c_ku[SEL_MAXK];
+  float c_lo[SEL_MAXK], c_hi[SEL_MAXK], c_l[SEL_MAXK];
+  int r_id[SEL_MAXK];  // winners in rank order
+  float r_l[SEL_MAXK], r_lo[SEL_MAXK], r_hi[SEL_MAXK];
+  float s_w[SEL_MAXK];
+  // every expert once for set membership, plus at most two per adjacent winner pair for order
+  int amb[SEL_MAXE + 2 * SEL_MAXK];
+  float amb_val[SEL_MAXE + 2 * SEL_MAXK];
+  int namb;
+  int q_id[SEL_NC];  // candidates (fast path)
+  uint32_t q_ku[SEL_NC];
+  float q_lo[SEL_NC], q_hi[SEL_NC], q_l[SEL_NC];
+};
+
+// Routing weights of the kk winners (L.r_id, L.r_l in rank order) into L.s_w, by wave 0: computed
+// by the lanes in parallel, the sums in rank order.
+__device__ __forceinline__ void winner_weights(SelLds &L, const SelParams &P, int kk) {
+  const int lane = threadIdx.x & 63;
+  float lv = 0.0f;
+  if (lane < kk) {
+    const int e = L.r_id[lane];
+    lv = P.logit_bias ? __fadd_rn(L.r_l[lane], P.logit_bias[e]) : L.r_l[lane];
+  }
+  if (P.family == RBT_FAMILY_QWEN38) {
+    // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
+    const float mx = __shfl(lv, 0, 64);
+    if (lane < kk) L.s_w[lane] = (float)exp((double)__fsub_rn(lv, mx));
+    __builtin_amdgcn_wave_barrier();
+    float sum = 0.0f;
+    for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, L.s_w[r]);
+    if (lane < kk) L.s_w[lane] = __fdiv_rn(L.s_w[lane], sum);
+  } else {
+    // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
+    if (lane < kk) L.s_w[lane] = sigmoid_ref(lv);
+    __builtin_amdgcn_wave_barrier();
+    if (P.norm_topk) {
+      float sum = -0.0f;
+      for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, L.s_w[r]);
+      sum = __fadd_rn(sum, 1e-20f);
+      if (lane < kk) L.s_w[lane] = __fdiv_rn(L.s_w[lane], sum);
+    }
+    if (lane < kk) L.s_w[lane] = __fmul_rn(L.s_w[lane], P.routed_scale);
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
 template <int MAXM>
-__device__ __forceinline__ void select3_body(const SelParams &P, const double *__restrict__ mid,
+__device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, const double *__restrict__ mid,
                                              const double *__restrict__ bnd, int32_t *__restrict__ ids,
                                              float *__restrict__ wts, float *__restrict__ sh_scale,
                                              int *__restrict__ stats, const GroupOut &G, int grp, int s) {
-  __shared__ int c_id[SEL_MAXK];  // winners in id order
-  __shared__ uint32_t c_ku[SEL_MAXK];
-  __shared__ float c_lo[SEL_MAXK], c_hi[SEL_MAXK], c_l[SEL_MAXK];
-  __shared__ int r_id[SEL_MAXK];  // winners in rank order
-  __shared__ float r_l[SEL_MAXK], r_lo[SEL_MAXK], r_hi[SEL_MAXK];
-  __shared__ float s_w[SEL_MAXK];
-  // every expert once for set membership, plus at most two per adjacent winner pair for order
-  __shared__ int amb[SEL_MAXE + 2 * SEL_MAXK];
-  __shared__ float amb_val[SEL_MAXE + 2 * SEL_MAXK];
-  __shared__ int namb;
-  __shared__ int q_id[SEL_NC];  // candidates (fast path)
-  __shared__ uint32_t q_ku[SEL_NC];
-  __shared__ float q_lo[SEL_NC], q_hi[SEL_NC], q_l[SEL_NC];
+  int(&c_id)[SEL_MAXK] = L.c_id;
+  uint32_t(&c_ku)[SEL_MAXK] = L.c_ku;
+  float(&c_lo)[SEL_MAXK] = L.c_lo, (&c_hi)[SEL_MAXK] = L.c_hi, (&c_l)[SEL_MAXK] = L.c_l;
+  int(&r_id)[SEL_MAXK] = L.r_id;
+  float(&r_l)[SEL_MAXK] = L.r_l, (&r_lo)[SEL_MAXK] = L.r_lo, (&r_hi)[SEL_MAXK] = L.r_hi;
+  float(&s_w)[SEL_MAXK] = L.s_w;
+  int(&amb)[SEL_MAXE + 2 * SEL_MAXK] = L.amb;
+  float(&amb_val)[SEL_MAXE + 2 * SEL_MAXK] = L.amb_val;
+  int &namb = L.namb;
+  int(&q_id)[SEL_NC] = L.q_id;
+  uint32_t(&q_ku)[SEL_NC] = L.q_ku;
+  float(&q_lo)[SEL_NC] = L.q_lo, (&q_hi)[SEL_NC] = L.q_hi, (&q_l)[SEL_NC] = L.q_l;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
   const double *ms = mid + (size_t)s * P.erows;
@@ -1491,33 +1539,7 @@ __device__ __forceinline__ void select3_body(const SelParams &P, const double *_
   }
   if (wave == 0) {
     if (lane == 0 && stats && total_amb) atomicAdd(stats, total_amb);
-    // weights, computed by the lanes in parallel; the sums run in rank order (lane 0)
-    float lv = 0.0f;
-    if (lane < kk) {
-      const int e = r_id[lane];
-      lv = P.logit_bias ? __fadd_rn(r_l[lane], P.logit_bias[e]) : r_l[lane];
-    }
-    if (P.family == RBT_FAMILY_QWEN38) {
-      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
-      const float mx = __shfl(lv, 0, 64);
-      if (lane < kk) s_w[lane] = (float)exp((double)__fsub_rn(lv, mx));
-      __builtin_amdgcn_wave_barrier();
-      float sum = 0.0f;
-      for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
-      if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
-    } else {
-      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
-      if (lane < kk) s_w[lane] = sigmoid_ref(lv);
-      __builtin_amdgcn_wave_barrier();
-      if (P.norm_topk) {
-        float sum = -0.0f;
-        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
-        sum = __fadd_rn(sum, 1e-20f);
-        if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
-      }
-      if (lane < kk) s_w[lane] = __fmul_rn(s_w[lane], P.routed_scale);
-    }
-    __builtin_amdgcn_wave_barrier();
+    winner_weights(L, P, kk);
     int32_t *io = ids + (size_t)s * k;
     float *wo = wts + (size_t)s * k;
     for (int r = lane; r < k; r += 64) {
@@ -1574,7 +1596,8 @@ __global__ __launch_bounds__(256) void k_router_select3(SelParams P, const doubl
                                                         const double *__restrict__ bnd, int32_t *__restrict__ ids,
                                                         float *__restrict__ wts, float *__restrict__ sh_scale,
                                                         int *__restrict__ stats, GroupOut G, int grp) {
-  select3_body<MAXM>(P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x);
+  __shared__ SelLds L;
+  select3_body<MAXM>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x);
 }
 
 // One token with a shared expert: workgroup 0 selects; the other workgroups stream the shared
@@ -1587,10 +1610,14 @@ __global__ __launch_bounds__(256) void k_router_select3_sh(SelParams P, const do
                                                            const RbtExpertDev *__restrict__ shared_dev,
                                                            const float *__restrict__ x, int I,
                                                            __bf16 *__restrict__ hp_shared) {
+  __shared__ union {
+    SelLds sel;
+    GuLds gu;
+  } L;
   if (blockIdx.x == 0)
-    select3_body<MAXM>(P, mid, bnd, ids, wts, sh_scale, stats, G, grp, 0);
+    select3_body<MAXM>(L.sel, P, mid, bnd, ids, wts, sh_scale, stats, G, grp, 0);
   else
-    xgateup1_body<NCH>(shared_dev, 1, x, I, hp_shared, blockIdx.x - 1, gridDim.x - 1);
+    xgateup1_body<NCH>(L.gu, shared_dev, 1, x, I, hp_shared, blockIdx.x - 1, gridDim.x - 1);
 }
 
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
@@ -1830,6 +1857,507 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
     else
       hipLaunchKernelGGL(k_router_select3<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
                          stats, G, g);
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// One token, the whole router in one launch (k_router1), one workgroup per CU:
+//  1. every workgroup computes router rows r = nwg-1-b, 2 nwg-1-b, ... with the block variant's
+//     arithmetic (products through padded LDS, per-thread fp64 segments, block scans, the same
+//     bound), the next row's loads in flight while the current one is reduced;
+//  2. each workgroup then counts itself done on a device counter (release); workgroup 0 waits for
+//     the full count (acquire; a bounded spin, whose timeout raises an error flag and skips the
+//     selection so that every wave ends) and runs the selection above;
+//  3. the other workgroups stream the shared expert's gate/up, which does not depend on the
+//     routing. Needs every workgroup resident at once: the grid is one workgroup per CU and the
+//     kernel's LDS admits one per CU.
+// The counter returns to 0 at the end of a normal call (workgroup 0 resets it after the full
+// count), so repeated launches and graph replays need no host reset.
+// ------------------------------------------------------------------------------------------------
+constexpr unsigned R1_SPIN_LIMIT = 1u << 24;
+// Sync area: word 0 is the epoch, workgroup b's flag is word R1_FLAG * (1 + b) (own 64-byte line).
+constexpr int R1_FLAG = 16;
+constexpr int R1_MAXWG = 1024;
+constexpr size_t R1_SYNC_BYTES = sizeof(unsigned) * R1_FLAG * (1 + R1_MAXWG);
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt = 0 only: expcnt 7 and lgkmcnt 15 are
+// their maxima (no wait), vmcnt bits [3:0] and [15:14] are zero.
+constexpr int RBT_WAIT_VMCNT0 = 0x0F70;
+typedef float rbt_f4v __attribute__((ext_vector_type(4)));  // polls of ~64 cycles: about 0.5 s
+
+// Key record of one expert for the one-launch router: the key interval, the order-preserving bits
+// of the midpoint key and the midpoint logit, computed exactly as the selection's own key setup
+// does from (mid, bnd).
+struct KeyRec {
+  float klo, khi;
+  uint32_t ku;
+  float lm;
+};
+
+__device__ __forceinline__ KeyRec make_key_rec(const SelParams &P, int e, double mv, double bv) {
+  const float lbv = P.logit_bias ? P.logit_bias[e] : 0.0f;
+  const float rbv = P.router_bias ? P.router_bias[e] : 0.0f;
+  const float lo = __double2float_rd(mv - bv * (1.0 + 1e-12));
+  const float hi = __double2float_ru(mv + bv * (1.0 + 1e-12));
+  const float md = fminf(fmaxf(__double2float_rn(mv), lo), hi);
+  KeyRec r;
+  r.lm = md;
+  const float kmid = sel_key_v(P, lbv, rbv, md);
+  r.ku = ord_key(kmid);
+  if (lo == hi) {
+    r.klo = r.khi = kmid;
+  } else {
+    r.klo = sel_key_v(P, lbv, rbv, lo);
+    r.khi = sel_key_v(P, lbv, rbv, hi);
+  }
+  return r;
+}
+
+// One token, wave 0: the fast path of the selection above from the key records, in registers (DPP
+// reductions, readlane loops over the candidates). The threshold M is the kk-th largest lane
+// maximum, taken by kk rounds of wave maximum that each retire one lane; candidates, ranking, set
+// and order certification are those of the general path. Returns true (every lane) when the result
+// is certified without exact recomputation, after writing ids, weights and the job table; false
+// leaves the call to the general path.
+template <int MAXM>
+__device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restrict__ rec,
+                             int32_t *__restrict__ ids, float *__restrict__ wts, const GroupOut &G, int grp) {
+  const int lane = threadIdx.x & 63;
+  const int E = P.E, k = P.k, kk = min(P.k, P.E);
+  uint32_t ku[MAXM];
+  float klo[MAXM], khi[MAXM], lm[MAXM];
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) {
+    const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads
+    const float4 v = *reinterpret_cast<const float4 *>(rec + e);
+    const bool ok = lane + 64 * m < E;
+    klo[m] = ok ? v.x : -INFINITY;
+    khi[m] = ok ? v.y : -INFINITY;
+    ku[m] = ok ? __float_as_uint(v.z) : 0u;
+    lm[m] = v.w;
+  }
+  uint32_t cur = 0;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) cur = max(cur, ku[m]);
+  uint32_t M = 0;
+  for (int r = 0; r < kk; r++) {
+    M = rbt_wave_max_u(cur);
+    const unsigned long long hit = __ballot(cur == M);
+    if (lane == __ffsll((unsigned long long)hit) - 1) cur = 0;
+  }
+  if (M == 0) return false;  // a key maps to 0 (a NaN)
+  int nc = 0;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) nc += __popcll(__ballot(ku[m] >= M));
+  if (nc > SEL_NC) return false;
+  uint32_t cm = 0;
+  int base = 0;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) {
+    const bool c = ku[m] >= M;
+    const unsigned long long cb = __ballot(c);
+    if (c) {
+      const int at = base + __popcll(cb & lanemask_lt());
+      L.q_id[at] = lane + 64 * m;
+      L.q_ku[at] = ku[m];
+      L.q_lo[at] = klo[m];
+      L.q_hi[at] = khi[m];
+      L.q_l[at] = lm[m];
+      cm |= 1u << m;
+    }
+    base += __popcll(cb);
+  }
+  float hi_out = -INFINITY;  // upper keys of the non-candidates (never winners)
+#pragma unroll
+  for (int m = 0; m < MAXM; m++)
+    if (!((cm >> m) & 1u) && ku[m] != 0) hi_out = fmaxf(hi_out, khi[m]);
+  __builtin_amdgcn_wave_barrier();
+  const bool cand = lane < nc;
+  const uint32_t cku = cand ? L.q_ku[lane] : 0u;
+  const int cid = cand ? L.q_id[lane] : 0x7fffffff;
+  const float clo = cand ? L.q_lo[lane] : INFINITY, chi = cand ? L.q_hi[lane] : -INFINITY;
+  const float cl = cand ? L.q_l[lane] : 0.0f;
+  // the candidate's job-table entry, in flight while the selection is certified
+  const uint8_t *pf_gd = nullptr, *pf_ud = nullptr, *pf_dd = nullptr;
+  const void *pf_gs = nullptr, *pf_us = nullptr, *pf_ds = nullptr;
+  if (grp && cand) {
+    const RbtExpertDev *src = G.table + cid;
+    pf_gd = src->gd;
+    pf_gs = src->gs;
+    pf_ud = src->ud;
+    pf_us = src->us;
+    pf_dd = src->dd;
+    pf_ds = src->ds;
+  }
+  // rank among the candidates: key desc, id asc
+  int rank = 0;
+  for (int j = 0; j < nc; j++) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)cku, j);
+    const int oid = __builtin_amdgcn_readlane(cid, j);
+    rank += (o > cku) || (o == cku && oid < cid);
+  }
+  if (!cand) rank = SEL_NC;
+  const bool iw = rank < kk;
+  const float lo_sel = rbt_wave_min_f(iw ? clo : INFINITY);
+  const float hi_uns = rbt_wave_max_f(fmaxf(hi_out, (cand && !iw) ? chi : -INFINITY));
+  // set membership: inexact experts on the wrong side of the other side's bound
+  bool amb = false;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++)
+    amb |= !((cm >> m) & 1u) && ku[m] != 0 && klo[m] != khi[m] && khi[m] >= lo_sel;
+  const bool cexact = clo == chi;
+  amb |= cand && !cexact && (iw ? clo <= hi_uns : chi >= lo_sel);
+  // order: every pair of winners strictly ordered, or both exact
+  for (int j = 0; j < nc; j++) {
+    const int rj = __builtin_amdgcn_readlane(rank, j);
+    const float lj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(clo), j));
+    const float hj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(chi), j));
+    if (iw && !cexact && rj < kk && rj != rank) amb |= !(rj < rank ? lj > chi : clo > hj);
+  }
+  if (__ballot(amb) != 0) return false;
+  // certified: weights in rank order, then the outputs
+  if (iw) {
+    L.r_id[rank] = cid;
+    L.r_l[rank] = cl;
+  }
+  __builtin_amdgcn_wave_barrier();
+  winner_weights(L, P, kk);
+  for (int r = lane; r < k; r += 64) {
+    ids[r] = r < kk ? L.r_id[r] : -1;
+    wts[r] = r < kk ? L.s_w[r] : 0.0f;
+  }
+  if (grp) {
+    // single token: pair j = slot j; the shared expert is pair k
+    if (iw) {
+      RbtExpertDev *dst = G.pair_job + rank;
+      if (pf_gd == nullptr || pf_dd == nullptr) atomicOr(G.err, 1);
+      dst->gd = pf_gd;
+      dst->gs = pf_gs;
+      dst->ud = pf_ud;
+      dst->us = pf_us;
+      dst->dd = pf_dd;
+      dst->ds = pf_ds;
+    }
+    for (int r = lane; r <= k; r += 64) {
+      if (r < k) {
+        if (r >= kk) {
+          RbtExpertDev *dst = G.pair_job + r;
+          dst->gd = nullptr;
+          dst->gs = nullptr;
+          dst->ud = nullptr;
+          dst->us = nullptr;
+          dst->dd = nullptr;
+          dst->ds = nullptr;
+        }
+        G.pair_tok[r] = 0;
+        G.tok_pair[r] = r < kk ? r : -1;
+        G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
+      } else {
+        G.pair_job[k] = *G.shared_dev;
+        G.pair_tok[k] = 0;
+      }
+    }
+  }
+  return true;
+}
+
+// Two router rows by the whole workgroup at once (one pass, shared scans and sums; per row the
+// block variant's arithmetic, with the cross-lane sums through DPP, which only reorders fp64
+// additions that the bound's slack covers): xv, wa, wb hold the thread's float4 chunks c * 256 + t
+// of x and of the two rows.
+struct LgLds {
+  __attribute__((aligned(16))) float lp[2][RT_MAXH + 4 * 256];
+  double sh[16];
+};
+
+__device__ __forceinline__ void store_key_rec(KeyRec *dst, const KeyRec &r) {
+  // two device-coherent 8-byte stores (the flag that publishes them waits for both)
+  const unsigned long long a = ((unsigned long long)__float_as_uint(r.khi) << 32) | __float_as_uint(r.klo);
+  const unsigned long long b = ((unsigned long long)__float_as_uint(r.lm) << 32) | r.ku;
+  unsigned long long *d = reinterpret_cast<unsigned long long *>(dst);
+  __hip_atomic_store(d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(d + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// KP/rec: when KP is set, thread 0 also stores the key records of rows ea and eb (eb < 0: none).
+__device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT_MAXH / 1024],
+                                                 const float4 (&wa)[RT_MAXH / 1024],
+                                                 const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
+                                                 double *bnd_a, double *mid_b, double *bnd_b,
+                                                 const SelParams *KP = nullptr, KeyRec *rec = nullptr, int ea = -1,
+                                                 int eb = -1) {
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int seg = H / 256, segp = seg + 4, nch = H / 1024;
+  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16;  // 2^-53
+#pragma unroll
+  for (int c = 0; c < RT_MAXH / 1024; c++) {
+    if (c < nch) {
+      const int j = c * 1024 + 4 * t;
+      const int dst = (j / seg) * segp + (j % seg);
+      float4 p, q;
+      p.x = __fmul_rn(xv[c].x, wa[c].x);
+      p.y = __fmul_rn(xv[c].y, wa[c].y);
+      p.z = __fmul_rn(xv[c].z, wa[c].z);
+      p.w = __fmul_rn(xv[c].w, wa[c].w);
+      q.x = __fmul_rn(xv[c].x, wb[c].x);
+      q.y = __fmul_rn(xv[c].y, wb[c].y);
+      q.z = __fmul_rn(xv[c].z, wb[c].z);
+      q.w = __fmul_rn(xv[c].w, wb[c].w);
+      *reinterpret_cast<float4 *>(&L.lp[0][dst]) = p;
+      *reinterpret_cast<float4 *>(&L.lp[1][dst]) = q;
+    }
+  }
+  __syncthreads();
+  const float *ma = L.lp[0] + t * segp, *mb = L.lp[1] + t * segp;
+  double la = 0.0, pa = 0.0, lb = 0.0, pb = 0.0;
+  for (int q = 0; q < seg; q += 4) {
+    const float4 p = *reinterpret_cast<const float4 *>(ma + q);
+    const float4 r = *reinterpret_cast<const float4 *>(mb + q);
+    la += (double)p.x;
+    lb += (double)r.x;
+    la += (double)p.y;
+    lb += (double)r.y;
+    la += (double)p.z;
+    lb += (double)r.z;
+    la += (double)p.w;
+    lb += (double)r.w;
+    pa += fabs((double)p.x) + fabs((double)p.y) + fabs((double)p.z) + fabs((double)p.w);
+    pb += fabs((double)r.x) + fabs((double)r.y) + fabs((double)r.z) + fabs((double)r.w);
+  }
+  // exclusive block scan of both segment sums (wave scans, then wave offsets through LDS)
+  const double ia = rbt_wave_scan_d(la), ib = rbt_wave_scan_d(lb);
+  if (lane == 63) {
+    L.sh[wid] = ia;
+    L.sh[4 + wid] = ib;
+  }
+  __syncthreads();
+  double offa = 0.0, offb = 0.0, tota = 0.0, totb = 0.0;
+  for (int w = 0; w < 4; w++) {
+    if (w < wid) {
+      offa += L.sh[w];
+      offb += L.sh[4 + w];
+    }
+    tota += L.sh[w];
+    totb += L.sh[4 + w];
+  }
+  __syncthreads();
+  double prea = offa + ia - la, preb = offb + ib - lb, Ta = 0.0, Tb = 0.0;
+  for (int q = 0; q < seg; q += 4) {
+    const float4 p = *reinterpret_cast<const float4 *>(ma + q);
+    const float4 r = *reinterpret_cast<const float4 *>(mb + q);
+    prea += (double)p.x;
+    preb += (double)r.x;
+    Ta += fabs(prea);
+    Tb += fabs(preb);
+    prea += (double)p.y;
+    preb += (double)r.y;
+    Ta += fabs(prea);
+    Tb += fabs(preb);
+    prea += (double)p.z;
+    preb += (double)r.z;
+    Ta += fabs(prea);
+    Tb += fabs(preb);
+    prea += (double)p.w;
+    preb += (double)r.w;
+    Ta += fabs(prea);
+    Tb += fabs(preb);
+  }
+  Ta = rbt_wave_total_d(Ta);
+  pa = rbt_wave_total_d(pa);
+  Tb = rbt_wave_total_d(Tb);
+  pb = rbt_wave_total_d(pb);
+  if (lane == 0) {
+    L.sh[wid] = Ta;
+    L.sh[4 + wid] = pa;
+    L.sh[8 + wid] = Tb;
+    L.sh[12 + wid] = pb;
+  }
+  __syncthreads();
+  if (t == 0) {
+    const double n = (double)H;
+    auto bound = [&](double T, double P) {
+      const double slack = 8.0 * n * e64 * (P + T) + n * n * e64 * P;
+      const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
+      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
+      return B * (1.0 + 1e-9) + 1e-300;
+    };
+    Ta = L.sh[0] + L.sh[1] + L.sh[2] + L.sh[3];
+    pa = L.sh[4] + L.sh[5] + L.sh[6] + L.sh[7];
+    Tb = L.sh[8] + L.sh[9] + L.sh[10] + L.sh[11];
+    pb = L.sh[12] + L.sh[13] + L.sh[14] + L.sh[15];
+    // device-coherent stores (write-through to the device's coherence point): the count-in that
+    // follows needs no cache write-back to publish them
+    if (mid_a) {
+      const double Ba = bound(Ta, pa);
+      __hip_atomic_store(mid_a, tota, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(bnd_a, Ba, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (KP && ea >= 0) store_key_rec(rec + ea, make_key_rec(*KP, ea, tota, Ba));
+    }
+    if (mid_b) {
+      const double Bb = bound(Tb, pb);
+      __hip_atomic_store(mid_b, totb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(bnd_b, Bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (KP && eb >= 0) store_key_rec(rec + eb, make_key_rec(*KP, eb, totb, Bb));
+    }
+  }
+  __syncthreads();  // lp and sh are rewritten next
+}
+
+template <int MAXM, int NCH>
+__global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
+                                                 double *__restrict__ mid, double *__restrict__ bnd,
+                                                 int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                 float *__restrict__ sh_scale, int *__restrict__ stats, GroupOut G,
+                                                 int grp, const RbtExpertDev *__restrict__ shared_dev, int I,
+                                                 __bf16 *__restrict__ hp_shared, unsigned *__restrict__ sync,
+                                                 int *__restrict__ err, KeyRec *__restrict__ rec) {
+  constexpr int MC = RT_MAXH / 1024;
+  __shared__ union {
+    LgLds lg;
+    SelLds sel;
+    GuLds gu;
+  } L;
+  __shared__ int go, fast_ok;
+  const int t = threadIdx.x, nwg = gridDim.x, b = blockIdx.x;
+  const int H = P.H, E = P.E, nch = H / 1024;
+  // this call's epoch: the value the previous call left (it changes only after every workgroup's
+  // flag is up, so every workgroup reads the same value)
+  const unsigned ep = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const float4 *x4 = reinterpret_cast<const float4 *>(P.x);
+  float4 xv[MC], wa[MC], wb[MC], wg[MC];
+  // unconditional loads (chunks past the row repeat its last one): no waits between the rows
+  auto load_row = [&](const float *w, float4(&wv)[MC]) {
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+#pragma unroll
+    for (int c = 0; c < MC; c++) {
+      const rbt_f4v v =
+          __builtin_nontemporal_load(reinterpret_cast<const rbt_f4v *>(w4 + min(c, nch - 1) * 256 + t));
+      wv[c] = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  };
+  // router rows ra = nwg-1-b and rb = ra + nwg (E <= 2 nwg is checked by the launcher; a missing
+  // row reads a valid one and is not written); the last workgroup also takes the shared-expert
+  // gate row, which the selection does not need
+  const int ra = nwg - 1 - b, rb = ra + nwg;
+  const int rac = min(ra, E - 1), rbc = rb < E ? rb : rac;
+  const bool gate_row = sgate != nullptr && b == nwg - 1;
+  load_row(P.W + (size_t)rac * H, wa);
+  load_row(P.W + (size_t)rbc * H, wb);
+  if (gate_row) load_row(sgate, wg);
+#pragma unroll
+  for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
+  if (ra < E)
+    logits_rows2_blk(L.lg, xv, wa, wb, H, mid + ra, bnd + ra, rb < E ? mid + rb : nullptr, rb < E ? bnd + rb : nullptr,
+                     &P, rec, ra, rb < E ? rb : -1);
+  // selection rows done: raise this workgroup's flag to epoch + 1. Its row results are device-scope
+  // stores made by this thread; waiting for their acknowledgement (vmcnt(0); a store at device
+  // scope is acknowledged once it is coherent there) orders them before the flag, with no L2
+  // write-back.
+  if (t == 0) {
+    __builtin_amdgcn_s_waitcnt(RBT_WAIT_VMCNT0);
+    __hip_atomic_store(sync + R1_FLAG * (1 + b), ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (gate_row) {
+    logits_rows2_blk(L.lg, xv, wg, wg, H, mid + E, bnd + E, nullptr, nullptr);
+    // gated shared expert: sigmoid of the fp32-rounded gate logit (qwen38/moe.rs:78-83)
+    if (t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
+  } else if (sgate == nullptr && b == nwg - 1 && t == 0) {
+    sh_scale[0] = 1.0f;
+  }
+  if (b == 0) {
+    if (t < 64) {
+      // wave 0 polls every flag (lane l: workgroups l, l + 64, ...) until all show epoch + 1
+      unsigned it = 0;
+      int ok = 1;
+      for (;;) {
+        bool done = true;
+        for (int w = t; w < nwg; w += 64)
+          done &= __hip_atomic_load(sync + R1_FLAG * (1 + w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ep + 1;
+        if (__ballot(!done) == 0) break;
+        __builtin_amdgcn_s_sleep(1);
+        if (++it > R1_SPIN_LIMIT) {
+          ok = 0;
+          break;
+        }
+      }
+      __threadfence();  // acquire: the other workgroups' rows
+      if (t == 0) {
+        // next call's epoch (every workgroup has read this one: its flag is up)
+        if (ok)
+          __hip_atomic_store(sync, ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          atomicOr(err, 1);
+        go = ok;
+      }
+    }
+    __syncthreads();
+    if (go) {
+      // the register fast path from the key records; anything it cannot certify by itself (an
+      // exact recomputation, many equal keys) goes through the general path from mid/bnd
+      if (t < 64) {
+        const bool ok = select4_fast<MAXM>(L.sel, P, rec, ids, wts, G, grp);
+        if (t == 0) fast_ok = ok;
+      }
+      __syncthreads();
+      if (!fast_ok) select3_body<MAXM>(L.sel, P, mid, bnd, ids, wts, nullptr, stats, G, grp, 0);
+    }
+  } else if (shared_dev != nullptr) {
+    xgateup1_body<NCH>(L.gu, shared_dev, 1, P.x, I, hp_shared, b - 1, nwg - 1);
+  }
+}
+
+size_t router1_sync_bytes() { return R1_SYNC_BYTES; }
+
+bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu) {
+  const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 512 && a.k <= SEL_MAXK &&
+         a.H % 1024 == 0 && a.H <= RT_MAXH && aligned && a.E <= 2 * num_cu && num_cu >= 2 &&
+         (sgu == nullptr || sgu->K == a.H) && (sgu == nullptr || a.H == 8192 || a.H == 7168);
+}
+
+hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
+                          int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs *grp,
+                          const SharedGateUp *sgu, unsigned *sync, int *err, void *rec_buf) {
+  KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
+  if (!router1_ok(a, c.num_cu, sgu) || (sgate && (uintptr_t)sgate % 16 != 0) || c.num_cu > R1_MAXWG)
+    return hipErrorInvalidValue;
+  SelParams P{};
+  P.family = a.family;
+  P.E = a.E;
+  P.erows = a.erows;
+  P.k = a.k;
+  P.H = a.H;
+  P.S = 1;
+  P.logit_bias = a.logit_bias;
+  P.router_bias = a.router_bias;
+  P.norm_topk = a.norm_topk;
+  P.routed_scale = a.routed_scale;
+  P.n_group = a.n_group;
+  P.topk_group = a.topk_group;
+  P.x = a.x;
+  P.W = a.W;
+  GroupOut G{};
+  int g = 0;
+  if (grp) {
+    G = GroupOut{grp->table, grp->shared_dev, grp->pair_job, grp->pair_tok, grp->tok_pair, grp->tok_w, grp->err};
+    g = 1;
+  }
+  const RbtExpertDev *sd = sgu ? sgu->dev : nullptr;
+  const int I = sgu ? sgu->I : 0;
+  __bf16 *hp = sgu ? sgu->hp : nullptr;
+  const dim3 grid(c.num_cu), block(256);
+  const bool m4 = a.E <= 256;
+  if (a.H == 7168) {
+    if (m4)
+      launch_k(c, k_router1<4, 14>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+    else
+      launch_k(c, k_router1<8, 14>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+  } else {
+    if (m4)
+      launch_k(c, k_router1<4, 16>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+    else
+      launch_k(c, k_router1<8, 16>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
   }
   return hipGetLastError();
 }

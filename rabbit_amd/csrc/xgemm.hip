@@ -222,7 +222,8 @@ __global__ __launch_bounds__(256) void k_xgateup(const RbtExpertDev *__restrict_
 template <int NCH>
 __global__ __launch_bounds__(256) void k_xgateup1(const RbtExpertDev *__restrict__ jobs, int npairs,
                                                   const float *__restrict__ x, int I, __bf16 *__restrict__ hp) {
-  xgateup1_body<NCH>(jobs, npairs, x, I, hp, blockIdx.x, gridDim.x);
+  __shared__ GuLds L;
+  xgateup1_body<NCH>(L, jobs, npairs, x, I, hp, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -424,34 +425,79 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   const int ntile = H >> 2;
   const int T0 = (int)((long)blockIdx.x * ntile / gridDim.x), T1 = (int)((long)(blockIdx.x + 1) * ntile / gridDim.x);
   const int nt = T1 - T0;
-  if (tid < 32) zb[tid] = (__bf16)0.0f;
-  if (tid < npairs) {
-    const int pp = tid;
-    float wv = 0.0f;
-    if (pp < k) {
-      for (int j = 0; j < k; j++)
-        if (tok_pair[j] == pp) wv = tok_w[j];
-    } else {
-      wv = gated ? sh_scale[0] : 1.0f;
-    }
-    const RbtExpertDev J = jobs[pp];
-    const int live = J.dd != nullptr && J.ds != nullptr;
-    plive[pp] = live;
-    padd[pp] = live && (pp < k || has_shared);
-    pd[pp] = J.dd;
-    ps[pp] = (const uint8_t *)J.ds;
-    pw[pp] = wv;
-  }
-  // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside hp)
-  const int npc = npairs * PPP;
-  rbt_u4 hr[HI];
-#pragma unroll
-  for (int i = 0; i < HI; i++) hr[i] = *(const rbt_gu4 *)(hp + 8L * min(tid + 64 * XD1_NW * i, npc - 1));
-  lds_barrier();  // tables
   const int NU = nt * npairs;
   const int u0 = w * NU / XD1_NW, u1 = (w + 1) * NU / XD1_NW;
   const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
   const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
+  const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
+  // First window (units u0 .. u0+3): pointers straight from the job table with wave-uniform
+  // (scalar) loads, so the weight stream starts at once; the tables in LDS serve the rest.
+  rbt_u4 ring[4][NCH], sv;
+  {
+    const uint8_t *sp[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int u = u0 + j;
+      const uint8_t *cp = dummy;
+      sp[j] = hb8 + 16 * s_seg;
+      if (u < u1) {
+        const int tl = u / npairs, pp = u - tl * npairs;
+        const uint8_t *dd = jobs[pp].dd;
+        const uint8_t *ds = (const uint8_t *)jobs[pp].ds;
+        if (dd != nullptr && ds != nullptr) {
+          cp = dd + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g;
+          sp[j] = ds + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp + 256 * c));
+    }
+    sv = *(const rbt_gu4 *)(s_q == 0 ? sp[0] : s_q == 1 ? sp[1] : s_q == 2 ? sp[2] : sp[3]);
+  }
+  // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside hp), in an order
+  // rotated by workgroup so that the grid does not read the same lines at the same time
+  const int npc = npairs * PPP;
+  rbt_u4 hr[HI];
+  const int rot = blockIdx.x % HI;
+#pragma unroll
+  for (int i = 0; i < HI; i++) {
+    const int ii = i + rot < HI ? i + rot : i + rot - HI;
+    hr[i] = *(const rbt_gu4 *)(hp + 8L * min(tid + 64 * XD1_NW * ii, npc - 1));
+  }
+  if (tid < 32) zb[tid] = (__bf16)0.0f;
+  if (w == 0) {
+    // pair tables: lane j holds slot j's pair and weight, lane p pair p's job; pair p's weight is
+    // the weight of the last slot that uses it (pair k: the shared expert, scaled when gated)
+    const int tp = lane < k ? tok_pair[lane] : -1;
+    const float tw = lane < k ? tok_w[lane] : 0.0f;
+    const RbtExpertDev *J = jobs + min(lane, npairs - 1);
+    const uint8_t *dd = J->dd;
+    const uint8_t *ds = (const uint8_t *)J->ds;
+    const float shv = gated ? sh_scale[0] : 1.0f;
+    float wv = lane < k ? 0.0f : shv;
+    for (int j = 0; j < k; j++) {
+      const int tpj = __builtin_amdgcn_readlane(tp, j);
+      const float twj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), j));
+      if (lane < k && tpj == lane) wv = twj;
+    }
+    if (lane < npairs) {
+      const int live = dd != nullptr && ds != nullptr;
+      plive[lane] = live;
+      padd[lane] = live && (lane < k || has_shared);
+      pd[lane] = dd;
+      ps[lane] = ds;
+      pw[lane] = wv;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < HI; i++) {
+    const int ii = i + rot < HI ? i + rot : i + rot - HI;
+    const int e = tid + 64 * XD1_NW * ii;
+    if (e < npc) {
+      const int pp = e / PPP, q = e - pp * PPP;
+      *reinterpret_cast<rbt_u4 *>(&hs[pp][(q / (KD / 8)) * stride + 8 * (q % (KD / 8))]) = hr[i];
+    }
+  }
   // lane pointer of unit u (chunk 0); past the wave's units or for a null job: cached dummy bytes
   auto uptr = [&](int u) -> const uint8_t * {
     if (u >= u1) return dummy;
@@ -459,7 +505,6 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     return plive[pp] ? pd[pp] + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
   };
   // scale window of units ub .. ub+3: lane l holds unit ub + l/16, row (l/4) % 4, bytes 16 (l % 4)
-  const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
   auto sload = [&](int ub) {
     const int u = ub + s_q;
     const uint8_t *p = hb8 + 16 * s_seg;
@@ -472,25 +517,9 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   auto sstore = [&](int buf, const rbt_u4 &v) {
     *reinterpret_cast<rbt_u4 *>(&sw[w][buf][s_q][s_row][16 * s_seg]) = v;
   };
-  rbt_u4 sv = sload(u0);
-  rbt_u4 ring[4][NCH];
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const uint8_t *p = uptr(u0 + j);
-#pragma unroll
-    for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(p + 256 * c));
-  }
-#pragma unroll
-  for (int i = 0; i < HI; i++) {
-    const int e = tid + 64 * XD1_NW * i;
-    if (e < npc) {
-      const int pp = e / PPP, q = e - pp * PPP;
-      *reinterpret_cast<rbt_u4 *>(&hs[pp][(q / (KD / 8)) * stride + 8 * (q % (KD / 8))]) = hr[i];
-    }
-  }
   sstore(0, sv);
+  lds_barrier();  // tables, h parts, first scale windows
   sv = sload(u0 + 4);
-  lds_barrier();  // h parts
   const int bq = col >> 2, bpart = col & 3;
   const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
   const int binc = bpart < 3 ? 1024 : 0;
