@@ -198,10 +198,12 @@ int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, fl
 
 /* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
 typedef struct {
-    double router_ms;    /* router logits + top-k selection + grouping */
-    double gateup_ms;    /* gate/up dequant-GEMV (all experts of the call) */
-    double down_ms;      /* silu(g)*u and the down dequant-GEMV */
-    double combine_ms;   /* weighted combine + shared expert */
+    double router_ms;    /* router logits + top-k selection + grouping (one-token MXFP4 calls: also
+                            the shared expert's gate/up, which runs in the same launch) */
+    double gateup_ms;    /* gate/up products + silu(g)*u (the experts this phase streams) */
+    double down_ms;      /* down products (with the ordered combine where it is fused in) */
+    double combine_ms;   /* the separate weighted combine + shared expert; where the combine is
+                            fused into the down kernel, only the time to the call's end */
     uint64_t calls;      /* rbt_moe_forward_d calls recorded */
     uint64_t ambiguous;  /* router logits recomputed exactly because of a near-tie */
     uint64_t gateup_experts; /* one-token calls: experts whose gate/up the gate/up phase streamed (a shared

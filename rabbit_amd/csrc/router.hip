@@ -2174,32 +2174,31 @@ __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT
     L.sh[12 + wid] = pb;
   }
   __syncthreads();
-  if (t == 0) {
+  // row a finishes on thread 0, row b on thread 64 (another wave), in parallel
+  if (t == 0 || t == 64) {
+    const bool rowb = t == 64;
     const double n = (double)H;
-    auto bound = [&](double T, double P) {
-      const double slack = 8.0 * n * e64 * (P + T) + n * n * e64 * P;
-      const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
-      double B = (u1 * Tu) / (1.0 - n * u1) + slack;
-      return B * (1.0 + 1e-9) + 1e-300;
-    };
-    Ta = L.sh[0] + L.sh[1] + L.sh[2] + L.sh[3];
-    pa = L.sh[4] + L.sh[5] + L.sh[6] + L.sh[7];
-    Tb = L.sh[8] + L.sh[9] + L.sh[10] + L.sh[11];
-    pb = L.sh[12] + L.sh[13] + L.sh[14] + L.sh[15];
-    // device-coherent stores (write-through to the device's coherence point): the count-in that
-    // follows needs no cache write-back to publish them
-    if (mid_a) {
-      const double Ba = bound(Ta, pa);
-      __hip_atomic_store(mid_a, tota, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(bnd_a, Ba, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (KP && ea >= 0) store_key_rec(rec + ea, make_key_rec(*KP, ea, tota, Ba));
+    const double T = rowb ? L.sh[8] + L.sh[9] + L.sh[10] + L.sh[11] : L.sh[0] + L.sh[1] + L.sh[2] + L.sh[3];
+    const double P = rowb ? L.sh[12] + L.sh[13] + L.sh[14] + L.sh[15] : L.sh[4] + L.sh[5] + L.sh[6] + L.sh[7];
+    const double tot = rowb ? totb : tota;
+    // B = u1 Tu / (1 - n u1) + slack, with 1/(1 - x) <= 1 + x + 2 x^2 (x = n u1 <= 1/2) in place of
+    // the division; the final factor covers the fp64 roundings
+    const double x = n * u1;
+    const double slack = 8.0 * n * e64 * (P + T) + n * n * e64 * P;
+    const double Tu = T * (1.0 + 8.0 * n * e64) + slack;
+    double B = u1 * Tu * (1.0 + x + 2.0 * x * x) + slack;
+    B = B * (1.0 + 1e-9) + 1e-300;
+    double *mo = rowb ? mid_b : mid_a, *bo = rowb ? bnd_b : bnd_a;
+    if (mo) {
+      // device-coherent stores (write-through to the device's coherence point): the flag that
+      // follows needs no cache write-back to publish them
+      __hip_atomic_store(mo, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(bo, B, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int e = rowb ? eb : ea;
+      if (KP && e >= 0) store_key_rec(rec + e, make_key_rec(*KP, e, tot, B));
     }
-    if (mid_b) {
-      const double Bb = bound(Tb, pb);
-      __hip_atomic_store(mid_b, totb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(bnd_b, Bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (KP && eb >= 0) store_key_rec(rec + eb, make_key_rec(*KP, eb, totb, Bb));
-    }
+    // acknowledged before the barrier below: thread 0's flag, raised after it, then covers both rows
+    __builtin_amdgcn_s_waitcnt(RBT_WAIT_VMCNT0);
   }
   __syncthreads();  // lp and sh are rewritten next
 }
