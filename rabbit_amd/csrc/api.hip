@@ -47,6 +47,9 @@ enum ScratchSlot {
   SC_PGRP,
   SC_RLOG,
   SC_RREC,
+  SC_DJOB,
+  SC_DSLOT,
+  SC_D1,
   SC_N
 };
 
@@ -563,14 +566,16 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
   RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
   RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
-  // k_group always writes the S shared-expert pair slots after the P routed ones.
-  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)(P + S), &pjob));
-  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)(P + S), &ptok));
+  // k_group always writes the S shared-expert pair slots after the P routed ones; one token may use
+  // k + D1_KX routed slots with the shared expert after them (a deferred router decision)
+  const size_t pslots = S == 1 ? std::max((size_t)(P + S), (size_t)(k + rbt::D1_KX + 1)) : (size_t)(P + S);
+  RBT_TRY(scratch_t(c, SC_PJOB, pslots, &pjob));
+  RBT_TRY(scratch_t(c, SC_PTOK, pslots, &ptok));
   RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
   RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
   size_t hi = std::max((size_t)I, L.shared_inter);
   // 2 * hi floats per pair: fp32 h for the GEMV path, or three bf16 parts (1.5 * I) for the MFMA path
-  RBT_TRY(scratch_t(c, SC_H, (size_t)npairs * hi * 2, &h));
+  RBT_TRY(scratch_t(c, SC_H, pslots * hi * 2, &h));
   RBT_TRY(scratch_t(c, SC_YY, (size_t)npairs * H, &yy));
   int *dflags = c->d_flags;
 
@@ -598,10 +603,32 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   // the router launch (it does not depend on the routing).
   const bool gu1 = mfma && S == 1 && (long)k * (I / 4) >= 4L * c->num_cu;
   const bool sh_in_select = gu1 && D.has_shared && grp_in_select;
-  rbt::SharedGateUp sgu{L.d_shared, x, H, I, reinterpret_cast<__bf16 *>(h) + (size_t)k * 3 * I};
+  rbt::SharedGateUp sgu{L.d_shared, x, H, I, nullptr};
   const float *sgate = gated ? D.shared_gate : nullptr;
   const bool r1 = grp_in_select && rbt::router1_ok(ra, c->num_cu, sh_in_select ? &sgu : nullptr) &&
                   (uintptr_t)(sgate ? sgate : x) % 16 == 0;
+  // One token on the matrix cores: the selection also writes the down launch's compact job list;
+  // with the one-launch router, a decision that needs exact folds is deferred to the gate/up
+  // launch, the routed pairs then taking up to k + D1_KX slots and the shared expert the one after.
+  const int kk = std::min(k, E);
+  const bool dn1 = gu1 && grp_in_select && rbt::xdown1_ok(kk + (D.has_shared ? 1 : 0), (size_t)I);
+  const bool defer = r1 && dn1;
+  const int sh_slot = defer ? k + rbt::D1_KX : k;
+  sgu.hp = reinterpret_cast<__bf16 *>(h) + (size_t)sh_slot * 3 * I;
+  RbtExpertDev *djob = nullptr;
+  int *dslot = nullptr;
+  rbt::D1Task *d1 = nullptr;
+  if (dn1) {
+    RBT_TRY(scratch_t(c, SC_DJOB, (size_t)(kk + 1), &djob));
+    RBT_TRY(scratch_t(c, SC_DSLOT, (size_t)(kk + 1), &dslot));
+    ga.down_job = djob;
+    ga.down_slot = dslot;
+    ga.shared_slot = sh_slot;
+  }
+  if (defer) {
+    RBT_TRY(scratch_t(c, SC_D1, 1, &d1));
+    ga.d1 = d1;
+  }
   if (r1) {
     // one token: logits, selection and the shared expert's gate/up in one launch
     float *rec;
@@ -639,16 +666,18 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     // h as three bf16 parts per pair (3 * I bf16 = 1.5 * I floats of the h scratch)
     __bf16 *hp = reinterpret_cast<__bf16 *>(h);
     if (c->prof) c->t_start = ev[2], c->t_stop = ev[3];
-    // every wave of the balanced grid has work; the shared pair is done when it ran in selection
-    const hipError_t e2 = gu1 ? rbt::launch_xgateup1(*c, pjob, sh_in_select ? k : npairs, x, H, I, hp)
-                              : rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp);
+    // every wave of the balanced grid has work; the shared pair is done when it ran in selection;
+    // a deferred router decision is settled by the gate/up launch's extra workgroup
+    const hipError_t e2 = defer ? rbt::launch_xgateup1_d1(*c, pjob, d1, x, H, I, hp, ra, ga, ids, wts, dflags + FLAG_AMB)
+                          : gu1 ? rbt::launch_xgateup1(*c, pjob, sh_in_select ? k : npairs, x, H, I, hp)
+                                : rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e2);
     if (c->prof) c->t_start = ev[4], c->t_stop = ev[5];
-    // one token: the balanced down (all pairs' h in LDS); batches: a grid of row blocks
+    // one token: the balanced down over the compact job list (all pairs' h in LDS); batches: a grid
+    // of row blocks
     const hipError_t e3 =
-        S == 1 && rbt::xdown1_ok(npairs, I)
-            ? rbt::launch_xdown1(*c, pjob, npairs, hp, I, H, k, tpair, tw, shs, D.has_shared, gated, out)
+        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out)
             : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e3);

@@ -71,10 +71,12 @@ hipError_t launch_xgateup(const Ctx &c, const RbtExpertDev *jobs, const int *tok
 hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const float *x, int K, int I,
                            __bf16 *hp);
 // hp: h as three bf16 parts per pair, hp[(p*3 + part)*I + k].
-// One token: down + ordered combine balanced over num_cu workgroups, every pair's h in LDS.
+// One token: down + ordered combine balanced over num_cu workgroups, every pair's h in LDS. The
+// pairs are the kk winners in slot order (down_job[j], h at pair slot down_slot[j], weight
+// tok_w[j]) and, with has_shared, the shared expert (down_job[kk], h at down_slot[kk]).
 bool xdown1_ok(int npairs, size_t i);
-hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int k,
-                         const int *tok_pair, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
+                         int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
                          float *out);
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
@@ -115,12 +117,38 @@ bool router_exact_ok(int S, int H);
 hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H, const float *W, int E,
                                       const float *sgate, float *logits);
 // Expert job-table outputs the selection kernel writes itself for a single token (S == 1).
+// One-token decode (router launch -> gate/up launch -> down launch). The router launch writes the
+// routed pairs at slots 0 .. nr-1 of the pair job table (the winners in rank order) and the shared
+// expert at slot `shared_slot`, and the down launch's compact job list: the winners in slot order,
+// then the shared expert, with the pair slot of each (where its h is). When it cannot certify the
+// top-k without the reference's sequential fp32 folds, it defers the decision instead: the routed
+// pairs are the certain winners in midpoint order followed by the undecided candidates, and the
+// gate/up launch's extra workgroup runs the folds while the pairs stream, then writes ids,
+// weights and the down job list.
+constexpr int D1_KX = 4;   // routed pair slots beyond top-k for undecided candidates
+constexpr int D1_NC = 32;  // most routed pairs a deferred decision carries
+struct D1Task {
+  int nr;       // routed pairs of the call: slots 0 .. nr-1
+  int pending;  // 1: the gate/up launch decides ids, weights and the down job list
+  int pad[2];
+  int id[D1_NC];       // expert of slot c
+  uint32_t ku[D1_NC];  // its midpoint order key
+  float lm[D1_NC];     // its midpoint logit
+  int flag[D1_NC];     // 1: its logit is recomputed as the reference folds it
+};
+
 struct GroupArgs {
   const RbtExpertDev *table, *shared_dev;
   RbtExpertDev *pair_job;
   int *pair_tok, *tok_pair;
   float *tok_w;
   int *err;
+  // one token (all optional): the down launch's job list and pair slots, the shared expert's slot
+  // (default: k), and the deferred-decision task
+  RbtExpertDev *down_job = nullptr;
+  int *down_slot = nullptr;
+  int shared_slot = -1;
+  D1Task *d1 = nullptr;
 };
 // The shared expert's gate/up for a one-token call (balanced body of xgemm), run by the selection
 // launch on the CUs its one selecting workgroup leaves idle. hp: the shared pair's output parts.
@@ -143,6 +171,12 @@ bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
                           int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs *grp,
                           const SharedGateUp *sgu, unsigned *sync, int *err, void *rec);
+// One token after launch_router1 with grp->d1: the gate/up of the published routed pairs on num_cu
+// workgroups, plus one workgroup that settles a deferred decision (exact folds of the flagged
+// logits, then ids, weights, tok_pair / tok_w and the down job list).
+hipError_t launch_xgateup1_d1(const Ctx &c, const RbtExpertDev *jobs, const D1Task *T, const float *x, int K, int I,
+                              __bf16 *hp, const RouterArgs &a, const GroupArgs &grp, int32_t *ids, float *wts,
+                              int *stats);
 // Device bytes of the key records launch_router1 writes (per router row).
 constexpr size_t ROUTER1_REC_BYTES = 16;
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);

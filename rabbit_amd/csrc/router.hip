@@ -967,7 +967,29 @@ struct GroupOut {
   int *pair_tok, *tok_pair;
   float *tok_w;
   int *err;
+  RbtExpertDev *down_job;  // optional (one token): winners in slot order, then the shared expert
+  int *down_slot;          // their pair slots
+  int shared_slot;         // pair slot of the shared expert
+  D1Task *d1;              // optional: routed pair count / deferred decision
 };
+
+__host__ __device__ inline GroupOut group_out(const GroupArgs &g, int k) {
+  return GroupOut{g.table,    g.shared_dev, g.pair_job, g.pair_tok, g.tok_pair,
+                  g.tok_w,    g.err,        g.down_job, g.down_slot, g.shared_slot >= 0 ? g.shared_slot : k,
+                  g.d1};
+}
+
+// Copy of a job-table entry field by field (a struct temporary ends up in scratch memory).
+__device__ __forceinline__ void copy_job(RbtExpertDev *dst, const RbtExpertDev *src) {
+  const uint8_t *gd = src->gd, *ud = src->ud, *dd = src->dd;
+  const void *gs = src->gs, *us = src->us, *ds = src->ds;
+  dst->gd = gd;
+  dst->gs = gs;
+  dst->ud = ud;
+  dst->us = us;
+  dst->dd = dd;
+  dst->ds = ds;
+}
 
 template <int MAXM>
 __device__ void bisect_topk(const uint32_t (&ku)[MAXM], uint32_t valid, int E, int kk, int *sel_id, uint32_t *sel_ku,
@@ -1548,43 +1570,58 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
     }
     if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
     if (grp) {
-      // single token: pair j = slot j; the shared expert is pair k
+      // single token: pair j = slot j; the shared expert is at G.shared_slot
+      auto put = [&](int r, const uint8_t *gd, const void *gs, const uint8_t *ud, const void *us, const uint8_t *dd,
+                     const void *ds) {
+        RbtExpertDev *dst = G.pair_job + r;
+        dst->gd = gd;
+        dst->gs = gs;
+        dst->ud = ud;
+        dst->us = us;
+        dst->dd = dd;
+        dst->ds = ds;
+        if (G.down_job && r < kk) {
+          RbtExpertDev *dn = G.down_job + r;
+          dn->gd = gd;
+          dn->gs = gs;
+          dn->ud = ud;
+          dn->us = us;
+          dn->dd = dd;
+          dn->ds = ds;
+          G.down_slot[r] = r;
+        }
+      };
       if (fast && my_rank >= 0 && my_rank < kk) {
         // winners of the fast path: the entries their candidate lanes loaded during certification
-        RbtExpertDev *dst = G.pair_job + my_rank;
         if (pf_gd == nullptr || pf_dd == nullptr) atomicOr(G.err, 1);
-        dst->gd = pf_gd;
-        dst->gs = pf_gs;
-        dst->ud = pf_ud;
-        dst->us = pf_us;
-        dst->dd = pf_dd;
-        dst->ds = pf_ds;
+        put(my_rank, pf_gd, pf_gs, pf_ud, pf_us, pf_dd, pf_ds);
       }
       for (int r = lane; r <= k; r += 64) {
         if (r < k) {
           if (!fast || r >= kk) {
-            // field copies (a struct temporary here ends up in scratch memory)
             const RbtExpertDev *src = G.table + (r < kk ? r_id[r] : 0);
-            RbtExpertDev *dst = G.pair_job + r;
             const bool use = r < kk;
             const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
             const uint8_t *dd = use ? src->dd : nullptr;
             const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
             const void *ds = use ? src->ds : nullptr;
             if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
-            dst->gd = gd;
-            dst->gs = gs;
-            dst->ud = ud;
-            dst->us = us;
-            dst->dd = dd;
-            dst->ds = ds;
+            put(r, gd, gs, ud, us, dd, ds);
           }
           G.pair_tok[r] = 0;
           G.tok_pair[r] = r < kk ? r : -1;
           G.tok_w[r] = r < kk ? s_w[r] : 0.0f;
         } else {
-          G.pair_job[k] = *G.shared_dev;
-          G.pair_tok[k] = 0;
+          copy_job(G.pair_job + G.shared_slot, G.shared_dev);
+          if (G.shared_slot == k) G.pair_tok[k] = 0;
+          if (G.down_job) {
+            copy_job(G.down_job + kk, G.shared_dev);
+            G.down_slot[kk] = G.shared_slot;
+          }
+          if (G.d1) {
+            G.d1->nr = kk;
+            G.d1->pending = 0;
+          }
         }
       }
     }
@@ -1821,7 +1858,7 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
     GroupOut G{};
     int g = 0;
     if (grp && a.S == 1) {
-      G = GroupOut{grp->table, grp->shared_dev, grp->pair_job, grp->pair_tok, grp->tok_pair, grp->tok_w, grp->err};
+      G = group_out(*grp, a.k);
       g = 1;
     }
     const int m = (a.E + 63) / 64;
@@ -1916,11 +1953,12 @@ __device__ __forceinline__ KeyRec make_key_rec(const SelParams &P, int e, double
 // One token, wave 0: the fast path of the selection above from the key records, in registers (DPP
 // reductions, readlane loops over the candidates). The threshold M is the kk-th largest lane
 // maximum, taken by kk rounds of wave maximum that each retire one lane; candidates, ranking, set
-// and order certification are those of the general path. Returns true (every lane) when the result
-// is certified without exact recomputation, after writing ids, weights and the job table; false
-// leaves the call to the general path.
+// and order certification are those of the general path. Returns (every lane) 1 when the result is
+// certified without exact recomputation, after writing ids, weights and the job tables; 2 when the
+// decision is deferred to the gate/up launch (task, routed pairs and the shared pair written); 0
+// to leave the call to the general path.
 template <int MAXM>
-__device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restrict__ rec,
+__device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restrict__ rec,
                              int32_t *__restrict__ ids, float *__restrict__ wts, const GroupOut &G, int grp) {
   const int lane = threadIdx.x & 63;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
@@ -1945,11 +1983,11 @@ __device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__rest
     const unsigned long long hit = __ballot(cur == M);
     if (lane == __ffsll((unsigned long long)hit) - 1) cur = 0;
   }
-  if (M == 0) return false;  // a key maps to 0 (a NaN)
+  if (M == 0) return 0;  // a key maps to 0 (a NaN)
   int nc = 0;
 #pragma unroll
   for (int m = 0; m < MAXM; m++) nc += __popcll(__ballot(ku[m] >= M));
-  if (nc > SEL_NC) return false;
+  if (nc > SEL_NC) return 0;
   uint32_t cm = 0;
   int base = 0;
 #pragma unroll
@@ -2000,21 +2038,78 @@ __device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__rest
   const bool iw = rank < kk;
   const float lo_sel = rbt_wave_min_f(iw ? clo : INFINITY);
   const float hi_uns = rbt_wave_max_f(fmaxf(hi_out, (cand && !iw) ? chi : -INFINITY));
-  // set membership: inexact experts on the wrong side of the other side's bound
-  bool amb = false;
+  // set membership: inexact experts on the wrong side of the other side's bound (nflag: the lane's
+  // non-candidate keys that might still win; cflag: the lane's candidate is not certain)
+  uint32_t nflag = 0;
 #pragma unroll
   for (int m = 0; m < MAXM; m++)
-    amb |= !((cm >> m) & 1u) && ku[m] != 0 && klo[m] != khi[m] && khi[m] >= lo_sel;
+    if (!((cm >> m) & 1u) && ku[m] != 0 && klo[m] != khi[m] && khi[m] >= lo_sel) nflag |= 1u << m;
   const bool cexact = clo == chi;
-  amb |= cand && !cexact && (iw ? clo <= hi_uns : chi >= lo_sel);
+  bool cflag = cand && !cexact && (iw ? clo <= hi_uns : chi >= lo_sel);
   // order: every pair of winners strictly ordered, or both exact
   for (int j = 0; j < nc; j++) {
     const int rj = __builtin_amdgcn_readlane(rank, j);
     const float lj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(clo), j));
     const float hj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(chi), j));
-    if (iw && !cexact && rj < kk && rj != rank) amb |= !(rj < rank ? lj > chi : clo > hj);
+    if (iw && !cexact && rj < kk && rj != rank) cflag |= !(rj < rank ? lj > chi : clo > hj);
   }
-  if (__ballot(amb) != 0) return false;
+  if (__ballot(cflag || nflag != 0) != 0) {
+    // Not certain. With a deferred-decision task: the routed pairs are the winners in midpoint
+    // rank order, then the candidates that might still win; the gate/up launch folds the flagged
+    // logits exactly and decides. Otherwise the general path recomputes here.
+    if (!grp || G.d1 == nullptr) return 0;
+    const bool undec = cand && !iw && cflag;
+    const unsigned long long um = __ballot(undec);
+    const int nuc = __popcll(um);
+    int nun = 0;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) nun += __popcll(__ballot((nflag >> m) & 1u));
+    const int nr = kk + nuc + nun;
+    if (nr > min(k + D1_KX, D1_NC)) return 0;
+    D1Task *T = G.d1;
+    auto task = [&](int slot, int id, uint32_t key, float logit, int flag) {
+      T->id[slot] = id;
+      T->ku[slot] = key;
+      T->lm[slot] = logit;
+      T->flag[slot] = flag;
+    };
+    auto put = [&](int slot) {
+      RbtExpertDev *dst = G.pair_job + slot;
+      dst->gd = pf_gd;
+      dst->gs = pf_gs;
+      dst->ud = pf_ud;
+      dst->us = pf_us;
+      dst->dd = pf_dd;
+      dst->ds = pf_ds;
+    };
+    if (iw) {
+      task(rank, cid, cku, cl, cflag ? 1 : 0);
+      put(rank);
+    }
+    if (undec) {
+      const int slot = kk + __popcll(um & lanemask_lt());
+      task(slot, cid, cku, cl, 1);
+      put(slot);
+    }
+    int base = kk + nuc;
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) {
+      const bool f = (nflag >> m) & 1u;
+      const unsigned long long fb = __ballot(f);
+      if (f) {
+        const int slot = base + __popcll(fb & lanemask_lt()), id = lane + 64 * m;
+        task(slot, id, ku[m], lm[m], 1);
+        copy_job(G.pair_job + slot, G.table + id);
+      }
+      base += __popcll(fb);
+    }
+    if (lane == 0) {
+      T->nr = nr;
+      T->pending = 1;
+      copy_job(G.pair_job + G.shared_slot, G.shared_dev);
+    }
+    return 2;
+  }
   // certified: weights in rank order, then the outputs
   if (iw) {
     L.r_id[rank] = cid;
@@ -2027,16 +2122,26 @@ __device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__rest
     wts[r] = r < kk ? L.s_w[r] : 0.0f;
   }
   if (grp) {
-    // single token: pair j = slot j; the shared expert is pair k
+    // single token: pair j = slot j; the shared expert is at G.shared_slot
     if (iw) {
-      RbtExpertDev *dst = G.pair_job + rank;
       if (pf_gd == nullptr || pf_dd == nullptr) atomicOr(G.err, 1);
+      RbtExpertDev *dst = G.pair_job + rank;
       dst->gd = pf_gd;
       dst->gs = pf_gs;
       dst->ud = pf_ud;
       dst->us = pf_us;
       dst->dd = pf_dd;
       dst->ds = pf_ds;
+      if (G.down_job) {
+        RbtExpertDev *dn = G.down_job + rank;
+        dn->gd = pf_gd;
+        dn->gs = pf_gs;
+        dn->ud = pf_ud;
+        dn->us = pf_us;
+        dn->dd = pf_dd;
+        dn->ds = pf_ds;
+        G.down_slot[rank] = rank;
+      }
     }
     for (int r = lane; r <= k; r += 64) {
       if (r < k) {
@@ -2053,12 +2158,20 @@ __device__ bool select4_fast(SelLds &L, const SelParams &P, const KeyRec *__rest
         G.tok_pair[r] = r < kk ? r : -1;
         G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
       } else {
-        G.pair_job[k] = *G.shared_dev;
-        G.pair_tok[k] = 0;
+        copy_job(G.pair_job + G.shared_slot, G.shared_dev);
+        if (G.shared_slot == k) G.pair_tok[k] = 0;
+        if (G.down_job) {
+          copy_job(G.down_job + kk, G.shared_dev);
+          G.down_slot[kk] = G.shared_slot;
+        }
+        if (G.d1) {
+          G.d1->nr = kk;
+          G.d1->pending = 0;
+        }
       }
     }
   }
-  return true;
+  return 1;
 }
 
 // Two router rows by the whole workgroup at once (one pass, shared scans and sums; per row the
@@ -2295,15 +2408,137 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
       // the register fast path from the key records; anything it cannot certify by itself (an
       // exact recomputation, many equal keys) goes through the general path from mid/bnd
       if (t < 64) {
-        const bool ok = select4_fast<MAXM>(L.sel, P, rec, ids, wts, G, grp);
-        if (t == 0) fast_ok = ok;
+        const int r = select4_fast<MAXM>(L.sel, P, rec, ids, wts, G, grp);
+        if (t == 0) fast_ok = r;
       }
       __syncthreads();
-      if (!fast_ok) select3_body<MAXM>(L.sel, P, mid, bnd, ids, wts, nullptr, stats, G, grp, 0);
+      if (fast_ok == 0) select3_body<MAXM>(L.sel, P, mid, bnd, ids, wts, nullptr, stats, G, grp, 0);
     }
   } else if (shared_dev != nullptr) {
     xgateup1_body<NCH>(L.gu, shared_dev, 1, P.x, I, hp_shared, b - 1, nwg - 1);
   }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Gate/up for one token with the router's decision deferred: workgroups 0 .. nwg-1 run the balanced
+// gate/up over the routed pairs the router launch published (nr of them, read on the device), and
+// workgroup nwg, when a decision is pending, folds the flagged logits as the reference does (the
+// sequential fp32 sum, four waves in parallel), ranks the published candidates with exact keys
+// where they were folded and midpoint keys elsewhere (an unflagged candidate's interval is
+// disjoint from every other candidate's, so its midpoint orders it), and writes ids, weights,
+// tok_pair / tok_w and the down job list.
+// ------------------------------------------------------------------------------------------------
+__device__ void d1_finish(SelLds &L, const SelParams &P, const D1Task *__restrict__ T, const GroupOut &G,
+                          int32_t *__restrict__ ids, float *__restrict__ wts, int *__restrict__ stats) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k = P.k, kk = min(P.k, P.E);
+  const int nc = T->nr;
+  if (threadIdx.x == 0) L.namb = 0;
+  __syncthreads();
+  if (wave == 0 && lane < nc && T->flag[lane]) L.amb[atomicAdd(&L.namb, 1)] = lane;
+  __syncthreads();
+  const int na = L.namb;
+  for (int j = wave; j < na; j += 4) {
+    const int c = L.amb[j];
+    const float l = exact_logit_wave(P.x, P.W + (size_t)T->id[c] * P.H, P.H);
+    if (lane == 0) L.amb_val[j] = l;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // candidate `lane` (pair slot `lane`) with its final key: exact where folded
+  const bool cand = lane < nc;
+  const int id = cand ? T->id[lane] : 0x7fffffff;
+  uint32_t key = cand ? T->ku[lane] : 0u;
+  float lm = cand ? T->lm[lane] : 0.0f;
+  for (int j = 0; j < na; j++)
+    if (L.amb[j] == lane) {
+      lm = L.amb_val[j];
+      const float lb = P.logit_bias ? P.logit_bias[id] : 0.0f;
+      const float rb = P.router_bias ? P.router_bias[id] : 0.0f;
+      key = ord_key(sel_key_v(P, lb, rb, lm));
+    }
+  int rank = 0;
+  for (int j = 0; j < nc; j++) {
+    const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)key, j);
+    const int oid = __builtin_amdgcn_readlane(id, j);
+    rank += (o > key) || (o == key && oid < id);
+  }
+  if (cand && rank < kk) {
+    L.r_id[rank] = id;
+    L.r_l[rank] = lm;
+    L.q_id[rank] = lane;  // pair slot of the rank-th winner
+  }
+  __builtin_amdgcn_wave_barrier();
+  winner_weights(L, P, kk);
+  for (int r = lane; r <= k; r += 64) {
+    if (r < k) {
+      ids[r] = r < kk ? L.r_id[r] : -1;
+      wts[r] = r < kk ? L.s_w[r] : 0.0f;
+      G.tok_pair[r] = r < kk ? L.q_id[r] : -1;
+      G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
+      if (r < kk) {
+        const RbtExpertDev *src = G.table + L.r_id[r];
+        if (src->gd == nullptr || src->dd == nullptr) atomicOr(G.err, 1);
+        copy_job(G.down_job + r, src);
+        G.down_slot[r] = L.q_id[r];
+      }
+    } else {
+      copy_job(G.down_job + kk, G.shared_dev);
+      G.down_slot[kk] = G.shared_slot;
+    }
+  }
+  if (lane == 0 && stats && na) atomicAdd(stats, na);
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void k_xgateup1f(const RbtExpertDev *__restrict__ jobs, const D1Task *__restrict__ T,
+                                                   const float *__restrict__ x, int I, __bf16 *__restrict__ hp,
+                                                   SelParams P, GroupOut G, int32_t *__restrict__ ids,
+                                                   float *__restrict__ wts, int *__restrict__ stats) {
+  __shared__ union {
+    GuLds gu;
+    SelLds sel;
+  } L;
+  const int nwg = gridDim.x - 1;
+  if ((int)blockIdx.x < nwg)
+    xgateup1_body<NCH>(L.gu, jobs, T->nr, x, I, hp, blockIdx.x, nwg);
+  else if (T->pending)
+    d1_finish(L.sel, P, T, G, ids, wts, stats);
+}
+
+static SelParams sel_params(const RouterArgs &a) {
+  SelParams P{};
+  P.family = a.family;
+  P.E = a.E;
+  P.erows = a.erows;
+  P.k = a.k;
+  P.H = a.H;
+  P.S = a.S;
+  P.logit_bias = a.logit_bias;
+  P.router_bias = a.router_bias;
+  P.norm_topk = a.norm_topk;
+  P.routed_scale = a.routed_scale;
+  P.n_group = a.n_group;
+  P.topk_group = a.topk_group;
+  P.x = a.x;
+  P.W = a.W;
+  return P;
+}
+
+hipError_t launch_xgateup1_d1(const Ctx &c, const RbtExpertDev *jobs, const D1Task *T, const float *x, int K, int I,
+                              __bf16 *hp, const RouterArgs &a, const GroupArgs &grp, int32_t *ids, float *wts,
+                              int *stats) {
+  if (I % 4 != 0 || c.num_cu < 2 || !grp.down_job || !grp.down_slot || !T) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  const GroupOut G = group_out(grp, a.k);
+  const dim3 grid(c.num_cu + 1);
+  if (K == 8192)
+    launch_k(c, k_xgateup1f<16>, grid, dim3(256), jobs, T, x, I, hp, P, G, ids, wts, stats);
+  else if (K == 7168)
+    launch_k(c, k_xgateup1f<14>, grid, dim3(256), jobs, T, x, I, hp, P, G, ids, wts, stats);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 size_t router1_sync_bytes() { return R1_SYNC_BYTES; }
@@ -2339,7 +2574,7 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
   GroupOut G{};
   int g = 0;
   if (grp) {
-    G = GroupOut{grp->table, grp->shared_dev, grp->pair_job, grp->pair_tok, grp->tok_pair, grp->tok_w, grp->err};
+    G = group_out(*grp, a.k);
     g = 1;
   }
   const RbtExpertDev *sd = sgu ? sgu->dev : nullptr;

@@ -385,9 +385,11 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
 // parts are staged in LDS once (no per-pair barriers); a wave streams its units' 16-byte code chunks
 // with four units (16 chunks) in flight, block scales for four units at a time through a
 // wave-private LDS window (one 16-byte load per lane), and leaves each unit's four row sums in LDS.
-// The ordered combine then runs per output row, in pair order with the shared pair last:
+// The ordered combine then runs per output row over the pair list: the winners in slot (rank)
+// order, the shared pair last:
 //   out[r] = (...(w_0 y_0[r] + w_1 y_1[r]) + ...) + w_s y_s[r]   (separate roundings)
-// the same order as the grid-per-row-block kernel above.
+// the reference's order (qwen38/generate.rs:303-349). The pair list is compact (its h may sit at
+// any pair slot), so the launch covers exactly the experts that are combined.
 // ------------------------------------------------------------------------------------------------
 constexpr int XD1_NP = 11;   // pairs whose h fits in LDS (top-10 + shared at I = 2048)
 constexpr int XD1_NW = 8;    // waves per workgroup
@@ -401,12 +403,15 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int NCH>
-__global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__restrict__ jobs, int npairs,
-                                                        const __bf16 *__restrict__ hp, int H, int k,
-                                                        const int *__restrict__ tok_pair,
+__global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__restrict__ jobs,
+                                                        const int *__restrict__ slots, int kk,
+                                                        const __bf16 *__restrict__ hp, int H,
                                                         const float *__restrict__ tok_w,
                                                         const float *__restrict__ sh_scale, int has_shared,
                                                         int gated, float *__restrict__ out) {
+  // pairs: the kk winners in slot order (jobs[j], h at pair slot slots[j], weight tok_w[j]), then
+  // the shared expert (jobs[kk], h at slots[kk], weight sh_scale when gated, else 1)
+  const int npairs = kk + (has_shared ? 1 : 0);
   constexpr int KD = NCH * 512, stride = KD + XG_PAD, SRD = KD >> 5;
   constexpr int PPP = 3 * KD / 8;                                  // 16-byte pieces of one pair's parts
   constexpr int HI = (XD1_NP * PPP + 64 * XD1_NW - 1) / (64 * XD1_NW);  // pieces per thread
@@ -454,40 +459,34 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     }
     sv = *(const rbt_gu4 *)(s_q == 0 ? sp[0] : s_q == 1 ? sp[1] : s_q == 2 ? sp[2] : sp[3]);
   }
-  // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside hp), in an order
-  // rotated by workgroup so that the grid does not read the same lines at the same time
+  // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside the pair list), in an
+  // order rotated by workgroup so that the grid does not read the same lines at the same time.
+  // Piece row ii spans pairs ii*512/PPP and the next one: their pair slots come from two
+  // wave-uniform loads.
   const int npc = npairs * PPP;
   rbt_u4 hr[HI];
   const int rot = blockIdx.x % HI;
 #pragma unroll
   for (int i = 0; i < HI; i++) {
     const int ii = i + rot < HI ? i + rot : i + rot - HI;
-    hr[i] = *(const rbt_gu4 *)(hp + 8L * min(tid + 64 * XD1_NW * ii, npc - 1));
+    const int e = min(tid + 64 * XD1_NW * ii, npc - 1), pp = e / PPP;
+    const int pa = min(64 * XD1_NW * ii / PPP, npairs - 1), pb = min(pa + 1, npairs - 1);
+    const int sa = slots[pa], sb = slots[pb];
+    const long slot = pp == pa ? sa : sb;
+    hr[i] = *(const rbt_gu4 *)(hp + 8L * (slot * PPP + (e - pp * PPP)));
   }
   if (tid < 32) zb[tid] = (__bf16)0.0f;
-  if (w == 0) {
-    // pair tables: lane j holds slot j's pair and weight, lane p pair p's job; pair p's weight is
-    // the weight of the last slot that uses it (pair k: the shared expert, scaled when gated)
-    const int tp = lane < k ? tok_pair[lane] : -1;
-    const float tw = lane < k ? tok_w[lane] : 0.0f;
-    const RbtExpertDev *J = jobs + min(lane, npairs - 1);
+  if (w == 0 && lane < npairs) {
+    // pair tables (lane p: pair p)
+    const RbtExpertDev *J = jobs + lane;
     const uint8_t *dd = J->dd;
     const uint8_t *ds = (const uint8_t *)J->ds;
-    const float shv = gated ? sh_scale[0] : 1.0f;
-    float wv = lane < k ? 0.0f : shv;
-    for (int j = 0; j < k; j++) {
-      const int tpj = __builtin_amdgcn_readlane(tp, j);
-      const float twj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tw), j));
-      if (lane < k && tpj == lane) wv = twj;
-    }
-    if (lane < npairs) {
-      const int live = dd != nullptr && ds != nullptr;
-      plive[lane] = live;
-      padd[lane] = live && (lane < k || has_shared);
-      pd[lane] = dd;
-      ps[lane] = ds;
-      pw[lane] = wv;
-    }
+    const int live = dd != nullptr && ds != nullptr;
+    plive[lane] = live;
+    padd[lane] = live;
+    pd[lane] = dd;
+    ps[lane] = ds;
+    pw[lane] = lane < kk ? tok_w[lane] : (gated ? sh_scale[0] : 1.0f);
   }
 #pragma unroll
   for (int i = 0; i < HI; i++) {
@@ -566,13 +565,13 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
 
 bool xdown1_ok(int npairs, size_t i) { return i == 2048 && npairs >= 1 && npairs <= XD1_NP; }
 
-hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int k,
-                         const int *tok_pair, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
+                         int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
                          float *out) {
   const int grid = c.num_cu;
-  if (!xdown1_ok(npairs, I) || H % 4 != 0 || grid <= 0 || (H / 4 + grid - 1) / grid > XD1_TPW)
+  if (!xdown1_ok(kk + (has_shared ? 1 : 0), I) || H % 4 != 0 || grid <= 0 || (H / 4 + grid - 1) / grid > XD1_TPW)
     return hipErrorInvalidValue;
-  launch_k(c, k_xdown1<4>, dim3(grid), dim3(64 * XD1_NW), jobs, npairs, hp, H, k, tok_pair, tok_w, sh_scale,
+  launch_k(c, k_xdown1<4>, dim3(grid), dim3(64 * XD1_NW), down_job, down_slot, kk, hp, H, tok_w, sh_scale,
            has_shared, gated, out);
   return hipGetLastError();
 }

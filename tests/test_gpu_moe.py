@@ -107,8 +107,13 @@ def test_moe_forward_full_config(ctx, orc, name, ntok):
 
 
 def test_router_ids_exact_over_many_tokens(ctx, orc):
-    """C1 router: ids bit-exact against the sequential fp32 fold for many tokens (exercises the
-    certified-interval path and its exact fallback on near-ties)."""
+    """C1 one-token calls (the three-launch decode): ids bit-exact against the sequential fp32 fold
+    over many tokens; for the tokens whose router decision needed exact folds (settled inside the
+    gate/up launch while the candidates stream) plus a sample of certified ones, outputs and weights
+    within 1e-5 relative L2 over the sample, and each token's output identical to the same token
+    through the two-token path (which settles its router decision before gate/up). A single
+    token's own relative L2 reaches about 1.1e-5 on both paths alike (fp32 accumulation order of
+    the matrix-core sums against the reference's sequential sums), hence the looser per-token bound."""
     import rabbit_amd.workloads as W
     from oracle.workload import HostLayer
     import torch
@@ -120,12 +125,29 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
     xt = torch.from_numpy(x).cuda()
     out = torch.empty(cfg.hidden, dtype=torch.float32, device="cuda")
     ids = torch.empty(cfg.topk, dtype=torch.int32, device="cuda")
-    got = []
+    w = torch.empty(cfg.topk, dtype=torch.float32, device="cuda")
+    ctx.profile_read(reset=True)
+    got, outs, ws, folded = [], {}, {}, []
     for t in range(ntok):
-        ctx.moe_forward(0, xt[t:t + 1].contiguous(), 1, out, ids)
+        ctx.moe_forward(0, xt[t:t + 1].contiguous(), 1, out, ids, w)
         got.append(ids.cpu().numpy().copy())
-    eids, _ = host.route(x)
+        if ctx.profile_read(reset=True)["ambiguous"]:
+            folded.append(t)
+        if folded and folded[-1] == t or t < 8:
+            outs[t], ws[t] = out.cpu().numpy().copy(), w.cpu().numpy().copy()
+    eids, ew = host.route(x)
     assert np.array_equal(np.stack(got), eids)
+    assert folded, "no token needed exact folds: the deferred decision was not exercised"
+    sample = sorted(set(folded[:24]) | set(range(8)))
+    exp, _, _ = host.forward(x[sample])
+    got_out = np.stack([outs[t] for t in sample])
+    assert rel_l2(got_out, exp.reshape(got_out.shape)) < RTOL
+    assert rel_l2(np.stack([ws[t] for t in sample]), ew[sample]) < RTOL
+    o2 = torch.empty(2 * cfg.hidden, dtype=torch.float32, device="cuda")
+    for i, t in enumerate(sample):
+        assert rel_l2(outs[t], exp[i]) < 3 * RTOL, (t, t in folded)
+        ctx.moe_forward(0, torch.cat([xt[t:t + 1], xt[t:t + 1]]).contiguous(), 2, o2)
+        assert np.array_equal(outs[t], o2[:cfg.hidden].cpu().numpy()), (t, t in folded)
 
 
 # ---- prefill: grouped GEMMs on the matrix cores (bf16 operands, fp32 accumulation) -------------
