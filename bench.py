@@ -32,7 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "MoE-layer decode µs/token + expert GEMV HBM GB/s (% of 8 TB/s), MXFP4"
 HBM_PEAK_GBPS = 8000.0
 # the gate/up kernel the MXFP4 decode path launches (its FETCH/WRITE counters: profiles/traffic_<cfg>.json)
-ROOFLINE_KERNEL = "rbt::k_xgateup1<16>"
+ROOFLINE_KERNEL = "rbt::k_xgateup1f<16>"
 
 
 def log(*a):
@@ -370,7 +370,7 @@ def main():
                    "topk": cfg.topk, "shared_expert": cfg.shared, "weights": "mxfp4" if cfg.kind == R.QT_MXFP4
                    else "int4-grouped", "tokens_per_step": 1, "resident_pool_gb": round(pool_gb, 2),
                    "graph_tokens": G},
-        "roofline": {"bound": "hbm", "kernel": "k_xgateup1 (gate/up + SiLU, MFMA on fp4->bf16 weights, balanced over all CUs)",
+        "roofline": {"bound": "hbm", "kernel": "k_xgateup1f (gate/up + SiLU, MFMA on fp4->bf16 weights, balanced over all CUs; settles deferred router decisions)",
                      "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": gu_bytes,
                      "launch_us": round(gu_us, 2), "traffic": traffic},

@@ -4,19 +4,22 @@
 // (kernels.rs:113-124, Iterator::sum) and selects on it; a tree reduction on the GPU would round
 // differently and could flip a near-tie at the k / k+1 boundary. Selection here is exact anyway:
 //
-//  1. k_router_logits: one workgroup per router row. It forms the products p_k = fl32(x_k w_k)
-//     exactly as the reference does, sums them in fp64 (S), and computes a rigorous bound B on
-//     |L_ref - S|, where L_ref is the reference's sequential fp32 result. With S_j the exact prefix
-//     sums, u = 2^-24, u' = u/(1-u) and T = sum_j |S_j|, the fold's error obeys
-//     |L_ref - S| <= u' T / (1 - n u'). T needs every prefix sum, so the workgroup runs a parallel
-//     fp64 scan. Extra slack covers the fp64 arithmetic itself.
-//  2. k_router_select: one wave per token. The fp32 interval [lo, hi] that must contain L_ref is
-//     pushed through the monotone key map (logit bias, sigmoid, selection bias), top-k is taken on
-//     the midpoints with the reference's tie rule (higher key first, lower expert id on ties), and
-//     then certified: every expert whose key interval could reach the selected set and overlaps
-//     another such interval gets its exact sequential fp32 fold recomputed (one lane each, same
-//     operation order as the reference). After that, every relevant comparison is either strict or
-//     an exact tie, so the ids are the reference's ids.
+//  1. Logits with certified intervals (k_router_logits_b / _t / _w, and inside k_router1): the
+//     products p_k = fl32(x_k w_k) exactly as the reference forms them, summed in fp64 (S), with a
+//     rigorous bound B on |L_ref - S|, where L_ref is the reference's sequential fp32 result. With
+//     S_j the exact prefix sums, u = 2^-24, u' = u/(1-u) and T = sum_j |S_j|, the fold's error
+//     obeys |L_ref - S| <= u' T / (1 - n u'). T needs every prefix sum (a parallel fp64 scan);
+//     extra slack covers the fp64 arithmetic itself. Batches of 64+ tokens instead fold every
+//     logit as the reference does (k_router_logits_exact), four folds per lane.
+//  2. Selection (select3_body, and its register fast path select4_fast): the fp32 interval
+//     [lo, hi] that must contain L_ref is pushed through the monotone key map (logit bias,
+//     sigmoid, selection bias), top-k is taken on the midpoints with the reference's tie rule
+//     (higher key first, lower expert id on ties), and then certified: every expert whose key
+//     interval could reach the selected set, or overlaps another winner's, gets its exact
+//     sequential fp32 fold recomputed (same operations in the same order as the reference). After
+//     that, every relevant comparison is either strict or an exact tie, so the ids are the
+//     reference's ids. One token: k_router1 runs logits, selection and the shared expert's gate/up
+//     in one launch, and may leave the exact folds to the gate/up launch (k_xgateup1f).
 //  3. k_group (several tokens): unique_experts order (glm52/moe.rs:333-344), per-expert token
 //     lists in token order, and per-token pick lists ordered by first occurrence.
 #include "rbt_device.h"
@@ -682,18 +685,8 @@ __global__ __launch_bounds__(64) void k_router_select_grouped(SelParams P, const
 }
 
 // ------------------------------------------------------------------------------------------------
-// Fast selection (n_group <= 1): 256 threads per token. Wave 0 holds lane-strided expert keys in
-// registers (expert e = lane + 64 m), takes the top-k with wave-wide argmax rounds and certifies
-// it; all four waves then recompute the ambiguous experts' logits exactly.
+// Exact recomputation of one router logit (selection near-ties)
 // ------------------------------------------------------------------------------------------------
-template <int MAXM>
-__device__ __forceinline__ float pick(const float (&a)[MAXM], int m) {
-  float v = a[0];
-#pragma unroll
-  for (int j = 1; j < MAXM; j++) v = (m == j) ? a[j] : v;
-  return v;
-}
-
 // The reference's sequential fold, computed by one whole wave: lanes form the products of a block
 // of 64 x 32 elements in parallel (the next block's loads are already in flight), then the running
 // fp32 sum walks the block lane by lane: lane l adds its 32 products in order and v_readlane hands
@@ -749,206 +742,10 @@ __device__ float exact_logit_wave(const float *__restrict__ xs, const float *__r
   return acc;
 }
 
-template <int MAXM>
-__device__ __forceinline__ void reg_topk(const SelParams &P, const float (&kmid)[MAXM], const float (&lmid)[MAXM],
-                                         const float (&klo)[MAXM], int kk, int *sel, float *sel_l, float *sel_lo,
-                                         uint32_t *taken_out) {
-  const int lane = threadIdx.x & 63;
-  uint32_t taken = 0;
-  for (int r = 0; r < kk; r++) {
-    float bk = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      if (e < P.E && !((taken >> m) & 1u) && (bi == 0x7fffffff || ranks_before(kmid[m], e, bk, bi))) {
-        bk = kmid[m];
-        bi = e;
-      }
-    }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-      const float ok = __shfl_xor(bk, d, 64);
-      const int oi = __shfl_xor(bi, d, 64);
-      if (oi != 0x7fffffff && (bi == 0x7fffffff || ranks_before(ok, oi, bk, bi))) {
-        bk = ok;
-        bi = oi;
-      }
-    }
-    if (bi != 0x7fffffff && (bi & 63) == lane) {
-      const int m = bi >> 6;
-      taken |= 1u << m;
-      sel[r] = bi;
-      sel_l[r] = pick<MAXM>(lmid, m);
-      sel_lo[r] = pick<MAXM>(klo, m);
-    }
-  }
-  *taken_out = taken;
-}
-
-template <int MAXM>
-__global__ __launch_bounds__(256) void k_router_select(SelParams P, const double *__restrict__ mid,
-                                                       const double *__restrict__ bnd, int32_t *__restrict__ ids,
-                                                       float *__restrict__ wts, float *__restrict__ sh_scale,
-                                                       int *__restrict__ stats) {
-  __shared__ int sel[SEL_MAXK];
-  __shared__ float sel_l[SEL_MAXK], sel_lo[SEL_MAXK];
-  __shared__ int rlist[SEL_MAXE];
-  __shared__ float rlo[SEL_MAXE], rhi[SEL_MAXE];
-  __shared__ unsigned char rex[SEL_MAXE];
-  __shared__ int amb[SEL_MAXE];
-  __shared__ float amb_val[SEL_MAXE];
-  __shared__ int namb, nR;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int s = blockIdx.x;
-  const int E = P.E, k = P.k, kk = min(P.k, P.E);
-  const double *ms = mid + (size_t)s * P.erows;
-  const double *bs = bnd + (size_t)s * P.erows;
-
-  float klo[MAXM], khi[MAXM], kmid[MAXM], lmid[MAXM];
-  uint32_t exact = 0, taken = 0;
-  if (wave == 0) {
-    // all loads first, so the wave waits on memory once rather than once per expert
-    double mv[MAXM], bv[MAXM];
-    float lbv[MAXM], rbv[MAXM];
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads batch together
-      mv[m] = ms[e];
-      bv[m] = bs[e];
-      lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
-      rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
-    }
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      klo[m] = khi[m] = kmid[m] = lmid[m] = -INFINITY;
-      if (e < E) {
-        const double mm = mv[m], b = bv[m];
-        const float lo = __double2float_rd(mm - b * (1.0 + 1e-12));
-        const float hi = __double2float_ru(mm + b * (1.0 + 1e-12));
-        const float md = fminf(fmaxf(__double2float_rn(mm), lo), hi);
-        lmid[m] = md;
-        kmid[m] = sel_key_v(P, lbv[m], rbv[m], md);
-        if (lo == hi) {
-          klo[m] = khi[m] = kmid[m];
-          exact |= 1u << m;
-        } else {
-          klo[m] = sel_key_v(P, lbv[m], rbv[m], lo);
-          khi[m] = sel_key_v(P, lbv[m], rbv[m], hi);
-        }
-      }
-    }
-    reg_topk<MAXM>(P, kmid, lmid, klo, kk, sel, sel_l, sel_lo, &taken);
-    // lowest lower key among the selected
-    float lo_sel = INFINITY;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++)
-      if ((taken >> m) & 1u) lo_sel = fminf(lo_sel, klo[m]);
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) lo_sel = fminf(lo_sel, __shfl_xor(lo_sel, d, 64));
-    // R = experts whose upper key reaches lo_sel, compacted in (m, lane) order.
-    int base = 0;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      const bool in = e < E && khi[m] >= lo_sel;
-      const unsigned long long mask = __ballot(in);
-      if (in) {
-        const int at = base + __popcll(mask & ((1ull << lane) - 1ull));
-        rlist[at] = e;
-        rlo[at] = klo[m];
-        rhi[at] = khi[m];
-        rex[at] = (exact >> m) & 1u;
-      }
-      base += __popcll(mask);
-    }
-    if (lane == 0) {
-      nR = base;
-      namb = 0;
-    }
-  }
-  __syncthreads();
-  if (wave == 0) {
-    const int n = nR;
-    for (int j = lane; j < n; j += 64) {
-      if (rex[j]) continue;
-      bool a = false;
-      for (int q = 0; q < n && !a; q++)
-        if (q != j && rlo[j] <= rhi[q] && rlo[q] <= rhi[j]) a = true;
-      if (a) amb[atomicAdd(&namb, 1)] = rlist[j];
-    }
-  }
-  __syncthreads();
-  const int na = namb;
-  if (na > 0) {
-    for (int j = wave; j < na; j += 4) {
-      const float l = exact_logit_wave(P.x + (size_t)s * P.H, P.W + (size_t)amb[j] * P.H, P.H);
-      if (lane == 0) amb_val[j] = l;
-    }
-    __syncthreads();
-    if (wave == 0) {
-      for (int j = 0; j < na; j++) {
-        const int e = amb[j];
-        if ((e & 63) == lane) {
-          const int mm = e >> 6;
-          const float l = amb_val[j];
-          const float key = sel_key(P, e, l);
-#pragma unroll
-          for (int m = 0; m < MAXM; m++)
-            if (m == mm) {
-              lmid[m] = l;
-              kmid[m] = klo[m] = khi[m] = key;
-            }
-        }
-      }
-      reg_topk<MAXM>(P, kmid, lmid, klo, kk, sel, sel_l, sel_lo, &taken);
-    }
-    if (wave == 0 && lane == 0 && stats) atomicAdd(stats, na);
-  }
-  __syncthreads();
-  if (wave == 0 && lane == 0) {
-    int32_t *io = ids + (size_t)s * k;
-    float *wo = wts + (size_t)s * k;
-    float *lv = sel_lo;  // reused as the weight workspace (LDS)
-    for (int r = 0; r < kk; r++) {
-      const int e = sel[r];
-      lv[r] = P.logit_bias ? __fadd_rn(sel_l[r], P.logit_bias[e]) : sel_l[r];
-    }
-    if (P.family == RBT_FAMILY_QWEN38) {
-      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
-      const float mx = lv[0];
-      float sum = 0.0f;
-      for (int r = 0; r < kk; r++) {
-        lv[r] = (float)exp((double)__fsub_rn(lv[r], mx));
-        sum = __fadd_rn(sum, lv[r]);
-      }
-      for (int r = 0; r < kk; r++) wo[r] = __fdiv_rn(lv[r], sum);
-    } else {
-      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
-      for (int r = 0; r < kk; r++) lv[r] = sigmoid_ref(lv[r]);
-      if (P.norm_topk) {
-        float sum = -0.0f;
-        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, lv[r]);
-        sum = __fadd_rn(sum, 1e-20f);
-        for (int r = 0; r < kk; r++) lv[r] = __fdiv_rn(lv[r], sum);
-      }
-      for (int r = 0; r < kk; r++) wo[r] = __fmul_rn(lv[r], P.routed_scale);
-    }
-    for (int r = 0; r < kk; r++) io[r] = sel[r];
-    for (int r = kk; r < k; r++) {
-      io[r] = -1;
-      wo[r] = 0.0f;
-    }
-    if (sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
-  }
-}
 
 // ------------------------------------------------------------------------------------------------
-// Selection v2 (n_group <= 1): the k-th largest key is found exactly by a bitwise bisection over
-// order-preserving key bits, counting with wave ballots (no cross-lane data movement); ties at that
-// key go to the lowest ids, as the reference's strict-> scans do; the k winners are then ranked in
-// parallel. With `grp` set (one token per call) the kernel also writes the expert job table.
+// Selection helpers: order-preserving key bits (0 is left for "no expert"), lane masks, and the
+// one-token job-table outputs.
 // ------------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t ord_key(float f) {
   const uint32_t b = __float_as_uint(f + 0.0f);  // -0 -> +0: equal keys compare equal
@@ -989,236 +786,6 @@ __device__ __forceinline__ void copy_job(RbtExpertDev *dst, const RbtExpertDev *
   dst->us = us;
   dst->dd = dd;
   dst->ds = ds;
-}
-
-template <int MAXM>
-__device__ void bisect_topk(const uint32_t (&ku)[MAXM], uint32_t valid, int E, int kk, int *sel_id, uint32_t *sel_ku,
-                            int *nsel_out) {
-  const int lane = threadIdx.x & 63;
-  uint32_t T = 0;
-  for (int bit = 31; bit >= 0; bit--) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) cnt += __popcll(__ballot(((valid >> m) & 1u) && ku[m] >= cand));
-    if (cnt >= kk) T = cand;
-  }
-  int ngt = 0;
-#pragma unroll
-  for (int m = 0; m < MAXM; m++) ngt += __popcll(__ballot(((valid >> m) & 1u) && ku[m] > T));
-  const int need = kk - ngt;  // >= 1 winners at exactly T, lowest ids first
-  int taken_eq = 0, base = 0;
-#pragma unroll
-  for (int m = 0; m < MAXM; m++) {
-    const bool v = (valid >> m) & 1u;
-    const unsigned long long eq = __ballot(v && ku[m] == T);
-    const bool win_eq = v && ku[m] == T && (taken_eq + __popcll(eq & lanemask_lt())) < need;
-    taken_eq += __popcll(eq);
-    const bool win = (v && ku[m] > T) || win_eq;
-    const unsigned long long wm = __ballot(win);
-    if (win) {
-      const int at = base + __popcll(wm & lanemask_lt());
-      sel_id[at] = lane + 64 * m;
-      sel_ku[at] = ku[m];
-    }
-    base += __popcll(wm);
-  }
-  if (lane == 0) *nsel_out = base;
-}
-
-template <int MAXM>
-__global__ __launch_bounds__(256) void k_router_select2(SelParams P, const double *__restrict__ mid,
-                                                        const double *__restrict__ bnd, int32_t *__restrict__ ids,
-                                                        float *__restrict__ wts, float *__restrict__ sh_scale,
-                                                        int *__restrict__ stats, GroupOut G, int grp) {
-  __shared__ int c_id[SEL_MAXK];      // winners in id order
-  __shared__ uint32_t c_ku[SEL_MAXK];
-  __shared__ int s_id[SEL_MAXK];      // winners in rank order
-  __shared__ float s_w[SEL_MAXK];
-  __shared__ float key_lo[SEL_MAXE], key_hi[SEL_MAXE], lval[SEL_MAXE];
-  __shared__ int rlist[SEL_MAXE];
-  __shared__ int amb[SEL_MAXE];
-  __shared__ float amb_val[SEL_MAXE];
-  __shared__ int nsel, namb;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int s = blockIdx.x;
-  const int E = P.E, k = P.k, kk = min(P.k, P.E);
-  const double *ms = mid + (size_t)s * P.erows;
-  const double *bs = bnd + (size_t)s * P.erows;
-
-  uint32_t ku[MAXM];
-  uint32_t valid = 0, exact = 0;
-  if (wave == 0) {
-    double mv[MAXM], bv[MAXM];
-    float lbv[MAXM], rbv[MAXM];
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads batch together
-      mv[m] = ms[e];
-      bv[m] = bs[e];
-      lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
-      rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
-    }
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      ku[m] = 0;
-      if (e < E) {
-        valid |= 1u << m;
-        const float lo = __double2float_rd(mv[m] - bv[m] * (1.0 + 1e-12));
-        const float hi = __double2float_ru(mv[m] + bv[m] * (1.0 + 1e-12));
-        const float md = fminf(fmaxf(__double2float_rn(mv[m]), lo), hi);
-        const float kmid = sel_key_v(P, lbv[m], rbv[m], md);
-        ku[m] = ord_key(kmid);
-        lval[e] = md;
-        if (lo == hi) {
-          key_lo[e] = key_hi[e] = kmid;
-          exact |= 1u << m;
-        } else {
-          key_lo[e] = sel_key_v(P, lbv[m], rbv[m], lo);
-          key_hi[e] = sel_key_v(P, lbv[m], rbv[m], hi);
-        }
-      }
-    }
-    bisect_topk<MAXM>(ku, valid, E, kk, c_id, c_ku, &nsel);
-    // certification: R = experts whose upper key reaches the lowest selected lower key
-    float lo = INFINITY;
-    for (int j = lane; j < kk; j += 64) lo = fminf(lo, key_lo[c_id[j]]);
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) lo = fminf(lo, __shfl_xor(lo, d, 64));
-    int base = 0;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      const bool in = ((valid >> m) & 1u) && !((exact >> m) & 1u) && key_hi[min(e, E - 1)] >= lo;
-      const unsigned long long msk = __ballot(in);
-      if (in) rlist[base + __popcll(msk & lanemask_lt())] = e;
-      base += __popcll(msk);
-    }
-    // exact members of R matter too: a non-exact expert overlapping an exact one is ambiguous
-    int nr_inexact = base;
-#pragma unroll
-    for (int m = 0; m < MAXM; m++) {
-      const int e = lane + 64 * m;
-      const bool in = ((valid >> m) & 1u) && ((exact >> m) & 1u) && key_hi[min(e, E - 1)] >= lo;
-      const unsigned long long msk = __ballot(in);
-      if (in) rlist[base + __popcll(msk & lanemask_lt())] = e;
-      base += __popcll(msk);
-    }
-    if (lane == 0) namb = 0;
-    __builtin_amdgcn_wave_barrier();
-    for (int j = lane; j < nr_inexact; j += 64) {
-      const int e = rlist[j];
-      bool a = false;
-      for (int q = 0; q < base && !a; q++) {
-        const int f = rlist[q];
-        if (f != e && key_lo[e] <= key_hi[f] && key_lo[f] <= key_hi[e]) a = true;
-      }
-      if (a) amb[atomicAdd(&namb, 1)] = e;
-    }
-  }
-  __syncthreads();
-  const int na = namb;
-  if (na > 0) {
-    for (int j = wave; j < na; j += 4) {
-      const float l = exact_logit_wave(P.x + (size_t)s * P.H, P.W + (size_t)amb[j] * P.H, P.H);
-      if (lane == 0) amb_val[j] = l;
-    }
-    __syncthreads();
-    if (wave == 0) {
-      for (int j = 0; j < na; j++) {
-        const int e = amb[j];
-        if ((e & 63) == lane) {
-          const int mm = e >> 6;
-          const float l = amb_val[j];
-          const float key = sel_key(P, e, l);
-          lval[e] = l;
-#pragma unroll
-          for (int m = 0; m < MAXM; m++)
-            if (m == mm) ku[m] = ord_key(key);
-        }
-      }
-      bisect_topk<MAXM>(ku, valid, E, kk, c_id, c_ku, &nsel);
-    }
-    if (wave == 0 && lane == 0 && stats) atomicAdd(stats, na);
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // rank the winners: (key desc, id asc)
-    if (lane < kk) {
-      const uint32_t my = c_ku[lane];
-      const int id = c_id[lane];
-      int rank = 0;
-      for (int j = 0; j < kk; j++) {
-        const uint32_t o = c_ku[j];
-        rank += (o > my) || (o == my && c_id[j] < id);
-      }
-      s_id[rank] = id;
-    }
-    __builtin_amdgcn_wave_barrier();
-    // weights, computed by the lanes in parallel; the sums run in rank order (lane 0)
-    float lv = 0.0f;
-    if (lane < kk) {
-      const int e = s_id[lane];
-      lv = P.logit_bias ? __fadd_rn(lval[e], P.logit_bias[e]) : lval[e];
-    }
-    if (P.family == RBT_FAMILY_QWEN38) {
-      // qwen38/moe.rs:66-74: softmax over the winners' logits, max-subtracted.
-      const float mx = __shfl(lv, 0, 64);
-      if (lane < kk) s_w[lane] = (float)exp((double)__fsub_rn(lv, mx));
-      __builtin_amdgcn_wave_barrier();
-      float sum = 0.0f;
-      for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
-      if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
-    } else {
-      // glm52/moe.rs:231-241: weight = plain sigmoid; norm_topk; routed_scale.
-      if (lane < kk) s_w[lane] = sigmoid_ref(lv);
-      __builtin_amdgcn_wave_barrier();
-      if (P.norm_topk) {
-        float sum = -0.0f;
-        for (int r = 0; r < kk; r++) sum = __fadd_rn(sum, s_w[r]);
-        sum = __fadd_rn(sum, 1e-20f);
-        if (lane < kk) s_w[lane] = __fdiv_rn(s_w[lane], sum);
-      }
-      if (lane < kk) s_w[lane] = __fmul_rn(s_w[lane], P.routed_scale);
-    }
-    __builtin_amdgcn_wave_barrier();
-    int32_t *io = ids + (size_t)s * k;
-    float *wo = wts + (size_t)s * k;
-    for (int r = lane; r < k; r += 64) {
-      io[r] = r < kk ? s_id[r] : -1;
-      wo[r] = r < kk ? s_w[r] : 0.0f;
-    }
-    if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
-    if (grp) {
-      // single token: pair j = slot j; the shared expert is pair k
-      for (int r = lane; r <= k; r += 64) {
-        if (r < k) {
-          // field copies (a struct temporary here ends up in scratch memory)
-          const RbtExpertDev *src = G.table + (r < kk ? s_id[r] : 0);
-          RbtExpertDev *dst = G.pair_job + r;
-          const bool use = r < kk;
-          const uint8_t *gd = use ? src->gd : nullptr, *ud = use ? src->ud : nullptr;
-          const uint8_t *dd = use ? src->dd : nullptr;
-          const void *gs = use ? src->gs : nullptr, *us = use ? src->us : nullptr;
-          const void *ds = use ? src->ds : nullptr;
-          if (use && (gd == nullptr || dd == nullptr)) atomicOr(G.err, 1);
-          dst->gd = gd;
-          dst->gs = gs;
-          dst->ud = ud;
-          dst->us = us;
-          dst->dd = dd;
-          dst->ds = ds;
-          G.pair_tok[r] = 0;
-          G.tok_pair[r] = r < kk ? r : -1;
-          G.tok_w[r] = r < kk ? s_w[r] : 0.0f;
-        } else {
-          G.pair_job[k] = *G.shared_dev;
-          G.pair_tok[k] = 0;
-        }
-      }
-    }
-  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2420,9 +1987,9 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
 }
 
 // ------------------------------------------------------------------------------------------------
-// Gate/up for one token with the router's decision deferred: workgroups 0 .. nwg-1 run the balanced
+// Gate/up for one token with the router's decision deferred: workgroups 1 .. num_cu run the balanced
 // gate/up over the routed pairs the router launch published (nr of them, read on the device), and
-// workgroup nwg, when a decision is pending, folds the flagged logits as the reference does (the
+// workgroup 0, when a decision is pending, folds the flagged logits as the reference does (the
 // sequential fp32 sum, four waves in parallel), ranks the published candidates with exact keys
 // where they were folded and midpoint keys elsewhere (an unflagged candidate's interval is
 // disjoint from every other candidate's, so its midpoint orders it), and writes ids, weights,
@@ -2499,11 +2066,15 @@ __global__ __launch_bounds__(256) void k_xgateup1f(const RbtExpertDev *__restric
     GuLds gu;
     SelLds sel;
   } L;
-  const int nwg = gridDim.x - 1;
-  if ((int)blockIdx.x < nwg)
-    xgateup1_body<NCH>(L.gu, jobs, T->nr, x, I, hp, blockIdx.x, nwg);
-  else if (T->pending)
+  // workgroup 0 (dispatched first) settles a pending decision at raised wave priority (its serial
+  // fold chains then win the issue arbitration of the CU it shares with a gate/up workgroup); the
+  // other num_cu workgroups run the balanced gate/up
+  if (blockIdx.x > 0) {
+    xgateup1_body<NCH>(L.gu, jobs, T->nr, x, I, hp, blockIdx.x - 1, gridDim.x - 1);
+  } else if (T->pending) {
+    __builtin_amdgcn_s_setprio(3);
     d1_finish(L.sel, P, T, G, ids, wts, stats);
+  }
 }
 
 static SelParams sel_params(const RouterArgs &a) {
