@@ -395,6 +395,7 @@ constexpr int XD1_NP = 11;   // pairs whose h fits in LDS (top-10 + shared at I 
 constexpr int XD1_NW = 8;    // waves per workgroup
 constexpr int XD1_TPW = 16;  // most 4-row tiles per workgroup
 
+
 // Barrier for LDS hand-offs only: global loads in flight stay in flight.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
@@ -435,34 +436,45 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
   const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
   const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
-  // First window (units u0 .. u0+3): pointers straight from the job table with wave-uniform
-  // (scalar) loads, so the weight stream starts at once; the tables in LDS serve the rest.
-  rbt_u4 ring[4][NCH], sv;
-  {
-    const uint8_t *sp[4];
+  // Prologue. vmcnt counts loads in issue order, so everything the staging barrier waits for (the h
+  // parts, the pair tables, the first scale window) is issued before the first window's weights:
+  // the h pieces come from L2 while the weights (128 KB per CU, all CUs at once) take the HBM's time,
+  // and waiting for the h pieces then does not mean waiting for the weights.
+  // Pair tables first, as one vector load per lane (lane p: pair p's pointers, slot and weight;
+  // clamped): the table was written by the previous launch, possibly on another XCD, so every load
+  // of it is a trip to memory, and chains of dependent scalar loads would pay that trip each time.
+  const int tp = min(lane, npairs - 1);
+  const RbtExpertDev *J = jobs + tp;
+  const uint8_t *t_dd = J->dd;
+  const uint8_t *t_ds = (const uint8_t *)J->ds;
+  const int t_slot = slots[tp];
+  const float t_w = tp < kk ? tok_w[min(tp, kk - 1)] : (gated ? sh_scale[0] : 1.0f);
+  auto lane_ptr = [](const uint8_t *p, int l) -> const uint8_t * {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+    return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+  };
+  // First window (units u0 .. u0+3): pointers from the tables' lanes (the pair is wave-uniform).
+  const uint8_t *cp[4], *sp[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int u = u0 + j;
-      const uint8_t *cp = dummy;
-      sp[j] = hb8 + 16 * s_seg;
-      if (u < u1) {
-        const int tl = u / npairs, pp = u - tl * npairs;
-        const uint8_t *dd = jobs[pp].dd;
-        const uint8_t *ds = (const uint8_t *)jobs[pp].ds;
-        if (dd != nullptr && ds != nullptr) {
-          cp = dd + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g;
-          sp[j] = ds + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
-        }
+  for (int j = 0; j < 4; j++) {
+    const int u = u0 + j;
+    cp[j] = dummy;
+    sp[j] = hb8 + 16 * s_seg;
+    if (u < u1) {
+      const int tl = u / npairs, pp = u - tl * npairs;
+      const uint8_t *dd = lane_ptr(t_dd, pp);
+      const uint8_t *ds = lane_ptr(t_ds, pp);
+      if (dd != nullptr && ds != nullptr) {
+        cp[j] = dd + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g;
+        sp[j] = ds + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
       }
-#pragma unroll
-      for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp + 256 * c));
     }
-    sv = *(const rbt_gu4 *)(s_q == 0 ? sp[0] : s_q == 1 ? sp[1] : s_q == 2 ? sp[2] : sp[3]);
   }
   // h parts of every pair: pieces e = tid + 512 i (clamped reads stay inside the pair list), in an
   // order rotated by workgroup so that the grid does not read the same lines at the same time.
-  // Piece row ii spans pairs ii*512/PPP and the next one: their pair slots come from two
-  // wave-uniform loads.
+  // Piece row ii spans pairs ii*512/PPP and the next one (their slots from the tables' lanes).
   const int npc = npairs * PPP;
   rbt_u4 hr[HI];
   const int rot = blockIdx.x % HI;
@@ -471,22 +483,26 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     const int ii = i + rot < HI ? i + rot : i + rot - HI;
     const int e = min(tid + 64 * XD1_NW * ii, npc - 1), pp = e / PPP;
     const int pa = min(64 * XD1_NW * ii / PPP, npairs - 1), pb = min(pa + 1, npairs - 1);
-    const int sa = slots[pa], sb = slots[pb];
+    const int sa = __builtin_amdgcn_readlane(t_slot, pa), sb = __builtin_amdgcn_readlane(t_slot, pb);
     const long slot = pp == pa ? sa : sb;
     hr[i] = *(const rbt_gu4 *)(hp + 8L * (slot * PPP + (e - pp * PPP)));
   }
+  rbt_u4 sv = *(const rbt_gu4 *)(s_q == 0 ? sp[0] : s_q == 1 ? sp[1] : s_q == 2 ? sp[2] : sp[3]);
+  __builtin_amdgcn_sched_barrier(0);
+  rbt_u4 ring[4][NCH];
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp[j] + 256 * c));
+  __builtin_amdgcn_sched_barrier(0);
   if (tid < 32) zb[tid] = (__bf16)0.0f;
   if (w == 0 && lane < npairs) {
-    // pair tables (lane p: pair p)
-    const RbtExpertDev *J = jobs + lane;
-    const uint8_t *dd = J->dd;
-    const uint8_t *ds = (const uint8_t *)J->ds;
-    const int live = dd != nullptr && ds != nullptr;
+    const int live = t_dd != nullptr && t_ds != nullptr;
     plive[lane] = live;
     padd[lane] = live;
-    pd[lane] = dd;
-    ps[lane] = ds;
-    pw[lane] = lane < kk ? tok_w[lane] : (gated ? sh_scale[0] : 1.0f);
+    pd[lane] = t_dd;
+    ps[lane] = t_ds;
+    pw[lane] = t_w;
   }
 #pragma unroll
   for (int i = 0; i < HI; i++) {
