@@ -743,6 +743,75 @@ __device__ float exact_logit_wave(const float *__restrict__ xs, const float *__r
 }
 
 
+// The same fold with the serial chain on one lane, for a wave that has a 2 x 1024-float LDS buffer
+// of its own: the wave forms the products of 1024-element blocks in parallel into the buffer, in
+// element order, and lane 0 walks the previous block with 16-byte LDS reads (two groups of eight in
+// flight) and dependent adds, the next block's loads already in flight. No exec-mask or readlane
+// hand-offs sit on the chain. Same operations in the same order as the reference. Needs H % 1024 ==
+// 0 and 16-byte aligned rows (else exact_logit_wave).
+__device__ float exact_logit_lds(const float *__restrict__ xs, const float *__restrict__ w, int H,
+                                 float (*buf)[1024]) {
+  const int lane = threadIdx.x & 63;
+  if ((H & 1023) || ((reinterpret_cast<uintptr_t>(xs) | reinterpret_cast<uintptr_t>(w)) & 15))
+    return exact_logit_wave(xs, w, H);
+  const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+  const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  const int nb = H >> 10;
+  float4 xa[4], wa[4];
+  auto fetch = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      xa[j] = x4[256 * b + 64 * j + lane];
+      wa[j] = w4[256 * b + 64 * j + lane];
+    }
+  };
+  auto put = [&](int b) {
+    float4 *d = reinterpret_cast<float4 *>(buf[b & 1]);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      d[64 * j + lane] = make_float4(__fmul_rn(xa[j].x, wa[j].x), __fmul_rn(xa[j].y, wa[j].y),
+                                     __fmul_rn(xa[j].z, wa[j].z), __fmul_rn(xa[j].w, wa[j].w));
+  };
+  fetch(0);
+  put(0);
+  if (nb > 1) fetch(1);
+  float acc = -0.0f;
+  for (int b = 0; b < nb; b++) {
+    if (lane == 0) {
+      const float4 *pb = reinterpret_cast<const float4 *>(buf[b & 1]);
+      float4 a[8], c[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) a[u] = pb[u];
+      for (int i = 0; i < 256; i += 16) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) c[u] = pb[i + 8 + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          acc = __fadd_rn(acc, a[u].x);
+          acc = __fadd_rn(acc, a[u].y);
+          acc = __fadd_rn(acc, a[u].z);
+          acc = __fadd_rn(acc, a[u].w);
+        }
+        const int jn = (i + 16) & 255;  // past the block: wraps to its start (read, unused)
+#pragma unroll
+        for (int u = 0; u < 8; u++) a[u] = pb[jn + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          acc = __fadd_rn(acc, c[u].x);
+          acc = __fadd_rn(acc, c[u].y);
+          acc = __fadd_rn(acc, c[u].z);
+          acc = __fadd_rn(acc, c[u].w);
+        }
+      }
+    }
+    if (b + 1 < nb) {
+      put(b + 1);
+      if (b + 2 < nb) fetch(b + 2);
+    }
+  }
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), 0));
+}
+
 // ------------------------------------------------------------------------------------------------
 // Selection helpers: order-preserving key bits (0 is left for "no expert"), lane masks, and the
 // one-token job-table outputs.
@@ -1995,8 +2064,9 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
 // disjoint from every other candidate's, so its midpoint orders it), and writes ids, weights,
 // tok_pair / tok_w and the down job list.
 // ------------------------------------------------------------------------------------------------
-__device__ void d1_finish(SelLds &L, const SelParams &P, const D1Task *__restrict__ T, const GroupOut &G,
-                          int32_t *__restrict__ ids, float *__restrict__ wts, int *__restrict__ stats) {
+__device__ void d1_finish(SelLds &L, float (*fold)[2][1024], const SelParams &P, const D1Task *__restrict__ T,
+                          const GroupOut &G, int32_t *__restrict__ ids, float *__restrict__ wts,
+                          int *__restrict__ stats) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int k = P.k, kk = min(P.k, P.E);
   const int nc = T->nr;
@@ -2007,7 +2077,7 @@ __device__ void d1_finish(SelLds &L, const SelParams &P, const D1Task *__restric
   const int na = L.namb;
   for (int j = wave; j < na; j += 4) {
     const int c = L.amb[j];
-    const float l = exact_logit_wave(P.x, P.W + (size_t)T->id[c] * P.H, P.H);
+    const float l = exact_logit_lds(P.x, P.W + (size_t)T->id[c] * P.H, P.H, fold[wave]);
     if (lane == 0) L.amb_val[j] = l;
   }
   __syncthreads();
@@ -2064,7 +2134,10 @@ __global__ __launch_bounds__(256) void k_xgateup1f(const RbtExpertDev *__restric
                                                    float *__restrict__ wts, int *__restrict__ stats) {
   __shared__ union {
     GuLds gu;
-    SelLds sel;
+    struct {
+      SelLds sel;
+      __attribute__((aligned(16))) float fold[4][2][1024];  // per wave: exact_logit_lds's blocks
+    } d1;
   } L;
   // workgroup 0 (dispatched first) settles a pending decision at raised wave priority (its serial
   // fold chains then win the issue arbitration of the CU it shares with a gate/up workgroup); the
@@ -2073,7 +2146,7 @@ __global__ __launch_bounds__(256) void k_xgateup1f(const RbtExpertDev *__restric
     xgateup1_body<NCH>(L.gu, jobs, T->nr, x, I, hp, blockIdx.x - 1, gridDim.x - 1);
   } else if (T->pending) {
     __builtin_amdgcn_s_setprio(3);
-    d1_finish(L.sel, P, T, G, ids, wts, stats);
+    d1_finish(L.d1.sel, L.d1.fold, P, T, G, ids, wts, stats);
   }
 }
 
