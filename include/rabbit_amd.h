@@ -196,6 +196,20 @@ int rbt_moe_forward(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, floa
 int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
                       int32_t *ids_out, float *w_out);
 
+/* ---- norms and the MoE sublayer -------------------------------------------------------------- */
+/* rmsnorm (kimi_linear/ops.rs:46-53) of rows v[s, n] in place, device memory:
+ * r = 1/sqrt(mean_f64(v^2) as f32 + eps), v *= r * w. */
+int rbt_rmsnorm_d(rbt_ctx *ctx, float *v, const float *w, size_t s, size_t n, float eps);
+/* rmsnorm_1p (qwen38/ops.rs:25-33): the same r, v *= r * (1 + w) (Qwen3_5MoeRMSNorm). */
+int rbt_rmsnorm_1p_d(rbt_ctx *ctx, float *v, const float *w, size_t s, size_t n, float eps);
+/* The MoE half of a Qwen 3.8 decoder layer (qwen38/generate.rs:397-413) in one device round trip:
+ * x[s, hidden] += moe_forward(rmsnorm_1p(x, post_ln, eps)), in place. post_ln f32[hidden].
+ * ids_out / w_out as for rbt_moe_forward. _d: device buffers, asynchronous on the context stream. */
+int rbt_moe_sublayer(rbt_ctx *ctx, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
+                     int32_t *ids_out, float *w_out);
+int rbt_moe_sublayer_d(rbt_ctx *ctx, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
+                       int32_t *ids_out, float *w_out);
+
 /* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
 typedef struct {
     double router_ms;    /* router logits + top-k selection + grouping (one-token MXFP4 calls: also

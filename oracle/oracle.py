@@ -89,6 +89,10 @@ def lib():
         L.orc_moe_forward.restype = I
         L.orc_moe_forward.argtypes = [C.POINTER(OrcMoeLayer), P, S, I, P, P, P]
         L.orc_router_logits.argtypes = [C.POINTER(OrcMoeLayer), P, S, P]
+        L.orc_rmsnorm.argtypes = [P, P, S, F]
+        L.orc_rmsnorm_1p.argtypes = [P, P, S, F]
+        L.orc_moe_sublayer.restype = I
+        L.orc_moe_sublayer.argtypes = [C.POINTER(OrcMoeLayer), P, S, P, F, I, P, P]
         L.orc_synth_mix64.restype = C.c_uint64
         L.orc_synth_mix64.argtypes = [C.c_uint64]
         L.orc_synth_mxfp4.argtypes = [P, P, S, S, C.c_uint64, C.c_uint32, C.c_uint32]
@@ -266,6 +270,30 @@ def sigmoid(x: float) -> float:
     return lib().orc_sigmoid(x)
 
 
+def rmsnorm(v, w, eps):
+    """kimi_linear/ops.rs:46-53 on each row of v (a copy)."""
+    v = np.array(v, dtype=np.float32, copy=True)
+    w = _f32(w)
+    rows = v.reshape(-1, w.size)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        lib().orc_rmsnorm(_p(row), _p(w), w.size, eps)
+        rows[r] = row
+    return rows.reshape(v.shape)
+
+
+def rmsnorm_1p(v, w, eps):
+    """qwen38/ops.rs:25-33 on each row of v (a copy)."""
+    v = np.array(v, dtype=np.float32, copy=True)
+    w = _f32(w)
+    rows = v.reshape(-1, w.size)
+    for r in range(rows.shape[0]):
+        row = np.ascontiguousarray(rows[r])
+        lib().orc_rmsnorm_1p(_p(row), _p(w), w.size, eps)
+        rows[r] = row
+    return rows.reshape(v.shape)
+
+
 # --- experts and layers ------------------------------------------------------------------------
 class Slot:
     """Host expert slot (mirrors ExpertSlot/GateUp). gate/up/gate_up/down are QT."""
@@ -326,3 +354,15 @@ class MoeLayer:
         if rc != 0:
             raise RuntimeError("orc_moe_forward: routed expert missing from the pool")
         return out.reshape(s, self.hidden), ids[:s * k].reshape(s, k), w[:s * k].reshape(s, k)
+
+    def sublayer(self, x, s, post_ln, eps, simd=False):
+        """x + moe_forward(rmsnorm_1p(x, post_ln)) (qwen38/generate.rs:397-413); returns a copy."""
+        xo = np.array(_f32(x), copy=True)
+        k = min(self.topk, self.n_experts)
+        ids = np.empty(max(s * k, 1), np.int32)
+        w = np.empty(max(s * k, 1), np.float32)
+        post_ln = _f32(post_ln)
+        rc = lib().orc_moe_sublayer(C.byref(self.c), _p(xo), s, _p(post_ln), eps, int(simd), _p(ids), _p(w))
+        if rc != 0:
+            raise RuntimeError("orc_moe_sublayer: routed expert missing from the pool")
+        return xo.reshape(s, self.hidden), ids[:s * k].reshape(s, k), w[:s * k].reshape(s, k)

@@ -341,6 +341,40 @@ void orc_apply_single_expert(const orc_slot *slot, const int32_t *ids, const flo
     free(rows);
 }
 
+/* kimi_linear/ops.rs:46-53: the f64 sum of squares in element order, (ms / n) rounded to f32. */
+static float orc_rms_scale(const float *v, size_t n, float eps) {
+    double ms = 0.0;
+    for (size_t i = 0; i < n; i++) ms += (double)v[i] * (double)v[i];
+    return 1.0f / sqrtf((float)(ms / (double)n) + eps);
+}
+
+void orc_rmsnorm(float *v, const float *w, size_t n, float eps) {
+    const float r = orc_rms_scale(v, n, eps);
+    for (size_t i = 0; i < n; i++) v[i] *= r * w[i];
+}
+
+/* qwen38/ops.rs:25-33 */
+void orc_rmsnorm_1p(float *v, const float *w, size_t n, float eps) {
+    const float r = orc_rms_scale(v, n, eps);
+    for (size_t i = 0; i < n; i++) v[i] *= r * (1.0f + w[i]);
+}
+
+/* qwen38/generate.rs:397-413: nrm = rmsnorm_1p(x) row by row, tmp = moe_forward(nrm), x += tmp. */
+int orc_moe_sublayer(const orc_moe_layer *L, float *x, size_t s, const float *post_ln, float eps, int simd,
+                     int32_t *ids_out, float *w_out) {
+    const size_t d = L->hidden;
+    float *nrm = (float *)malloc((s ? s : 1) * d * sizeof(float));
+    float *tmp = (float *)malloc((s ? s : 1) * d * sizeof(float));
+    memcpy(nrm, x, s * d * sizeof(float));
+    for (size_t si = 0; si < s; si++) orc_rmsnorm_1p(nrm + si * d, post_ln, d, eps);
+    const int rc = orc_moe_forward(L, nrm, s, simd, tmp, ids_out, w_out);
+    if (rc == 0)
+        for (size_t z = 0; z < s * d; z++) x[z] += tmp[z];
+    free(tmp);
+    free(nrm);
+    return rc;
+}
+
 /* qwen38/generate.rs:279-281 (router matmul) plus the synthetic pre-activation skew. */
 void orc_router_logits(const orc_moe_layer *L, const float *x, size_t s, float *logits) {
     orc_matmul(logits, x, L->router, s, L->hidden, L->n_experts);

@@ -116,6 +116,17 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, 
 /* Router logits plus optional synthetic skew, [s, n_experts] (generate.rs:279-281). */
 void orc_router_logits(const orc_moe_layer *L, const float *x, size_t s, float *logits);
 
+/* --- norms and the MoE sublayer ----------------------------------------------------------- */
+/* kimi_linear/ops.rs:46-53 rmsnorm, in place: r = 1 / sqrt((sum_f64(v^2) / n) as f32 + eps), then
+ * v[i] *= r * w[i]. */
+void orc_rmsnorm(float *v, const float *w, size_t n, float eps);
+/* qwen38/ops.rs:25-33 rmsnorm_1p, in place: the same r, then v[i] *= r * (1 + w[i]). */
+void orc_rmsnorm_1p(float *v, const float *w, size_t n, float eps);
+/* The MoE half of a Qwen 3.8 decoder layer (qwen38/generate.rs:397-413): per token row,
+ * nrm = rmsnorm_1p(x, post_ln), then x += moe_forward(nrm). x[s, hidden] is updated in place. */
+int orc_moe_sublayer(const orc_moe_layer *L, float *x, size_t s, const float *post_ln, float eps, int simd,
+                     int32_t *ids_out, float *w_out);
+
 /* --- synthetic workload generator (shared bit-for-bit with rabbit_amd's device generator) --- */
 uint64_t orc_synth_mix64(uint64_t z);
 void orc_synth_mxfp4(uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,

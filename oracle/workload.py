@@ -65,3 +65,9 @@ class HostLayer:
         ids, _ = self.route(x)
         self.ensure(ids)
         return self._layer().forward(x, x.shape[0], simd=simd)
+
+    def sublayer(self, x: np.ndarray, post_ln: np.ndarray, eps: float, simd: bool = False):
+        """x + moe_forward(rmsnorm_1p(x, post_ln)) (qwen38/generate.rs:397-413)."""
+        ids, _ = self.route(O.rmsnorm_1p(x, post_ln, eps))
+        self.ensure(ids)
+        return self._layer().sublayer(x, x.shape[0], post_ln, eps, simd=simd)

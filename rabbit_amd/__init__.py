@@ -285,6 +285,31 @@ class Context:
         else:
             self.check(self.lib.rbt_moe_layer_set(self.h, layer, C.byref(d)))
 
+    def rmsnorm(self, v, w, s, n, eps, one_plus=False, sync=True):
+        """rmsnorm (kimi_linear/ops.rs:46) or rmsnorm_1p (qwen38/ops.rs:25) of device rows v[s, n] in
+        place."""
+        if sync:
+            self._torch_sync()
+        fn = self.lib.rbt_rmsnorm_1p_d if one_plus else self.lib.rbt_rmsnorm_d
+        self.check(fn(self.h, _ptr(v), _ptr(w), s, n, eps))
+        if sync:
+            self.sync()
+        return v
+
+    def moe_sublayer(self, layer, x, s, post_ln, eps, ids_out=None, w_out=None, sync=True):
+        """x += moe_forward(rmsnorm_1p(x, post_ln)) in place (qwen38/generate.rs:397-413)."""
+        if _is_torch(x):
+            if sync:
+                self._torch_sync()
+            self.check(self.lib.rbt_moe_sublayer_d(self.h, layer, _ptr(x), s, _ptr(post_ln), eps, _ptr(ids_out),
+                                                   _ptr(w_out)))
+            if sync:
+                self.sync()
+        else:
+            self.check(self.lib.rbt_moe_sublayer(self.h, layer, _ptr(x), s, _ptr(post_ln), eps, _ptr(ids_out),
+                                                 _ptr(w_out)))
+        return x
+
     def moe_forward(self, layer, x, s, out, ids_out=None, w_out=None, sync=True):
         if _is_torch(x):
             if sync:

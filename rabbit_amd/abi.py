@@ -90,6 +90,10 @@ SIGNATURES = {
     "rbt_moe_layer_set_device": (_I, [_CTX, _U32, C.POINTER(RbtMoeLayerDesc)]),
     "rbt_moe_forward": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
     "rbt_moe_forward_d": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
+    "rbt_rmsnorm_d": (_I, [_CTX, _P, _P, _S, _S, _F]),
+    "rbt_rmsnorm_1p_d": (_I, [_CTX, _P, _P, _S, _S, _F]),
+    "rbt_moe_sublayer": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),
+    "rbt_moe_sublayer_d": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),
     "rbt_profile_enable": (_I, [_CTX, _I]),
     "rbt_profile_read": (_I, [_CTX, C.POINTER(RbtProfile), _I]),
     "rbt_synth_mxfp4_d": (_I, [_CTX, _P, _P, _S, _S, _U64, _U32, _U32]),

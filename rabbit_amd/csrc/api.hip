@@ -50,6 +50,9 @@ enum ScratchSlot {
   SC_DJOB,
   SC_DSLOT,
   SC_D1,
+  SC_NRM,   // sublayer: the normalised rows
+  SC_SUB,   // sublayer: the MoE output before the residual add
+  SC_PLN,   // sublayer (host call): post_ln staged
   SC_N
 };
 
@@ -1131,6 +1134,68 @@ int rbt_moe_layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
 int rbt_moe_layer_set_device(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
   if (!c) return RBT_E_INVALID;
   return layer_set(c, layer, d, true);
+}
+
+int rbt_rmsnorm_d(rbt_ctx *c, float *v, const float *w, size_t s, size_t n, float eps) {
+  if (!c) return RBT_E_INVALID;
+  if (s == 0 || n == 0) return RBT_OK;
+  if (!v || !w) return fail(c, RBT_E_INVALID, "null v or w");
+  HIP_OK(c, rbt::launch_rmsnorm(*c, v, w, eps, v, s, n, false));
+  return RBT_OK;
+}
+
+int rbt_rmsnorm_1p_d(rbt_ctx *c, float *v, const float *w, size_t s, size_t n, float eps) {
+  if (!c) return RBT_E_INVALID;
+  if (s == 0 || n == 0) return RBT_OK;
+  if (!v || !w) return fail(c, RBT_E_INVALID, "null v or w");
+  HIP_OK(c, rbt::launch_rmsnorm(*c, v, w, eps, v, s, n, true));
+  return RBT_OK;
+}
+
+// qwen38/generate.rs:397-413: nrm = rmsnorm_1p(x, post_ln) per row, tmp = moe_forward(nrm), x += tmp.
+static int moe_sublayer_dev(rbt_ctx *c, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
+                            int32_t *ids_out, float *w_out) {
+  auto lit = c->layers.find(layer);
+  if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
+  if (s == 0) return RBT_OK;
+  if (!x || !post_ln) return fail(c, RBT_E_INVALID, "null x or post_ln");
+  const size_t H = lit->second.desc.hidden;
+  float *nrm, *tmp;
+  RBT_TRY(scratch_t(c, SC_NRM, s * H, &nrm));
+  RBT_TRY(scratch_t(c, SC_SUB, s * H, &tmp));
+  HIP_OK(c, rbt::launch_rmsnorm(*c, x, post_ln, eps, nrm, s, H, true));
+  RBT_TRY(moe_forward_dev(c, layer, nrm, s, tmp, ids_out, w_out));
+  HIP_OK(c, rbt::launch_add_rows(*c, x, tmp, s * H));
+  return RBT_OK;
+}
+
+int rbt_moe_sublayer_d(rbt_ctx *c, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
+                       int32_t *ids_out, float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  return moe_sublayer_dev(c, layer, x, s, post_ln, eps, ids_out, w_out);
+}
+
+int rbt_moe_sublayer(rbt_ctx *c, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
+                     int32_t *ids_out, float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  auto lit = c->layers.find(layer);
+  if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
+  if (s == 0) return RBT_OK;
+  if (!x || !post_ln) return fail(c, RBT_E_INVALID, "null x or post_ln");
+  const rbt_moe_layer_desc &D = lit->second.desc;
+  const size_t H = D.hidden, k = std::min(D.topk, D.n_experts);
+  void *dx, *dp;
+  float *dw;
+  int32_t *di;
+  RBT_TRY(stage_in(c, SC_X, x, s * H * 4, &dx));
+  RBT_TRY(stage_in(c, SC_PLN, post_ln, H * 4, &dp));
+  RBT_TRY(scratch_t(c, SC_IDS_OUT, s * k, &di));
+  RBT_TRY(scratch_t(c, SC_W_OUT, s * k, &dw));
+  RBT_TRY(moe_sublayer_dev(c, layer, (float *)dx, s, (const float *)dp, eps, di, dw));
+  HIP_OK(c, hipMemcpyAsync(x, dx, s * H * 4, hipMemcpyDeviceToHost, c->stream));
+  if (ids_out) HIP_OK(c, hipMemcpyAsync(ids_out, di, s * k * 4, hipMemcpyDeviceToHost, c->stream));
+  if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, dw, s * k * 4, hipMemcpyDeviceToHost, c->stream));
+  return sync_and_check(c);
 }
 
 int rbt_moe_forward_d(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,

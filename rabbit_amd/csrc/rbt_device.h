@@ -45,6 +45,17 @@ __device__ __forceinline__ float rbt_e2m1(uint32_t n) {
 #define RBT_FP4X2(w, scale, sel) __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((w), (scale), (sel))
 
 __device__ __forceinline__ float rbt_silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Correctly rounded fp32 square root for positive normal x. v_sqrt_f32 is only faithful (within
+// one ulp), so the neighbours of its result are tested with one fma residual each and the rounded
+// value picked: the lowering LLVM uses for a correctly rounded llvm.sqrt.f32.
+__device__ __forceinline__ float rbt_sqrt_rn(float x) {
+  const float s = __builtin_amdgcn_sqrtf(x);
+  const float sd = __int_as_float(__float_as_int(s) - 1), su = __int_as_float(__float_as_int(s) + 1);
+  const float rd = __builtin_fmaf(-sd, s, x), ru = __builtin_fmaf(-su, s, x);
+  const float r = rd <= 0.0f ? sd : s;
+  return ru > 0.0f ? su : r;
+}
 __device__ __forceinline__ float rbt_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
 
 // v + (v from another lane of the same 16-lane DPP row), one v_add_f32_dpp.

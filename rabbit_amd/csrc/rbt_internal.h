@@ -38,6 +38,12 @@ struct RouterArgs {
   const float *x, *W;
 };
 
+// norm.hip: rmsnorm (kimi_linear/ops.rs:46) or, with one_plus, rmsnorm_1p (qwen38/ops.rs:25) of
+// rows x n (x may equal y); x += t over n floats.
+hipError_t launch_rmsnorm(const Ctx &c, const float *x, const float *w, float eps, float *y, size_t rows, size_t n,
+                          bool one_plus);
+hipError_t launch_add_rows(const Ctx &c, float *x, const float *t, size_t n);
+
 // gemv.hip
 hipError_t launch_generic(const Ctx &c, int kind, float *y, const float *x, const void *data, const void *scale,
                           size_t gs, size_t s, size_t i, size_t o);

@@ -330,3 +330,71 @@ def test_synth_generator_distribution(orc):
     assert q.scale.min() == 119 and q.scale.max() == 123
     g = orc.synth_i4g(64, 256, 32, seed=1)
     assert g.scale.min() >= 0.005 and g.scale.max() < 0.02
+
+
+# ---- norms and the MoE sublayer -----------------------------------------------------------------
+def _np_rms_scale(v, eps):
+    # the reference's r: f64 sum of squares in element order, mean rounded to f32, f32 sqrt/divide
+    ms = 0.0
+    for a in np.asarray(v, np.float32):
+        ms += float(a) * float(a)
+    return np.float32(1.0) / np.sqrt(np.float32(ms / len(v)) + np.float32(eps))
+
+
+def test_rmsnorm_1p_kats(orc):
+    # qwen38/ops.rs:42-52: a zero weight leaves the normalised vector alone (1.0); the plain norm
+    # zeroes it
+    assert np.all(np.abs(orc.rmsnorm_1p([2.0] * 4, [0.0] * 4, 1e-6) - 1.0) < 1e-4)
+    assert np.all(orc.rmsnorm([2.0] * 4, [0.0] * 4, 1e-6) == 0.0)
+    # :55-69 the formula elementwise (f32 mean square as the test writes it)
+    v0 = np.array([1.0, -2.0, 3.0, -4.0, 0.5, 0.25], np.float32)
+    w = np.array([0.1, -0.2, 0.0, 0.5, -0.75, 1.0], np.float32)
+    ms = np.float32(np.sum(v0 * v0, dtype=np.float32) / np.float32(6))
+    want = v0 / np.sqrt(ms + np.float32(1e-6)) * (np.float32(1) + w)
+    assert np.all(np.abs(orc.rmsnorm_1p(v0, w, 1e-6) - want) < 1e-5)
+    # :73-81 1 + w against w
+    assert abs(orc.rmsnorm_1p([3.0] * 8, [0.05] * 8, 1e-6)[0] - 1.05) < 1e-4
+    assert abs(orc.rmsnorm([3.0] * 8, [0.05] * 8, 1e-6)[0] - 0.05) < 1e-4
+
+
+def test_rmsnorm_kats(orc):
+    # kimi_linear/ops.rs:159-173 against the naive unfused form; :175-182 unit weights give unit RMS
+    v = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    w = np.array([1.0, 0.5, 2.0, 1.0], np.float32)
+    ms = np.float32(np.sum(v * v, dtype=np.float32) / np.float32(4))
+    r = np.float32(1.0) / np.sqrt(ms + np.float32(1e-5))
+    assert np.all(np.abs(orc.rmsnorm(v, w, 1e-5) - v * r * w) < 1e-5)
+    u = orc.rmsnorm([2.0, -6.0, 3.0, 1.0], [1.0] * 4, 1e-8)
+    assert abs(math.sqrt(float(np.mean(u.astype(np.float64) ** 2))) - 1.0) < 1e-4
+
+
+def test_rmsnorm_closed_form_and_one_plus_relation(orc):
+    # bit for bit: r from an f64 sum in order (an f32 sum, a dropped eps or a fused multiply would
+    # change the last bits on these rows), and rmsnorm_1p(v, w) == rmsnorm(v, f32(1 + w))
+    rng = np.random.default_rng(17)
+    for n in (5, 256, 6144, 8192):
+        v = (rng.standard_normal(n) * 3).astype(np.float32)
+        w = (rng.standard_normal(n) * 0.1).astype(np.float32)
+        r = _np_rms_scale(v, 1e-6)
+        assert bits_equal(orc.rmsnorm(v, w, 1e-6), v * (r * w))
+        assert bits_equal(orc.rmsnorm_1p(v, w, 1e-6), v * (r * (np.float32(1) + w)))
+        assert bits_equal(orc.rmsnorm_1p(v, w, 1e-6), orc.rmsnorm(v, np.float32(1) + w, 1e-6))
+
+
+def test_moe_sublayer_is_residual_plus_forward_of_normalised(orc):
+    # qwen38/generate.rs:397-413: x + moe_forward(rmsnorm_1p(x)), not moe_forward(x) + x
+    d, i, E, s = 64, 32, 6, 3
+    experts = {e: orc.Slot(e, orc.synth_mxfp4(d, i, seed=12 + 3 * e), gate=orc.synth_mxfp4(i, d, seed=10 + 3 * e),
+                           up=orc.synth_mxfp4(i, d, seed=11 + 3 * e)) for e in range(E)}
+    rng = np.random.default_rng(5)
+    router = (rng.standard_normal((E, d)) * 0.3).astype(np.float32)
+    L = orc.MoeLayer(orc.FAMILY_QWEN38, d, i, E, 2, router, experts)
+    x = (rng.standard_normal((s, d)) * 2).astype(np.float32)
+    ln = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    got, ids, w = L.sublayer(x, s, ln, 1e-6)
+    nrm = orc.rmsnorm_1p(x, ln, 1e-6)
+    out, ids2, w2 = L.forward(nrm, s)
+    assert np.array_equal(ids, ids2) and bits_equal(w, w2)
+    assert bits_equal(got, x + out)
+    plain, _, _ = L.forward(x, s)
+    assert not np.allclose(got, x + plain)
