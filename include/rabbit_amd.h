@@ -39,6 +39,10 @@ extern "C" {
 #define RBT_E_NOT_RESIDENT (-4) /* routed expert missing from the pool (ExpertCache::get -> None) */
 #define RBT_E_NOMEM (-5)        /* device allocation failed */
 #define RBT_E_UNSUPPORTED (-6)  /* valid in the reference but not offered on this path */
+#define RBT_E_NOT_FOUND (-7)    /* tensor absent from the checkpoint (SafetensorsError::MissingTensor) */
+#define RBT_E_FORMAT (-8)       /* malformed safetensors header or unknown dtype (BadHeader, Json,
+                                   UnknownDtype) */
+#define RBT_E_IO (-9)           /* file system error (SafetensorsError::Io) */
 
 typedef struct rbt_ctx rbt_ctx;
 
@@ -155,6 +159,44 @@ const rbt_expert_slot *rbt_pool_alloc(rbt_ctx *ctx, uint32_t layer, uint32_t eid
 const rbt_expert_slot *rbt_pool_get(rbt_ctx *ctx, uint32_t layer, uint32_t eid);
 /* Bytes resident in the pool (all layers). */
 size_t rbt_pool_resident_bytes(rbt_ctx *ctx);
+
+/* ---- on-disk checkpoints: safetensors shards (safetensors.rs:215-488) ------------------------- */
+/* The index of every *.safetensors file in a directory, in file-name order (Shards::open). Host
+ * only, no context; the calls below return a status and describe a failure in
+ * rbt_shards_last_error() (per thread). */
+typedef struct rbt_shards rbt_shards;
+typedef struct {
+    int32_t file_index;      /* shard (file-name order) */
+    uint64_t offset;         /* byte offset of the tensor's data in that file */
+    uint64_t nbytes;
+    char dtype[16];          /* the header's dtype string */
+    int32_t ndim;            /* shape entries kept (at most 8) */
+    uint64_t shape[8];
+} rbt_tensor_info;
+int rbt_shards_open(const char *dir, rbt_shards **out);
+void rbt_shards_close(rbt_shards *sh);
+const char *rbt_shards_last_error(void);
+size_t rbt_shards_count(const rbt_shards *sh);
+/* Shards::find / tensor_location: RBT_OK, or RBT_E_NOT_FOUND. */
+int rbt_shards_find(const rbt_shards *sh, const char *name, rbt_tensor_info *info);
+/* Shards::read_raw: the tensor's bytes into host dst (cap bytes). */
+int rbt_shards_read(const rbt_shards *sh, const char *name, void *dst, size_t cap);
+/* n bytes from byte `offset` of the tensor. */
+int rbt_shards_read_range(const rbt_shards *sh, const char *name, uint64_t offset, void *dst, size_t n);
+
+/* MXFP4 routed experts as the checkpoints name them (ExpertNaming, expert_cache.rs:93-208). */
+typedef enum {
+    RBT_NAMING_QWEN38_MXFP4 = 0, /* model.layers.{L}.mlp.experts.{E}.{gate,up,down}_proj.weight (+ .weight_scale) */
+    RBT_NAMING_KIMI_K3_MXFP4 = 1 /* language_model.model.layers.{L}.block_sparse_moe.experts.{E}.{w1,w3,w2}
+                                    .weight_packed (+ .weight_scale) */
+} rbt_naming;
+/* ensure_loaded (expert_cache.rs:890) for MXFP4 experts: each expert's packed and scale tensors
+ * (gate/w1, up/w3 [moe_inter, hidden]; down/w2 [hidden, moe_inter]) are read verbatim into a new
+ * pool slot of `layer`, their byte lengths checked as mxfp4_from_raw does (expert_cache.rs:
+ * 1245-1256: RBT_E_SHAPE naming the tensor). A missing tensor is RBT_E_NOT_FOUND. Experts before a
+ * failing one stay loaded; the failing one is not inserted. Synchronous. */
+int rbt_pool_load_mxfp4(rbt_ctx *ctx, const rbt_shards *sh, int32_t naming, uint32_t layer, const uint32_t *eids,
+                        size_t n, size_t hidden, size_t moe_inter);
 
 /* ---- MoE layer: family dispatch (model.rs:22-140) and moe_forward / moe ------------------------ */
 typedef enum {

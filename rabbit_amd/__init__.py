@@ -25,8 +25,10 @@ from . import abi
 from .abi import (ACT_SILU, FAMILY_GLM52, FAMILY_KIMI_K3, FAMILY_QWEN38, QT_F32, QT_I4_GROUPED, QT_MXFP4,
                   RbtExpertSlot, RbtMoeLayerDesc, RbtQT)
 
-__all__ = ["Context", "QT", "Slot", "RbtError", "load", "QT_F32", "QT_I4_GROUPED", "QT_MXFP4",
-           "FAMILY_QWEN38", "FAMILY_GLM52", "FAMILY_KIMI_K3", "ACT_SILU"]
+__all__ = ["Context", "QT", "Slot", "Shards", "RbtError", "load", "QT_F32", "QT_I4_GROUPED", "QT_MXFP4",
+           "FAMILY_QWEN38", "FAMILY_GLM52", "FAMILY_KIMI_K3", "ACT_SILU", "NAMING_QWEN38_MXFP4",
+           "NAMING_KIMI_K3_MXFP4"]
+from .abi import NAMING_KIMI_K3_MXFP4, NAMING_QWEN38_MXFP4  # noqa: E402
 
 
 class RbtError(RuntimeError):
@@ -91,6 +93,51 @@ class QT:
     def resident_bytes(self) -> int:
         q = self.c()
         return abi.load().rbt_qt_resident_bytes(C.byref(q))
+
+
+class Shards:
+    """The safetensors shards of a checkpoint directory (Shards::open, safetensors.rs:230-349); host
+    only, no GPU needed."""
+
+    def __init__(self, directory: str):
+        self.lib = abi.load()
+        h = C.c_void_p()
+        st = self.lib.rbt_shards_open(directory.encode(), C.byref(h))
+        if st != 0:
+            raise RbtError(st, self.lib.rbt_shards_last_error().decode())
+        self.h = h
+
+    def _check(self, st):
+        if st != 0:
+            raise RbtError(st, self.lib.rbt_shards_last_error().decode())
+
+    def __len__(self):
+        return self.lib.rbt_shards_count(self.h)
+
+    def find(self, name: str) -> dict:
+        ti = abi.RbtTensorInfo()
+        self._check(self.lib.rbt_shards_find(self.h, name.encode(), C.byref(ti)))
+        return {"file_index": ti.file_index, "offset": ti.offset, "nbytes": ti.nbytes,
+                "dtype": ti.dtype.decode(), "shape": [ti.shape[i] for i in range(ti.ndim)]}
+
+    def read(self, name: str) -> np.ndarray:
+        n = self.find(name)["nbytes"]
+        out = np.empty(max(n, 1), np.uint8)
+        self._check(self.lib.rbt_shards_read(self.h, name.encode(), out.ctypes.data, out.size))
+        return out[:n]
+
+    def read_range(self, name: str, offset: int, n: int) -> np.ndarray:
+        out = np.empty(max(n, 1), np.uint8)
+        self._check(self.lib.rbt_shards_read_range(self.h, name.encode(), offset, out.ctypes.data, n))
+        return out[:n]
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.rbt_shards_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 class Slot:
@@ -295,6 +342,13 @@ class Context:
         if sync:
             self.sync()
         return v
+
+    def pool_load_mxfp4(self, shards: Shards, naming, layer, eids, hidden, moe_inter):
+        """ensure_loaded for MXFP4 experts read verbatim from safetensors shards (expert_cache.rs:
+        1227-1256): the experts `eids` of `layer` into the HBM pool."""
+        e = np.ascontiguousarray(np.asarray(eids, np.uint32))
+        self.check(self.lib.rbt_pool_load_mxfp4(self.h, shards.h, naming, layer, e.ctypes.data, e.size, hidden,
+                                                moe_inter))
 
     def moe_sublayer(self, layer, x, s, post_ln, eps, ids_out=None, w_out=None, sync=True):
         """x += moe_forward(rmsnorm_1p(x, post_ln)) in place (qwen38/generate.rs:397-413)."""

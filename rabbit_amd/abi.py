@@ -21,7 +21,8 @@ RBT_E_NOT_RESIDENT = -4
 RBT_E_NOMEM = -5
 RBT_E_UNSUPPORTED = -6
 STATUS_NAMES = {0: "RBT_OK", -1: "RBT_E_INVALID", -2: "RBT_E_SHAPE", -3: "RBT_E_HIP",
-                -4: "RBT_E_NOT_RESIDENT", -5: "RBT_E_NOMEM", -6: "RBT_E_UNSUPPORTED"}
+                -4: "RBT_E_NOT_RESIDENT", -5: "RBT_E_NOMEM", -6: "RBT_E_UNSUPPORTED", -7: "RBT_E_NOT_FOUND",
+                -8: "RBT_E_FORMAT", -9: "RBT_E_IO"}
 
 QT_F32, QT_I4_GROUPED, QT_MXFP4 = 0, 1, 2
 FAMILY_QWEN38, FAMILY_GLM52, FAMILY_KIMI_K3 = 0, 1, 2
@@ -54,6 +55,14 @@ class RbtProfile(C.Structure):
 
 _P, _S, _I, _F, _U32, _U64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_float, C.c_uint32, C.c_uint64
 _CTX = C.c_void_p
+
+
+class RbtTensorInfo(C.Structure):
+    _fields_ = [("file_index", C.c_int32), ("offset", C.c_uint64), ("nbytes", C.c_uint64),
+                ("dtype", C.c_char * 16), ("ndim", C.c_int32), ("shape", C.c_uint64 * 8)]
+
+
+NAMING_QWEN38_MXFP4, NAMING_KIMI_K3_MXFP4 = 0, 1
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -90,6 +99,14 @@ SIGNATURES = {
     "rbt_moe_layer_set_device": (_I, [_CTX, _U32, C.POINTER(RbtMoeLayerDesc)]),
     "rbt_moe_forward": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
     "rbt_moe_forward_d": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
+    "rbt_shards_open": (_I, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "rbt_shards_close": (None, [C.c_void_p]),
+    "rbt_shards_last_error": (C.c_char_p, []),
+    "rbt_shards_count": (_S, [C.c_void_p]),
+    "rbt_shards_find": (_I, [C.c_void_p, C.c_char_p, C.POINTER(RbtTensorInfo)]),
+    "rbt_shards_read": (_I, [C.c_void_p, C.c_char_p, _P, _S]),
+    "rbt_shards_read_range": (_I, [C.c_void_p, C.c_char_p, _U64, _P, _S]),
+    "rbt_pool_load_mxfp4": (_I, [_CTX, C.c_void_p, _I, _U32, _P, _S, _S, _S]),
     "rbt_rmsnorm_d": (_I, [_CTX, _P, _P, _S, _S, _F]),
     "rbt_rmsnorm_1p_d": (_I, [_CTX, _P, _P, _S, _S, _F]),
     "rbt_moe_sublayer": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),

@@ -1108,6 +1108,110 @@ const rbt_expert_slot *rbt_pool_alloc(rbt_ctx *c, uint32_t layer, uint32_t eid, 
   return &c->pool[((uint64_t)layer << 32) | eid].slot;
 }
 
+// ensure_loaded for MXFP4 experts from safetensors shards (expert_cache.rs:1227-1256): validate all
+// six tensors of an expert, allocate its slot, then stream the bytes through two pinned staging
+// buffers (pread into one while the other's copy to HBM runs on the context stream).
+int rbt_pool_load_mxfp4(rbt_ctx *c, const rbt_shards *sh, int32_t naming, uint32_t layer, const uint32_t *eids,
+                        size_t n, size_t hidden, size_t moe_inter) {
+  if (!c) return RBT_E_INVALID;
+  if (!sh || (!eids && n)) return fail(c, RBT_E_INVALID, "null shards or eids");
+  if (naming != RBT_NAMING_QWEN38_MXFP4 && naming != RBT_NAMING_KIMI_K3_MXFP4)
+    return fail(c, RBT_E_INVALID, "unknown expert naming %d", naming);
+  if (hidden == 0 || moe_inter == 0) return fail(c, RBT_E_INVALID, "zero hidden or moe_inter");
+  if (n == 0) return RBT_OK;
+  constexpr size_t STAGE = 32u << 20;
+  void *stage[2] = {nullptr, nullptr};
+  hipEvent_t done[2] = {nullptr, nullptr};
+  int rc = RBT_OK;
+  auto cleanup = [&]() {
+    if (done[0] || done[1]) (void)hipStreamSynchronize(c->stream);
+    for (int b = 0; b < 2; b++) {
+      if (stage[b]) (void)hipHostFree(stage[b]);
+      if (done[b]) (void)hipEventDestroy(done[b]);
+    }
+  };
+  for (int b = 0; b < 2; b++) {
+    if (hipHostMalloc(&stage[b], STAGE, hipHostMallocDefault) != hipSuccess ||
+        hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      cleanup();
+      return fail(c, RBT_E_NOMEM, "pinned staging buffers");
+    }
+  }
+  int cur = 0;
+  bool pending[2] = {false, false};
+  for (size_t j = 0; j < n && rc == RBT_OK; j++) {
+    const uint32_t eid = eids[j];
+    std::string base[3];
+    size_t rows[3], cols[3];
+    const char *psuf;
+    (void)rbt::mxfp4_specs(naming, layer, eid, hidden, moe_inter, base, rows, cols, &psuf);
+    // mxfp4_from_raw's checks on every tensor before anything is allocated
+    std::string names[6];
+    uint64_t want[6];
+    for (int m = 0; m < 3 && rc == RBT_OK; m++) {
+      names[2 * m] = base[m] + psuf;
+      names[2 * m + 1] = base[m] + ".weight_scale";
+      want[2 * m] = (uint64_t)rows[m] * ((cols[m] + 1) / 2);
+      want[2 * m + 1] = (uint64_t)rows[m] * ((cols[m] + 31) / 32);
+      for (int q = 0; q < 2; q++) {
+        rbt_tensor_info ti;
+        const int f = rbt_shards_find(sh, names[2 * m + q].c_str(), &ti);
+        if (f != RBT_OK) {
+          rc = fail(c, f, "%s", rbt_shards_last_error());
+          break;
+        }
+        if (ti.nbytes != want[2 * m + q]) {
+          rc = fail(c, RBT_E_SHAPE, "shape mismatch: %s: expected %llu bytes, got %llu", names[2 * m + q].c_str(),
+                    (unsigned long long)want[2 * m + q], (unsigned long long)ti.nbytes);
+          break;
+        }
+      }
+    }
+    if (rc != RBT_OK) break;
+    const rbt_expert_slot *slot = rbt_pool_alloc(c, layer, eid, RBT_QT_MXFP4, hidden, moe_inter, 0);
+    if (!slot) {
+      rc = RBT_E_NOMEM;
+      break;
+    }
+    const rbt_qt *qs[3] = {&slot->gate, &slot->up, &slot->down};
+    for (int t = 0; t < 6 && rc == RBT_OK; t++) {
+      uint8_t *dst = (uint8_t *)(t % 2 ? qs[t / 2]->scale : qs[t / 2]->data);
+      for (uint64_t off = 0; off < want[t] && rc == RBT_OK; off += STAGE) {
+        const size_t len = (size_t)std::min<uint64_t>(STAGE, want[t] - off);
+        if (pending[cur] && hipEventSynchronize(done[cur]) != hipSuccess) {
+          rc = fail(c, RBT_E_HIP, "staging copy failed");
+          break;
+        }
+        const int r = rbt_shards_read_range(sh, names[t].c_str(), off, stage[cur], len);
+        if (r != RBT_OK) {
+          rc = fail(c, r, "%s", rbt_shards_last_error());
+          break;
+        }
+        if (hipMemcpyAsync(dst + off, stage[cur], len, hipMemcpyHostToDevice, c->stream) != hipSuccess ||
+            hipEventRecord(done[cur], c->stream) != hipSuccess) {
+          rc = fail(c, RBT_E_HIP, "host-to-device copy of %s", names[t].c_str());
+          break;
+        }
+        pending[cur] = true;
+        cur ^= 1;
+      }
+    }
+    if (rc != RBT_OK) {
+      // the expert that failed part-way is not left in the pool
+      (void)hipStreamSynchronize(c->stream);
+      auto it = c->pool.find(((uint64_t)layer << 32) | eid);
+      if (it != c->pool.end()) {
+        if (it->second.alloc) (void)hipFree(it->second.alloc);
+        c->pool.erase(it);
+      }
+    }
+  }
+  cleanup();
+  if (rc == RBT_OK) HIP_OK(c, hipStreamSynchronize(c->stream));
+  return rc;
+}
+
 const rbt_expert_slot *rbt_pool_get(rbt_ctx *c, uint32_t layer, uint32_t eid) {
   if (!c) return nullptr;
   auto it = c->pool.find(((uint64_t)layer << 32) | eid);

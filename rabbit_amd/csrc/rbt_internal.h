@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "../../include/rabbit_amd.h"
 #include "rbt_device.h"
 
@@ -37,6 +39,11 @@ struct RouterArgs {
   int n_group, topk_group;
   const float *x, *W;
 };
+
+// shards.hip: base names, shapes and the packed tensor's suffix of one MXFP4 expert's three
+// matrices in read order (ExpertNaming::tensor_specs / packed_suffix, expert_cache.rs:154-208).
+int mxfp4_specs(int naming, uint32_t layer, uint32_t eid, size_t hidden, size_t moe_inter, std::string base[3],
+                size_t rows[3], size_t cols[3], const char **packed_suffix);
 
 // norm.hip: rmsnorm (kimi_linear/ops.rs:46) or, with one_plus, rmsnorm_1p (qwen38/ops.rs:25) of
 // rows x n (x may equal y); x += t over n floats.

@@ -32,3 +32,21 @@ def bits_equal(a, b) -> bool:
     same = a.view(np.uint32) == b.view(np.uint32)
     both_nan = np.isnan(a) & np.isnan(b)
     return bool(np.all(same | both_nan))
+
+
+def write_safetensors(path, tensors, metadata=None, raw_header=None):
+    """Writes a safetensors file: tensors is a list of (name, dtype, shape, bytes) in data order.
+    raw_header (bytes), when given, replaces the JSON header (for malformed-header tests)."""
+    import json
+    header, data = {}, bytearray()
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, dtype, shape, b in tensors:
+        b = bytes(b)
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [len(data), len(data) + len(b)]}
+        data += b
+    hb = raw_header if raw_header is not None else json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(len(hb).to_bytes(8, "little"))
+        f.write(hb)
+        f.write(data)
