@@ -132,7 +132,14 @@ int rbt_route_sigmoid_topk_d(rbt_ctx *ctx, const float *logits, const float *bia
 int rbt_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq);
 
 /* ---- one expert ------------------------------------------------------------------------------ */
-enum { RBT_ACT_SILU = 0 }; /* Activation::Silu (glm52/moe.rs:49-80) */
+enum { RBT_ACT_SILU = 0, RBT_ACT_SITU = 1 }; /* Activation::{Silu, Situ} (glm52/moe.rs:49-80) */
+/* Activation with its parameters: Situ { beta, linear_beta: Option<f32> } (glm52/moe.rs:49-52). */
+typedef struct {
+    int32_t kind;            /* RBT_ACT_* */
+    float beta;              /* Situ */
+    float linear_beta;       /* Situ, when has_linear_beta */
+    int32_t has_linear_beta;
+} rbt_activation;
 /* apply_single_expert (glm52/moe.rs:463-513): the tokens that routed to slot->eid (ids/w are
  * [s, k]) run gate, up, silu(gate)*up, down, and out[t, :] += w * result. Host buffers; the slot's
  * weights may be host (uploaded for the call) or a pool slot from rbt_pool_get (device). */
@@ -142,6 +149,15 @@ int rbt_apply_single_expert(rbt_ctx *ctx, const rbt_expert_slot *slot, const int
 int rbt_apply_single_expert_d(rbt_ctx *ctx, const rbt_expert_slot *slot, const int32_t *ids,
                               const float *w, size_t s, size_t k, const float *x, size_t d, size_t i,
                               int32_t activation, float *out);
+/* The same with a parameterised activation (Situ needs its beta; activation = RBT_ACT_SITU in the
+ * two calls above is RBT_E_INVALID). act NULL = SiLU. Situ divides by beta and linear_beta: a zero
+ * or non-finite value is RBT_E_INVALID (the reference leaves them unchecked). */
+int rbt_apply_single_expert_act(rbt_ctx *ctx, const rbt_expert_slot *slot, const int32_t *ids, const float *w,
+                                size_t s, size_t k, const float *x, size_t d, size_t i, const rbt_activation *act,
+                                float *out);
+int rbt_apply_single_expert_act_d(rbt_ctx *ctx, const rbt_expert_slot *slot, const int32_t *ids, const float *w,
+                                  size_t s, size_t k, const float *x, size_t d, size_t i,
+                                  const rbt_activation *act, float *out);
 
 /* ---- HBM-resident expert pool (ExpertCache, expert_cache.rs) ---------------------------------- */
 /* ensure_loaded (expert_cache.rs:890) for one expert: copies a host slot's bytes into HBM,
@@ -237,6 +253,26 @@ int rbt_moe_forward(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, floa
                     float *w_out);
 int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
                       int32_t *ids_out, float *w_out);
+
+/* ---- K3 latent MoE (kimi_k3/moe.rs) ----------------------------------------------------------- */
+/* LatentMoeWeights (kimi_k3/moe.rs:41-57) plus the layer's expert width and activation. Device
+ * memory. */
+typedef struct {
+    size_t moe_hidden;       /* routed_expert_hidden_size: the width the routed experts run at */
+    rbt_qt down_proj;        /* [moe_hidden, hidden] */
+    rbt_qt up_proj;          /* [hidden, moe_hidden] */
+    const float *norm;       /* f32 [moe_hidden] (latent_moe_use_norm), or NULL */
+    float eps;
+    rbt_activation act;
+} rbt_latent_moe_desc;
+/* latent_moe (kimi_k3/moe.rs:64-116): route x[s, hidden] with `layer`'s router at full width,
+ * x_latent = matmul_qt(x, down_proj), every routed expert of `layer`'s pool (shaped for moe_hidden:
+ * gate/up [moe_inter, moe_hidden], down [moe_hidden, moe_inter]) accumulated at moe_hidden with
+ * lw->act, rmsnorm of each summed row when lw->norm, then out[s, hidden] = matmul_qt(routed,
+ * up_proj), overwritten; the shared expert is the caller's, as in the reference. Device buffers,
+ * asynchronous on the context stream. */
+int rbt_latent_moe_d(rbt_ctx *ctx, uint32_t layer, const rbt_latent_moe_desc *lw, const float *x, size_t s,
+                     float *out, int32_t *ids_out, float *w_out);
 
 /* ---- norms and the MoE sublayer -------------------------------------------------------------- */
 /* rmsnorm (kimi_linear/ops.rs:46-53) of rows v[s, n] in place, device memory:

@@ -40,6 +40,23 @@ class OrcMoeLayer(C.Structure):
                 ("experts", C.c_void_p)]
 
 
+ACT_SILU, ACT_SITU = 0, 1
+
+
+class OrcAct(C.Structure):
+    _fields_ = [("kind", C.c_int), ("beta", C.c_float), ("linear_beta", C.c_float), ("has_linear_beta", C.c_int)]
+
+
+def situ(beta, linear_beta=None) -> OrcAct:
+    """Activation::Situ { beta, linear_beta } (glm52/moe.rs:49-52)."""
+    return OrcAct(ACT_SITU, beta, 0.0 if linear_beta is None else linear_beta, int(linear_beta is not None))
+
+
+class OrcLatent(C.Structure):
+    _fields_ = [("moe_hidden", C.c_size_t), ("down_proj", OrcQT), ("up_proj", OrcQT), ("norm", C.c_void_p),
+                ("eps", C.c_float), ("act", OrcAct)]
+
+
 def build(force: bool = False) -> str:
     """Compile liboracle.so with oracle/Makefile (gcc, -ffp-contract=off)."""
     import subprocess
@@ -90,6 +107,12 @@ def lib():
         L.orc_moe_forward.argtypes = [C.POINTER(OrcMoeLayer), P, S, I, P, P, P]
         L.orc_router_logits.argtypes = [C.POINTER(OrcMoeLayer), P, S, P]
         L.orc_rmsnorm.argtypes = [P, P, S, F]
+        L.orc_act_combine.restype = F
+        L.orc_act_combine.argtypes = [C.POINTER(OrcAct), F, F]
+        L.orc_apply_single_expert_act.argtypes = [C.POINTER(OrcSlot), P, P, S, S, P, S, S, I, C.POINTER(OrcAct), P]
+        L.orc_moe_route.argtypes = [C.POINTER(OrcMoeLayer), P, S, P, P]
+        L.orc_latent_moe.restype = I
+        L.orc_latent_moe.argtypes = [C.POINTER(OrcMoeLayer), C.POINTER(OrcLatent), P, S, I, P, P, P]
         L.orc_rmsnorm_1p.argtypes = [P, P, S, F]
         L.orc_moe_sublayer.restype = I
         L.orc_moe_sublayer.argtypes = [C.POINTER(OrcMoeLayer), P, S, P, F, I, P, P]
@@ -305,13 +328,19 @@ class Slot:
                          gate_up.c if gate_up else empty, down.c)
 
 
-def apply_single_expert(slot: Slot, ids, wts, x, d, i, out, simd=False):
+def act_combine(act: OrcAct | None, g: float, u: float) -> float:
+    """Activation::combine (glm52/moe.rs:58-70)."""
+    return lib().orc_act_combine(C.byref(act) if act is not None else None, g, u)
+
+
+def apply_single_expert(slot: Slot, ids, wts, x, d, i, out, simd=False, act: OrcAct | None = None):
     ids = np.ascontiguousarray(ids, np.int32)
     wts = _f32(wts)
     s, k = ids.shape
     x = _f32(x)
     assert out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
-    lib().orc_apply_single_expert(C.byref(slot.c), _p(ids), _p(wts), s, k, _p(x), d, i, int(simd), _p(out))
+    lib().orc_apply_single_expert_act(C.byref(slot.c), _p(ids), _p(wts), s, k, _p(x), d, i, int(simd),
+                                      C.byref(act) if act is not None else None, _p(out))
     return out
 
 
@@ -354,6 +383,32 @@ class MoeLayer:
         if rc != 0:
             raise RuntimeError("orc_moe_forward: routed expert missing from the pool")
         return out.reshape(s, self.hidden), ids[:s * k].reshape(s, k), w[:s * k].reshape(s, k)
+
+    def route(self, x, s):
+        """The layer's routing alone: ids, w [s, min(topk, E)]."""
+        x = _f32(x)
+        k = min(self.topk, self.n_experts)
+        ids = np.empty(max(s * k, 1), np.int32)
+        w = np.empty(max(s * k, 1), np.float32)
+        lib().orc_moe_route(C.byref(self.c), _p(x), s, _p(ids), _p(w))
+        return ids[:s * k].reshape(s, k), w[:s * k].reshape(s, k)
+
+    def latent(self, x, s, moe_hidden, down_proj: QT, up_proj: QT, norm=None, eps=1e-5,
+               act: OrcAct | None = None, simd=False):
+        """K3's latent MoE (kimi_k3/moe.rs:64-116): this layer's router at full width, its experts at
+        moe_hidden. Returns out [s, hidden], ids, w."""
+        x = _f32(x)
+        norm = None if norm is None else _f32(norm)
+        lw = OrcLatent(moe_hidden, down_proj.c, up_proj.c, _p(norm), eps,
+                       act if act is not None else OrcAct(ACT_SILU, 0.0, 0.0, 0))
+        out = np.empty(s * up_proj.rows, np.float32)
+        k = min(self.topk, self.n_experts)
+        ids = np.empty(max(s * k, 1), np.int32)
+        w = np.empty(max(s * k, 1), np.float32)
+        rc = lib().orc_latent_moe(C.byref(self.c), C.byref(lw), _p(x), s, int(simd), _p(out), _p(ids), _p(w))
+        if rc != 0:
+            raise RuntimeError("orc_latent_moe: routed expert missing from the pool")
+        return out.reshape(s, up_proj.rows), ids[:s * k].reshape(s, k), w[:s * k].reshape(s, k)
 
     def sublayer(self, x, s, post_ln, eps, simd=False):
         """x + moe_forward(rmsnorm_1p(x, post_ln)) (qwen38/generate.rs:397-413); returns a copy."""

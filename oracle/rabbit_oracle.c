@@ -302,9 +302,23 @@ size_t orc_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq)
 float orc_siluf(float x) { return x / (1.0f + expf(-x)); }
 float orc_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-/* glm52/moe.rs:463-513 apply_single_expert with Activation::Silu. */
+/* glm52/moe.rs:58-70 Activation::combine */
+float orc_act_combine(const orc_act *a, float g, float u) {
+    if (!a || a->kind == ORC_ACT_SILU) return orc_siluf(g) * u;
+    if (a->has_linear_beta) u = a->linear_beta * tanhf(u / a->linear_beta);
+    const float situ = a->beta * tanhf(g / a->beta) * (1.0f / (1.0f + expf(-g)));
+    return situ * u;
+}
+
 void orc_apply_single_expert(const orc_slot *slot, const int32_t *ids, const float *wts, size_t s,
                              size_t k, const float *x, size_t d, size_t i, int simd, float *out) {
+    orc_apply_single_expert_act(slot, ids, wts, s, k, x, d, i, simd, NULL, out);
+}
+
+/* glm52/moe.rs:463-513 apply_single_expert */
+void orc_apply_single_expert_act(const orc_slot *slot, const int32_t *ids, const float *wts, size_t s,
+                                 size_t k, const float *x, size_t d, size_t i, int simd, const orc_act *act,
+                                 float *out) {
     size_t *rows = (size_t *)malloc((s ? s : 1) * sizeof(size_t));
     float *rw = (float *)malloc((s ? s : 1) * sizeof(float));
     size_t nr = 0;
@@ -321,13 +335,13 @@ void orc_apply_single_expert(const orc_slot *slot, const int32_t *ids, const flo
         float *uu = (float *)malloc(nr * i * sizeof(float));
         orc_matmul_qt(gg, xg, &slot->gate, nr, simd);
         orc_matmul_qt(uu, xg, &slot->up, nr, simd);
-        for (size_t z = 0; z < nr * i; z++) gg[z] = orc_siluf(gg[z]) * uu[z];
+        for (size_t z = 0; z < nr * i; z++) gg[z] = orc_act_combine(act, gg[z], uu[z]);
         free(uu);
     } else {
         float *gu = (float *)malloc(nr * 2 * i * sizeof(float));
         orc_matmul_qt(gu, xg, &slot->gate_up, nr, simd);
         for (size_t r = 0; r < nr; r++)
-            for (size_t c = 0; c < i; c++) gg[r * i + c] = orc_siluf(gu[r * 2 * i + c]) * gu[r * 2 * i + i + c];
+            for (size_t c = 0; c < i; c++) gg[r * i + c] = orc_act_combine(act, gu[r * 2 * i + c], gu[r * 2 * i + i + c]);
         free(gu);
     }
     float *hh = (float *)malloc(nr * d * sizeof(float));
@@ -386,13 +400,11 @@ void orc_router_logits(const orc_moe_layer *L, const float *x, size_t s, float *
 /* qwen38/generate.rs:262-351 (Qwen: softmax router, sigmoid-gated shared expert) and
  * glm52/moe.rs:350-451 (GLM/K3: sigmoid router, ungated shared expert). Every routed expert is
  * resident, so experts are applied in unique_experts order and the shared expert is added last. */
-int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, float *out,
-                    int32_t *ids_out, float *w_out) {
-    size_t d = L->hidden, i = L->moe_inter, E = L->n_experts, k = L->topk;
+/* qwen38/generate.rs:279-287 / glm52/moe.rs:365-376: router logits, then the family's route. */
+void orc_moe_route(const orc_moe_layer *L, const float *x, size_t s, int32_t *ids, float *wts) {
+    size_t E = L->n_experts, k = L->topk;
     if (k > E) k = E;
     float *logits = (float *)malloc((s ? s : 1) * E * sizeof(float));
-    int32_t *ids = (int32_t *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(int32_t));
-    float *wts = (float *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(float));
     orc_router_logits(L, x, s, logits);
     for (size_t si = 0; si < s; si++) {
         if (L->family == ORC_FAMILY_QWEN38)
@@ -401,6 +413,49 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, 
             orc_route_sigmoid(logits + si * E, L->router_bias, E, k, L->norm_topk, L->routed_scale,
                               L->n_group, L->topk_group, ids + si * k, wts + si * k);
     }
+    free(logits);
+}
+
+/* kimi_k3/moe.rs:64-116 latent_moe */
+int orc_latent_moe(const orc_moe_layer *L, const orc_latent *lw, const float *x, size_t s, int simd, float *out,
+                   int32_t *ids_out, float *w_out) {
+    const size_t mh = lw->moe_hidden, i = L->moe_inter, E = L->n_experts;
+    size_t k = L->topk;
+    if (k > E) k = E;
+    int32_t *ids = (int32_t *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(int32_t));
+    float *wts = (float *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(float));
+    orc_moe_route(L, x, s, ids, wts);
+    if (ids_out) memcpy(ids_out, ids, s * k * sizeof(int32_t));
+    if (w_out) memcpy(w_out, wts, s * k * sizeof(float));
+    float *xl = (float *)malloc((s ? s : 1) * mh * sizeof(float));
+    float *routed = (float *)calloc((s ? s : 1) * mh, sizeof(float));
+    orc_matmul_qt(xl, x, &lw->down_proj, s, simd);
+    int32_t *uniq = (int32_t *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(int32_t));
+    const size_t nu = orc_unique_experts(ids, s, k, uniq);
+    int rc = 0;
+    for (size_t u = 0; u < nu; u++) {
+        const orc_slot *slot = L->experts[uniq[u]];
+        if (!slot) { rc = -1; break; }
+        orc_apply_single_expert_act(slot, ids, wts, s, k, xl, mh, i, simd, &lw->act, routed);
+    }
+    if (lw->norm)
+        for (size_t si = 0; si < s; si++) orc_rmsnorm(routed + si * mh, lw->norm, mh, lw->eps);
+    orc_matmul_qt(out, routed, &lw->up_proj, s, simd);
+    free(uniq);
+    free(routed);
+    free(xl);
+    free(wts);
+    free(ids);
+    return rc;
+}
+
+int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, float *out,
+                    int32_t *ids_out, float *w_out) {
+    size_t d = L->hidden, i = L->moe_inter, E = L->n_experts, k = L->topk;
+    if (k > E) k = E;
+    int32_t *ids = (int32_t *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(int32_t));
+    float *wts = (float *)malloc((s ? s : 1) * (k ? k : 1) * sizeof(float));
+    orc_moe_route(L, x, s, ids, wts);
     if (ids_out) memcpy(ids_out, ids, s * k * sizeof(int32_t));
     if (w_out) memcpy(w_out, wts, s * k * sizeof(float));
     memset(out, 0, s * d * sizeof(float));
@@ -451,7 +506,6 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, 
     free(uniq);
     free(wts);
     free(ids);
-    free(logits);
     return rc;
 }
 

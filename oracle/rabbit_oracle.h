@@ -28,7 +28,15 @@ extern "C" {
 #endif
 
 enum { ORC_QT_F32 = 0, ORC_QT_I4_GROUPED = 1, ORC_QT_MXFP4 = 2 };
-enum { ORC_ACT_SILU = 0 };
+enum { ORC_ACT_SILU = 0, ORC_ACT_SITU = 1 };
+
+/* Activation (glm52/moe.rs:49-52): Silu, or Situ { beta, linear_beta: Option<f32> }. */
+typedef struct {
+    int kind;              /* ORC_ACT_* */
+    float beta;
+    float linear_beta;
+    int has_linear_beta;
+} orc_act;
 enum { ORC_FAMILY_QWEN38 = 0, ORC_FAMILY_GLM52 = 1, ORC_FAMILY_KIMI_K3 = 2 };
 
 /* One quantized matrix, mirrors QT / QTKind (quant.rs:77-110). Host pointers. */
@@ -88,9 +96,18 @@ size_t orc_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq)
 float orc_siluf(float x);                                                /* glm52/moe.rs:33-35 */
 float orc_sigmoid(float x);                                              /* kimi_linear/ops.rs:26-28 */
 
-/* apply_single_expert (glm52/moe.rs:463-513): accumulates into out[s, d]. */
+/* Activation::combine (glm52/moe.rs:58-70): silu(g) * u, or
+ * (beta * tanh(g / beta)) * (1 / (1 + exp(-g))) * u' with u' = linear_beta * tanh(u / linear_beta)
+ * when linear_beta is set (else u). */
+float orc_act_combine(const orc_act *a, float g, float u);
+
+/* apply_single_expert (glm52/moe.rs:463-513): accumulates into out[s, d]. _act: with an
+ * activation (NULL = Silu). */
 void orc_apply_single_expert(const orc_slot *slot, const int32_t *ids, const float *wts, size_t s,
                              size_t k, const float *x, size_t d, size_t i, int simd, float *out);
+void orc_apply_single_expert_act(const orc_slot *slot, const int32_t *ids, const float *wts, size_t s,
+                                 size_t k, const float *x, size_t d, size_t i, int simd, const orc_act *act,
+                                 float *out);
 
 /* One MoE layer's weights (router + shared expert), by family. */
 typedef struct {
@@ -115,6 +132,24 @@ int orc_moe_forward(const orc_moe_layer *L, const float *x, size_t s, int simd, 
                     int32_t *ids_out, float *w_out);
 /* Router logits plus optional synthetic skew, [s, n_experts] (generate.rs:279-281). */
 void orc_router_logits(const orc_moe_layer *L, const float *x, size_t s, float *logits);
+
+/* The layer's routing alone (the router half of moe_forward / moe): ids, w [s, min(topk, E)]. */
+void orc_moe_route(const orc_moe_layer *L, const float *x, size_t s, int32_t *ids, float *w);
+
+/* K3's latent MoE (kimi_k3/moe.rs:64-116): route x [s, hidden] with L's router at full width,
+ * x_latent = matmul_qt(x, down_proj [moe_hidden, hidden]), every unique routed expert
+ * (L->experts, shaped for moe_hidden) accumulated at moe_hidden with `act`, optional rmsnorm of
+ * each summed row (norm [moe_hidden], eps), then out = matmul_qt(routed, up_proj [hidden,
+ * moe_hidden]) (overwritten; no shared expert). Returns 0, or -1 on a missing expert. */
+typedef struct {
+    size_t moe_hidden;
+    orc_qt down_proj, up_proj;
+    const float *norm;     /* NULL: no norm */
+    float eps;
+    orc_act act;
+} orc_latent;
+int orc_latent_moe(const orc_moe_layer *L, const orc_latent *lw, const float *x, size_t s, int simd, float *out,
+                   int32_t *ids_out, float *w_out);
 
 /* --- norms and the MoE sublayer ----------------------------------------------------------- */
 /* kimi_linear/ops.rs:46-53 rmsnorm, in place: r = 1 / sqrt((sum_f64(v^2) / n) as f32 + eps), then

@@ -27,8 +27,13 @@ from .abi import (ACT_SILU, FAMILY_GLM52, FAMILY_KIMI_K3, FAMILY_QWEN38, QT_F32,
 
 __all__ = ["Context", "QT", "Slot", "Shards", "RbtError", "load", "QT_F32", "QT_I4_GROUPED", "QT_MXFP4",
            "FAMILY_QWEN38", "FAMILY_GLM52", "FAMILY_KIMI_K3", "ACT_SILU", "NAMING_QWEN38_MXFP4",
-           "NAMING_KIMI_K3_MXFP4"]
-from .abi import NAMING_KIMI_K3_MXFP4, NAMING_QWEN38_MXFP4  # noqa: E402
+           "NAMING_KIMI_K3_MXFP4", "ACT_SITU", "situ"]
+from .abi import NAMING_KIMI_K3_MXFP4, NAMING_QWEN38_MXFP4, ACT_SITU  # noqa: E402
+
+
+def situ(beta, linear_beta=None):
+    """Activation::Situ { beta, linear_beta } (glm52/moe.rs:49-52) for apply_single_expert / latent_moe."""
+    return abi.RbtActivation(ACT_SITU, beta, 0.0 if linear_beta is None else linear_beta, int(linear_beta is not None))
 
 
 class RbtError(RuntimeError):
@@ -266,16 +271,41 @@ class Context:
 
     # -- experts ----------------------------------------------------------------------------
     def apply_single_expert(self, slot, ids, w, s, k, x, d, i, out, activation=ACT_SILU):
-        """slot: a Slot (host or device weights) or a pool pointer from pool_get()."""
-        sc = slot if isinstance(slot, C._Pointer) else C.pointer(slot.c())
-        if _is_torch(x):
-            self._torch_sync()
-            self.check(self.lib.rbt_apply_single_expert_d(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i,
-                                                          activation, _ptr(out)))
-            self.sync()
+        """slot: a Slot (host or device weights) or a pool pointer from pool_get(). activation: ACT_SILU
+        or an abi.RbtActivation (situ(beta, linear_beta))."""
+        if isinstance(slot, C._Pointer):
+            sc = slot
+        elif isinstance(slot, (int, C.c_void_p)):
+            sc = C.cast(slot, C.POINTER(RbtExpertSlot))
         else:
-            self.check(self.lib.rbt_apply_single_expert(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i,
-                                                        activation, _ptr(out)))
+            sc = C.pointer(slot.c())
+        par = isinstance(activation, abi.RbtActivation)
+        dev = _is_torch(x)
+        if dev:
+            self._torch_sync()
+        if par:
+            fn = self.lib.rbt_apply_single_expert_act_d if dev else self.lib.rbt_apply_single_expert_act
+            self.check(fn(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i, C.byref(activation), _ptr(out)))
+        else:
+            fn = self.lib.rbt_apply_single_expert_d if dev else self.lib.rbt_apply_single_expert
+            self.check(fn(self.h, sc, _ptr(ids), _ptr(w), s, k, _ptr(x), d, i, activation, _ptr(out)))
+        if dev:
+            self.sync()
+        return out
+
+    def latent_moe(self, layer, moe_hidden, down_proj: QT, up_proj: QT, x, s, out, norm=None, eps=1e-5,
+                   activation=None, ids_out=None, w_out=None, sync=True):
+        """K3's latent MoE (kimi_k3/moe.rs:64-116) on device buffers: route with `layer`'s router at
+        full width, its experts (pool, shaped for moe_hidden) on down_proj(x), optional rmsnorm, then
+        up_proj. out [s, hidden] is overwritten."""
+        act = activation if activation is not None else abi.RbtActivation(ACT_SILU, 0.0, 0.0, 0)
+        lw = abi.RbtLatentMoeDesc(moe_hidden, down_proj.c(), up_proj.c(), _ptr(norm), eps, act)
+        if sync:
+            self._torch_sync()
+        self.check(self.lib.rbt_latent_moe_d(self.h, layer, C.byref(lw), _ptr(x), s, _ptr(out), _ptr(ids_out),
+                                             _ptr(w_out)))
+        if sync:
+            self.sync()
         return out
 
     # -- pool (ExpertCache) -----------------------------------------------------------------

@@ -26,7 +26,7 @@ STATUS_NAMES = {0: "RBT_OK", -1: "RBT_E_INVALID", -2: "RBT_E_SHAPE", -3: "RBT_E_
 
 QT_F32, QT_I4_GROUPED, QT_MXFP4 = 0, 1, 2
 FAMILY_QWEN38, FAMILY_GLM52, FAMILY_KIMI_K3 = 0, 1, 2
-ACT_SILU = 0
+ACT_SILU, ACT_SITU = 0, 1
 
 
 class RbtQT(C.Structure):
@@ -34,9 +34,19 @@ class RbtQT(C.Structure):
                 ("data", C.c_void_p), ("scale", C.c_void_p), ("group_size", C.c_size_t)]
 
 
+class RbtActivation(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("beta", C.c_float), ("linear_beta", C.c_float),
+                ("has_linear_beta", C.c_int32)]
+
+
 class RbtExpertSlot(C.Structure):
     _fields_ = [("eid", C.c_uint32), ("fused", C.c_int32), ("gate", RbtQT), ("up", RbtQT),
                 ("gate_up", RbtQT), ("down", RbtQT)]
+
+
+class RbtLatentMoeDesc(C.Structure):
+    _fields_ = [("moe_hidden", C.c_size_t), ("down_proj", RbtQT), ("up_proj", RbtQT), ("norm", C.c_void_p),
+                ("eps", C.c_float), ("act", RbtActivation)]
 
 
 class RbtMoeLayerDesc(C.Structure):
@@ -90,6 +100,11 @@ SIGNATURES = {
     "rbt_unique_experts": (_I, [_P, _S, _S, _P]),
     "rbt_apply_single_expert": (_I, [_CTX, C.POINTER(RbtExpertSlot), _P, _P, _S, _S, _P, _S, _S, _I, _P]),
     "rbt_apply_single_expert_d": (_I, [_CTX, C.POINTER(RbtExpertSlot), _P, _P, _S, _S, _P, _S, _S, _I, _P]),
+    "rbt_apply_single_expert_act": (_I, [_CTX, C.POINTER(RbtExpertSlot), _P, _P, _S, _S, _P, _S, _S,
+                                         C.POINTER(RbtActivation), _P]),
+    "rbt_apply_single_expert_act_d": (_I, [_CTX, C.POINTER(RbtExpertSlot), _P, _P, _S, _S, _P, _S, _S,
+                                           C.POINTER(RbtActivation), _P]),
+    "rbt_latent_moe_d": (_I, [_CTX, _U32, C.POINTER(RbtLatentMoeDesc), _P, _S, _P, _P, _P]),
     "rbt_pool_put": (_I, [_CTX, _U32, C.POINTER(RbtExpertSlot)]),
     "rbt_pool_put_device": (_I, [_CTX, _U32, C.POINTER(RbtExpertSlot)]),
     "rbt_pool_alloc": (C.POINTER(RbtExpertSlot), [_CTX, _U32, _U32, _I, _S, _S, _S]),

@@ -53,6 +53,9 @@ enum ScratchSlot {
   SC_NRM,   // sublayer: the normalised rows
   SC_SUB,   // sublayer: the MoE output before the residual add
   SC_PLN,   // sublayer (host call): post_ln staged
+  SC_LTAB,  // latent MoE: expert table at the latent width
+  SC_XL,    // latent MoE: x projected down
+  SC_ROUTED,  // latent MoE: summed routed rows
   SC_N
 };
 
@@ -313,16 +316,16 @@ int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) 
 
 // Runs gate/up (+SiLU) then down for `njobs` (expert, token) pairs.
 //   x: [tokens, d], x_index[p] = token of pair p; y: [njobs, d].
-//   h: scratch of njobs * 2i floats. The fast path writes the stacked gate|up dot products there
-//   and the down kernel applies silu(g) * u while loading its activations; the generic path writes
-//   the activated [njobs, i] directly.
+//   h: scratch of njobs * 2i floats. The fast path writes the stacked gate|up dot products to a
+//   second scratch and a small kernel writes act(g, u) (SiLU, or K3's Situ) to h; the generic path
+//   writes the activated [njobs, i] to h directly.
 int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                  const int *njobs_dev, const float *x, const int *x_index, size_t d, size_t i, float *h, float *y,
-                 hipEvent_t *mark = nullptr) {
+                 hipEvent_t *mark = nullptr, const RbtAct &act = RbtAct{}) {
   const bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
   const bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
   if (fast_gu && fast_dn) {
-    // stacked gate|up dot products (column parts) into gu, silu(g) * u into h, down from h.
+    // stacked gate|up dot products (column parts) into gu, act(g, u) into h, down from h.
     const int parts = rbt::decode_parts((int)d);
     const long gs_stride = (long)(2 * parts * i);
     float *gu;
@@ -333,13 +336,13 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
       HIP_OK(c, hipEventRecord(mark[0], c->stream));
       HIP_OK(c, hipEventRecord(mark[1], c->stream));
     }
-    HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h));
+    HIP_OK(c, rbt::launch_swiglu(*c, gu, gs_stride, (int)i, njobs, njobs_dev, parts, h, act));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
                                  (int)i, (int)d, y, (long)d));
     return RBT_OK;
   }
   HIP_OK(c, rbt::launch_pair_generic(*c, true, kind, gs, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d,
-                                     (int)i, h, (long)i));
+                                     (int)i, h, (long)i, act));
   if (mark) {
     HIP_OK(c, hipEventRecord(mark[0], c->stream));
     HIP_OK(c, hipEventRecord(mark[1], c->stream));
@@ -734,9 +737,24 @@ int route_dev(rbt_ctx *c, bool softmax, const float *logits, const float *bias, 
   return RBT_OK;
 }
 
+// rbt_activation -> the kernels' RbtAct.
+int to_act(rbt_ctx *c, const rbt_activation *a, RbtAct *out) {
+  *out = RbtAct{};
+  if (!a || a->kind == RBT_ACT_SILU) return RBT_OK;
+  if (a->kind != RBT_ACT_SITU) return fail(c, RBT_E_INVALID, "activation %d", (int)a->kind);
+  // Situ divides by beta (and linear_beta): zero or non-finite values have no defined result
+  if (!std::isfinite(a->beta) || a->beta == 0.0f) return fail(c, RBT_E_INVALID, "situ beta %g", (double)a->beta);
+  if (a->has_linear_beta && (!std::isfinite(a->linear_beta) || a->linear_beta == 0.0f))
+    return fail(c, RBT_E_INVALID, "situ linear_beta %g", (double)a->linear_beta);
+  out->kind = 1;
+  out->beta = a->beta;
+  out->lbeta = a->linear_beta;
+  out->has_lb = a->has_linear_beta ? 1 : 0;
+  return RBT_OK;
+}
+
 int apply_single_dev(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s, size_t k,
-                     const float *x, size_t d, size_t i, int32_t act, float *out) {
-  if (act != RBT_ACT_SILU) return fail(c, RBT_E_UNSUPPORTED, "activation %d", (int)act);
+                     const float *x, size_t d, size_t i, const RbtAct &act, float *out) {
   if (!slot || !ids || !w || !x || !out) return fail(c, RBT_E_INVALID, "null argument");
   if (s == 0 || k == 0) return RBT_OK;
   RbtExpertDev v;
@@ -751,8 +769,90 @@ int apply_single_dev(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids
   RBT_TRY(scratch_t(c, SC_H, s * i, &h));
   RBT_TRY(scratch_t(c, SC_YY, s * d, &yy));
   HIP_OK(c, rbt::launch_single_rows(*c, ids, w, (int)s, (int)k, (int)slot->eid, ptok, pw, nr));
-  RBT_TRY(expert_pairs(c, kind, gs, nullptr, v, (int)s, nr, x, ptok, d, i, h, yy));
+  RBT_TRY(expert_pairs(c, kind, gs, nullptr, v, (int)s, nr, x, ptok, d, i, h, yy, nullptr, act));
   HIP_OK(c, rbt::launch_accumulate(*c, yy, (int)s, (int)d, ptok, pw, nr, out));
+  return RBT_OK;
+}
+
+// kimi_k3/moe.rs:64-116: route at full width, project down, the routed experts at moe_hidden, the
+// optional norm of each summed row, project up.
+static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc *lw, const float *x, size_t s,
+                          float *out, int32_t *ids_out, float *w_out) {
+  auto lit = c->layers.find(layer);
+  if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
+  if (!lw) return fail(c, RBT_E_INVALID, "null latent descriptor");
+  if (s == 0) return RBT_OK;
+  if (!x || !out) return fail(c, RBT_E_INVALID, "null x or out");
+  const rbt_moe_layer_desc &D = lit->second.desc;
+  const size_t H = D.hidden, MH = lw->moe_hidden, I = D.moe_inter, E = D.n_experts;
+  const size_t k = std::min(D.topk, E);
+  if (MH == 0 || lw->down_proj.rows != MH || lw->down_proj.cols != H || lw->up_proj.rows != H ||
+      lw->up_proj.cols != MH)
+    return fail(c, RBT_E_SHAPE, "latent projections must be [moe_hidden, hidden] and [hidden, moe_hidden]");
+  if (s > (size_t)INT32_MAX / std::max<size_t>(k, 1)) return fail(c, RBT_E_INVALID, "too many tokens");
+  RbtAct act;
+  RBT_TRY(to_act(c, &lw->act, &act));
+  const int S = (int)s, K = (int)k, P = S * K;
+  // the layer's pool slots seen at (moe_hidden, moe_inter), plus a zero job for the shared slots
+  std::vector<RbtExpertDev> t(E + 1);
+  memset(t.data(), 0, (E + 1) * sizeof(RbtExpertDev));
+  int kind = -1;
+  size_t gs = 0;
+  for (auto &kv : c->pool) {
+    if ((uint32_t)(kv.first >> 32) != layer) continue;
+    const uint32_t eid = (uint32_t)kv.first;
+    if (eid >= E) continue;
+    int kd;
+    size_t g;
+    RBT_TRY(slot_view(c, &kv.second.slot, MH, I, &t[eid], &kd, &g));
+    if (kind >= 0 && (kd != kind || g != gs)) return fail(c, RBT_E_UNSUPPORTED, "layer %u: experts mix formats", layer);
+    kind = kd;
+    gs = g;
+  }
+  if (kind < 0) return fail(c, RBT_E_NOT_RESIDENT, "layer %u has no resident experts", layer);
+  double *mid, *bnd;
+  int32_t *ids;
+  float *wts, *shs, *tw, *xl, *h, *yy, *routed;
+  RbtExpertDev *table, *pjob;
+  int *ptok, *tpair;
+  RBT_TRY(scratch_t(c, SC_MID, (size_t)S * E, &mid));
+  RBT_TRY(scratch_t(c, SC_BND, (size_t)S * E, &bnd));
+  RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
+  RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
+  RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
+  RBT_TRY(scratch_t(c, SC_LTAB, E + 1, &table));
+  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)(P + S), &pjob));
+  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)(P + S), &ptok));
+  RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
+  RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
+  RBT_TRY(scratch_t(c, SC_XL, (size_t)S * MH, &xl));
+  RBT_TRY(scratch_t(c, SC_H, (size_t)P * I * 2, &h));
+  RBT_TRY(scratch_t(c, SC_YY, (size_t)P * MH, &yy));
+  RBT_TRY(scratch_t(c, SC_ROUTED, (size_t)S * MH, &routed));
+  HIP_OK(c, hipMemcpyAsync(table, t.data(), (E + 1) * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
+  int *dflags = c->d_flags;
+  // routing of the full-width x (certified logits, exact folds where the order is not certain)
+  rbt::RouterArgs ra{D.family, (int)E, (int)E, K, (int)H, S, D.logit_bias, D.router_bias, D.norm_topk,
+                     D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
+  if (rbt::router_exact_ok(S, (int)H) && (uintptr_t)x % 16 == 0) {
+    float *lg;
+    RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * E, &lg));
+    HIP_OK(c, rbt::launch_router_logits_exact(*c, x, S, (int)H, D.router, (int)E, nullptr, lg));
+    HIP_OK(c, rbt::launch_logits_to_mid(*c, lg, (size_t)S * E, mid, bnd));
+  } else {
+    HIP_OK(c, rbt::launch_router_logits(*c, x, S, (int)H, D.router, (int)E, nullptr, mid, bnd));
+  }
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB));
+  RBT_TRY(matmul_dev(c, xl, x, &lw->down_proj, s));
+  HIP_OK(c, rbt::launch_group(*c, ids, wts, S, K, (int)E, table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
+                              dflags + FLAG_UNIQ));
+  RbtExpertDev none{};
+  RBT_TRY(expert_pairs(c, kind, gs, pjob, none, P, nullptr, xl, ptok, MH, I, h, yy, nullptr, act));
+  HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
+  if (lw->norm) HIP_OK(c, rbt::launch_rmsnorm(*c, routed, lw->norm, lw->eps, routed, s, MH, false));
+  RBT_TRY(matmul_dev(c, out, routed, &lw->up_proj, s));
+  if (ids_out) HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
+  if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, wts, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
   return RBT_OK;
 }
 
@@ -762,6 +862,12 @@ int apply_single_dev(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids
 // C ABI
 // ================================================================================================
 extern "C" {
+
+int rbt_latent_moe_d(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc *lw, const float *x, size_t s,
+                     float *out, int32_t *ids_out, float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  return latent_moe_dev(c, layer, lw, x, s, out, ids_out, w_out);
+}
 
 const char *rbt_version(void) { return "rabbit_amd 0.1.0 (gfx950)"; }
 
@@ -997,15 +1103,36 @@ int rbt_unique_experts(const int32_t *ids, size_t s, size_t k, int32_t *uniq) {
   return n;
 }
 
+int rbt_apply_single_expert_act_d(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w,
+                                  size_t s, size_t k, const float *x, size_t d, size_t i, const rbt_activation *act,
+                                  float *out) {
+  if (!c) return RBT_E_INVALID;
+  RbtAct a;
+  RBT_TRY(to_act(c, act, &a));
+  return apply_single_dev(c, slot, ids, w, s, k, x, d, i, a, out);
+}
+
 int rbt_apply_single_expert_d(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s,
                               size_t k, const float *x, size_t d, size_t i, int32_t act, float *out) {
   if (!c) return RBT_E_INVALID;
-  return apply_single_dev(c, slot, ids, w, s, k, x, d, i, act, out);
+  if (act != RBT_ACT_SILU) return fail(c, RBT_E_INVALID, "activation %d needs its parameters", (int)act);
+  return apply_single_dev(c, slot, ids, w, s, k, x, d, i, RbtAct{}, out);
 }
 
 int rbt_apply_single_expert(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w, size_t s,
                             size_t k, const float *x, size_t d, size_t i, int32_t act, float *out) {
   if (!c) return RBT_E_INVALID;
+  if (act != RBT_ACT_SILU) return fail(c, RBT_E_INVALID, "activation %d needs its parameters", (int)act);
+  const rbt_activation silu{RBT_ACT_SILU, 0.0f, 0.0f, 0};
+  return rbt_apply_single_expert_act(c, slot, ids, w, s, k, x, d, i, &silu, out);
+}
+
+int rbt_apply_single_expert_act(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids, const float *w,
+                                size_t s, size_t k, const float *x, size_t d, size_t i, const rbt_activation *act,
+                                float *out) {
+  if (!c) return RBT_E_INVALID;
+  RbtAct a;
+  RBT_TRY(to_act(c, act, &a));
   if (!slot || !ids || !w || !x || !out) return fail(c, RBT_E_INVALID, "null argument");
   if (s == 0 || k == 0) return RBT_OK;
   rbt_expert_slot dslot;
@@ -1027,7 +1154,7 @@ int rbt_apply_single_expert(rbt_ctx *c, const rbt_expert_slot *slot, const int32
   RBT_TRY(stage_in(c, SC_W_OUT, w, s * k * 4, &dw));
   RBT_TRY(scratch_t(c, SC_OUT, s * d, &dout));
   HIP_OK(c, hipMemcpyAsync(dout, out, s * d * 4, hipMemcpyHostToDevice, c->stream));
-  RBT_TRY(apply_single_dev(c, use, (const int32_t *)dids, (const float *)dw, s, k, (const float *)dx, d, i, act,
+  RBT_TRY(apply_single_dev(c, use, (const int32_t *)dids, (const float *)dw, s, k, (const float *)dx, d, i, a,
                            dout));
   HIP_OK(c, hipMemcpyAsync(out, dout, s * d * 4, hipMemcpyDeviceToHost, c->stream));
   return sync_and_check(c);

@@ -305,12 +305,13 @@ __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restr
   }
 }
 
-// Activation between the stacked gate/up GEMV and the down GEMV: h[p, k] = silu(g) * u with g and
+// Activation between the stacked gate/up GEMV and the down GEMV: h[p, k] = act(g, u) with g and
 // u summed over the producer's column parts (gu per pair: PARTS gate vectors, then PARTS up vectors
-// of `half` floats each). silu(g) * u rounds as the reference writes it (glm52/moe.rs:33-35, :58).
+// of `half` floats each). The activation rounds as the reference writes it (glm52/moe.rs:33-35,
+// :58-70).
 template <int PARTS>
 __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, long gu_stride, int half, int npairs,
-                                                const int *__restrict__ npairs_dev, float *__restrict__ h) {
+                                                const int *__restrict__ npairs_dev, RbtAct act, float *__restrict__ h) {
   int np = npairs;
   if (npairs_dev) np = min(np, *npairs_dev);
   const long n = (long)np * half;
@@ -323,19 +324,21 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, lo
       gv += g[j * half + k];
       uv += g[(PARTS + j) * half + k];
     }
-    h[idx] = rbt_silu(gv) * uv;
+    h[idx] = rbt_act(act, gv, uv);
   }
 }
 
 hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
-                         int parts, float *h) {
+                         int parts, float *h, const RbtAct &act) {
   const long n = (long)npairs * half;
   if (n <= 0) return hipSuccess;
   const int blocks = (int)std::min<long>((n + 255) / 256, (long)c.num_cu * 4);
   if (parts == 2)
-    hipLaunchKernelGGL(k_swiglu<2>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev, h);
+    hipLaunchKernelGGL(k_swiglu<2>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev,
+                       act, h);
   else
-    hipLaunchKernelGGL(k_swiglu<1>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev, h);
+    hipLaunchKernelGGL(k_swiglu<1>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev,
+                       act, h);
   return hipGetLastError();
 }
 
@@ -346,7 +349,7 @@ __global__ __launch_bounds__(256) void k_pair_generic(const RbtExpertDev *__rest
                                                       int njobs, const int *__restrict__ njobs_dev, int kind, int gs,
                                                       const float *__restrict__ x, const int *__restrict__ x_index,
                                                       long x_stride, int cols, int rows, float *__restrict__ y,
-                                                      long y_stride) {
+                                                      long y_stride, RbtAct act) {
   const int lane = threadIdx.x & 63;
   const long item = (long)blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
   int nj = njobs;
@@ -380,7 +383,7 @@ __global__ __launch_bounds__(256) void k_pair_generic(const RbtExpertDev *__rest
     }
     acc[m] = rbt_group_sum<64>(a);
   }
-  if (lane == 0) y[(long)u * y_stride + r] = GATEUP ? rbt_silu(acc[0]) * acc[1] : acc[0];
+  if (lane == 0) y[(long)u * y_stride + r] = GATEUP ? rbt_act(act, acc[0], acc[1]) : acc[0];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -588,16 +591,17 @@ hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *j
 
 hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,
                                const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
-                               const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride) {
+                               const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride,
+                               const RbtAct &act) {
   long items = (long)njobs * rows;
   if (items <= 0) return hipSuccess;
   dim3 grid((unsigned)((items + 3) / 4)), block(256);
   if (gateup)
     hipLaunchKernelGGL(k_pair_generic<true>, grid, block, 0, c.stream, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
-                       x_index, x_stride, cols, rows, y, y_stride);
+                       x_index, x_stride, cols, rows, y, y_stride, act);
   else
     hipLaunchKernelGGL(k_pair_generic<false>, grid, block, 0, c.stream, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
-                       x_index, x_stride, cols, rows, y, y_stride);
+                       x_index, x_stride, cols, rows, y, y_stride, act);
   return hipGetLastError();
 }
 

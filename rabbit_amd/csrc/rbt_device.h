@@ -46,6 +46,21 @@ __device__ __forceinline__ float rbt_e2m1(uint32_t n) {
 
 __device__ __forceinline__ float rbt_silu(float g) { return g / (1.0f + expf(-g)); }
 
+// Activation::combine (glm52/moe.rs:58-70): silu(g) * u, or Situ
+// (beta * tanh(g / beta)) * (1 / (1 + exp(-g))) * u' with u' = lbeta * tanh(u / lbeta) when has_lb.
+// Each fp32 operation rounded on its own, in the reference's order (tanh and exp are the device's).
+struct RbtAct {
+  int kind = 0;  // 0: Silu, 1: Situ (RBT_ACT_*)
+  float beta = 0.0f, lbeta = 0.0f;
+  int has_lb = 0;
+};
+__device__ __forceinline__ float rbt_act(const RbtAct &a, float g, float u) {
+  if (a.kind != 1) return rbt_silu(g) * u;
+  if (a.has_lb) u = __fmul_rn(a.lbeta, tanhf(__fdiv_rn(u, a.lbeta)));
+  const float situ = __fmul_rn(__fmul_rn(a.beta, tanhf(__fdiv_rn(g, a.beta))), __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g))));
+  return __fmul_rn(situ, u);
+}
+
 // Correctly rounded fp32 square root for positive normal x. v_sqrt_f32 is only faithful (within
 // one ulp), so the neighbours of its result are tested with one fma residual each and the rounded
 // value picked: the lowering LLVM uses for a correctly rounded llvm.sqrt.f32.

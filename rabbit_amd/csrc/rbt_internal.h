@@ -68,13 +68,14 @@ hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *j
                          int rows, float *y, long y_stride, int parts = 1);
 // h[p, k] = silu(sum of gate parts) * (sum of up parts) for the stacked producer's output.
 hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
-                         int parts, float *h);
+                         int parts, float *h, const RbtAct &act = RbtAct{});
 // Column parts the stacked gate/up kernel splits a row of `cols` columns into; its output per job
 // is 2 * parts vectors of `half` floats (gate parts, then up parts).
 int decode_parts(int cols);
 hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,
                                const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
-                               const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride);
+                               const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride,
+                               const RbtAct &act = RbtAct{});
 
 // xgemm.hip: MXFP4 expert products on the matrix cores (decode shapes).
 bool xgemm_ok(int kind, size_t d, size_t i, int S, int k, int has_shared);

@@ -398,3 +398,159 @@ def test_moe_sublayer_is_residual_plus_forward_of_normalised(orc):
     assert bits_equal(got, x + out)
     plain, _, _ = L.forward(x, s)
     assert not np.allclose(got, x + plain)
+
+
+# ---- K3: Situ activation and the latent MoE ----------------------------------------------------------
+def _situ64(g, u, beta, lb):
+    g = np.asarray(g, np.float64)
+    u = np.asarray(u, np.float64)
+    if lb is not None:
+        u = lb * np.tanh(u / lb)
+    return beta * np.tanh(g / beta) / (1.0 + np.exp(-g)) * u
+
+
+@pytest.mark.parametrize("gate,up,lb", [([-3.0, -0.5, 0.0, 0.5, 3.0, 10.0], [2.0, -1.0, 4.0, -4.0, 0.1, 30.0], 25.0),
+                                        ([-2.0, 0.0, 1.5], [3.0, -2.0, 0.5], None)])
+def test_situ_kats(orc, gate, up, lb):
+    # kimi_linear/ops.rs:236-260: beta 4, with and without linear_beta, against the formula in fp64
+    act = orc.situ(4.0, lb)
+    got = np.array([orc.act_combine(act, g, u) for g, u in zip(gate, up)])
+    assert np.max(np.abs(got - _situ64(gate, up, 4.0, lb))) < 1e-5
+
+
+def test_situ_special_values(orc):
+    # kimi_linear/ops.rs:262-277: gate 0 gives exactly 0 whatever up is; gate >> beta saturates to beta * up
+    act = orc.situ(4.0, 25.0)
+    assert orc.act_combine(act, 0.0, 123.0) == 0.0 and orc.act_combine(act, 0.0, -456.0) == 0.0
+    assert abs(orc.act_combine(orc.situ(4.0), 1000.0, 2.0) - 8.0) < 1e-3
+    # linear_beta saturates up: lb * tanh(u / lb) -> lb for u >> lb
+    assert abs(orc.act_combine(orc.situ(4.0, 2.0), 1000.0, 1e4) - 8.0) < 1e-3
+    # beta -> inf: beta * tanh(g / beta) -> g, so Situ -> SiLU (a dropped sigmoid or tanh fails this)
+    for g, u in ((-2.5, 0.7), (0.3, -1.1), (4.0, 2.0)):
+        silu = orc.act_combine(None, g, u)
+        assert abs(orc.act_combine(orc.situ(1e4), g, u) - silu) < 1e-5 * max(1.0, abs(silu))
+        assert abs(silu - g / (1.0 + math.exp(-g)) * u) < 1e-6
+
+
+def test_situ_expert_matches_independent_and_differs_from_silu(orc):
+    # glm52/moe.rs:842-883: an expert with Situ(4, 25) against an independent fp64 re-derivation
+    d, i = 4, 3
+    g, u, dn = xorshift_vec(i * d, 5), xorshift_vec(i * d, 6), xorshift_vec(d * i, 7)
+    slot = orc.Slot(0, orc.QT.f32(dn, d, i), gate=orc.QT.f32(g, i, d), up=orc.QT.f32(u, i, d))
+    x = xorshift_vec(d, 8)
+    ids, w = np.zeros((1, 1), np.int32), np.ones((1, 1), np.float32)
+    act = orc.situ(4.0, 25.0)
+    out = orc.apply_single_expert(slot, ids, w, x, d, i, np.zeros(d, np.float32), act=act)
+    x64 = x.astype(np.float64)
+    hg = g.reshape(i, d).astype(np.float64) @ x64
+    hu = u.reshape(i, d).astype(np.float64) @ x64
+    exp = dn.reshape(d, i).astype(np.float64) @ _situ64(hg, hu, 4.0, 25.0)
+    assert np.max(np.abs(out - exp)) < 1e-5
+    silu = orc.apply_single_expert(slot, ids, w, x, d, i, np.zeros(d, np.float32))
+    assert not np.array_equal(out, silu)
+
+
+def test_situ_fused_gate_up_matches_separate_bit_exact(orc):
+    # glm52/moe.rs:885-919: the fused branch's per-element combine agrees with the separate branch's
+    d, i = 6, 8
+    gate, up, down = xorshift_vec(i * d, 17), xorshift_vec(i * d, 18), xorshift_vec(d * i, 19)
+    sep = orc.Slot(0, orc.QT.f32(down, d, i), gate=orc.QT.f32(gate, i, d), up=orc.QT.f32(up, i, d))
+    fus = orc.Slot(0, orc.QT.f32(down, d, i), gate_up=orc.QT.f32(np.concatenate([gate, up]), 2 * i, d))
+    x = xorshift_vec(3 * d, 20)
+    ids = np.zeros((3, 1), np.int32)
+    w = np.array([[0.6], [1.3], [-0.4]], np.float32)
+    act = orc.situ(4.0, 25.0)
+    a = orc.apply_single_expert(sep, ids, w, x, d, i, np.zeros(3 * d, np.float32), act=act)
+    b = orc.apply_single_expert(fus, ids, w, x, d, i, np.zeros(3 * d, np.float32), act=act)
+    assert bits_equal(a, b)
+
+
+def _latent_fixture(orc, seed, E=4, H=6, MH=4, I=3, k=2):
+    # kimi_k3/moe.rs:232-262's shapes: a sigmoid router with a correction bias over the full width,
+    # experts at moe_hidden, projections [MH, H] and [H, MH]
+    dense = {}
+    experts = {}
+    for e in range(E):
+        g, u, dn = (xorshift_vec(I * MH, seed + 10 * e + j) for j in range(3))
+        experts[e] = orc.Slot(e, orc.QT.f32(dn, MH, I), gate=orc.QT.f32(g, I, MH), up=orc.QT.f32(u, I, MH))
+        dense[e] = (g.reshape(I, MH), u.reshape(I, MH), dn.reshape(MH, I))
+    router = xorshift_vec(E * H, seed + 100)
+    bias = xorshift_vec(E, seed + 101)
+    L = orc.MoeLayer(orc.FAMILY_GLM52, H, I, E, k, router, experts, router_bias=bias, norm_topk=False)
+    down = xorshift_vec(MH * H, seed + 102).reshape(MH, H)
+    up = xorshift_vec(H * MH, seed + 103).reshape(H, MH)
+    return L, dense, down, up
+
+
+def _latent_expected(L, dense, down, up, x, s, norm=None, eps=1e-5, act=None):
+    ids, w = L.route(x, s)
+    x64 = x.reshape(s, -1).astype(np.float64)
+    xl = x64 @ down.astype(np.float64).T
+    routed = np.zeros((s, down.shape[0]))
+    for t in range(s):
+        for j in range(ids.shape[1]):
+            g, u, dn = (a.astype(np.float64) for a in dense[int(ids[t, j])])
+            hg, hu = g @ xl[t], u @ xl[t]
+            h = hg / (1.0 + np.exp(-hg)) * hu if act is None else _situ64(hg, hu, *act)
+            routed[t] += w[t, j] * (dn @ h)
+    if norm is not None:
+        routed = routed / np.sqrt(np.mean(routed ** 2, axis=1, keepdims=True) + eps) * norm.astype(np.float64)
+    return routed @ up.astype(np.float64).T, routed, ids, w
+
+
+def test_latent_moe_matches_independent_without_norm(orc):
+    # kimi_k3/moe.rs:232-281: route at full width, down-project, experts at moe_hidden, up-project
+    L, dense, down, up = _latent_fixture(orc, 11)
+    s = 3
+    x = xorshift_vec(s * 6, 50)
+    out, ids, w = L.latent(x, s, 4, orc.QT.f32(down.ravel(), 4, 6), orc.QT.f32(up.ravel(), 6, 4))
+    exp, _, eids, ew = _latent_expected(L, dense, down, up, x, s)
+    assert np.array_equal(ids, eids) and bits_equal(w, ew)
+    assert np.max(np.abs(out - exp)) < 1e-5
+    # routing is the layer's own (full-width x), not that of the projected x
+    rid, _ = orc.route_sigmoid(L.router_logits(x, s)[0], 2, bias=L.router_bias, norm_topk=False)
+    assert list(rid) == list(ids[0])
+
+
+def test_latent_moe_norm_applies_to_the_summed_rows(orc):
+    # kimi_k3/moe.rs:283-330: rmsnorm of each token's summed routed output, before up_proj
+    L, dense, down, up = _latent_fixture(orc, 23)
+    s = 2
+    x = xorshift_vec(s * 6, 60)
+    norm = np.abs(xorshift_vec(4, 61)) + np.float32(0.5)
+    dq, uq = orc.QT.f32(down.ravel(), 4, 6), orc.QT.f32(up.ravel(), 6, 4)
+    out, _, _ = L.latent(x, s, 4, dq, uq, norm=norm, eps=1e-5)
+    exp, routed, _, _ = _latent_expected(L, dense, down, up, x, s, norm=norm)
+    unnormed = _latent_expected(L, dense, down, up, x, s)[1]
+    assert not np.allclose(routed, unnormed)
+    assert np.max(np.abs(out - exp)) < 1e-5
+    # per-expert normalisation would be a different (wrong) answer
+    plain, _, _ = L.latent(x, s, 4, dq, uq)
+    assert not np.allclose(out, plain)
+
+
+def test_latent_moe_with_situ(orc):
+    L, dense, down, up = _latent_fixture(orc, 31)
+    s = 3
+    x = xorshift_vec(s * 6, 70)
+    out, _, _ = L.latent(x, s, 4, orc.QT.f32(down.ravel(), 4, 6), orc.QT.f32(up.ravel(), 6, 4),
+                         act=orc.situ(4.0, 25.0))
+    exp, _, _, _ = _latent_expected(L, dense, down, up, x, s, act=(4.0, 25.0))
+    assert np.max(np.abs(out - exp)) < 1e-5
+
+
+def test_latent_moe_identity_projections_equal_routed_forward(orc):
+    # with moe_hidden == hidden and identity projections the latent MoE is the routed part of
+    # moe_forward exactly (same routing, same per-expert accumulation order)
+    d, i, E, s, k = 64, 32, 6, 3, 3
+    experts = {e: orc.Slot(e, orc.synth_mxfp4(d, i, seed=40 + 3 * e), gate=orc.synth_mxfp4(i, d, seed=41 + 3 * e),
+                           up=orc.synth_mxfp4(i, d, seed=42 + 3 * e)) for e in range(E)}
+    rng = np.random.default_rng(9)
+    router = (rng.standard_normal((E, d)) * 0.3).astype(np.float32)
+    L = orc.MoeLayer(orc.FAMILY_GLM52, d, i, E, k, router, experts, routed_scale=2.5)
+    x = rng.standard_normal((s, d)).astype(np.float32)
+    eye = orc.QT.f32(np.eye(d, dtype=np.float32).ravel(), d, d)
+    lat, lid, lw = L.latent(x, s, d, eye, eye)
+    fwd, fid, fw = L.forward(x, s)
+    assert np.array_equal(lid, fid) and bits_equal(lw, fw)
+    assert np.array_equal(lat, fwd)
