@@ -14,6 +14,10 @@ cpu_baseline = the reference's AVX-512 (or AVX2) MXFP4 tier, restated in oracle/
            host's cores over a bounded sample of the same tokens.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c1]
+
+--config c4 times the 512-token prefill instead, and --config k3l Kimi K3's latent MoE (896 experts
+at moe_hidden 3584, top-16, Situ, the routed-expert norm) one token per call; neither is the
+default line.
 """
 from __future__ import annotations
 
@@ -216,6 +220,124 @@ def bench_prefill(args, ctx, cfg, pool_gb):
     ctx.close()
 
 
+def cpu_baseline_latent(cfg, seed, x_tokens, budget_s, gpu_out=None):
+    """The oracle's SIMD tier on the latent workload (router, projections, routed experts, norm),
+    experts regenerated on the host first (not timed)."""
+    from oracle import oracle as O
+    from oracle.workload import HostLatentLayer
+    threads = physical_cores()
+    O.set_threads(threads)
+    tier = "avx512" if O.lib().orc_cpu_has_avx512() else ("avx2" if O.lib().orc_cpu_has_avx2() else "scalar")
+    host = HostLatentLayer(cfg, seed)
+    done, t_total, outs = 0, 0.0, []
+    for t in range(x_tokens.shape[0]):
+        xt = x_tokens[t:t + 1]
+        ids, _ = host.route(xt)
+        host.ensure(ids)
+        t0 = time.perf_counter()
+        out, _, _ = host._layer().latent(xt, 1, host.mh, host.down, host.up, norm=host.norm, eps=1e-5,
+                                         act=host.act, simd=True)
+        t_total += time.perf_counter() - t0
+        outs.append(out)
+        done += 1
+        if t_total >= budget_s and done >= 3:
+            break
+        if len(host.experts) > 160:
+            host.experts.clear()
+    us = t_total / done * 1e6
+    res = {"value": round(us, 1), "unit": "us/token", "cores": threads, "kind": "port",
+           "sample": f"{done} tokens of {cfg.name} (router + down projection + {cfg.topk} routed experts + norm + "
+                     f"up projection), {tier} tier of the reference's matmul kernels restated in C, rows in "
+                     f"parallel on {threads} threads; {cpu_model()}"}
+    if gpu_out is not None:
+        g = gpu_out[:done].astype(np.float64).ravel()
+        c = np.concatenate(outs).astype(np.float64).ravel()
+        res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+    return res
+
+
+def bench_latent(args, ctx, hip, cfg):
+    """K3's latent MoE, one token per call (rbt_latent_moe_d), timed as HIP-graph replays like the
+    decode line. value = us per token; the effective rate counts the router matrix, both
+    projections and the routed experts' bytes once per token."""
+    import torch
+    import rabbit_amd.workloads as W
+    t0 = time.perf_counter()
+    lat = W.build_latent_layer(ctx, cfg, layer=0, seed=args.seed)
+    pool_gb = ctx.pool_resident_bytes() / 1e9
+    log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
+    H, MH, I, k, E = cfg.hidden, cfg.extra["moe_hidden"], cfg.inter, cfg.topk, cfg.n_experts
+    G = max(1, min(args.graph_tokens, args.steps))
+    reps = (args.steps + G - 1) // G
+    steps = reps * G
+    ntok = steps + args.warmup
+    x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
+    out_all = torch.empty_like(x_all)
+    rows = [x_all[t] for t in range(ntok)]
+    outs = [out_all[t] for t in range(ntok)]
+
+    def call(t):
+        ctx.latent_moe(0, MH, lat["down"], lat["up"], rows[t], 1, outs[t], norm=lat["norm"], eps=1e-5,
+                       activation=lat["act"], sync=False)
+
+    for t in range(args.warmup):
+        call(t)
+    ctx.sync()
+    graphs = []
+    for r in range(reps):
+        g = Graph(hip, ctx.stream)
+        g.begin()
+        for j in range(G):
+            call(args.warmup + r * G + j)
+        g.end()
+        graphs.append(g)
+    torch.cuda.synchronize()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for g in graphs:
+        g.launch()
+    ctx.sync()
+    wall = time.perf_counter() - t0
+    us_per_token = wall / steps * 1e6
+    for g in graphs:
+        g.destroy()
+    t1 = time.perf_counter()
+    for t in range(args.warmup, ntok):
+        call(t)
+    ctx.sync()
+    eager_us = (time.perf_counter() - t1) / steps * 1e6
+    log(f"[bench] timed {steps} tokens: {us_per_token:.2f} us/token (eager {eager_us:.2f})")
+
+    gs = cfg.extra["proj_gs"]
+    per_exp = 2 * I * (MH // 2 + MH // 32) + MH * (I // 2 + I // 32)
+    proj = 2 * (MH * H // 2 + MH * (H // gs) * 4)
+    router = E * H * 4
+    tok_bytes = k * per_exp + proj + router
+    gbps = tok_bytes / (us_per_token * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        n_cpu = min(8, ntok)
+        cpu = cpu_baseline_latent(cfg, args.seed, x_all[:n_cpu].cpu().numpy(), args.cpu_budget,
+                                  gpu_out=out_all[:n_cpu].cpu().numpy())
+    res = {
+        "metric": "K3 latent-MoE decode us/token + effective HBM GB/s over the call (% of 8 TB/s), MXFP4 experts",
+        "value": round(us_per_token, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(us_per_token / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg.name, "hidden": H, "moe_hidden": MH, "moe_inter": I, "n_experts": E, "topk": k,
+                   "activation": "situ(4, 25)", "latent_norm": cfg.extra["latent_norm"],
+                   "projections": f"int4-grouped gs{gs}", "tokens_per_step": 1,
+                   "resident_pool_gb": round(pool_gb, 2), "graph_tokens": G},
+        "call_rate": {"bytes_per_token": tok_bytes, "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                      "note": "routed experts + router + both projections over the whole call; per-kernel "
+                              "durations are in the rocprofv3 summary"},
+        "eager_us_per_token": round(eager_us, 2),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -241,6 +363,9 @@ def main():
 
     torch.zeros(1, device="cuda")
     cfg = W.CONFIGS[args.config]
+    if args.config == "k3l":
+        ctx = R.Context(0)
+        return bench_latent(args, ctx, hip_runtime(), cfg)
     if cfg.tokens != 1 and args.config != "c4":
         raise SystemExit(f"bench.py times batch-1 decode (c1) or the 512-token prefill (c4); {args.config} is a "
                          "parity-test configuration")

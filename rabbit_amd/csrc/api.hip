@@ -53,7 +53,6 @@ enum ScratchSlot {
   SC_NRM,   // sublayer: the normalised rows
   SC_SUB,   // sublayer: the MoE output before the residual add
   SC_PLN,   // sublayer (host call): post_ln staged
-  SC_LTAB,  // latent MoE: expert table at the latent width
   SC_XL,    // latent MoE: x projected down
   SC_ROUTED,  // latent MoE: summed routed rows
   SC_N
@@ -78,6 +77,12 @@ struct Layer {
   size_t shared_gs = 0, shared_inter = 0;
   int routed_kind = -1;
   size_t routed_gs = 0;
+  // the latent MoE's view of the pool at (moe_hidden, moe_inter): n_experts jobs, then a zero job
+  bool lat_dirty = true;
+  RbtExpertDev *d_lat = nullptr;
+  size_t lat_cap = 0, lat_mh = 0;
+  int lat_kind = -1;
+  size_t lat_gs = 0;
 };
 
 }  // namespace
@@ -386,6 +391,43 @@ int refresh_table(rbt_ctx *c, uint32_t layer, Layer &L) {
   return RBT_OK;
 }
 
+// The latent MoE's table: the layer's pool slots viewed at (mh, moe_inter), rebuilt only after the
+// pool or the layer changed or for another width, so a steady-state call copies nothing.
+int refresh_latent(rbt_ctx *c, uint32_t layer, Layer &L, size_t mh) {
+  const size_t E = L.desc.n_experts;
+  if (!L.lat_dirty && L.lat_mh == mh) return RBT_OK;
+  std::vector<RbtExpertDev> t(E + 1);
+  memset(t.data(), 0, (E + 1) * sizeof(RbtExpertDev));
+  int kind = -1;
+  size_t gs = 0;
+  for (auto it = c->pool.lower_bound((uint64_t)layer << 32); it != c->pool.end() && (uint32_t)(it->first >> 32) == layer;
+       ++it) {
+    const uint32_t eid = (uint32_t)it->first;
+    if (eid >= E) continue;
+    int kd;
+    size_t g;
+    RBT_TRY(slot_view(c, &it->second.slot, mh, L.desc.moe_inter, &t[eid], &kd, &g));
+    if (kind >= 0 && (kd != kind || g != gs)) return fail(c, RBT_E_UNSUPPORTED, "layer %u: experts mix formats", layer);
+    kind = kd;
+    gs = g;
+  }
+  if (kind < 0) return fail(c, RBT_E_NOT_RESIDENT, "layer %u has no resident experts", layer);
+  if (L.lat_cap < E + 1) {
+    if (L.d_lat) HIP_OK(c, hipFree(L.d_lat));
+    L.d_lat = nullptr;
+    L.lat_cap = 0;
+    HIP_OK(c, hipMalloc(&L.d_lat, (E + 1) * sizeof(RbtExpertDev)));
+    L.lat_cap = E + 1;
+  }
+  HIP_OK(c, hipMemcpyAsync(L.d_lat, t.data(), (E + 1) * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  L.lat_kind = kind;
+  L.lat_gs = gs;
+  L.lat_mh = mh;
+  L.lat_dirty = false;
+  return RBT_OK;
+}
+
 void free_layer(Layer &L) {
   for (void *p : L.owned) (void)hipFree(p);
   L.owned.clear();
@@ -394,6 +436,9 @@ void free_layer(Layer &L) {
   L.table_n = 0;
   if (L.d_shared) (void)hipFree(L.d_shared);
   L.d_shared = nullptr;
+  if (L.d_lat) (void)hipFree(L.d_lat);
+  L.d_lat = nullptr;
+  L.lat_cap = 0;
 }
 
 int dev_copy_of(rbt_ctx *c, Layer &L, const void *host, size_t bytes, const void **out) {
@@ -467,6 +512,7 @@ int layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d, bool devi
   }
   L.set = true;
   L.dirty = true;
+  L.lat_dirty = true;
   return RBT_OK;
 }
 
@@ -483,7 +529,7 @@ int pool_insert(rbt_ctx *c, uint32_t layer, const rbt_expert_slot &slot, void *a
   e.alloc = alloc;
   e.bytes = bytes;
   auto lit = c->layers.find(layer);
-  if (lit != c->layers.end()) lit->second.dirty = true;
+  if (lit != c->layers.end()) lit->second.dirty = lit->second.lat_dirty = true;
   return RBT_OK;
 }
 
@@ -783,7 +829,8 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   if (!lw) return fail(c, RBT_E_INVALID, "null latent descriptor");
   if (s == 0) return RBT_OK;
   if (!x || !out) return fail(c, RBT_E_INVALID, "null x or out");
-  const rbt_moe_layer_desc &D = lit->second.desc;
+  Layer &Ly = lit->second;
+  const rbt_moe_layer_desc &D = Ly.desc;
   const size_t H = D.hidden, MH = lw->moe_hidden, I = D.moe_inter, E = D.n_experts;
   const size_t k = std::min(D.topk, E);
   if (MH == 0 || lw->down_proj.rows != MH || lw->down_proj.cols != H || lw->up_proj.rows != H ||
@@ -794,33 +841,20 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   RBT_TRY(to_act(c, &lw->act, &act));
   const int S = (int)s, K = (int)k, P = S * K;
   // the layer's pool slots seen at (moe_hidden, moe_inter), plus a zero job for the shared slots
-  std::vector<RbtExpertDev> t(E + 1);
-  memset(t.data(), 0, (E + 1) * sizeof(RbtExpertDev));
-  int kind = -1;
-  size_t gs = 0;
-  for (auto &kv : c->pool) {
-    if ((uint32_t)(kv.first >> 32) != layer) continue;
-    const uint32_t eid = (uint32_t)kv.first;
-    if (eid >= E) continue;
-    int kd;
-    size_t g;
-    RBT_TRY(slot_view(c, &kv.second.slot, MH, I, &t[eid], &kd, &g));
-    if (kind >= 0 && (kd != kind || g != gs)) return fail(c, RBT_E_UNSUPPORTED, "layer %u: experts mix formats", layer);
-    kind = kd;
-    gs = g;
-  }
-  if (kind < 0) return fail(c, RBT_E_NOT_RESIDENT, "layer %u has no resident experts", layer);
+  RBT_TRY(refresh_latent(c, layer, Ly, MH));
+  const int kind = Ly.lat_kind;
+  const size_t gs = Ly.lat_gs;
+  const RbtExpertDev *table = Ly.d_lat;
   double *mid, *bnd;
   int32_t *ids;
   float *wts, *shs, *tw, *xl, *h, *yy, *routed;
-  RbtExpertDev *table, *pjob;
+  RbtExpertDev *pjob;
   int *ptok, *tpair;
   RBT_TRY(scratch_t(c, SC_MID, (size_t)S * E, &mid));
   RBT_TRY(scratch_t(c, SC_BND, (size_t)S * E, &bnd));
   RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
   RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
   RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
-  RBT_TRY(scratch_t(c, SC_LTAB, E + 1, &table));
   RBT_TRY(scratch_t(c, SC_PJOB, (size_t)(P + S), &pjob));
   RBT_TRY(scratch_t(c, SC_PTOK, (size_t)(P + S), &ptok));
   RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
@@ -829,7 +863,6 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   RBT_TRY(scratch_t(c, SC_H, (size_t)P * I * 2, &h));
   RBT_TRY(scratch_t(c, SC_YY, (size_t)P * MH, &yy));
   RBT_TRY(scratch_t(c, SC_ROUTED, (size_t)S * MH, &routed));
-  HIP_OK(c, hipMemcpyAsync(table, t.data(), (E + 1) * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
   int *dflags = c->d_flags;
   // routing of the full-width x (certified logits, exact folds where the order is not certain)
   rbt::RouterArgs ra{D.family, (int)E, (int)E, K, (int)H, S, D.logit_bias, D.router_bias, D.norm_topk,
@@ -842,10 +875,15 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   } else {
     HIP_OK(c, rbt::launch_router_logits(*c, x, S, (int)H, D.router, (int)E, nullptr, mid, bnd));
   }
-  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB));
+  // one token: the selection writes the pair list itself (pair j = slot j)
+  const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
+  rbt::GroupArgs ga{table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
+  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
+                                      grp_in_select ? &ga : nullptr));
   RBT_TRY(matmul_dev(c, xl, x, &lw->down_proj, s));
-  HIP_OK(c, rbt::launch_group(*c, ids, wts, S, K, (int)E, table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR,
-                              dflags + FLAG_UNIQ));
+  if (!grp_in_select)
+    HIP_OK(c, rbt::launch_group(*c, ids, wts, S, K, (int)E, table, table + E, pjob, ptok, tpair, tw,
+                                dflags + FLAG_ERR, dflags + FLAG_UNIQ));
   RbtExpertDev none{};
   RBT_TRY(expert_pairs(c, kind, gs, pjob, none, P, nullptr, xl, ptok, MH, I, h, yy, nullptr, act));
   HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));

@@ -5,7 +5,7 @@
 // with every fp32 operation rounded on its own, as the reference does. The squares are exact in
 // fp64; their sum is a parallel fp64 reduction (the reference's is sequential), so the fp32 mean
 // square equals the reference's unless the exact value lies within a few fp64 ulps of an fp32
-// rounding boundary. One workgroup per row: the row is read twice from L2, the work is tiny.
+// rounding boundary. One workgroup per row.
 #include "rbt_device.h"
 #include "rbt_internal.h"
 
@@ -14,23 +14,48 @@ namespace rbt {
 template <bool ONE_PLUS>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float eps,
                                                  float *__restrict__ y, int n) {
+  // rows up to 256 * R elements stay in registers: the row and the weights are loaded once, all
+  // loads issued together (an element-by-element walk waits on memory once per element)
+  constexpr int R = 32;
   __shared__ double part[4];
   const float *xr = x + (long)blockIdx.x * n;
   float *yr = y + (long)blockIdx.x * n;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const bool held = n <= 256 * R;
+  float v[R], wv[R];
   double acc = 0.0;
-  for (int i = t; i < n; i += 256) {
-    const double v = (double)xr[i];
-    acc += v * v;
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int i = t + 256 * j;
+      v[j] = i < n ? xr[i] : 0.0f;
+      wv[j] = i < n ? w[i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < R; j++) acc += (double)v[j] * (double)v[j];
+  } else {
+    for (int i = t; i < n; i += 256) {
+      const double e = (double)xr[i];
+      acc += e * e;
+    }
   }
   acc = rbt_wave_total_d(acc);
   if (lane == 0) part[wave] = acc;
   __syncthreads();
   const double ms = (part[0] + part[1]) + (part[2] + part[3]);
   const float r = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)n), eps)));
-  for (int i = t; i < n; i += 256) {
-    const float s = ONE_PLUS ? __fmul_rn(r, __fadd_rn(1.0f, w[i])) : __fmul_rn(r, w[i]);
-    yr[i] = __fmul_rn(xr[i], s);
+  if (held) {
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int i = t + 256 * j;
+      const float s = ONE_PLUS ? __fmul_rn(r, __fadd_rn(1.0f, wv[j])) : __fmul_rn(r, wv[j]);
+      if (i < n) yr[i] = __fmul_rn(v[j], s);
+    }
+  } else {
+    for (int i = t; i < n; i += 256) {
+      const float s = ONE_PLUS ? __fmul_rn(r, __fadd_rn(1.0f, w[i])) : __fmul_rn(r, w[i]);
+      yr[i] = __fmul_rn(xr[i], s);
+    }
   }
 }
 

@@ -1406,10 +1406,23 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y, in
   if (idx >= (size_t)S * H) return;
   int t = (int)(idx / H), d = (int)(idx % H);
   float acc = 0.0f;
-  for (int j = 0; j < k; j++) {
-    int p = tok_pair[t * k + j];
-    if (p < 0) continue;
-    acc = __fadd_rn(acc, __fmul_rn(tok_w[t * k + j], y[(size_t)p * H + d]));
+  // pairs in slot order, 16 at a time: the slots' pair ids and weights, then their rows, each
+  // group of loads issued together (a pair-by-pair walk waits on two loads per pair)
+  constexpr int CH = 16;
+  for (int j0 = 0; j0 < k; j0 += CH) {
+    int pp[CH];
+    float ww[CH], vv[CH];
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+      const int j = min(j0 + u, k - 1);
+      pp[u] = tok_pair[t * k + j];
+      ww[u] = tok_w[t * k + j];
+    }
+#pragma unroll
+    for (int u = 0; u < CH; u++) vv[u] = y[(size_t)max(pp[u], 0) * H + d];
+#pragma unroll
+    for (int u = 0; u < CH; u++)
+      if (j0 + u < k && pp[u] >= 0) acc = __fadd_rn(acc, __fmul_rn(ww[u], vv[u]));
   }
   if (has_shared) {
     float sh = y[((size_t)S * k + t) * H + d];

@@ -44,6 +44,11 @@ CONFIGS = {
     "c2": Config("c2_glm_i4g_decode_b1", FAMILY_GLM52, 6144, 2048, 256, 8, QT_I4_GROUPED, 1),
     "c3": Config("c3_k3_decode_b8_zipf", FAMILY_KIMI_K3, 7168, 2048, 384, 8, QT_MXFP4, 8, zipf_logit_bias=True),
     "c4": Config("c4_qwen38_prefill_512", FAMILY_QWEN38, 8192, 2048, 512, 10, QT_MXFP4, 512, gated_shared=True),
+    # Kimi K3's routed MoE (kimi_k3/config.rs:245-275): 896 MXFP4 experts at moe_hidden 3584 with
+    # moe_inter 3072, top-16 by sigmoid with a correction bias, Situ(4, 25), the routed-expert norm;
+    # the latent projections as grouped int4 (group 32), the converter's --dense-bits 4 form
+    "k3l": Config("k3_latent_decode_b1", FAMILY_KIMI_K3, 7168, 3072, 896, 16, QT_MXFP4, 1, shared=False,
+                  extra={"moe_hidden": 3584, "proj_gs": 32, "situ": (4.0, 25.0), "latent_norm": True}),
 }
 
 
@@ -124,3 +129,45 @@ def build_layer(ctx, cfg: Config, layer: int = 0, seed: int = 1000, n_resident: 
                       logit_bias=t_lb, norm_topk=True, routed_scale=1.0)
     torch.cuda.synchronize()
     return {"router": router, "shared_gate": gate, "logit_bias": logit_bias, "shared": shared, "seed": seed}
+
+
+def latent_host_params(cfg: Config, seed: int):
+    """Router, correction bias and norm weight of the latent workload (host arrays)."""
+    rng = np.random.default_rng(seed + 7)
+    router = (rng.standard_normal((cfg.n_experts, cfg.hidden)) * cfg.router_std).astype(np.float32)
+    bias = (rng.standard_normal(cfg.n_experts) * 0.01).astype(np.float32)
+    norm = (1.0 + rng.standard_normal(cfg.extra["moe_hidden"]) * 0.1).astype(np.float32)
+    return router, bias, norm
+
+
+def build_latent_layer(ctx, cfg: Config, layer: int = 0, seed: int = 1000):
+    """K3's latent MoE layer in HBM: routed experts at (moe_hidden, moe_inter) in the pool (tensor
+    seeds as build_layer's), the router at full width, and the two projections (grouped int4,
+    tensor seeds of eid n_experts and n_experts + 1). Returns the device pieces rbt_latent_moe_d
+    takes."""
+    import torch
+    from . import situ
+    MH, I, H, gs = cfg.extra["moe_hidden"], cfg.inter, cfg.hidden, cfg.extra["proj_gs"]
+    for e in range(cfg.n_experts):
+        p = ctx.pool_alloc(layer, e, cfg.kind, MH, I, cfg.gs)
+        s = p.contents
+        for m, q in enumerate((s.gate, s.up, s.down)):
+            _synth(ctx, cfg.kind, q.data, q.scale, q.rows, q.cols, tensor_seed(seed, e, m), cfg)
+    router, bias, norm = latent_host_params(cfg, seed)
+    dev = torch.device("cuda")
+    proj = []
+    for j, (rows, cols) in enumerate(((MH, H), (H, MH))):
+        data = torch.empty(rows * cols // 2, dtype=torch.uint8, device=dev)
+        scale = torch.empty(rows * (cols // gs), dtype=torch.float32, device=dev)
+        ctx.synth_i4g(data.data_ptr(), scale.data_ptr(), rows, cols, gs, tensor_seed(seed, cfg.n_experts + j, 0),
+                      cfg.s_lo, cfg.s_hi)
+        proj.append(QT.i4g(data, scale, rows, cols, gs))
+    t_router = torch.from_numpy(router).to(dev)
+    t_bias = torch.from_numpy(bias).to(dev)
+    ctx.sync()
+    ctx.moe_layer_set(layer, cfg.family, H, I, cfg.n_experts, cfg.topk, t_router, router_bias=t_bias,
+                      norm_topk=True, routed_scale=1.0)
+    torch.cuda.synchronize()
+    beta, lb = cfg.extra["situ"]
+    return {"down": proj[0], "up": proj[1], "norm": torch.from_numpy(norm).to(dev) if cfg.extra["latent_norm"]
+            else None, "act": situ(beta, lb), "router": t_router, "bias": t_bias}
