@@ -938,11 +938,33 @@ __device__ __forceinline__ void winner_weights(SelLds &L, const SelParams &P, in
   __builtin_amdgcn_wave_barrier();
 }
 
-template <int MAXM>
+// Selection keys of one expert from its logit interval: key at the clamped midpoint (kmid, and its
+// order key ku), and the interval of keys [klo, khi] (a point when the logit interval is).
+__device__ __forceinline__ void sel_keys(const SelParams &P, double mv, double bv, float lb, float rb, float &lmid,
+                                         uint32_t &ku, float &klo, float &khi) {
+  const float lo = __double2float_rd(mv - bv * (1.0 + 1e-12));
+  const float hi = __double2float_ru(mv + bv * (1.0 + 1e-12));
+  const float md = fminf(fmaxf(__double2float_rn(mv), lo), hi);
+  lmid = md;
+  const float kmid = sel_key_v(P, lb, rb, md);
+  ku = ord_key(kmid);
+  if (lo == hi) {
+    klo = khi = kmid;
+  } else {
+    klo = sel_key_v(P, lb, rb, lo);
+    khi = sel_key_v(P, lb, rb, hi);
+  }
+}
+
+// MW: the keys of all experts are computed by the four waves together (for the sigmoid families
+// each key costs three fp64-exp sigmoids) and handed to wave 0 through kbuf, LDS of 4 * 64 * MAXM
+// words; otherwise wave 0 computes them alone and kbuf is unused.
+template <int MAXM, bool MW = false>
 __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, const double *__restrict__ mid,
                                              const double *__restrict__ bnd, int32_t *__restrict__ ids,
                                              float *__restrict__ wts, float *__restrict__ sh_scale,
-                                             int *__restrict__ stats, const GroupOut &G, int grp, int s) {
+                                             int *__restrict__ stats, const GroupOut &G, int grp, int s,
+                                             float *kbuf = nullptr) {
   int(&c_id)[SEL_MAXK] = L.c_id;
   uint32_t(&c_ku)[SEL_MAXK] = L.c_ku;
   float(&c_lo)[SEL_MAXK] = L.c_lo, (&c_hi)[SEL_MAXK] = L.c_hi, (&c_l)[SEL_MAXK] = L.c_l;
@@ -962,7 +984,48 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
 
   float klo[MAXM], khi[MAXM], lmid[MAXM], lbv[MAXM], rbv[MAXM];
   uint32_t ku[MAXM];
-  if (wave == 0) {
+  if (MW) {
+    constexpr int MQ = (MAXM + 3) / 4, NE = 64 * MAXM;
+    {
+      double mv[MQ], bv[MQ];
+      float lb[MQ], rb[MQ];
+#pragma unroll
+      for (int i = 0; i < MQ; i++) {
+        const int e = min(lane + 64 * (wave + 4 * i), E - 1);  // unconditional (in-bounds) loads batch together
+        mv[i] = ms[e];
+        bv[i] = bs[e];
+        lb[i] = P.logit_bias ? P.logit_bias[e] : 0.0f;
+        rb[i] = P.router_bias ? P.router_bias[e] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < MQ; i++) {
+        const int e = lane + 64 * (wave + 4 * i);
+        if (wave + 4 * i < MAXM && e < E) {
+          float lm, kl, kh;
+          uint32_t u;
+          sel_keys(P, mv[i], bv[i], lb[i], rb[i], lm, u, kl, kh);
+          kbuf[e] = kl;
+          kbuf[NE + e] = kh;
+          kbuf[2 * NE + e] = lm;
+          kbuf[3 * NE + e] = __uint_as_float(u);
+        }
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int m = 0; m < MAXM; m++) {
+        const int e = min(lane + 64 * m, E - 1);
+        lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
+        rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
+        const bool in = lane + 64 * m < E;
+        ku[m] = in ? __float_as_uint(kbuf[3 * NE + e]) : 0u;
+        klo[m] = in ? kbuf[e] : -INFINITY;
+        khi[m] = in ? kbuf[NE + e] : -INFINITY;
+        lmid[m] = in ? kbuf[2 * NE + e] : -INFINITY;
+      }
+    }
+  } else if (wave == 0) {
     double mv[MAXM], bv[MAXM];
 #pragma unroll
     for (int m = 0; m < MAXM; m++) {
@@ -976,20 +1039,7 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
     for (int m = 0; m < MAXM; m++) {
       ku[m] = 0;
       klo[m] = khi[m] = lmid[m] = -INFINITY;
-      if (lane + 64 * m < E) {
-        const float lo = __double2float_rd(mv[m] - bv[m] * (1.0 + 1e-12));
-        const float hi = __double2float_ru(mv[m] + bv[m] * (1.0 + 1e-12));
-        const float md = fminf(fmaxf(__double2float_rn(mv[m]), lo), hi);
-        lmid[m] = md;
-        const float kmid = sel_key_v(P, lbv[m], rbv[m], md);
-        ku[m] = ord_key(kmid);
-        if (lo == hi) {
-          klo[m] = khi[m] = kmid;
-        } else {
-          klo[m] = sel_key_v(P, lbv[m], rbv[m], lo);
-          khi[m] = sel_key_v(P, lbv[m], rbv[m], hi);
-        }
-      }
+      if (lane + 64 * m < E) sel_keys(P, mv[m], bv[m], lbv[m], rbv[m], lmid[m], ku[m], klo[m], khi[m]);
     }
   }
   int total_amb = 0;
@@ -1048,8 +1098,19 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
           clo = q_lo[lane];
           chi = q_hi[lane];
           cl = q_l[lane];
-          int rank = 0;
-          for (int j = 0; j < nc; j++) {
+          int rank = 0, j = 0;
+          for (; j + 8 <= nc; j += 8) {  // eight candidates' LDS reads in flight at once
+            uint32_t o[8];
+            int oi[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              o[u] = q_ku[j + u];
+              oi[u] = q_id[j + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) rank += (o[u] > my) || (o[u] == my && oi[u] < my_id);
+          }
+          for (; j < nc; j++) {
             const uint32_t o = q_ku[j];
             rank += (o > my) || (o == my && q_id[j] < my_id);
           }
@@ -1085,7 +1146,22 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
         // order: every pair of winners must be strictly ordered or an exact tie-broken pair (checking
         // all pairs, not only neighbours, keeps one recomputation pass enough)
         if (iw && !cexact) {
-          for (int q = 0; q < kk; q++) {
+          int q = 0;
+          for (; q + 8 <= kk; q += 8) {  // eight winners' LDS reads in flight at once
+            float ql[8], qh[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              ql[u] = r_lo[q + u];
+              qh[u] = r_hi[q + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+              const int qq = q + u;
+              const bool sure = qq < my_rank ? ql[u] > chi : (qq > my_rank ? clo > qh[u] : true);
+              amb_me |= !sure;
+            }
+          }
+          for (; q < kk; q++) {
             const float ql = r_lo[q], qh = r_hi[q];
             const bool sure = q < my_rank ? ql > chi : (q > my_rank ? clo > qh : true);
             amb_me |= !sure;
@@ -1270,7 +1346,8 @@ __global__ __launch_bounds__(256) void k_router_select3(SelParams P, const doubl
                                                         float *__restrict__ wts, float *__restrict__ sh_scale,
                                                         int *__restrict__ stats, GroupOut G, int grp) {
   __shared__ SelLds L;
-  select3_body<MAXM>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x);
+  __shared__ float kbuf[4 * 64 * MAXM];
+  select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x, kbuf);
 }
 
 // One token with a shared expert: workgroup 0 selects; the other workgroups stream the shared
