@@ -15,9 +15,9 @@ cpu_baseline = the reference's AVX-512 (or AVX2) MXFP4 tier, restated in oracle/
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c1]
 
---config c4 times the 512-token prefill instead, and --config k3l Kimi K3's latent MoE (896 experts
-at moe_hidden 3584, top-16, Situ, the routed-expert norm) one token per call; neither is the
-default line.
+--config c4 times the 512-token prefill instead, --config k3l Kimi K3's latent MoE (896 experts
+at moe_hidden 3584, top-16, Situ, the routed-expert norm) one token per call, and --config c1s the
+MoE sublayer (rmsnorm_1p, C1's layer, residual add); none of them is the default line.
 """
 from __future__ import annotations
 
@@ -338,6 +338,71 @@ def bench_latent(args, ctx, hip, cfg):
     ctx.close()
 
 
+def graph_us_per_call(hip, ctx, call, ntok, warmup, G):
+    """Warms up, then times graph replays of G consecutive calls call(t) over tokens warmup..ntok."""
+    import torch
+    for t in range(warmup):
+        call(t)
+    ctx.sync()
+    steps = ntok - warmup
+    graphs = []
+    for r in range(steps // G):
+        g = Graph(hip, ctx.stream)
+        g.begin()
+        for j in range(G):
+            call(warmup + r * G + j)
+        g.end()
+        graphs.append(g)
+    torch.cuda.synchronize()
+    ctx.sync()
+    t0 = time.perf_counter()
+    for g in graphs:
+        g.launch()
+    ctx.sync()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    for g in graphs:
+        g.destroy()
+    return us
+
+
+def bench_sublayer(args, ctx, hip, cfg):
+    """The MoE half of a Qwen 3.8 decoder layer on C1's layer (rbt_moe_sublayer_d):
+    x += moe_forward(rmsnorm_1p(x, post_ln)), one token per call, graph-replayed; the plain layer call
+    is timed beside it in the same process, so the difference is the norm and the residual add."""
+    import torch
+    import rabbit_amd.workloads as W
+    W.build_layer(ctx, cfg, layer=0, seed=args.seed)
+    pool_gb = ctx.pool_resident_bytes() / 1e9
+    G = max(1, min(args.graph_tokens, args.steps))
+    steps = ((args.steps + G - 1) // G) * G
+    ntok = steps + args.warmup
+    H = cfg.hidden
+    x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
+    out_all = torch.empty_like(x_all)
+    ln = torch.from_numpy((np.random.default_rng(args.seed + 9).standard_normal(H) * 0.1).astype(np.float32)).cuda()
+    rows = [x_all[t] for t in range(ntok)]
+    outs = [out_all[t] for t in range(ntok)]
+    layer_us = graph_us_per_call(hip, ctx, lambda t: ctx.moe_forward(0, rows[t], 1, outs[t], sync=False), ntok,
+                                 args.warmup, G)
+    sub_us = graph_us_per_call(hip, ctx, lambda t: ctx.moe_sublayer(0, rows[t], 1, ln, 1e-6, sync=False), ntok,
+                               args.warmup, G)
+    log(f"[bench] sublayer {sub_us:.2f} us/token, layer alone {layer_us:.2f}")
+    res = {
+        "metric": "MoE sublayer decode us/token (rmsnorm_1p + MoE layer + residual add), MXFP4",
+        "value": round(sub_us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(sub_us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg.name + "_sublayer", "hidden": H, "moe_inter": cfg.inter, "n_experts": cfg.n_experts,
+                   "topk": cfg.topk, "shared_expert": cfg.shared, "weights": "mxfp4", "tokens_per_step": 1,
+                   "resident_pool_gb": round(pool_gb, 2), "graph_tokens": G},
+        "layer_us_per_token": round(layer_us, 3),
+        "norm_and_residual_us": round(sub_us - layer_us, 3),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -362,6 +427,8 @@ def main():
     import rabbit_amd.workloads as W
 
     torch.zeros(1, device="cuda")
+    if args.config == "c1s":
+        return bench_sublayer(args, R.Context(0), hip_runtime(), W.CONFIGS["c1"])
     cfg = W.CONFIGS[args.config]
     if args.config == "k3l":
         ctx = R.Context(0)

@@ -589,8 +589,10 @@ int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H
   return RBT_OK;
 }
 
+// accumulate: out += the layer's output (x and out must not overlap). The one-token down launch adds
+// in its own store; the other paths write the output to a scratch and add it after.
 int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
-                    float *w_out) {
+                    float *w_out, bool accumulate = false) {
   auto lit = c->layers.find(layer);
   if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
   Layer &L = lit->second;
@@ -664,6 +666,8 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   // launch, the routed pairs then taking up to k + D1_KX slots and the shared expert the one after.
   const int kk = std::min(k, E);
   const bool dn1 = gu1 && grp_in_select && rbt::xdown1_ok(kk + (D.has_shared ? 1 : 0), (size_t)I);
+  float *dst = out;
+  if (accumulate && !dn1) RBT_TRY(scratch_t(c, SC_SUB, (size_t)S * H, &dst));
   const bool defer = r1 && dn1;
   const int sh_slot = defer ? k + rbt::D1_KX : k;
   sgu.hp = reinterpret_cast<__bf16 *>(h) + (size_t)sh_slot * 3 * I;
@@ -704,7 +708,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool grouped = !mfma && S > 1 && (merge || !D.has_shared) &&
                        rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
   if (grouped) {
-    RBT_TRY(prefill_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, out,
+    RBT_TRY(prefill_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, dst,
                         c->prof ? ev.data() : nullptr));
   } else {
   if (!grp_in_select)
@@ -729,8 +733,8 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     // one token: the balanced down over the compact job list (all pairs' h in LDS); batches: a grid
     // of row blocks
     const hipError_t e3 =
-        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out)
-            : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, out);
+        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out, accumulate)
+            : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, dst);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e3);
   } else {
@@ -749,7 +753,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
       }
     }
     if (c->prof) HIP_OK(c, hipEventRecord(ev[5], c->stream));
-    HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, out));
+    HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, dst));
   }
   }
   if (c->prof) {
@@ -759,6 +763,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     const uint64_t ne = S == 1 ? (uint64_t)npairs : 0;
     c->ev_experts.push_back({S == 1 ? ne - (sh_in_select ? 1 : 0) : 0, ne});
   }
+  if (dst != out) HIP_OK(c, rbt::launch_add_rows(*c, out, dst, (size_t)S * H));
   if (ids_out)
     HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
   if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, wts, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
@@ -1429,12 +1434,11 @@ static int moe_sublayer_dev(rbt_ctx *c, uint32_t layer, float *x, size_t s, cons
   if (s == 0) return RBT_OK;
   if (!x || !post_ln) return fail(c, RBT_E_INVALID, "null x or post_ln");
   const size_t H = lit->second.desc.hidden;
-  float *nrm, *tmp;
+  float *nrm;
   RBT_TRY(scratch_t(c, SC_NRM, s * H, &nrm));
-  RBT_TRY(scratch_t(c, SC_SUB, s * H, &tmp));
   HIP_OK(c, rbt::launch_rmsnorm(*c, x, post_ln, eps, nrm, s, H, true));
-  RBT_TRY(moe_forward_dev(c, layer, nrm, s, tmp, ids_out, w_out));
-  HIP_OK(c, rbt::launch_add_rows(*c, x, tmp, s * H));
+  // x += layer(nrm): the residual add rides in the layer's last store where it can
+  RBT_TRY(moe_forward_dev(c, layer, nrm, s, x, ids_out, w_out, true));
   return RBT_OK;
 }
 

@@ -88,10 +88,11 @@ hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, c
 // One token: down + ordered combine balanced over num_cu workgroups, every pair's h in LDS. The
 // pairs are the kk winners in slot order (down_job[j], h at pair slot down_slot[j], weight
 // tok_w[j]) and, with has_shared, the shared expert (down_job[kk], h at down_slot[kk]).
+// accumulate: out += the combined row instead of out = (one rounding, as x[i] += tmp[i]).
 bool xdown1_ok(int npairs, size_t i);
 hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
                          int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
-                         float *out);
+                         float *out, bool accumulate = false);
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);

@@ -409,7 +409,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
                                                         const __bf16 *__restrict__ hp, int H,
                                                         const float *__restrict__ tok_w,
                                                         const float *__restrict__ sh_scale, int has_shared,
-                                                        int gated, float *__restrict__ out) {
+                                                        int gated, float *__restrict__ out, int accumulate) {
   // pairs: the kk winners in slot order (jobs[j], h at pair slot slots[j], weight tok_w[j]), then
   // the shared expert (jobs[kk], h at slots[kk], weight sh_scale when gated, else 1)
   const int npairs = kk + (has_shared ? 1 : 0);
@@ -575,6 +575,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     float o = 0.0f;
     for (int pp = 0; pp < npairs; pp++)
       if (padd[pp]) o = __fadd_rn(o, __fmul_rn(pw[pp], yb[tl][pp][r]));
+    if (accumulate) o = __fadd_rn(out[4 * (T0 + tl) + r], o);  // x += layer(x) (qwen38/generate.rs:411-413)
     out[4 * (T0 + tl) + r] = o;
   }
 }
@@ -583,12 +584,12 @@ bool xdown1_ok(int npairs, size_t i) { return i == 2048 && npairs >= 1 && npairs
 
 hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
                          int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
-                         float *out) {
+                         float *out, bool accumulate) {
   const int grid = c.num_cu;
   if (!xdown1_ok(kk + (has_shared ? 1 : 0), I) || H % 4 != 0 || grid <= 0 || (H / 4 + grid - 1) / grid > XD1_TPW)
     return hipErrorInvalidValue;
   launch_k(c, k_xdown1<4>, dim3(grid), dim3(64 * XD1_NW), down_job, down_slot, kk, hp, H, tok_w, sh_scale,
-           has_shared, gated, out);
+           has_shared, gated, out, (int)accumulate);
   return hipGetLastError();
 }
 
