@@ -692,7 +692,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router1(*c, ra, sgate, mid, bnd, ids, wts, shs, dflags + FLAG_AMB, &ga,
                                   sh_in_select ? &sgu : nullptr, c->d_sync, dflags + FLAG_SYNC, rec));
   } else {
-    if (rbt::router_exact_ok(S, H) && (uintptr_t)x % 16 == 0) {
+    if (rbt::router_exact_ok(S, H) && ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0) {
       // batches: the reference's sequential fp32 logits themselves, then point intervals
       float *lg;
       RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * erows, &lg));
@@ -872,7 +872,7 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   // routing of the full-width x (certified logits, exact folds where the order is not certain)
   rbt::RouterArgs ra{D.family, (int)E, (int)E, K, (int)H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
-  if (rbt::router_exact_ok(S, (int)H) && (uintptr_t)x % 16 == 0) {
+  if (rbt::router_exact_ok(S, (int)H) && ((uintptr_t)x | (uintptr_t)D.router) % 16 == 0) {
     float *lg;
     RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * E, &lg));
     HIP_OK(c, rbt::launch_router_logits_exact(*c, x, S, (int)H, D.router, (int)E, nullptr, lg));

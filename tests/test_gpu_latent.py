@@ -87,9 +87,10 @@ def test_apply_single_expert_activation_errors(ctx, orc):
         ctx.apply_single_expert(rs, ids, w, 1, 1, x, H, I, out, activation=R.ACT_SITU)
 
 
-def _latent_case(ctx, orc, layer, H, MH, I, E, k, seed, proj_kind, x_std):
+def _latent_case(ctx, orc, layer, H, MH, I, E, k, seed, proj_kind, x_std, misalign=False):
     """Pool experts at (moe_hidden, moe_inter), a sigmoid router with a correction bias at full width
-    (kimi_k3/moe.rs:232-262's layer shape), and the two projections."""
+    (kimi_k3/moe.rs:232-262's layer shape), and the two projections. misalign: the device router
+    starts 4 bytes past a 16-byte boundary."""
     import rabbit_amd as R
     import torch
     experts = {}
@@ -102,7 +103,12 @@ def _latent_case(ctx, orc, layer, H, MH, I, E, k, seed, proj_kind, x_std):
     router = normal((E, H), seed + 500, 0.05)
     bias = normal(E, seed + 501, 0.1)
     L = orc.MoeLayer(orc.FAMILY_GLM52, H, I, E, k, router, experts, router_bias=bias, norm_topk=False)
-    ctx.moe_layer_set(layer, R.FAMILY_GLM52, H, I, E, k, torch.from_numpy(router).cuda(),
+    t_router = torch.from_numpy(router).cuda()
+    if misalign:
+        buf = torch.zeros(E * H + 4, device="cuda")
+        t_router = buf[1:1 + E * H]
+        t_router.copy_(torch.from_numpy(router.ravel()).cuda())
+    ctx.moe_layer_set(layer, R.FAMILY_GLM52, H, I, E, k, t_router,
                       router_bias=torch.from_numpy(bias).cuda(), norm_topk=False)
     if proj_kind == "f32":
         dq = orc.QT.f32(normal((MH, H), seed + 502, 0.05), MH, H)
@@ -146,11 +152,25 @@ def test_latent_moe_matches_oracle(ctx, orc, proj_kind, S):
     assert rel_l2(situ, normed) > 1e-3
 
 
+@pytest.mark.parametrize("misalign", [False, True])
+def test_latent_moe_batch_exact_logits(ctx, orc, misalign):
+    # 64 tokens: the router's logits are the reference's sequential folds themselves; a router that
+    # is not 16-byte aligned takes the certified kernel instead, with the same ids
+    import rabbit_amd as R
+    H, MH, I, E, k, S = 256, 128, 64, 16, 4, 64
+    layer = 60 + int(misalign)
+    L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 6000 + layer, "mxfp4", 1.0, misalign=misalign)
+    x = normal((S, H), layer, 1.0)
+    norm = np.abs(normal(MH, layer + 1, 1.0)) + np.float32(0.5)
+    _run_latent(ctx, R, layer, L, dq, uq, x, S, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
+
+
 def test_latent_moe_k3_dims(ctx, orc):
     # Kimi K3's widths: hidden 7168, routed experts at moe_hidden 3584 with moe_inter 3072, top-8,
-    # Situ(beta 4, linear_beta 25) and the routed-expert norm; 32 resident experts, 2 tokens
+    # Situ(beta 4, linear_beta 25) and the routed-expert norm; 32 resident experts, 4 tokens (at
+    # this shape about one token in four needs exact logit folds in the selection)
     import rabbit_amd as R
-    H, MH, I, E, k, S = 7168, 3584, 3072, 32, 8, 2
+    H, MH, I, E, k, S = 7168, 3584, 3072, 32, 8, 4
     L, dq, uq, _ = _latent_case(ctx, orc, 50, H, MH, I, E, k, 7000, "mxfp4", 0.05)
     x = normal((S, H), 51, 0.05)
     norm = np.abs(normal(MH, 52, 0.2)) + np.float32(0.5)
