@@ -329,6 +329,18 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
                  hipEvent_t *mark = nullptr, const RbtAct &act = RbtAct{}) {
   const bool fast_gu = rbt::decode_shape_ok(d, kind, gs) && ((uintptr_t)x % 16 == 0);
   const bool fast_dn = rbt::decode_shape_ok(i, kind, gs);
+  if (fast_gu && fast_dn && rbt::gu_act_ok(d, kind, gs)) {
+    // gate/up and act(g, u) into h in one launch, down from h
+    HIP_OK(c, rbt::launch_gu_act(*c, kind, jobs, single, njobs, njobs_dev, x, x_index, (long)d, (int)d, (int)i, h,
+                                 act));
+    if (mark) {
+      HIP_OK(c, hipEventRecord(mark[0], c->stream));
+      HIP_OK(c, hipEventRecord(mark[1], c->stream));
+    }
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, jobs, single, njobs, njobs_dev, h, nullptr, (long)i,
+                                 (int)i, (int)d, y, (long)d));
+    return RBT_OK;
+  }
   if (fast_gu && fast_dn) {
     // stacked gate|up dot products (column parts) into gu, act(g, u) into h, down from h.
     const int parts = rbt::decode_parts((int)d);

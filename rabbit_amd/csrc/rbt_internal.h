@@ -67,6 +67,12 @@ hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *j
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
                          int rows, float *y, long y_stride, int parts = 1);
 // h[p, k] = silu(sum of gate parts) * (sum of up parts) for the stacked producer's output.
+// Gate/up and the activation in one pass into h [njobs, I] (rows of 2049..4096 columns, the shapes
+// decode_shape_ok accepts): the same h as the stacked decode + launch_swiglu.
+bool gu_act_ok(size_t cols, int kind, size_t gs);
+hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
+                         const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols, int I,
+                         float *h, const RbtAct &act);
 hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
                          int parts, float *h, const RbtAct &act = RbtAct{});
 // Column parts the stacked gate/up kernel splits a row of `cols` columns into; its output per job
