@@ -904,8 +904,20 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   RbtExpertDev none{};
   RBT_TRY(expert_pairs(c, kind, gs, pjob, none, P, nullptr, xl, ptok, MH, I, h, yy, nullptr, act));
   HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
-  if (lw->norm) HIP_OK(c, rbt::launch_rmsnorm(*c, routed, lw->norm, lw->eps, routed, s, MH, false));
-  RBT_TRY(matmul_dev(c, out, routed, &lw->up_proj, s));
+  const rbt_qt &U = lw->up_proj;
+  if (lw->norm && U.kind != RBT_QT_F32 && rbt::decode_shape_ok(MH, U.kind, U.group_size) &&
+      ((uintptr_t)U.data | (uintptr_t)lw->norm) % 16 == 0) {
+    // the norm of each summed row inside the up projection's waves, which read the whole row
+    RBT_TRY(check_qt(c, &U, "matmul"));
+    RbtExpertDev one{};
+    one.dd = (const uint8_t *)U.data;
+    one.ds = U.scale;
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_NORM, U.kind, nullptr, one, S, nullptr, routed, nullptr, (long)MH,
+                                 (int)MH, (int)H, out, (long)H, 1, lw->norm, lw->eps));
+  } else {
+    if (lw->norm) HIP_OK(c, rbt::launch_rmsnorm(*c, routed, lw->norm, lw->eps, routed, s, MH, false));
+    RBT_TRY(matmul_dev(c, out, routed, &lw->up_proj, s));
+  }
   if (ids_out) HIP_OK(c, hipMemcpyAsync(ids_out, ids, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
   if (w_out) HIP_OK(c, hipMemcpyAsync(w_out, wts, (size_t)P * 4, hipMemcpyDeviceToDevice, c->stream));
   return RBT_OK;

@@ -85,6 +85,49 @@ __device__ __forceinline__ void load_x_slice(float (&xr)[NB][32], float (&xs)[NB
   }
 }
 
+// rmsnorm of a row held as a whole wave's x slice (64 lanes, blocks q + 64j), in place:
+// r = 1/sqrt((sum_f64(v^2) / n) as f32 + eps), v *= r * w (kimi_linear/ops.rs:46-53), then the
+// block sums again as load_x_slice forms them. The fp64 sum runs in another order than k_rmsnorm's.
+template <int NB>
+__device__ __forceinline__ void norm_x_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ w,
+                                             float eps, int q, int nblk, int n) {
+  // the weights' loads go out first and land while the sum of squares is reduced
+  const rbt_gf4 *wg = (const rbt_gf4 *)w;
+  float4 wv[NB][8];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const int bb = min(q + 64 * j, nblk - 1);
+#pragma unroll
+    for (int t = 0; t < 8; t++) wv[j][t] = wg[8 * bb + t];
+  }
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < NB; j++)
+#pragma unroll
+    for (int t = 0; t < 32; t++) acc += (double)xr[j][t] * (double)xr[j][t];  // zero past the row
+  acc = rbt_wave_total_d(acc);
+  const float r = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(acc / (double)n), eps)));
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const bool ok = q + 64 * j < nblk;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const float4 v = wv[j][t];
+      xr[j][4 * t + 0] = ok ? __fmul_rn(xr[j][4 * t + 0], __fmul_rn(r, v.x)) : 0.0f;
+      xr[j][4 * t + 1] = ok ? __fmul_rn(xr[j][4 * t + 1], __fmul_rn(r, v.y)) : 0.0f;
+      xr[j][4 * t + 2] = ok ? __fmul_rn(xr[j][4 * t + 2], __fmul_rn(r, v.z)) : 0.0f;
+      xr[j][4 * t + 3] = ok ? __fmul_rn(xr[j][4 * t + 3], __fmul_rn(r, v.w)) : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 32; t++) s += xr[j][t];
+    xs[j] = s;
+  }
+}
+
 
 
 // ------------------------------------------------------------------------------------------------
@@ -102,7 +145,7 @@ __device__ __forceinline__ void load_x_slice(float (&xr)[NB][32], float (&xs)[NB
 // U > 1 the host guarantees rows % (U * 64/LPR) == 0 (an iteration never straddles two jobs). A
 // job whose weights are absent (null pointers) yields zeros.
 // ------------------------------------------------------------------------------------------------
-enum { MODE_DOWN = 0, MODE_STACKED = 1, MODE_ACT = 2 };
+enum { MODE_DOWN = 0, MODE_STACKED = 1, MODE_ACT = 2, MODE_NORM = 3 };  // NORM: MODE_DOWN of rmsnorm(x)
 
 template <int NB, int U>
 struct DecodeFrag {
@@ -230,7 +273,8 @@ __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restr
                                                      int njobs, const int *__restrict__ njobs_dev,
                                                      const float *__restrict__ x, const int *__restrict__ x_index,
                                                      long x_stride, int cols, int rows, float *__restrict__ y,
-                                                     long y_stride) {
+                                                     long y_stride, const float *__restrict__ nw, float eps) {
+  static_assert(MODE != MODE_NORM || (LPR == 64 && CS == 1), "the norm needs the whole row in one wave");
   constexpr int RPI = RBT_WAVE / LPR;  // rows side by side in one wave
   constexpr int IPI = U * RPI;         // rows per iteration
   const int lane = threadIdx.x & (RBT_WAVE - 1);
@@ -288,6 +332,7 @@ __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restr
         load_act_slice<NB, LPR, PARTS>(xr, xs, x + tok * x_stride, q, nblk, cols);
       else
         load_x_slice<NB, LPR>(xr, xs, x + tok * x_stride + (long)h * pcols, q, nblk);
+      if constexpr (MODE == MODE_NORM) norm_x_slice<NB>(xr, xs, nw, eps, q, nblk, cols);
       cur = tok * CS + h;
     }
     // The prefetch is unconditional: past the segment's last iteration it re-reads that iteration
@@ -648,7 +693,7 @@ bool decode_shape_ok(size_t cols, int kind, size_t gs) {
 template <int NB, int LPR, int U, int MODE, bool I4G, int CS, int PARTS>
 static hipError_t launch_decode_t(const Ctx &c, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                                   const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                                  int rows, float *y, long y_stride, int wpc) {
+                                  int rows, float *y, long y_stride, int wpc, const float *nw, float eps) {
   constexpr int IPI = U * (RBT_WAVE / LPR);
   const long total = (long)njobs * rows * CS;
   if (total >= (1L << 31)) return hipErrorInvalidValue;
@@ -660,7 +705,7 @@ static hipError_t launch_decode_t(const Ctx &c, const RbtExpertDev *jobs, const 
   if (waves < 1) waves = 1;
   int blocks = (int)((waves + 3) / 4);
   hipLaunchKernelGGL((k_decode_gemv<NB, LPR, U, MODE, I4G, CS, PARTS>), dim3(blocks), dim3(256), 0, c.stream, jobs,
-                     single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride);
+                     single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride, nw, eps);
   return hipGetLastError();
 }
 
@@ -673,25 +718,27 @@ static int long_split(int cols) { return cols >= 4096 && cols % 64 == 0 && (cols
 template <int MODE, bool I4G, int PARTS>
 static hipError_t launch_decode_k(const Ctx &c, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                                   const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                                  int rows, float *y, long y_stride) {
+                                  int rows, float *y, long y_stride, const float *nw, float eps) {
 #define RBT_DEC(NB, LPR, U, CS)                                                                                    \
   return launch_decode_t<NB, LPR, U, MODE, I4G, CS, PARTS>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, \
-                                                           cols, rows, y, y_stride, wpc)
+                                                           cols, rows, y, y_stride, wpc, nw, eps)
   const int seg = MODE == MODE_STACKED ? rows / 2 : rows;  // rows of one matrix
   // One matrix of rows longer than 2048 columns (a projection): every wave reloads the whole x
   // slice for few rows, so half the waves, each with twice the rows, read less of it in total
   // (3584 x 7168 grouped int4: 10.3 us against 14.7 us at 8 waves per CU).
-  const int wpc = (MODE == MODE_DOWN && njobs == 1 && cols > 2048) ? 4 : 8;
-  if (MODE == MODE_STACKED && long_split(cols) == 2 && seg % 2 == 0) {  // parts summed by MODE_ACT
-    const int nblk = cols / 64;  // blocks per part
-    if (nblk <= 64) RBT_DEC(1, 64, 2, 2);
-    if (nblk <= 128) RBT_DEC(2, 64, 2, 2);
-  }
+  const int wpc = ((MODE == MODE_DOWN || MODE == MODE_NORM) && njobs == 1 && cols > 2048) ? 4 : 8;
   const int nblk = cols / 32;
+  if constexpr (MODE != MODE_NORM) {  // the norm keeps a row in one wave: none of the 16-lane shapes
+  if (MODE == MODE_STACKED && long_split(cols) == 2 && seg % 2 == 0) {  // parts summed by MODE_ACT
+    const int pblk = cols / 64;  // blocks per part
+    if (pblk <= 64) RBT_DEC(1, 64, 2, 2);
+    if (pblk <= 128) RBT_DEC(2, 64, 2, 2);
+  }
   if (nblk <= 64 && nblk > 32 && seg % 4 == 0) RBT_DEC(1, 64, 4, 1);  // one x copy per wave
   if (nblk <= 64 && seg % 4 == 0) {
     if (nblk <= 16) RBT_DEC(1, 16, 1, 1);
     if (nblk <= 32) RBT_DEC(2, 16, 1, 1);
+  }
   }
   if (nblk <= 64) RBT_DEC(1, 64, 1, 1);
   if (nblk <= 128) {  // 2080..4096 columns: two rows per iteration (K3's 3584 / 3072: 5.1 and 4.1 TB/s, U=1 4.4 and 3.5)
@@ -709,14 +756,18 @@ int decode_parts(int cols) { return long_split(cols); }
 // SiLU-gated activation built from a stacked g|u input produced with `parts` column parts.
 hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                         int rows, float *y, long y_stride, int parts) {
+                         int rows, float *y, long y_stride, int parts, const float *nw, float eps) {
   if (njobs <= 0 || rows <= 0) return hipSuccess;
   const bool i4 = kind == RBT_QT_I4_GROUPED;
 #define RBT_MODE(M, P)                                                                                              \
   return i4 ? launch_decode_k<M, true, P>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y,   \
-                                          y_stride)                                                                 \
+                                          y_stride, nw, eps)                                                        \
             : launch_decode_k<M, false, P>(c, jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y,  \
-                                           y_stride)
+                                           y_stride, nw, eps)
+  if (mode == MODE_NORM) {
+    if (nw == nullptr || cols % 32 != 0 || cols > 64 * 32 * 4) return hipErrorInvalidValue;
+    RBT_MODE(MODE_NORM, 1);
+  }
   if (mode == MODE_STACKED) RBT_MODE(MODE_STACKED, 1);
   if (mode == MODE_ACT) {
     if (parts == 2) RBT_MODE(MODE_ACT, 2);

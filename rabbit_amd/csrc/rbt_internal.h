@@ -60,19 +60,21 @@ bool decode_shape_ok(size_t cols, int kind, size_t gs);
 // Decode GEMV over a job table (see gemv.hip). jobs == nullptr uses `single` for every job.
 // njobs_dev (optional) caps the job count from device memory.
 // mode: 0 = plain rows, 1 = stacked gate|up rows (raw dots), 2 = plain rows whose activation is
-// silu(g) * u built from a stacked g|u input.
-enum { DECODE_DOWN = 0, DECODE_STACKED = 1, DECODE_ACT = 2 };
+// silu(g) * u built from a stacked g|u input, 3 = plain rows of rmsnorm(x) with weight nw and eps
+// (each x row normalised in the wave that reads it; rows up to 8192 columns).
+enum { DECODE_DOWN = 0, DECODE_STACKED = 1, DECODE_ACT = 2, DECODE_NORM = 3 };
 // parts: for DECODE_ACT, the column-part count the stacked producer used (decode_parts(hidden)).
 hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single,
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
-                         int rows, float *y, long y_stride, int parts = 1);
-// h[p, k] = silu(sum of gate parts) * (sum of up parts) for the stacked producer's output.
+                         int rows, float *y, long y_stride, int parts = 1, const float *nw = nullptr,
+                         float eps = 0.0f);
 // Gate/up and the activation in one pass into h [njobs, I] (rows of 2049..4096 columns, the shapes
 // decode_shape_ok accepts): the same h as the stacked decode + launch_swiglu.
 bool gu_act_ok(size_t cols, int kind, size_t gs);
 hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                          const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols, int I,
                          float *h, const RbtAct &act);
+// h[p, k] = act(sum of gate parts, sum of up parts) for the stacked producer's output.
 hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
                          int parts, float *h, const RbtAct &act = RbtAct{});
 // Column parts the stacked gate/up kernel splits a row of `cols` columns into; its output per job
