@@ -419,7 +419,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (this build has no "
-              "multi-GPU path; see DESIGN.md for how the layer would shard)", file=sys.stderr)
+              "multi-GPU path: it measures one GPU's share of the layer at its real shape)", file=sys.stderr)
         sys.exit(2)
 
     import torch
