@@ -33,12 +33,18 @@ def _host_qt(R, q):
 
 
 def _synth(orc, kind, rows, cols, seed):
-    return orc.synth_i4g(rows, cols, 16, seed) if kind == "i4g" else orc.synth_mxfp4(rows, cols, seed)
+    if kind == "i4g":
+        return orc.synth_i4g(rows, cols, 16, seed)
+    if kind == "i4g32":
+        return orc.synth_i4g(rows, cols, 32, seed)
+    return orc.synth_mxfp4(rows, cols, seed)
 
 
-# x_std puts the gate dot products at O(1-10), where Situ and SiLU differ
+# x_std puts the gate dot products at O(1-10), where Situ and SiLU differ. Hidden 3584 takes the
+# one-launch gate/up + activation kernel (MXFP4 and grouped int4 with group 32), 8192 the stacked
+# GEMV and the activation kernel, 70 x 24 the generic per-pair kernel.
 @pytest.mark.parametrize("kind,H,I,x_std", [("mxfp4", 8192, 2048, 0.5), ("mxfp4", 3584, 3072, 0.5),
-                                            ("i4g", 70, 24, 20.0)])
+                                            ("i4g32", 3584, 1024, 1.0), ("i4g", 70, 24, 20.0)])
 @pytest.mark.parametrize("lb", [25.0, None])
 def test_apply_single_expert_situ(ctx, orc, kind, H, I, x_std, lb):
     import rabbit_amd as R
@@ -113,6 +119,8 @@ def _latent_case(ctx, orc, layer, H, MH, I, E, k, seed, proj_kind, x_std, misali
     if proj_kind == "f32":
         dq = orc.QT.f32(normal((MH, H), seed + 502, 0.05), MH, H)
         uq = orc.QT.f32(normal((H, MH), seed + 503, 0.05), H, MH)
+    elif proj_kind == "i4g":
+        dq, uq = orc.synth_i4g(MH, H, 32, seed + 502), orc.synth_i4g(H, MH, 32, seed + 503)
     else:
         dq, uq = orc.synth_mxfp4(MH, H, seed + 502), orc.synth_mxfp4(H, MH, seed + 503)
     torch.cuda.synchronize()
@@ -136,12 +144,14 @@ def _run_latent(ctx, R, layer, L, dq, uq, x, S, MH, norm, act_o, act_r):
     return got
 
 
-@pytest.mark.parametrize("proj_kind", ["f32", "mxfp4"])
+# f32 projections take the separate norm kernel; MXFP4 and grouped-int4 ones the norm inside the up
+# projection's GEMV
+@pytest.mark.parametrize("proj_kind", ["f32", "mxfp4", "i4g"])
 @pytest.mark.parametrize("S", [1, 3])
 def test_latent_moe_matches_oracle(ctx, orc, proj_kind, S):
     import rabbit_amd as R
     H, MH, I, E, k = 256, 128, 64, 16, 4
-    layer = 40 + (proj_kind == "mxfp4") * 2 + (S == 3)
+    layer = 40 + {"f32": 0, "mxfp4": 2, "i4g": 4}[proj_kind] + (S == 3)
     L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 900 + layer, proj_kind, 1.0)
     x = normal((S, H), layer, 1.0)
     norm = np.abs(normal(MH, layer + 1, 1.0)) + np.float32(0.5)
