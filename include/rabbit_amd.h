@@ -306,6 +306,17 @@ typedef struct {
 int rbt_profile_enable(rbt_ctx *ctx, int32_t on);
 /* Synchronises the stream and returns the accumulated phase times; reset != 0 clears them. */
 int rbt_profile_read(rbt_ctx *ctx, rbt_profile *out, int32_t reset);
+/* Per-kernel timing: while on, every kernel the context launches records HIP events at its own
+ * start and end (the dispatch records them, so dispatch gaps are excluded). */
+typedef struct {
+    char name[160];          /* the kernel's name as the runtime reports it */
+    uint64_t launches;
+    double total_ms;
+} rbt_kernel_stat;
+int rbt_profile_kernels(rbt_ctx *ctx, int32_t on);
+/* Synchronises, folds the recorded launches into per-kernel sums and copies up to cap of them
+ * into out; *n receives the number of kernels recorded. reset != 0 clears the sums. */
+int rbt_profile_kernels_read(rbt_ctx *ctx, rbt_kernel_stat *out, size_t cap, size_t *n, int32_t reset);
 
 /* ---- synthetic workload generator (benchmarks and tests; bit-identical to oracle/) ------------ */
 /* Fills an MXFP4 [rows, cols] matrix in device memory: nibbles uniform over 0..15, E8M0 bytes

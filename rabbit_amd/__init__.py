@@ -344,6 +344,23 @@ class Context:
         self.check(self.lib.rbt_profile_read(self.h, C.byref(p), int(reset)))
         return {f: getattr(p, f) for f, _ in abi.RbtProfile._fields_}
 
+    def profile_kernels(self, on: bool = True):
+        """Per-kernel timing: every launch records events at its own start and end."""
+        self.check(self.lib.rbt_profile_kernels(self.h, int(on)))
+
+    def profile_kernels_read(self, reset: bool = True) -> dict:
+        """{kernel name: (launches, mean microseconds)} of the launches recorded so far."""
+        cap = 64
+        buf = (abi.RbtKernelStat * cap)()
+        n = C.c_size_t()
+        self.check(self.lib.rbt_profile_kernels_read(self.h, buf, cap, C.byref(n), int(reset)))
+        out = {}
+        for i in range(min(n.value, cap)):
+            s = buf[i]
+            if s.launches:
+                out[s.name.decode(errors="replace")] = (int(s.launches), 1e3 * s.total_ms / s.launches)
+        return out
+
     # -- MoE layer ----------------------------------------------------------------------------
     def moe_layer_set(self, layer, family, hidden, moe_inter, n_experts, topk, router, shared: Slot | None = None,
                       shared_gate=None, router_bias=None, logit_bias=None, norm_topk=True, routed_scale=1.0,

@@ -67,6 +67,10 @@ _P, _S, _I, _F, _U32, _U64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_float, C.c_u
 _CTX = C.c_void_p
 
 
+class RbtKernelStat(C.Structure):
+    _fields_ = [("name", C.c_char * 160), ("launches", C.c_uint64), ("total_ms", C.c_double)]
+
+
 class RbtTensorInfo(C.Structure):
     _fields_ = [("file_index", C.c_int32), ("offset", C.c_uint64), ("nbytes", C.c_uint64),
                 ("dtype", C.c_char * 16), ("ndim", C.c_int32), ("shape", C.c_uint64 * 8)]
@@ -128,6 +132,8 @@ SIGNATURES = {
     "rbt_moe_sublayer_d": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),
     "rbt_profile_enable": (_I, [_CTX, _I]),
     "rbt_profile_read": (_I, [_CTX, C.POINTER(RbtProfile), _I]),
+    "rbt_profile_kernels": (_I, [_CTX, _I]),
+    "rbt_profile_kernels_read": (_I, [_CTX, C.POINTER(RbtKernelStat), _S, C.POINTER(C.c_size_t), _I]),
     "rbt_synth_mxfp4_d": (_I, [_CTX, _P, _P, _S, _S, _U64, _U32, _U32]),
     "rbt_synth_i4g_d": (_I, [_CTX, _P, _P, _S, _S, _S, _U64, _F, _F]),
 }

@@ -102,7 +102,37 @@ struct rbt_ctx : rbt::Ctx {
   std::vector<std::array<hipEvent_t, 7>> ev_rows;
   std::vector<std::array<uint64_t, 2>> ev_experts;  // per recorded call: gate/up and down experts
   rbt_profile acc{};
+  // per-kernel profiling: one start/end pair per launch while kprof is on, summed per kernel by
+  // rbt_profile_kernels_read
+  struct KRec {
+    const void *fn;
+    hipEvent_t start, stop;
+  };
+  std::vector<KRec> krecs;
+  std::map<const void *, std::pair<uint64_t, double>> kacc;  // kernel -> (launches, ms)
 };
+
+namespace rbt {
+bool kernel_events(const Ctx &base, const void *fn, hipEvent_t *start, hipEvent_t *stop) {
+  // every Ctx the library launches on is the base of an rbt_ctx
+  rbt_ctx *c = static_cast<rbt_ctx *>(const_cast<Ctx *>(&base));
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  for (auto &e : ev) {
+    if (!c->ev_free.empty()) {
+      e = c->ev_free.back();
+      c->ev_free.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+      (void)hipGetLastError();
+      if (ev[0]) c->ev_free.push_back(ev[0]);
+      return false;
+    }
+  }
+  c->krecs.push_back({fn, ev[0], ev[1]});
+  *start = ev[0];
+  *stop = ev[1];
+  return true;
+}
+}  // namespace rbt
 
 namespace {
 
@@ -994,6 +1024,10 @@ void rbt_destroy(rbt_ctx *c) {
   if (c->d_sync) (void)hipFree(c->d_sync);
   for (auto &r : c->ev_rows)
     for (auto e : r) c->ev_free.push_back(e);
+  for (auto &r : c->krecs) {
+    c->ev_free.push_back(r.start);
+    c->ev_free.push_back(r.stop);
+  }
   for (auto e : c->ev_free) (void)hipEventDestroy(e);
   (void)hipStreamDestroy(c->stream);
   delete c;
@@ -1558,6 +1592,42 @@ int rbt_profile_read(rbt_ctx *c, rbt_profile *out, int32_t reset) {
     c->acc = rbt_profile{};
     HIP_OK(c, hipMemset(c->d_flags + FLAG_AMB, 0, sizeof(int)));
   }
+  return RBT_OK;
+}
+
+int rbt_profile_kernels(rbt_ctx *c, int32_t on) {
+  if (!c) return RBT_E_INVALID;
+  c->kprof = on != 0;
+  return RBT_OK;
+}
+
+int rbt_profile_kernels_read(rbt_ctx *c, rbt_kernel_stat *out, size_t cap, size_t *n, int32_t reset) {
+  if (!c || (cap && !out)) return RBT_E_INVALID;
+  HIP_OK(c, hipStreamSynchronize(c->stream));
+  for (auto &r : c->krecs) {
+    float ms = 0.0f;
+    HIP_OK(c, hipEventElapsedTime(&ms, r.start, r.stop));
+    auto &a = c->kacc[r.fn];
+    a.first += 1;
+    a.second += ms;
+    c->ev_free.push_back(r.start);
+    c->ev_free.push_back(r.stop);
+  }
+  c->krecs.clear();
+  size_t i = 0;
+  for (auto &kv : c->kacc) {
+    if (i < cap) {
+      rbt_kernel_stat &s = out[i];
+      s = rbt_kernel_stat{};
+      const char *name = hipKernelNameRefByPtr(kv.first, c->stream);
+      snprintf(s.name, sizeof s.name, "%s", name ? name : "?");
+      s.launches = kv.second.first;
+      s.total_ms = kv.second.second;
+    }
+    i++;
+  }
+  if (n) *n = i;
+  if (reset) c->kacc.clear();
   return RBT_OK;
 }
 

@@ -509,10 +509,10 @@ hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half
   if (n <= 0) return hipSuccess;
   const int blocks = (int)std::min<long>((n + 255) / 256, (long)c.num_cu * 4);
   if (parts == 2)
-    hipLaunchKernelGGL(k_swiglu<2>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev,
+    launch_k(c, k_swiglu<2>, dim3(blocks), dim3(256), gu, gu_stride, half, npairs, npairs_dev,
                        act, h);
   else
-    hipLaunchKernelGGL(k_swiglu<1>, dim3(blocks), dim3(256), 0, c.stream, gu, gu_stride, half, npairs, npairs_dev,
+    launch_k(c, k_swiglu<1>, dim3(blocks), dim3(256), gu, gu_stride, half, npairs, npairs_dev,
                        act, h);
   return hipGetLastError();
 }
@@ -660,13 +660,13 @@ hipError_t launch_generic(const Ctx &c, int kind, float *y, const float *x, cons
                           size_t gs, size_t s, size_t i, size_t o) {
   dim3 grid(grid_for_rows((long)o)), block(256);
   if (kind == RBT_QT_MXFP4)
-    hipLaunchKernelGGL(k_mxfp4_generic, grid, block, 0, c.stream, y, x, (const uint8_t *)data,
+    launch_k(c, k_mxfp4_generic, grid, block, y, x, (const uint8_t *)data,
                        (const uint8_t *)scale, (int)s, (int)i, (int)o);
   else if (kind == RBT_QT_I4_GROUPED)
-    hipLaunchKernelGGL(k_i4g_generic, grid, block, 0, c.stream, y, x, (const uint8_t *)data, (const float *)scale,
+    launch_k(c, k_i4g_generic, grid, block, y, x, (const uint8_t *)data, (const float *)scale,
                        (int)gs, (int)s, (int)i, (int)o);
   else
-    hipLaunchKernelGGL(k_f32_generic, grid, block, 0, c.stream, y, x, (const float *)data, (int)s, (int)i, (int)o);
+    launch_k(c, k_f32_generic, grid, block, y, x, (const float *)data, (int)s, (int)i, (int)o);
   return hipGetLastError();
 }
 
@@ -676,7 +676,7 @@ hipError_t launch_dequant(const Ctx &c, float *out, int kind, const void *data, 
   size_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_dequant_rows, dim3((unsigned)blocks), dim3(256), 0, c.stream, out, kind, data, scale, cols, gs,
+  launch_k(c, k_dequant_rows, dim3((unsigned)blocks), dim3(256), out, kind, data, scale, cols, gs,
                      row0, nrows);
   return hipGetLastError();
 }
@@ -704,7 +704,7 @@ static hipError_t launch_decode_t(const Ctx &c, const RbtExpertDev *jobs, const 
   if (waves > iters) waves = iters;
   if (waves < 1) waves = 1;
   int blocks = (int)((waves + 3) / 4);
-  hipLaunchKernelGGL((k_decode_gemv<NB, LPR, U, MODE, I4G, CS, PARTS>), dim3(blocks), dim3(256), 0, c.stream, jobs,
+  launch_k(c, (k_decode_gemv<NB, LPR, U, MODE, I4G, CS, PARTS>), dim3(blocks), dim3(256), jobs,
                      single, njobs, njobs_dev, x, x_index, x_stride, cols, rows, y, y_stride, nw, eps);
   return hipGetLastError();
 }
@@ -785,10 +785,10 @@ hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, c
   if (items <= 0) return hipSuccess;
   dim3 grid((unsigned)((items + 3) / 4)), block(256);
   if (gateup)
-    hipLaunchKernelGGL(k_pair_generic<true>, grid, block, 0, c.stream, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
+    launch_k(c, k_pair_generic<true>, grid, block, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
                        x_index, x_stride, cols, rows, y, y_stride, act);
   else
-    hipLaunchKernelGGL(k_pair_generic<false>, grid, block, 0, c.stream, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
+    launch_k(c, k_pair_generic<false>, grid, block, jobs, single, njobs, njobs_dev, kind, (int)gs, x,
                        x_index, x_stride, cols, rows, y, y_stride, act);
   return hipGetLastError();
 }

@@ -37,7 +37,7 @@ __global__ void k_accumulate(const float *__restrict__ y, int S, int H, const in
 
 hipError_t launch_single_rows(const Ctx &c, const int32_t *ids, const float *w, int S, int k, int eid, int *pair_tok,
                               float *pair_w, int *nr) {
-  hipLaunchKernelGGL(k_single_rows, dim3(1), dim3(64), 0, c.stream, ids, w, S, k, eid, pair_tok, pair_w, nr);
+  launch_k(c, k_single_rows, dim3(1), dim3(64), ids, w, S, k, eid, pair_tok, pair_w, nr);
   return hipGetLastError();
 }
 
@@ -45,7 +45,7 @@ hipError_t launch_accumulate(const Ctx &c, const float *y, int S, int H, const i
                              const int *nr, float *out) {
   size_t n = (size_t)S * H;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_accumulate, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c.stream, y, S, H, pair_tok,
+  launch_k(c, k_accumulate, dim3((unsigned)((n + 255) / 256)), dim3(256), y, S, H, pair_tok,
                      pair_w, nr, out);
   return hipGetLastError();
 }

@@ -566,7 +566,7 @@ hipError_t launch_pgroup(const Ctx &c, const int32_t *ids, const float *wts, int
                          const RbtExpertDev *table, uint32_t *bits, uint32_t *pc, PSeg *segs, PTile *tiles,
                          int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
   if (E > PG_MAXE) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_pgroup, dim3(1), dim3(1024), 0, c.stream, ids, wts, S, k, E, has_shared, table, bits, pc, segs,
+  launch_k(c, k_pgroup, dim3(1), dim3(1024), ids, wts, S, k, E, has_shared, table, bits, pc, segs,
                      tiles, ntiles, pair_tok, tok_pair, tok_w, err, nuniq);
   return hipGetLastError();
 }
@@ -575,7 +575,7 @@ hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb) {
   if (n <= 0) return hipSuccess;
   const long threads = (n + 3) / 4;
   const int vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)xb % 8 == 0);
-  hipLaunchKernelGGL(k_to_bf16, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, c.stream, x, n, xb, vec);
+  launch_k(c, k_to_bf16, dim3((unsigned)((threads + 255) / 256)), dim3(256), x, n, xb, vec);
   return hipGetLastError();
 }
 

@@ -20,15 +20,29 @@ struct Ctx {
   // Profiling: when set, the next timed launch records these events itself at the kernel's start
   // and end (hipExtLaunchKernelGGL), so the interval excludes dispatch gaps.
   hipEvent_t t_start = nullptr, t_stop = nullptr;
+  // Per-kernel profiling: when set, every launch records a start/end event pair of its own
+  // (kernel_events in api.hip hands them out and files them under the kernel).
+  bool kprof = false;
 };
 
-// Launch on the context's stream; timed by the dispatch when the context holds kernel events.
+// Events for one profiled launch of `fn` (false when none could be created: the launch is untimed).
+bool kernel_events(const Ctx &c, const void *fn, hipEvent_t *start, hipEvent_t *stop);
+
+// Launch on the context's stream with `smem` bytes of dynamic LDS; timed by the dispatch when the
+// context holds phase events or profiles every kernel.
+template <typename K, typename... A>
+inline void launch_ks(const Ctx &c, K kernel, dim3 grid, dim3 block, unsigned smem, A... args) {
+  hipEvent_t s = c.t_start, e = c.t_stop;
+  if (!s && c.kprof && !kernel_events(c, reinterpret_cast<const void *>(kernel), &s, &e)) s = e = nullptr;
+  if (s)
+    hipExtLaunchKernelGGL(kernel, grid, block, smem, c.stream, s, e, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, smem, c.stream, args...);
+}
+
 template <typename K, typename... A>
 inline void launch_k(const Ctx &c, K kernel, dim3 grid, dim3 block, A... args) {
-  if (c.t_start)
-    hipExtLaunchKernelGGL(kernel, grid, block, 0, c.stream, c.t_start, c.t_stop, 0, args...);
-  else
-    hipLaunchKernelGGL(kernel, grid, block, 0, c.stream, args...);
+  launch_ks(c, kernel, grid, block, 0u, args...);
 }
 
 struct RouterArgs {

@@ -1537,14 +1537,14 @@ hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, cons
   int erows = E + (sgate ? 1 : 0);
   bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0) && (!sgate || (uintptr_t)sgate % 16 == 0);
   if (H % 1024 == 0 && H <= RT_MAXH && aligned)
-    hipLaunchKernelGGL(k_router_logits_b, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+    launch_k(c, k_router_logits_b, dim3(erows), dim3(256), x, S, H, W, E, sgate, mid, bnd, erows);
   else if (H % 256 == 0 && H <= RT_MAXH && aligned)
-    hipLaunchKernelGGL(k_router_logits_t, dim3(erows), dim3(64), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+    launch_k(c, k_router_logits_t, dim3(erows), dim3(64), x, S, H, W, E, sgate, mid, bnd, erows);
   else if (H % 256 == 0 && aligned)
-    hipLaunchKernelGGL(k_router_logits_w, dim3((erows + 3) / 4), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid,
+    launch_k(c, k_router_logits_w, dim3((erows + 3) / 4), dim3(256), x, S, H, W, E, sgate, mid,
                        bnd, erows);
   else
-    hipLaunchKernelGGL(k_router_logits, dim3(erows), dim3(256), 0, c.stream, x, S, H, W, E, sgate, mid, bnd, erows);
+    launch_k(c, k_router_logits, dim3(erows), dim3(256), x, S, H, W, E, sgate, mid, bnd, erows);
   return hipGetLastError();
 }
 
@@ -1556,7 +1556,7 @@ hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H
   if (H % RX_KC != 0 || ((uintptr_t)x | (uintptr_t)W | (uintptr_t)(sgate ? sgate : W)) % 16 != 0)
     return hipErrorInvalidValue;
   const dim3 grid((erows + RX_E - 1) / RX_E, (S + RX_T - 1) / RX_T);
-  hipLaunchKernelGGL(k_router_logits_exact, grid, dim3(256), 0, c.stream, x, S, H, W, E, sgate, logits, erows);
+  launch_k(c, k_router_logits_exact, grid, dim3(256), x, S, H, W, E, sgate, logits, erows);
   return hipGetLastError();
 }
 
@@ -1578,7 +1578,7 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
   P.x = a.x;
   P.W = a.W;
   if (a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) {
-    hipLaunchKernelGGL(k_router_select_grouped, dim3(a.S), dim3(64), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+    launch_k(c, k_router_select_grouped, dim3(a.S), dim3(64), P, mid, bnd, ids, wts, sh_scale,
                        stats);
   } else {
     GroupOut G{};
@@ -1592,33 +1592,33 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
       const dim3 grid(max(2, c.num_cu));
       if (m <= 4) {
         if (sgu->K == 8192)
-          hipLaunchKernelGGL((k_router_select3_sh<4, 16>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+          launch_k(c, (k_router_select3_sh<4, 16>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale,
                              stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
         else
-          hipLaunchKernelGGL((k_router_select3_sh<4, 14>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+          launch_k(c, (k_router_select3_sh<4, 14>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale,
                              stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
       } else {
         if (sgu->K == 8192)
-          hipLaunchKernelGGL((k_router_select3_sh<8, 16>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+          launch_k(c, (k_router_select3_sh<8, 16>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale,
                              stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
         else
-          hipLaunchKernelGGL((k_router_select3_sh<8, 14>), grid, dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+          launch_k(c, (k_router_select3_sh<8, 14>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale,
                              stats, G, g, sgu->dev, sgu->x, sgu->I, sgu->hp);
       }
       return hipGetLastError();
     }
     if (sgu) return hipErrorInvalidValue;
     if (m <= 4)
-      hipLaunchKernelGGL(k_router_select3<4>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+      launch_k(c, k_router_select3<4>, dim3(a.S), dim3(256), P, mid, bnd, ids, wts, sh_scale, stats,
                          G, g);
     else if (m <= 8)
-      hipLaunchKernelGGL(k_router_select3<8>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale, stats,
+      launch_k(c, k_router_select3<8>, dim3(a.S), dim3(256), P, mid, bnd, ids, wts, sh_scale, stats,
                          G, g);
     else if (m <= 16)
-      hipLaunchKernelGGL(k_router_select3<16>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+      launch_k(c, k_router_select3<16>, dim3(a.S), dim3(256), P, mid, bnd, ids, wts, sh_scale,
                          stats, G, g);
     else
-      hipLaunchKernelGGL(k_router_select3<32>, dim3(a.S), dim3(256), 0, c.stream, P, mid, bnd, ids, wts, sh_scale,
+      launch_k(c, k_router_select3<32>, dim3(a.S), dim3(256), P, mid, bnd, ids, wts, sh_scale,
                          stats, G, g);
   }
   return hipGetLastError();
@@ -2332,7 +2332,7 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
 
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_logits_to_mid, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c.stream, logits, n, mid, bnd);
+  launch_k(c, k_logits_to_mid, dim3((unsigned)((n + 255) / 256)), dim3(256), logits, n, mid, bnd);
   return hipGetLastError();
 }
 
@@ -2340,11 +2340,11 @@ hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int 
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,
                         int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
   if (S == 1) {
-    hipLaunchKernelGGL(k_group_s1, dim3(1), dim3(((k + 1 + 63) / 64) * 64), 0, c.stream, ids, wts, k, E, table,
+    launch_k(c, k_group_s1, dim3(1), dim3(((k + 1 + 63) / 64) * 64), ids, wts, k, E, table,
                        shared_dev, pair_job, pair_tok, tok_pair, tok_w, err);
   } else {
     size_t smem = (size_t)3 * E * sizeof(int);
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), smem, c.stream, ids, wts, S, k, E, table, shared_dev, pair_job,
+    launch_ks(c, k_group, dim3(1), dim3(1024), smem, ids, wts, S, k, E, table, shared_dev, pair_job,
                        pair_tok, tok_pair, tok_w, err, nuniq);
   }
   return hipGetLastError();
@@ -2353,7 +2353,7 @@ hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int 
 hipError_t launch_combine(const Ctx &c, const float *y, int S, int k, int H, const int *tok_pair, const float *tok_w,
                           const float *sh_scale, int has_shared, int gated, float *out) {
   size_t n = (size_t)S * H;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, c.stream, y, S, k, H, tok_pair, tok_w,
+  launch_k(c, k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), y, S, k, H, tok_pair, tok_w,
                      sh_scale, has_shared, gated, out);
   return hipGetLastError();
 }

@@ -59,8 +59,8 @@ hipError_t launch_synth_mxfp4(const Ctx &c, uint8_t *data, uint8_t *scale, size_
                               uint32_t lo, uint32_t hi) {
   uint64_t sd = mix64(seed * 2 + 1), ss = mix64(seed * 2 + 2);
   size_t nb = rows * ((cols + 1) / 2), ns = rows * ((cols + 31) / 32);
-  hipLaunchKernelGGL(k_synth_bytes, dim3(grid_for((nb + 7) / 8)), dim3(256), 0, c.stream, data, nb, sd);
-  hipLaunchKernelGGL(k_synth_e8m0, dim3(grid_for(ns)), dim3(256), 0, c.stream, scale, ns, ss, lo,
+  launch_k(c, k_synth_bytes, dim3(grid_for((nb + 7) / 8)), dim3(256), data, nb, sd);
+  launch_k(c, k_synth_e8m0, dim3(grid_for(ns)), dim3(256), scale, ns, ss, lo,
                      (uint64_t)(hi - lo + 1));
   return hipGetLastError();
 }
@@ -69,8 +69,8 @@ hipError_t launch_synth_i4g(const Ctx &c, uint8_t *data, float *scale, size_t ro
                             uint64_t seed, float lo, float hi) {
   uint64_t sd = mix64(seed * 2 + 1), ss = mix64(seed * 2 + 2);
   size_t nb = rows * ((cols + 1) / 2), ns = rows * ((cols + gs - 1) / gs);
-  hipLaunchKernelGGL(k_synth_bytes, dim3(grid_for((nb + 7) / 8)), dim3(256), 0, c.stream, data, nb, sd);
-  hipLaunchKernelGGL(k_synth_f32scale, dim3(grid_for(ns)), dim3(256), 0, c.stream, scale, ns, ss, lo, hi);
+  launch_k(c, k_synth_bytes, dim3(grid_for((nb + 7) / 8)), dim3(256), data, nb, sd);
+  launch_k(c, k_synth_f32scale, dim3(grid_for(ns)), dim3(256), scale, ns, ss, lo, hi);
   return hipGetLastError();
 }
 
