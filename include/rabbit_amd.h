@@ -254,6 +254,19 @@ int rbt_moe_forward(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, floa
 int rbt_moe_forward_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
                       int32_t *ids_out, float *w_out);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): rbt_moe_forward_d with every
+ * per-call device buffer carved out of one fixed array of RBT_NOALLOC_SCRATCH_BYTES per device
+ * (allocated when the library is loaded and held until the process ends), so the call itself
+ * allocates nothing. Same kernels and results as rbt_moe_forward_d. A call whose buffers would not
+ * fit returns RBT_E_UNSUPPORTED (e.g. the Qwen3.8-shaped layer fits up to 16 tokens, not a
+ * 512-token prefill). Every call on one device shares that device's array: calls that overlap on
+ * one GPU (two contexts, two host threads) race. The layer must have been set (rbt_moe_layer_set*),
+ * which sizes the layer's own tables. */
+#define RBT_NOALLOC_SCRATCH_BYTES (16u << 20)
+int rbt_moe_forward_noalloc_d(rbt_ctx *ctx, uint32_t layer, const float *x, size_t s, float *out,
+                              int32_t *ids_out, float *w_out);
+
 /* ---- K3 latent MoE (kimi_k3/moe.rs) ----------------------------------------------------------- */
 /* LatentMoeWeights (kimi_k3/moe.rs:41-57) plus the layer's expert width and activation. Device
  * memory. */

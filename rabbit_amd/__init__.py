@@ -411,6 +411,17 @@ class Context:
                                                  _ptr(w_out)))
         return x
 
+    def moe_forward_noalloc(self, layer, x, s, out, ids_out=None, w_out=None, sync=True):
+        """rbt_moe_forward_noalloc_d: moe_forward on device tensors with every per-call buffer taken
+        from the device's fixed scratch array (no allocation in the call)."""
+        if sync:
+            self._torch_sync()
+        self.check(self.lib.rbt_moe_forward_noalloc_d(self.h, layer, _ptr(x), s, _ptr(out), _ptr(ids_out),
+                                                      _ptr(w_out)))
+        if sync:
+            self.sync()
+        return out
+
     def moe_forward(self, layer, x, s, out, ids_out=None, w_out=None, sync=True):
         if _is_torch(x):
             if sync:

@@ -118,6 +118,7 @@ SIGNATURES = {
     "rbt_moe_layer_set_device": (_I, [_CTX, _U32, C.POINTER(RbtMoeLayerDesc)]),
     "rbt_moe_forward": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
     "rbt_moe_forward_d": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
+    "rbt_moe_forward_noalloc_d": (_I, [_CTX, _U32, _P, _S, _P, _P, _P]),
     "rbt_shards_open": (_I, [C.c_char_p, C.POINTER(C.c_void_p)]),
     "rbt_shards_close": (None, [C.c_void_p]),
     "rbt_shards_last_error": (C.c_char_p, []),

@@ -19,7 +19,41 @@
 
 #include "rbt_internal.h"
 
+#include <mutex>
+
+// Device scratch of the allocation-free entry point (rbt_moe_forward_noalloc_d): one copy per
+// device, held until the process ends. On the host this name is only a stand-in for the symbol, not
+// a device address: host code uses the address hipGetSymbolAddress returned for the device
+// (noalloc_base, resolved once per device by rbt_init) wherever it needs the array's memory.
+static __device__ __align__(256) uint8_t noalloc_scratch[RBT_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int NOALLOC_MAX_DEV = 64;
+std::mutex g_noalloc_mu;
+uint8_t *g_noalloc_ptr[NOALLOC_MAX_DEV];
+hipError_t g_noalloc_err[NOALLOC_MAX_DEV];
+bool g_noalloc_done[NOALLOC_MAX_DEV];
+
+// The device address of noalloc_scratch on `device`, which must be current: looked up on the
+// device's first context, then kept (nullptr when the lookup failed; *err says why).
+uint8_t *noalloc_base(int device, hipError_t *err) {
+  std::lock_guard<std::mutex> g(g_noalloc_mu);
+  if (device < 0 || device >= NOALLOC_MAX_DEV) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  if (!g_noalloc_done[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc_scratch));
+    if (e != hipSuccess) (void)hipGetLastError();
+    g_noalloc_err[device] = e;
+    g_noalloc_ptr[device] = e == hipSuccess ? static_cast<uint8_t *>(p) : nullptr;
+    g_noalloc_done[device] = true;
+  }
+  *err = g_noalloc_err[device];
+  return g_noalloc_ptr[device];
+}
 
 enum ScratchSlot {
   SC_X,
@@ -69,8 +103,9 @@ struct Layer {
   std::vector<void *> owned;
   bool set = false;
   bool dirty = true;
-  RbtExpertDev *d_table = nullptr;
+  RbtExpertDev *d_table = nullptr;  // n_experts entries, allocated with the layer
   size_t table_n = 0;
+  std::vector<RbtExpertDev> h_table;  // host image of d_table (sized with the layer: refreshing it allocates nothing)
   RbtExpertDev *d_shared = nullptr;
   RbtExpertDev h_shared{};
   int shared_kind = -1;
@@ -91,6 +126,13 @@ struct rbt_ctx : rbt::Ctx {
   std::string err;
   void *scratch[SC_N] = {};
   size_t scratch_cap[SC_N] = {};
+  // allocation-free calls: the device's fixed scratch array (its device address, or nullptr when the
+  // lookup failed), carved per slot for one call
+  uint8_t *noalloc = nullptr;
+  hipError_t noalloc_err = hipSuccess;
+  uint8_t *arena = nullptr;
+  size_t arena_cap = 0, arena_used = 0;
+  size_t arena_off[SC_N] = {}, arena_sz[SC_N] = {};
   std::map<uint64_t, PoolEntry> pool;
   std::map<uint32_t, Layer> layers;
   int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts
@@ -168,9 +210,27 @@ size_t div_ceil(size_t a, size_t b) { return (a + b - 1) / b; }
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 // Grow-only device scratch. Growth synchronises the stream first, so in-flight work never sees a
-// freed buffer.
+// freed buffer. Inside an allocation-free call (c->arena set) the slots are carved out of the
+// device's fixed scratch array instead, a slot keeping its region for the rest of the call.
 int scratch(rbt_ctx *c, int slot, size_t bytes, void **out) {
   if (bytes == 0) bytes = 256;
+  if (c->arena) {
+    if (c->arena_sz[slot] == 0) {
+      const size_t need = align256(bytes);
+      if (need > c->arena_cap - c->arena_used)
+        return fail(c, RBT_E_UNSUPPORTED,
+                    "the allocation-free call needs more than its %zu bytes of device scratch (slot %d wants %zu "
+                    "bytes with %zu already used): fewer tokens per call, or the allocating entry point",
+                    c->arena_cap, slot, need, c->arena_used);
+      c->arena_off[slot] = c->arena_used;
+      c->arena_sz[slot] = need;
+      c->arena_used += need;
+    } else if (c->arena_sz[slot] < bytes) {
+      return fail(c, RBT_E_UNSUPPORTED, "scratch slot %d asked for twice with a larger size in one call", slot);
+    }
+    *out = c->arena + c->arena_off[slot];
+    return RBT_OK;
+  }
   if (c->scratch_cap[slot] < bytes) {
     HIP_OK(c, hipStreamSynchronize(c->stream));
     if (c->scratch[slot]) HIP_OK(c, hipFree(c->scratch[slot]));
@@ -403,11 +463,15 @@ int expert_pairs(rbt_ctx *c, int kind, size_t gs, const RbtExpertDev *jobs, cons
   return RBT_OK;
 }
 
+// Rebuilds the layer's device table of resident experts after the pool or the layer changed. The
+// host image and the device table were sized when the layer was set, so this allocates nothing.
 int refresh_table(rbt_ctx *c, uint32_t layer, Layer &L) {
   size_t E = L.desc.n_experts;
   if (!L.dirty && L.table_n == E) return RBT_OK;
-  std::vector<RbtExpertDev> t(E);
-  memset(t.data(), 0, E * sizeof(RbtExpertDev));
+  if (L.h_table.size() != E || L.table_n != E || !L.d_table)
+    return fail(c, RBT_E_INVALID, "layer %u: expert table not sized", layer);
+  RbtExpertDev *t = L.h_table.data();
+  memset(t, 0, E * sizeof(RbtExpertDev));
   L.routed_kind = -1;
   for (auto &kv : c->pool) {
     if ((uint32_t)(kv.first >> 32) != layer) continue;
@@ -421,13 +485,7 @@ int refresh_table(rbt_ctx *c, uint32_t layer, Layer &L) {
     L.routed_kind = kind;
     L.routed_gs = gs;
   }
-  if (L.table_n < E) {
-    if (L.d_table) HIP_OK(c, hipFree(L.d_table));
-    L.d_table = nullptr;
-    HIP_OK(c, hipMalloc(&L.d_table, E * sizeof(RbtExpertDev)));
-  }
-  L.table_n = E;
-  HIP_OK(c, hipMemcpyAsync(L.d_table, t.data(), E * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
+  HIP_OK(c, hipMemcpyAsync(L.d_table, t, E * sizeof(RbtExpertDev), hipMemcpyHostToDevice, c->stream));
   HIP_OK(c, hipStreamSynchronize(c->stream));
   L.dirty = false;
   return RBT_OK;
@@ -552,6 +610,10 @@ int layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d, bool devi
     HIP_OK(c, hipMalloc(&L.d_shared, sizeof(RbtExpertDev)));
     HIP_OK(c, hipMemset(L.d_shared, 0, sizeof(RbtExpertDev)));
   }
+  // the table of resident experts: sized here, refreshed (without allocating) after pool changes
+  L.h_table.assign(E, RbtExpertDev{});
+  HIP_OK(c, hipMalloc(&L.d_table, E * sizeof(RbtExpertDev)));
+  L.table_n = E;
   L.set = true;
   L.dirty = true;
   L.lat_dirty = true;
@@ -999,6 +1061,8 @@ int rbt_init(rbt_ctx **out, int device) {
   else if ((e = hipMemset(c->d_flags, 0, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMemset";
   else if ((e = hipMalloc((void **)&c->d_sync, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMalloc";
   else if ((e = hipMemset(c->d_sync, 0, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMemset";
+  // the allocation-free entry point's scratch on this device (the device is current)
+  if (!what) c->noalloc = noalloc_base(device, &c->noalloc_err);
   if (what) {
     int rc = init_fail(RBT_E_HIP, what, e);
     if (c->d_sync) (void)hipFree(c->d_sync);
@@ -1533,6 +1597,28 @@ int rbt_moe_forward_d(rbt_ctx *c, uint32_t layer, const float *x, size_t s, floa
                       float *w_out) {
   if (!c) return RBT_E_INVALID;
   return moe_forward_dev(c, layer, x, s, out, ids_out, w_out);
+}
+
+int rbt_moe_forward_noalloc_d(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
+                              float *w_out) {
+  if (!c) return RBT_E_INVALID;
+  if (!c->noalloc)
+    return fail(c, RBT_E_HIP, "no allocation-free scratch on device %d: hipGetSymbolAddress: %s", c->device,
+                hipGetErrorString(c->noalloc_err));
+  // every per-call buffer comes from the device's fixed array; profiling (which creates events) is
+  // off for the call
+  const bool prof = c->prof, kprof = c->kprof;
+  c->prof = c->kprof = false;
+  c->arena = c->noalloc;
+  c->arena_cap = RBT_NOALLOC_SCRATCH_BYTES;
+  c->arena_used = 0;
+  memset(c->arena_sz, 0, sizeof c->arena_sz);
+  const int rc = moe_forward_dev(c, layer, x, s, out, ids_out, w_out);
+  c->arena = nullptr;
+  c->arena_cap = c->arena_used = 0;
+  c->prof = prof;
+  c->kprof = kprof;
+  return rc;
 }
 
 int rbt_moe_forward(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
