@@ -5,19 +5,24 @@ top-10, the 10 routed MXFP4 SwiGLU experts plus the gated shared expert, ordered
 experts (13.7 GB) are resident in HBM; every step feeds a different token, so the selected experts
 rotate over the whole pool and the 256 MB Infinity Cache cannot serve them.
 
-value    = microseconds per token (whole layer), timed over --steps tokens replayed through a HIP
-           graph of --graph-tokens consecutive layer calls (the way a decode step would run).
-roofline = the dominant kernel, the gate/up dequant-GEMV: algorithmic bytes per launch / its mean
-           duration, measured live with HIP events on the library's stream (second pass; the events
-           are recorded by the kernel dispatch itself, at its start and end).
-cpu_baseline = the reference's AVX-512 (or AVX2) MXFP4 tier, restated in oracle/, timed on this
-           host's cores over a bounded sample of the same tokens.
+value    = microseconds per token (whole layer) over exactly --steps tokens, replayed through HIP
+           graphs of at most --graph-tokens consecutive layer calls; every graph is launched once
+           untimed first, so the timed launches are warm replays.
+roofline = the dominant kernel (the most time per call): its algorithmic bytes per launch (the
+           weight bytes of the experts it actually streamed) over its mean duration, measured live
+           with HIP events that the kernel dispatch itself records (an eager pass after the timed
+           one); traffic = its FETCH_SIZE + WRITE_SIZE bytes per launch from rocprofv3 counter runs
+           (profiles/traffic_<config>.json, scaled by a plain copy's counters), when it is there.
+cpu_baseline = the reference's AVX-512 (or AVX2; scalar for grouped int4, the reference's only
+           tier) kernels restated in oracle/, timed on this host's cores over a bounded sample of
+           the same tokens, warm (experts just generated) and cold (a 256 MiB eviction first).
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config c1]
 
---config c4 times the 512-token prefill instead, --config k3l Kimi K3's latent MoE (896 experts
-at moe_hidden 3584, top-16, Situ, the routed-expert norm) one token per call, and --config c1s the
-MoE sublayer (rmsnorm_1p, C1's layer, residual add); none of them is the default line.
+Other configurations (never the default line): c0 (one expert FFN, rbt_apply_single_expert_d), mm
+(rbt_matmul_mxfp4_d at the reference's micro-benchmark shapes and C0's three matrices), c2 (GLM
+grouped-int4 decode), c3 (K3 batch-8 Zipf decode), c4 (512-token prefill), k3l (K3's latent MoE),
+c1s (the MoE sublayer: rmsnorm_1p, C1's layer, residual add).
 """
 from __future__ import annotations
 
@@ -25,6 +30,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
 import sys
 import time
 
@@ -35,8 +41,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "MoE-layer decode µs/token + expert GEMV HBM GB/s (% of 8 TB/s), MXFP4"
 HBM_PEAK_GBPS = 8000.0
-# the gate/up kernel the MXFP4 decode path launches (its FETCH/WRITE counters: profiles/traffic_<cfg>.json)
-ROOFLINE_KERNEL = "rbt::k_xgateup1f<16>"
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
 
 
 def log(*a):
@@ -79,80 +84,335 @@ class Graph:
             self.hip.hipGraphDestroy(self.graph)
 
 
-def physical_cores() -> int:
+def graph_time(hip, ctx, call, first, n, G):
+    """Times calls call(first) .. call(first + n - 1) captured into HIP graphs of at most G calls.
+    Each graph is launched once untimed (and synchronised) first; the timed region then launches
+    every graph once. Returns (wall seconds, event milliseconds) of the timed region."""
+    import torch
+    graphs = []
+    for g0 in range(first, first + n, G):
+        g = Graph(hip, ctx.stream)
+        g.begin()
+        for t in range(g0, min(g0 + G, first + n)):
+            call(t)
+        g.end()
+        graphs.append(g)
+    for g in graphs:  # untimed first launch of every graph
+        g.launch()
+    ctx.sync()
+    ext = ctx.torch_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(ext)
+    for g in graphs:
+        g.launch()
+    ev1.record(ext)
+    ctx.sync()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ev0.elapsed_time(ev1)
+    for g in graphs:
+        g.destroy()
+    return wall, ev_ms
+
+
+def kernel_table(ctx, run):
+    """Per-kernel mean durations of the launches run() makes (eager, events recorded by each
+    dispatch): {name: (launches, mean us)}."""
+    ctx.sync()
+    ctx.profile_kernels_read(reset=True)
+    ctx.profile_kernels(True)
     try:
-        avail = len(os.sched_getaffinity(0))
+        run()
+        ctx.sync()
+    finally:
+        ctx.profile_kernels(False)
+    return ctx.profile_kernels_read(reset=True)
+
+
+def kernel_role(name: str) -> str:
+    """gateup / down / router / proj / other, from the kernel's (possibly mangled) name."""
+    if any(s in name for s in ("xgateup", "pgateup", "decode_gu_act")):
+        return "gateup"
+    if any(s in name for s in ("xdown", "pdown")):
+        return "down"
+    m = re.search(r"k_decode_gemvILi\d+ELi\d+ELi\d+ELi(\d+)E", name) or \
+        re.search(r"k_decode_gemv<\s*\d+,\s*\d+,\s*\d+,\s*(\d+)", name)
+    if m:
+        return {"0": "down", "1": "gateup", "2": "down", "3": "proj"}[m.group(1)]
+    if "router" in name or "select" in name:
+        return "router"
+    return "other"
+
+
+def short_name(name: str) -> str:
+    m = re.search(r"(k_[a-z0-9_]+)", name)
+    return m.group(1) if m else name[:60]
+
+
+def per_call(tab, ncalls):
+    """{short name: [launches per call, mean us, us per call, role]} sorted by time per call."""
+    rows = []
+    for name, (launches, mean_us) in tab.items():
+        rows.append((short_name(name), launches / ncalls, mean_us, launches * mean_us / ncalls, kernel_role(name),
+                     name))
+    rows.sort(key=lambda r: -r[3])
+    return rows
+
+
+def roofline(rows, role, bytes_per_launch, traffic_cfg, note=""):
+    """The roofline object for the slowest kernel of `role` (rows from per_call)."""
+    cand = [r for r in rows if r[4] == role]
+    if not cand:
+        return None
+    r = cand[0]
+    gbps = bytes_per_launch / (r[2] * 1e-6) / 1e9
+    res = {"bound": "hbm", "kernel": r[0], "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+           "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": int(bytes_per_launch),
+           "launch_us": round(r[2], 3), "traffic": traffic_of(traffic_cfg, r[5])}
+    if note:
+        res["note"] = note
+    return res
+
+
+def traffic_of(cfg_name, kernel_name):
+    """FETCH_SIZE + WRITE_SIZE bytes per launch of `kernel_name` from profiles/traffic_<cfg>.json
+    (written from two rocprofv3 --pmc runs of this benchmark), or None."""
+    tf = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    try:
+        t = json.load(open(tf))
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(short_name(kernel_name))
+    return k.get("bytes_per_launch") if k else None
+
+
+def kernels_json(rows):
+    out = {}
+    for r in rows:
+        key = r[0] if r[0] not in out else f"{r[0]}[{r[4]}]"
+        out[key] = {"per_call": round(r[1], 3), "mean_us": round(r[2], 3), "role": r[4]}
+    return out
+
+
+# ---- CPU baseline ------------------------------------------------------------------------------
+def cpu_info() -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        cpus = sorted(os.sched_getaffinity(0))
     except AttributeError:
-        avail = os.cpu_count() or 1
+        cpus = list(range(os.cpu_count() or 1))
     cores = set()
-    try:
-        for cpu in os.sched_getaffinity(0):
+    for cpu in cpus:
+        try:
             with open(f"/sys/devices/system/cpu/cpu{cpu}/topology/core_id") as f:
                 core = f.read().strip()
             with open(f"/sys/devices/system/cpu/cpu{cpu}/topology/physical_package_id") as f:
                 pkg = f.read().strip()
             cores.add((pkg, core))
-    except OSError:
-        pass
-    n = len(cores) if cores else avail
+        except OSError:
+            pass
+    physical = len(cores) if cores else len(cpus)
+    threads = physical
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit():
-        n = min(n, int(env))
-    return max(1, n)
+        threads = min(threads, int(env))
+    return {"model": model, "physical_cores": physical, "logical_cpus": len(cpus), "threads": max(1, threads)}
 
 
-def cpu_model() -> str:
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+class Evictor:
+    """256 MiB written before a cold call: the reference's cold benchmark evicts 64 MiB+
+    (benches/kernels.rs:355-383); this host's last-level cache is smaller than 256 MiB."""
+
+    def __init__(self):
+        self.buf = np.ones(64 << 20, np.float32)
+
+    def __call__(self):
+        self.buf += 1.0
 
 
-def cpu_baseline(cfg, seed, x_tokens, budget_s, gpu_out=None):
-    """Times the oracle's SIMD tier (the reference's AVX-512/AVX2 MXFP4 kernels, restated) on the
-    same layer and tokens. Experts are regenerated on the host first (not timed)."""
-    from oracle import oracle as O
-    from oracle.workload import HostLayer
-    threads = physical_cores()
-    O.set_threads(threads)
-    tier = "avx512" if O.lib().orc_cpu_has_avx512() else ("avx2" if O.lib().orc_cpu_has_avx2() else "scalar")
-    host = HostLayer(cfg, seed)
-    done, t_total, outs = 0, 0.0, []
-    for t in range(x_tokens.shape[0]):
-        xt = x_tokens[t:t + 1]
-        ids, _ = host.route(xt)
-        host.ensure(ids)
-        t0 = time.perf_counter()
-        out, _, _ = host._layer().forward(xt, 1, simd=True)
-        t_total += time.perf_counter() - t0
-        outs.append(out)
-        done += 1
-        if t_total >= budget_s and done >= 3:
-            break
-        if len(host.experts) > 160:  # bound host memory (~4 GB of regenerated experts)
-            host.experts.clear()
-    us = t_total / done * 1e6
-    res = {"value": round(us, 1), "unit": "us/token", "cores": threads, "kind": "port",
-           "sample": f"{done} tokens of {cfg.name} (router + {cfg.topk} routed + shared expert), "
-                     f"{tier} tier of the reference's matmul_mxfp4 restated in C, rows in parallel "
-                     f"on {threads} threads; {cpu_model()}"}
-    if gpu_out is not None:
-        g = gpu_out[:done].astype(np.float64).ravel()
-        c = np.concatenate(outs).astype(np.float64).ravel()
-        res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+def simd_tier(O):
+    L = O.lib()
+    return "avx512" if L.orc_cpu_has_avx512() else ("avx2" if L.orc_cpu_has_avx2() else "scalar")
+
+
+def cpu_line(us_warm, us_cold, unit, bytes_per_unit, info, kind, sample, extra=None):
+    res = {"value": round(us_warm, 2), "unit": unit, "cores": info["threads"], "kind": kind, "sample": sample,
+           "cold": round(us_cold, 2) if us_cold is not None else None,
+           "gbps_warm": round(bytes_per_unit / (us_warm * 1e-6) / 1e9, 2),
+           "gbps_cold": round(bytes_per_unit / (us_cold * 1e-6) / 1e9, 2) if us_cold else None,
+           "cpu": info}
+    if extra:
+        res.update(extra)
     return res
 
 
-MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+def cpu_baseline_layer(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token, simd=True):
+    """The oracle's restated reference kernels on the same layer and tokens, one token per call.
+    Experts the tokens route to are regenerated on the host first (not timed); each token runs warm
+    (right after that) and cold (after an eviction)."""
+    from oracle import oracle as O
+    from oracle.workload import HostLayer
+    info = cpu_info()
+    O.set_threads(info["threads"])
+    tier = simd_tier(O) if simd and cfg.kind == O.QT_MXFP4 else "scalar"
+    host = HostLayer(cfg, seed)
+    ev = Evictor()
+    S = cfg.tokens
+    warm, cold, outs, done = 0.0, 0.0, [], 0
+    for t in range(0, x_tokens.shape[0], S):
+        xt = x_tokens[t:t + S]
+        if xt.shape[0] < S:
+            break
+        ids, _ = host.route(xt)
+        host.ensure(ids)
+        lay = host._layer()
+        t0 = time.perf_counter()
+        out, _, _ = lay.forward(xt, S, simd=simd)
+        warm += time.perf_counter() - t0
+        ev()
+        t0 = time.perf_counter()
+        lay.forward(xt, S, simd=simd)
+        cold += time.perf_counter() - t0
+        outs.append(out)
+        done += S
+        if warm + cold >= budget_s and done >= 3 * S:
+            break
+        if len(host.experts) > 160:  # bound host memory (~4 GB of regenerated experts)
+            host.experts.clear()
+    per = lambda v: v / done * 1e6  # noqa: E731
+    sample = (f"{done} tokens of {cfg.name} ({S} per call: router + {cfg.topk} routed"
+              f"{' + shared' if cfg.shared else ''} experts), {tier} tier of the reference's kernels restated "
+              f"in C, rows in parallel on {info['threads']} threads")
+    res = cpu_line(per(warm), per(cold), "us/token", bytes_per_token, info, "port", sample)
+    g = gpu_out[:done].astype(np.float64).ravel()
+    c = np.concatenate(outs).astype(np.float64).ravel()
+    res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+    return res
 
 
-def bench_prefill(args, ctx, cfg, pool_gb):
+# ---- layer configurations (c1, c2, c3) ---------------------------------------------------------
+def expert_matrix_bytes(cfg, rows, cols):
+    import rabbit_amd as R
+    if cfg.kind == R.QT_MXFP4:
+        return rows * cols // 2 + rows * cols // 32
+    return rows * cols // 2 + rows * (cols // cfg.gs) * 4
+
+
+def bench_layer(args, ctx, hip, cfg, pool_gb):
+    """Decode configurations: one layer call of cfg.tokens tokens per graph node."""
+    import torch
+    import rabbit_amd.workloads as W
+    S, H, I, k = cfg.tokens, cfg.hidden, cfg.inter, cfg.topk
+    calls = max(1, args.steps // S) if S > 1 else args.steps
+    steps = calls * S
+    wcalls = max(1, args.warmup // S) if S > 1 else args.warmup
+    ncalls = wcalls + calls
+    x_all = torch.from_numpy(W.tokens(cfg, ncalls * S, args.seed + 5)).cuda()
+    out_all = torch.empty_like(x_all)
+    ids_all = torch.empty(ncalls * S * k, dtype=torch.int32, device="cuda")
+    xs = [x_all[c * S:(c + 1) * S] for c in range(ncalls)]
+    outs = [out_all[c * S:(c + 1) * S] for c in range(ncalls)]
+    idv = [ids_all[c * S * k:(c + 1) * S * k] for c in range(ncalls)]
+
+    def call(c):
+        ctx.moe_forward(0, xs[c], S, outs[c], idv[c], sync=False)
+
+    for c in range(wcalls):  # also sizes every scratch buffer, so capture allocates nothing
+        call(c)
+    ctx.sync()
+    G = max(1, min(args.graph_tokens // S if S > 1 else args.graph_tokens, calls))
+    wall, ev_ms = graph_time(hip, ctx, call, wcalls, calls, G)
+    us_tok = wall / steps * 1e6
+    log(f"[bench] {cfg.name}: timed {steps} tokens ({calls} calls): wall {wall * 1e3:.2f} ms "
+        f"({us_tok:.2f} us/token), events {ev_ms:.2f} ms")
+
+    # eager passes: per-kernel durations, then the phase profile (streamed experts, exact folds)
+    tab = kernel_table(ctx, lambda: [call(c) for c in range(wcalls, ncalls)])
+    rows = per_call(tab, calls)
+    ctx.profile_read(reset=True)
+    ctx.profile_enable(True)
+    t1 = time.perf_counter()
+    for c in range(wcalls, ncalls):
+        call(c)
+    ctx.sync()
+    eager_us = (time.perf_counter() - t1) / steps * 1e6
+    prof = ctx.profile_read(reset=True)
+    ctx.profile_enable(False)
+    ids_np = ids_all.cpu().numpy().reshape(ncalls, S * k)[wcalls:]
+    U = float(np.mean([len(np.unique(r[r >= 0])) for r in ids_np]))
+
+    per_gu = 2 * expert_matrix_bytes(cfg, I, H)
+    per_dn = expert_matrix_bytes(cfg, H, I)
+    nsh = 1 if cfg.shared else 0
+    n = max(1, prof["calls"])
+    # experts each phase streamed: one token counts on the device what the gate/up launch streamed
+    # (deferred decisions stream extra candidates; the shared expert's gate/up runs inside the
+    # router launch); batches stream every unique expert plus the shared one
+    if S == 1 and prof["gateup_experts"]:
+        gu_exp, dn_exp = prof["gateup_experts"] / n, prof["down_experts"] / n
+    else:
+        gu_exp = dn_exp = U + nsh
+    gu_bytes, dn_bytes = gu_exp * per_gu, dn_exp * per_dn
+    rl = roofline(rows, "gateup", gu_bytes, args.config,
+                  note=f"algorithmic bytes: gate+up weights of the {gu_exp:.2f} experts the kernel streams per call")
+    gu = next((r for r in rows if r[4] == "gateup"), None)
+    dn = next((r for r in rows if r[4] == "down"), None)
+    ex = None
+    if gu and dn:
+        t_ex = gu[3] + dn[3]
+        gb = (gu_bytes + dn_bytes) / (t_ex * 1e-6) / 1e9
+        ex = {"bytes_per_call": int(gu_bytes + dn_bytes), "us_per_call": round(t_ex, 2), "gbps": round(gb, 1),
+              "frac": round(gb / HBM_PEAK_GBPS, 4), "gateup_experts": round(gu_exp, 3),
+              "down_experts": round(dn_exp, 3),
+              "note": "the weight bytes the gate/up and down kernels stream over their own durations"}
+    router_bytes = cfg.n_experts * H * 4 + (H * 4 if cfg.gated_shared else 0)
+    call_bytes = (U + nsh) * (per_gu + per_dn) + router_bytes + 2 * S * H * 4
+    call_gbps = call_bytes / (us_tok * S * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        ntok_cpu = min(x_all.shape[0] - wcalls * S, max(S, 64 if S == 1 else 4 * S))
+        x0 = wcalls * S
+        cpu = cpu_baseline_layer(cfg, args.seed, x_all[x0:x0 + ntok_cpu].cpu().numpy(), args.cpu_budget,
+                                 out_all[x0:x0 + ntok_cpu].cpu().numpy(), call_bytes / S)
+    import rabbit_amd as R
+    res = {
+        "metric": METRIC if args.config == "c1" else
+        f"MoE-layer decode µs/token + expert GEMV HBM GB/s (% of 8 TB/s), {'MXFP4' if cfg.kind == R.QT_MXFP4 else 'grouped int4'}",
+        "value": round(us_tok, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": wcalls * S,
+        "ms_per_step": round(us_tok / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg.name, "hidden": H, "moe_inter": I, "n_experts": cfg.n_experts, "topk": k,
+                   "shared_expert": cfg.shared, "weights": "mxfp4" if cfg.kind == R.QT_MXFP4 else f"int4-grouped gs{cfg.gs}",
+                   "tokens_per_call": S, "resident_pool_gb": round(pool_gb, 2), "graph_calls": G,
+                   "unique_experts_per_call": round(U, 2)},
+        "roofline": rl,
+        "expert_gemv": ex,
+        "call": {"bytes_per_call": int(call_bytes), "us_per_call": round(us_tok * S, 2), "gbps": round(call_gbps, 1),
+                 "frac": round(call_gbps / HBM_PEAK_GBPS, 4),
+                 "note": "router + unique experts + shared expert + x/out over the whole call"},
+        "kernels": kernels_json(rows),
+        "eager_us_per_token": round(eager_us, 2),
+        "router_exact_recomputes": int(prof["ambiguous"]),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
+# ---- prefill (c4) ------------------------------------------------------------------------------
+def bench_prefill(args, ctx, hip, cfg, pool_gb):
     """C4: one MoE-layer call over cfg.tokens tokens (512) per step. value = us per layer call;
-    roofline = the grouped gate/up GEMM (HBM: weights of every unique expert + shared; also its
-    MFMA utilisation); the down GEMM is reported beside it."""
+    roofline = the grouped gate/up GEMM (HBM: weights of every unique expert + shared; its MFMA
+    utilisation beside it); the down GEMM is reported beside it."""
     import torch
     import rabbit_amd.workloads as W
     S, H, I, k = cfg.tokens, cfg.hidden, cfg.inter, cfg.topk
@@ -161,40 +421,41 @@ def bench_prefill(args, ctx, cfg, pool_gb):
     nb = steps + warm
     xs = [torch.from_numpy(W.tokens(cfg, S, args.seed + 5 + b)).cuda() for b in range(nb)]
     out = torch.empty(S * H, dtype=torch.float32, device="cuda")
-    ids = torch.empty(S * k, dtype=torch.int32, device="cuda")
-    uniq = []
+    ids = torch.empty(nb, S * k, dtype=torch.int32, device="cuda")
+
+    def call(b):
+        ctx.moe_forward(0, xs[b], S, out, ids[b], sync=False)
+
     for b in range(warm):
-        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
+        call(b)
     ctx.sync()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for b in range(warm, nb):
-        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
-    ctx.sync()
-    wall = time.perf_counter() - t0
+    wall, ev_ms = graph_time(hip, ctx, call, warm, steps, steps)
     us_call = wall / steps * 1e6
-    log(f"[bench] prefill: {steps} calls of {S} tokens, {us_call:.1f} us/call")
-    ctx.profile_read(reset=True)
-    ctx.profile_enable(True)
-    for b in range(warm, nb):
-        ctx.moe_forward(0, xs[b], S, out, ids, sync=False)
-        ctx.sync()
-        uniq.append(len(np.unique(ids.cpu().numpy())))
-    prof = ctx.profile_read(reset=True)
-    ctx.profile_enable(False)
-    n = max(1, prof["calls"])
-    gu_us = prof["gateup_ms"] / n * 1e3
-    dn_us = prof["down_ms"] / n * 1e3
-    rt_us = prof["router_ms"] / n * 1e3
-    cb_us = prof["combine_ms"] / n * 1e3
-    U = float(np.mean(uniq))
+    log(f"[bench] prefill: {steps} calls of {S} tokens, {us_call:.1f} us/call (events {ev_ms / steps * 1e3:.1f})")
+    tab = kernel_table(ctx, lambda: [call(b) for b in range(warm, nb)])
+    rows = per_call(tab, steps)
+    U = float(np.mean([len(np.unique(r)) for r in ids[warm:].cpu().numpy()]))
     nexp = U + 1  # + shared
-    gu_bytes = nexp * 2 * I * (H // 2 + H // 32)
-    dn_bytes = nexp * H * (I // 2 + I // 32)
+    per_gu = 2 * I * (H // 2 + H // 32)
+    per_dn = H * (I // 2 + I // 32)
     pairs = S * k + S
     gu_flops = 2.0 * pairs * 2 * I * H
     dn_flops = 2.0 * pairs * H * I
-    gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
+    rl = roofline(rows, "gateup", nexp * per_gu, "c4",
+                  note=f"algorithmic bytes: gate+up weights of the {nexp:.1f} experts of the call, each read once")
+    gu = next((r for r in rows if r[4] == "gateup"), None)
+    dn = next((r for r in rows if r[4] == "down"), None)
+    if rl and gu:
+        rl["mfma_tflops"] = round(gu_flops / (gu[2] * 1e-6) / 1e12, 1)
+        rl["mfma_util"] = round(gu_flops / (gu[2] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+    down = None
+    if dn:
+        down = {"kernel": dn[0], "bytes": int(nexp * per_dn), "us": round(dn[2], 2),
+                "gbps": round(nexp * per_dn / (dn[2] * 1e-6) / 1e9, 1),
+                "mfma_util": round(dn_flops / (dn[2] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_prefill(cfg, args.seed, xs[warm].cpu().numpy(), nexp * (per_gu + per_dn))
     res = {
         "metric": "MoE-layer prefill us/call (512 tokens) + grouped-GEMM HBM GB/s and MFMA utilisation, MXFP4",
         "value": round(us_call, 1), "unit": "us/call", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -204,62 +465,289 @@ def bench_prefill(args, ctx, cfg, pool_gb):
                    "n_experts": cfg.n_experts, "topk": k, "shared_expert": cfg.shared, "weights": "mxfp4",
                    "resident_pool_gb": round(pool_gb, 2), "unique_experts_mean": round(U, 1)},
         "us_per_token": round(us_call / S, 3),
-        "roofline": {"bound": "hbm", "kernel": "k_pgateup (grouped gate/up GEMM + SiLU)",
-                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": int(gu_bytes),
-                     "launch_us": round(gu_us, 2), "traffic": None,
-                     "mfma_tflops": round(gu_flops / (gu_us * 1e-6) / 1e12, 1),
-                     "mfma_util": round(gu_flops / (gu_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
-        "down": {"bytes": int(dn_bytes), "us": round(dn_us, 2), "gbps": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1),
-                 "mfma_util": round(dn_flops / (dn_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
-        "phase_us": {"router+group": round(rt_us, 2), "gateup": round(gu_us, 2), "down": round(dn_us, 2),
-                     "combine": round(cb_us, 2)},
-        "cpu_baseline": None,
+        "roofline": rl,
+        "down": down,
+        "kernels": kernels_json(rows),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
     ctx.close()
 
 
-def cpu_baseline_latent(cfg, seed, x_tokens, budget_s, gpu_out=None):
+def cpu_baseline_prefill(cfg, seed, x, bytes_per_call):
+    """The whole 512-token call on the host (the oracle's SIMD tier, the reference's order: every
+    unique expert once over its tokens, the shared expert, the combine), experts generated first
+    (not timed). One call; its working set (every expert, 13.7 GB) is far past any cache, so warm
+    and cold coincide and one run is reported."""
+    from oracle import oracle as O
+    from oracle.workload import HostLayer
+    info = cpu_info()
+    O.set_threads(info["threads"])
+    host = HostLayer(cfg, seed)
+    S = x.shape[0]
+    t0 = time.perf_counter()
+    ids, _ = host.route(x)
+    host.ensure(ids)
+    gen_s = time.perf_counter() - t0
+    lay = host._layer()
+    t0 = time.perf_counter()
+    lay.forward(x, S, simd=True)
+    us = (time.perf_counter() - t0) * 1e6
+    log(f"[bench] cpu prefill: {us / 1e3:.0f} ms per call ({len(host.experts)} experts generated in {gen_s:.0f} s)")
+    return cpu_line(us, None, "us/call", bytes_per_call, info, "port",
+                    f"one {S}-token call of {cfg.name} ({len(host.experts)} unique experts + shared), "
+                    f"{simd_tier(O)} tier of the reference's matmul_mxfp4 restated in C, rows in parallel on "
+                    f"{info['threads']} threads")
+
+
+# ---- one expert (c0) and bare matrices (mm) ------------------------------------------------------
+def rotating_pool(ctx, cfg, n, seed):
+    """n C0-shaped experts in the pool of layer 0 (n x 26.7 MB, past the 256 MB Infinity Cache)."""
+    import rabbit_amd.workloads as W
+    H, I = cfg.hidden, cfg.inter
+    for e in range(n):
+        p = ctx.pool_alloc(0, e, cfg.kind, H, I, cfg.gs)
+        s = p.contents
+        for m, q in enumerate((s.gate, s.up, s.down)):
+            W._synth(ctx, cfg.kind, q.data, q.scale, q.rows, q.cols, W.tensor_seed(seed, e, m), cfg)
+    ctx.sync()
+
+
+def bench_c0(args, ctx, hip, cfg):
+    """C0: one MXFP4 SwiGLU expert FFN for one token (apply_single_expert, glm52/moe.rs:463), each
+    call on another of 96 resident experts (2.6 GB) so the weights stream from HBM."""
+    import torch
+    import rabbit_amd as R
+    import rabbit_amd.workloads as W
+    from oracle import oracle as O
+    from oracle.workload import host_expert
+    H, I = cfg.hidden, cfg.inter
+    NE = 96
+    rotating_pool(ctx, cfg, NE, args.seed)
+    slots = [ctx.pool_get(0, e) for e in range(NE)]
+    steps, warm = args.steps, args.warmup
+    ntok = steps + warm
+    x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
+    out_all = torch.zeros_like(x_all)
+    w1 = torch.ones(1, dtype=torch.float32, device="cuda")
+    # each call routes its one token to the slot it runs (ids = the slot's expert id)
+    ids_per = torch.tensor([slots[e].contents.eid for e in range(NE)], dtype=torch.int32, device="cuda")
+
+    def call(t):
+        s = slots[t % NE].contents
+        ctx.check(ctx.lib.rbt_apply_single_expert_d(ctx.h, C.byref(s), R._ptr(ids_per[t % NE:t % NE + 1]),
+                                                    R._ptr(w1), 1, 1, R._ptr(x_all[t]), H, I, 0,
+                                                    R._ptr(out_all[t])))
+
+    ctx._torch_sync()
+    for t in range(warm):
+        call(t)
+    ctx.sync()
+    G = max(1, min(args.graph_tokens, steps))
+    wall, ev_ms = graph_time(hip, ctx, call, warm, steps, G)
+    us = wall / steps * 1e6
+    out_all.zero_()
+    torch.cuda.synchronize()
+    tab = kernel_table(ctx, lambda: [call(t) for t in range(warm, ntok)])
+    rows = per_call(tab, steps)
+    per_gu = 2 * expert_matrix_bytes(cfg, I, H)
+    per_dn = expert_matrix_bytes(cfg, H, I)
+    rl = roofline(rows, "gateup", per_gu, "c0", note="gate+up weights of the one expert")
+    ex_bytes = per_gu + per_dn
+    gb = (ex_bytes + 2 * H * 4) / (us * 1e-6) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        info = cpu_info()
+        O.set_threads(info["threads"])
+        ev = Evictor()
+        warm_s = cold_s = 0.0
+        n = 0
+        outs = []
+        for t in range(warm, min(ntok, warm + 16)):
+            sl = host_expert(cfg, args.seed, t % NE)
+            xt = x_all[t].cpu().numpy().reshape(1, H)
+            o = np.zeros(H, np.float32)
+            t0 = time.perf_counter()
+            O.apply_single_expert(sl, np.array([[t % NE]], np.int32), np.ones((1, 1), np.float32), xt, H, I, o,
+                                  simd=True)
+            warm_s += time.perf_counter() - t0
+            ev()
+            o2 = np.zeros(H, np.float32)
+            t0 = time.perf_counter()
+            O.apply_single_expert(sl, np.array([[t % NE]], np.int32), np.ones((1, 1), np.float32), xt, H, I, o2,
+                                  simd=True)
+            cold_s += time.perf_counter() - t0
+            outs.append(o)
+            n += 1
+        cpu = cpu_line(warm_s / n * 1e6, cold_s / n * 1e6, "us/call", ex_bytes, info, "port",
+                       f"{n} calls of one C0 expert (gate, up, silu*up, down) for one token, {simd_tier(O)} tier "
+                       f"of the reference's matmul_mxfp4 restated in C on {info['threads']} threads")
+        g = out_all[warm:warm + n].cpu().numpy().astype(np.float64).ravel()
+        c = np.stack(outs).astype(np.float64).ravel()
+        cpu["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+    res = {
+        "metric": "Single-expert decode µs/call + HBM GB/s (% of 8 TB/s), MXFP4 (apply_single_expert, 1 token)",
+        "value": round(us, 3), "unit": "us/call", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": cfg.name, "hidden": H, "moe_inter": I, "weights": "mxfp4", "rotating_experts": NE,
+                   "graph_calls": G},
+        "roofline": rl,
+        "call": {"bytes_per_call": ex_bytes + 2 * H * 4, "gbps": round(gb, 1), "frac": round(gb / HBM_PEAK_GBPS, 4)},
+        "kernels": kernels_json(rows),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
+def bench_mm(args, ctx, hip):
+    """rbt_matmul_mxfp4_d (matmul_mxfp4, kernels.rs:233) for one token at the reference's own
+    micro-benchmark shapes (benches/kernels.rs:209-240,310-343: I = O = 4096, and K3's I = 3584,
+    O = 3072) and C0's three matrices. GPU: each call on another of enough matrices to pass the
+    256 MB Infinity Cache ("rotating"), and on one matrix over and over ("same": cache-resident).
+    CPU: the reference's AVX-512 tier restated, warm (same matrix) and cold (256 MiB evicted)."""
+    import torch
+    import rabbit_amd as R
+    from oracle import oracle as O
+    shapes = [("k3_3584x3072", 3584, 3072), ("ref_4096x4096", 4096, 4096), ("c0_gate_8192x2048", 8192, 2048),
+              ("c0_down_2048x8192", 2048, 8192)]
+    info = cpu_info()
+    O.set_threads(info["threads"])
+    ev = Evictor()
+    out = []
+    steps = max(16, args.steps)
+    for name, I, Ow in shapes:
+        nbytes = Ow * (I // 2 + I // 32)
+        nm = max(8, int(np.ceil(768e6 / nbytes)))
+        data = torch.empty(nm, Ow * I // 2, dtype=torch.uint8, device="cuda")
+        scale = torch.empty(nm, Ow * I // 32, dtype=torch.uint8, device="cuda")
+        for m in range(nm):
+            ctx.synth_mxfp4(data[m].data_ptr(), scale[m].data_ptr(), Ow, I, 77 + m)
+        x = torch.from_numpy(np.random.default_rng(3).standard_normal((steps, I)).astype(np.float32)).cuda()
+        y = torch.empty(steps, Ow, device="cuda")
+        ctx.sync()
+
+        def call_rot(t):
+            ctx.check(ctx.lib.rbt_matmul_mxfp4_d(ctx.h, R._ptr(y[t]), R._ptr(x[t]), R._ptr(data[t % nm]),
+                                                 R._ptr(scale[t % nm]), 1, I, Ow))
+
+        def call_same(t):
+            ctx.check(ctx.lib.rbt_matmul_mxfp4_d(ctx.h, R._ptr(y[t]), R._ptr(x[t]), R._ptr(data[0]),
+                                                 R._ptr(scale[0]), 1, I, Ow))
+
+        for t in range(4):
+            call_rot(t)
+        ctx.sync()
+        G = min(args.graph_tokens, steps)
+        w_rot, _ = graph_time(hip, ctx, call_rot, 0, steps, G)
+        w_same, _ = graph_time(hip, ctx, call_same, 0, steps, G)
+        us_rot, us_same = w_rot / steps * 1e6, w_same / steps * 1e6
+        tab = kernel_table(ctx, lambda: [call_rot(t) for t in range(steps)])
+        rows = per_call(tab, steps)
+        k = rows[0]
+        kgb = nbytes / (k[2] * 1e-6) / 1e9
+        # CPU: matrix 0 on the host, warm (repeated) and cold (evicted before each call)
+        hq = O.synth_mxfp4(Ow, I, 77)
+        xh = x[0].cpu().numpy()
+        reps = 20
+        O.matmul_mxfp4_tier(xh, hq.data, hq.scale, 1, I, Ow)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            O.matmul_mxfp4_tier(xh, hq.data, hq.scale, 1, I, Ow)
+        cw = (time.perf_counter() - t0) / reps * 1e6
+        cc = 0.0
+        for _ in range(reps):
+            ev()
+            t0 = time.perf_counter()
+            O.matmul_mxfp4_tier(xh, hq.data, hq.scale, 1, I, Ow)
+            cc += time.perf_counter() - t0
+        cc = cc / reps * 1e6
+        yh = O.matmul_mxfp4_scalar(xh, hq.data, hq.scale, 1, I, Ow)
+        ctx.check(ctx.lib.rbt_matmul_mxfp4_d(ctx.h, R._ptr(y[0]), R._ptr(x[0]), R._ptr(data[0]), R._ptr(scale[0]), 1,
+                                             I, Ow))
+        ctx.sync()
+        yg = y[0].cpu().numpy()
+        err = float(np.linalg.norm(yg.astype(np.float64) - yh) / np.linalg.norm(yh.astype(np.float64)))
+        out.append({"shape": name, "i": I, "o": Ow, "bytes": nbytes,
+                    "gpu_us_rotating": round(us_rot, 3), "gpu_us_same_matrix": round(us_same, 3),
+                    "kernel": k[0], "kernel_us": round(k[2], 3), "kernel_gbps": round(kgb, 1),
+                    "kernel_frac": round(kgb / HBM_PEAK_GBPS, 4),
+                    "cpu_us_warm": round(cw, 1), "cpu_us_cold": round(cc, 1),
+                    "cpu_gbps_warm": round(nbytes / (cw * 1e-6) / 1e9, 1), "rel_l2_vs_scalar": err})
+        log(f"[bench] mm {name}: gpu {us_rot:.2f} us rotating / {us_same:.2f} same, kernel {k[2]:.2f} us "
+            f"({kgb:.0f} GB/s); cpu {cw:.1f} warm / {cc:.1f} cold")
+        del data, scale
+        torch.cuda.empty_cache()
+    head = out[0]
+    res = {
+        "metric": "matmul_mxfp4 µs/call (1 token) at the reference's micro-benchmark shapes, HBM GB/s",
+        "value": head["gpu_us_rotating"], "unit": "us/call", "n_gpus": 1, "steps": steps, "warmup": 4,
+        "ms_per_step": round(head["gpu_us_rotating"] / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "matmul_mxfp4_i3584_o3072", "shapes": [s[0] for s in shapes]},
+        "roofline": {"bound": "hbm", "kernel": head["kernel"], "achieved": head["kernel_gbps"], "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": head["kernel_frac"], "bytes_per_launch": head["bytes"],
+                     "launch_us": head["kernel_us"], "traffic": None},
+        "shapes": out,
+        "cpu_baseline": {"value": head["cpu_us_warm"], "unit": "us/call", "cores": info["threads"], "kind": "port",
+                         "cold": head["cpu_us_cold"],
+                         "sample": f"{reps} calls per shape on one matrix, the reference's {simd_tier(O)} tier "
+                                   f"restated in C, rows in parallel on {info['threads']} threads; cold = 256 MiB "
+                                   f"written before each call",
+                         "cpu": info},
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
+# ---- K3 latent MoE (k3l) and the sublayer (c1s) -------------------------------------------------
+def cpu_baseline_latent(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token):
     """The oracle's SIMD tier on the latent workload (router, projections, routed experts, norm),
     experts regenerated on the host first (not timed)."""
     from oracle import oracle as O
     from oracle.workload import HostLatentLayer
-    threads = physical_cores()
-    O.set_threads(threads)
-    tier = "avx512" if O.lib().orc_cpu_has_avx512() else ("avx2" if O.lib().orc_cpu_has_avx2() else "scalar")
+    info = cpu_info()
+    O.set_threads(info["threads"])
     host = HostLatentLayer(cfg, seed)
-    done, t_total, outs = 0, 0.0, []
+    ev = Evictor()
+    warm, cold, outs, done = 0.0, 0.0, [], 0
     for t in range(x_tokens.shape[0]):
         xt = x_tokens[t:t + 1]
         ids, _ = host.route(xt)
         host.ensure(ids)
+        lay = host._layer()
+
+        def run():
+            return lay.latent(xt, 1, host.mh, host.down, host.up, norm=host.norm, eps=1e-5, act=host.act, simd=True)
+
         t0 = time.perf_counter()
-        out, _, _ = host._layer().latent(xt, 1, host.mh, host.down, host.up, norm=host.norm, eps=1e-5,
-                                         act=host.act, simd=True)
-        t_total += time.perf_counter() - t0
+        out, _, _ = run()
+        warm += time.perf_counter() - t0
+        ev()
+        t0 = time.perf_counter()
+        run()
+        cold += time.perf_counter() - t0
         outs.append(out)
         done += 1
-        if t_total >= budget_s and done >= 3:
+        if warm + cold >= budget_s and done >= 3:
             break
         if len(host.experts) > 160:
             host.experts.clear()
-    us = t_total / done * 1e6
-    res = {"value": round(us, 1), "unit": "us/token", "cores": threads, "kind": "port",
-           "sample": f"{done} tokens of {cfg.name} (router + down projection + {cfg.topk} routed experts + norm + "
-                     f"up projection), {tier} tier of the reference's matmul kernels restated in C, rows in "
-                     f"parallel on {threads} threads; {cpu_model()}"}
-    if gpu_out is not None:
-        g = gpu_out[:done].astype(np.float64).ravel()
-        c = np.concatenate(outs).astype(np.float64).ravel()
-        res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+    res = cpu_line(warm / done * 1e6, cold / done * 1e6, "us/token", bytes_per_token, info, "port",
+                   f"{done} tokens of {cfg.name} (router + down projection + {cfg.topk} routed experts + norm + "
+                   f"up projection), {simd_tier(O)} tier of the reference's matmul kernels restated in C, rows in "
+                   f"parallel on {info['threads']} threads")
+    g = gpu_out[:done].astype(np.float64).ravel()
+    c = np.concatenate(outs).astype(np.float64).ravel()
+    res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
     return res
 
 
 def bench_latent(args, ctx, hip, cfg):
-    """K3's latent MoE, one token per call (rbt_latent_moe_d), timed as HIP-graph replays like the
-    decode line. value = us per token; the effective rate counts the router matrix, both
-    projections and the routed experts' bytes once per token."""
+    """K3's latent MoE, one token per call (rbt_latent_moe_d), graph-replayed like the decode line.
+    value = us per token; the call rate counts the router matrix, both projections and the routed
+    experts' bytes once per token."""
     import torch
     import rabbit_amd.workloads as W
     t0 = time.perf_counter()
@@ -267,102 +755,56 @@ def bench_latent(args, ctx, hip, cfg):
     pool_gb = ctx.pool_resident_bytes() / 1e9
     log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
     H, MH, I, k, E = cfg.hidden, cfg.extra["moe_hidden"], cfg.inter, cfg.topk, cfg.n_experts
-    G = max(1, min(args.graph_tokens, args.steps))
-    reps = (args.steps + G - 1) // G
-    steps = reps * G
-    ntok = steps + args.warmup
+    steps, warm = args.steps, args.warmup
+    ntok = steps + warm
     x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
     out_all = torch.empty_like(x_all)
-    rows = [x_all[t] for t in range(ntok)]
+    rows_x = [x_all[t] for t in range(ntok)]
     outs = [out_all[t] for t in range(ntok)]
 
     def call(t):
-        ctx.latent_moe(0, MH, lat["down"], lat["up"], rows[t], 1, outs[t], norm=lat["norm"], eps=1e-5,
+        ctx.latent_moe(0, MH, lat["down"], lat["up"], rows_x[t], 1, outs[t], norm=lat["norm"], eps=1e-5,
                        activation=lat["act"], sync=False)
 
-    for t in range(args.warmup):
+    for t in range(warm):
         call(t)
     ctx.sync()
-    graphs = []
-    for r in range(reps):
-        g = Graph(hip, ctx.stream)
-        g.begin()
-        for j in range(G):
-            call(args.warmup + r * G + j)
-        g.end()
-        graphs.append(g)
-    torch.cuda.synchronize()
-    ctx.sync()
-    t0 = time.perf_counter()
-    for g in graphs:
-        g.launch()
-    ctx.sync()
-    wall = time.perf_counter() - t0
+    G = max(1, min(args.graph_tokens, steps))
+    wall, _ = graph_time(hip, ctx, call, warm, steps, G)
     us_per_token = wall / steps * 1e6
-    for g in graphs:
-        g.destroy()
-    t1 = time.perf_counter()
-    for t in range(args.warmup, ntok):
-        call(t)
-    ctx.sync()
-    eager_us = (time.perf_counter() - t1) / steps * 1e6
-    log(f"[bench] timed {steps} tokens: {us_per_token:.2f} us/token (eager {eager_us:.2f})")
-
+    tab = kernel_table(ctx, lambda: [call(t) for t in range(warm, ntok)])
+    rows = per_call(tab, steps)
+    log(f"[bench] timed {steps} tokens: {us_per_token:.2f} us/token")
     gs = cfg.extra["proj_gs"]
     per_exp = 2 * I * (MH // 2 + MH // 32) + MH * (I // 2 + I // 32)
     proj = 2 * (MH * H // 2 + MH * (H // gs) * 4)
     router = E * H * 4
     tok_bytes = k * per_exp + proj + router
     gbps = tok_bytes / (us_per_token * 1e-6) / 1e9
+    rl = roofline(rows, "gateup", k * 2 * I * (MH // 2 + MH // 32), "k3l",
+                  note=f"gate+up weights of the {k} routed experts")
     cpu = None
     if not args.no_cpu:
-        n_cpu = min(8, ntok)
-        cpu = cpu_baseline_latent(cfg, args.seed, x_all[:n_cpu].cpu().numpy(), args.cpu_budget,
-                                  gpu_out=out_all[:n_cpu].cpu().numpy())
+        n_cpu = min(8, steps)
+        cpu = cpu_baseline_latent(cfg, args.seed, x_all[warm:warm + n_cpu].cpu().numpy(), args.cpu_budget,
+                                  out_all[warm:warm + n_cpu].cpu().numpy(), tok_bytes)
     res = {
         "metric": "K3 latent-MoE decode us/token + effective HBM GB/s over the call (% of 8 TB/s), MXFP4 experts",
-        "value": round(us_per_token, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "value": round(us_per_token, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(us_per_token / 1e3, 6), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": cfg.name, "hidden": H, "moe_hidden": MH, "moe_inter": I, "n_experts": E, "topk": k,
                    "activation": "situ(4, 25)", "latent_norm": cfg.extra["latent_norm"],
                    "projections": f"int4-grouped gs{gs}", "tokens_per_step": 1,
                    "resident_pool_gb": round(pool_gb, 2), "graph_tokens": G},
-        "call_rate": {"bytes_per_token": tok_bytes, "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                      "note": "routed experts + router + both projections over the whole call; per-kernel "
-                              "durations are in the rocprofv3 summary"},
-        "eager_us_per_token": round(eager_us, 2),
+        "roofline": rl,
+        "call": {"bytes_per_token": tok_bytes, "gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                 "note": "routed experts + router + both projections over the whole call"},
+        "kernels": kernels_json(rows),
         "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
     ctx.close()
-
-
-def graph_us_per_call(hip, ctx, call, ntok, warmup, G):
-    """Warms up, then times graph replays of G consecutive calls call(t) over tokens warmup..ntok."""
-    import torch
-    for t in range(warmup):
-        call(t)
-    ctx.sync()
-    steps = ntok - warmup
-    graphs = []
-    for r in range(steps // G):
-        g = Graph(hip, ctx.stream)
-        g.begin()
-        for j in range(G):
-            call(warmup + r * G + j)
-        g.end()
-        graphs.append(g)
-    torch.cuda.synchronize()
-    ctx.sync()
-    t0 = time.perf_counter()
-    for g in graphs:
-        g.launch()
-    ctx.sync()
-    us = (time.perf_counter() - t0) / steps * 1e6
-    for g in graphs:
-        g.destroy()
-    return us
 
 
 def bench_sublayer(args, ctx, hip, cfg):
@@ -373,23 +815,32 @@ def bench_sublayer(args, ctx, hip, cfg):
     import rabbit_amd.workloads as W
     W.build_layer(ctx, cfg, layer=0, seed=args.seed)
     pool_gb = ctx.pool_resident_bytes() / 1e9
-    G = max(1, min(args.graph_tokens, args.steps))
-    steps = ((args.steps + G - 1) // G) * G
-    ntok = steps + args.warmup
+    steps, warm = args.steps, args.warmup
+    ntok = steps + warm
     H = cfg.hidden
     x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
     out_all = torch.empty_like(x_all)
     ln = torch.from_numpy((np.random.default_rng(args.seed + 9).standard_normal(H) * 0.1).astype(np.float32)).cuda()
-    rows = [x_all[t] for t in range(ntok)]
+    rows_x = [x_all[t] for t in range(ntok)]
     outs = [out_all[t] for t in range(ntok)]
-    layer_us = graph_us_per_call(hip, ctx, lambda t: ctx.moe_forward(0, rows[t], 1, outs[t], sync=False), ntok,
-                                 args.warmup, G)
-    sub_us = graph_us_per_call(hip, ctx, lambda t: ctx.moe_sublayer(0, rows[t], 1, ln, 1e-6, sync=False), ntok,
-                               args.warmup, G)
+    G = max(1, min(args.graph_tokens, steps))
+
+    def layer_call(t):
+        ctx.moe_forward(0, rows_x[t], 1, outs[t], sync=False)
+
+    def sub_call(t):
+        ctx.moe_sublayer(0, rows_x[t], 1, ln, 1e-6, sync=False)
+
+    for t in range(warm):
+        layer_call(t)
+    ctx.sync()
+    lw, _ = graph_time(hip, ctx, layer_call, warm, steps, G)
+    sw, _ = graph_time(hip, ctx, sub_call, warm, steps, G)
+    layer_us, sub_us = lw / steps * 1e6, sw / steps * 1e6
     log(f"[bench] sublayer {sub_us:.2f} us/token, layer alone {layer_us:.2f}")
     res = {
         "metric": "MoE sublayer decode us/token (rmsnorm_1p + MoE layer + residual add), MXFP4",
-        "value": round(sub_us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "value": round(sub_us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(sub_us / 1e3, 6), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": cfg.name + "_sublayer", "hidden": H, "moe_inter": cfg.inter, "n_experts": cfg.n_experts,
@@ -408,7 +859,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c1")
+    ap.add_argument("--config", default="c1", choices=["c0", "c1", "c2", "c3", "c4", "mm", "k3l", "c1s"])
     ap.add_argument("--graph-tokens", type=int, default=64)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
@@ -427,18 +878,6 @@ def main():
     import rabbit_amd.workloads as W
 
     torch.zeros(1, device="cuda")
-    if args.config == "c1s":
-        return bench_sublayer(args, R.Context(0), hip_runtime(), W.CONFIGS["c1"])
-    cfg = W.CONFIGS[args.config]
-    if args.config == "k3l":
-        ctx = R.Context(0)
-        return bench_latent(args, ctx, hip_runtime(), cfg)
-    if cfg.tokens != 1 and args.config != "c4":
-        raise SystemExit(f"bench.py times batch-1 decode (c1) or the 512-token prefill (c4); {args.config} is a "
-                         "parity-test configuration")
-    ctx = R.Context(0)
-    hip = hip_runtime()
-
     if args.calibrate_copy:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
@@ -447,138 +886,24 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-
+    ctx = R.Context(0)
+    hip = hip_runtime()
+    if args.config == "c1s":
+        return bench_sublayer(args, ctx, hip, W.CONFIGS["c1"])
+    if args.config == "mm":
+        return bench_mm(args, ctx, hip)
+    cfg = W.CONFIGS[args.config]
+    if args.config == "k3l":
+        return bench_latent(args, ctx, hip, cfg)
+    if args.config == "c0":
+        return bench_c0(args, ctx, hip, cfg)
     t0 = time.perf_counter()
     W.build_layer(ctx, cfg, layer=0, seed=args.seed)
     pool_gb = ctx.pool_resident_bytes() / 1e9
     log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
-    if cfg.tokens != 1:
-        return bench_prefill(args, ctx, cfg, pool_gb)
-
-    G = max(1, min(args.graph_tokens, args.steps))
-    reps = (args.steps + G - 1) // G
-    steps = reps * G
-    ntok = steps + args.warmup
-    x_all = torch.from_numpy(W.tokens(cfg, ntok, args.seed + 5)).cuda()
-    out_all = torch.empty_like(x_all)
-    H = cfg.hidden
-    rows = [x_all[t] for t in range(ntok)]
-    outs = [out_all[t] for t in range(ntok)]
-
-    # warmup (also sizes every scratch buffer, so capture allocates nothing)
-    for t in range(args.warmup):
-        ctx.moe_forward(0, rows[t], 1, outs[t], sync=False)
-    ctx.sync()
-
-    # --- pass 1: timed region, HIP-graph replay of G consecutive layer calls per launch ----------
-    graphs = []
-    for r in range(reps):
-        g = Graph(hip, ctx.stream)
-        g.begin()
-        for j in range(G):
-            t = args.warmup + r * G + j
-            ctx.moe_forward(0, rows[t], 1, outs[t], sync=False)
-        g.end()
-        graphs.append(g)
-    ext = ctx.torch_stream()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ctx.sync()
-    t0 = time.perf_counter()
-    ev0.record(ext)
-    for g in graphs:
-        g.launch()
-    ev1.record(ext)
-    ctx.sync()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ev_ms = ev0.elapsed_time(ev1)
-    us_per_token = wall / steps * 1e6
-    log(f"[bench] timed {steps} tokens: wall {wall * 1e3:.2f} ms ({us_per_token:.2f} us/token), "
-        f"events {ev_ms:.2f} ms")
-    for g in graphs:
-        g.destroy()
-
-    # --- pass 2: per-phase kernel durations (HIP events on the library's stream) ----------------
-    ctx.profile_read(reset=True)
-    ctx.profile_enable(True)
-    t1 = time.perf_counter()
-    for t in range(args.warmup, ntok):
-        ctx.moe_forward(0, rows[t], 1, outs[t], sync=False)
-    ctx.sync()
-    eager_us = (time.perf_counter() - t1) / steps * 1e6
-    prof = ctx.profile_read(reset=True)
-    ctx.profile_enable(False)
-    n = max(1, prof["calls"])
-    gu_us = prof["gateup_ms"] / n * 1e3
-    dn_us = prof["down_ms"] / n * 1e3
-    rt_us = prof["router_ms"] / n * 1e3
-    cb_us = prof["combine_ms"] / n * 1e3
-
-    nexp = cfg.topk + (1 if cfg.shared else 0)
-    per_gu = 2 * cfg.inter * (H // 2 + H // 32)  # gate + up bytes of one expert
-    per_dn = H * (cfg.inter // 2 + cfg.inter // 32)
-    # experts each kernel actually streamed per call (the shared expert's gate/up may run inside the
-    # router's selection launch, on the CUs it leaves idle)
-    gu_exp = prof["gateup_experts"] / n if prof["gateup_experts"] else nexp
-    dn_exp = prof["down_experts"] / n if prof["down_experts"] else nexp
-    gu_bytes = int(round(gu_exp * per_gu))
-    dn_bytes = int(round(dn_exp * per_dn))
-    gu_gbps = gu_bytes / (gu_us * 1e-6) / 1e9
-    # every expert's bytes over the time the layer spends in its expert kernels
-    ex_bytes = nexp * (per_gu + per_dn)
-    ex_gbps = ex_bytes / ((gu_us + dn_us) * 1e-6) / 1e9
-
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", f"traffic_{args.config}.json")
-    if os.path.exists(tf):
-        try:
-            t = json.load(open(tf))
-            # only a measurement of the kernel this build launches counts
-            traffic = t.get("gateup_bytes_per_launch") if t.get("kernel") == ROOFLINE_KERNEL else None
-        except (OSError, ValueError):
-            traffic = None
-
-    cpu = None
-    if not args.no_cpu:
-        n_cpu = min(64, ntok)
-        cpu = cpu_baseline(cfg, args.seed, x_all[:n_cpu].cpu().numpy(), args.cpu_budget,
-                           gpu_out=out_all[:n_cpu].cpu().numpy())
-
-    res = {
-        "metric": METRIC,
-        "value": round(us_per_token, 3),
-        "unit": "us/token",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(us_per_token / 1e3, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {"workload": cfg.name, "hidden": H, "moe_inter": cfg.inter, "n_experts": cfg.n_experts,
-                   "topk": cfg.topk, "shared_expert": cfg.shared, "weights": "mxfp4" if cfg.kind == R.QT_MXFP4
-                   else "int4-grouped", "tokens_per_step": 1, "resident_pool_gb": round(pool_gb, 2),
-                   "graph_tokens": G},
-        "roofline": {"bound": "hbm", "kernel": "k_xgateup1f (gate/up + SiLU, MFMA on fp4->bf16 weights, balanced over all CUs; settles deferred router decisions)",
-                     "achieved": round(gu_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gu_gbps / HBM_PEAK_GBPS, 4), "bytes_per_launch": gu_bytes,
-                     "launch_us": round(gu_us, 2), "traffic": traffic},
-        "expert_gemv": {"bytes_per_token": ex_bytes, "us": round(gu_us + dn_us, 2),
-                        "gbps": round(ex_gbps, 1), "frac": round(ex_gbps / HBM_PEAK_GBPS, 4),
-                        "experts": nexp, "gateup_kernel_experts": gu_exp, "down_kernel_experts": dn_exp,
-                        "note": "all experts' bytes over the gate/up + down kernel times; experts the gate/up "
-                                "kernel does not stream ran inside the router phase"},
-        "phase_us": {"router": round(rt_us, 2), "gateup": round(gu_us, 2), "down": round(dn_us, 2),
-                     "combine": round(cb_us, 2)},
-        "eager_us_per_token": round(eager_us, 2),
-        "router_exact_recomputes": int(prof["ambiguous"]),
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(res), flush=True)
-    ctx.close()
+    if args.config == "c4":
+        return bench_prefill(args, ctx, hip, cfg, pool_gb)
+    return bench_layer(args, ctx, hip, cfg, pool_gb)
 
 
 if __name__ == "__main__":

@@ -376,9 +376,11 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, lo
 // Gate/up and the activation in one pass, for rows of 2049..4096 columns (one token per pair, one
 // column part): a wave takes a contiguous run of (pair, r) items; for each it streams gate row r and
 // up row r of the pair's expert, reduces both as k_decode_gemv does (block_dots, the wave sum), and
-// lane 0 writes h[p, r] = act(g, u). The g and u values are the stacked kernel's, so h is the same
-// as k_decode_gemv (stacked) + k_swiglu; the gate|up scratch and one launch are saved. Two items in
-// flight per wave.
+// lane 0 writes h[p, r] = act(g, u). Below 4096 columns the g and u values are the stacked kernel's,
+// so h is bit-identical to k_decode_gemv (stacked) + k_swiglu; at exactly 4096 columns the stacked
+// kernel sums two column parts (g0 + g1) where this one reduces the whole row, so the two agree
+// only within the fp32 accumulation tolerance there. The gate|up scratch and one launch are saved.
+// Two items in flight per wave.
 template <int NB, bool I4G>
 __device__ __forceinline__ void frag_load_gu(DecodeFrag<NB, 2> &f, const RbtExpertDev &J, int row, int q, int nblk,
                                              unsigned rb) {

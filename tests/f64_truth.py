@@ -1,0 +1,112 @@
+"""fp64 truth of an MoE layer's output (test infrastructure).
+
+The reference's layer output is a function of fp32 inputs and exactly representable dequantized
+weights (quant.rs:325-339: e2m1 * 2^(b-127) is exact in fp32). Its own sequential fp32 sums
+(kernels.rs:247-267) carry a rounding error of their own; this module computes the same function
+with every product and sum in float64 (torch, on the GPU when there is one), for the routing the
+reference selected, so a test can tell whose error a device-vs-oracle difference is.
+
+  weights (qwen38/moe.rs:66-74):   w_j = exp(l_j - max) / sum_i exp(l_i - max) over the k winners
+  weights (glm52/moe.rs:231-241):  w_j = sigmoid(l_j), then / (sum + 1e-20) when norm_topk, * scale
+  expert (glm52/moe.rs:453-513):   y = down . (silu(gate . x) * (up . x))
+  layer (qwen38/generate.rs:262-351): sum_j w_j y_j + sigmoid(g . x) * y_shared   (Qwen, gated)
+                                      sum_j w_j y_j + y_shared                      (GLM / K3)
+
+Weight dequantization here is a vectorised restatement of row_f32; tests/test_f64_truth.py pins it
+bit for bit (after rounding to fp32) against the oracle's row_f32 over every code and scale byte.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+E2M1 = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+QT_I4_GROUPED, QT_MXFP4 = 1, 2
+FAMILY_QWEN38 = 0
+
+
+def _dev():
+    import torch
+    return torch.device("cuda" if torch.cuda.is_available() else "cpu")
+
+
+def dense64(q, dev=None):
+    """[rows, cols] float64 of an oracle QT (host arrays): the dequantized weights, exactly."""
+    import torch
+    dev = dev or _dev()
+    R, Cn = q.rows, q.cols
+    data = torch.from_numpy(np.ascontiguousarray(q.data)).to(dev).reshape(R, -1)
+    codes = torch.stack([data & 15, data >> 4], dim=-1).reshape(R, -1)[:, :Cn].long()
+    if q.kind == QT_MXFP4:
+        mag = torch.tensor(E2M1, dtype=torch.float64, device=dev)[codes & 7]
+        val = torch.where((codes & 8) != 0, -mag, mag)  # code 8 is -0.0 (quant.rs:353-356)
+        b = torch.from_numpy(np.ascontiguousarray(q.scale)).to(dev).reshape(R, -1).double()
+        sc = torch.where(b == 0, torch.full_like(b, 2.0 ** -127), torch.exp2(b - 127.0))  # quant.rs:391-396
+        sc = torch.where(b == 255, torch.full_like(b, float("inf")), sc)
+        return val * sc.repeat_interleave(32, dim=1)[:, :Cn]
+    if q.kind == QT_I4_GROUPED:
+        gs = q.group_size
+        sc = torch.from_numpy(np.ascontiguousarray(q.scale)).to(dev).reshape(R, -1).double()
+        return (codes - 8).double() * sc.repeat_interleave(gs, dim=1)[:, :Cn]
+    raise ValueError(f"kind {q.kind}")
+
+
+def _silu(v):
+    return v / (1.0 + (-v).exp())
+
+
+def expert64(slot, x64, dev=None):
+    """down . (silu(gate . x) * (up . x)) in float64 for one expert slot (separate gate/up)."""
+    g = dense64(slot.gate, dev) @ x64
+    u = dense64(slot.up, dev) @ x64
+    return dense64(slot.down, dev) @ (_silu(g) * u)
+
+
+def layer64(host, x, ids):
+    """fp64 output [S, hidden] of a HostLayer (oracle/workload.py) for tokens x [S, hidden] and the
+    reference's ids [S, k]. Experts are generated on demand by the host layer."""
+    import torch
+    dev = _dev()
+    cfg = host.cfg
+    host.ensure(ids)
+    S = x.shape[0]
+    X = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev).double()
+    R = torch.from_numpy(np.ascontiguousarray(host.router, np.float32)).to(dev).double().reshape(cfg.n_experts, -1)
+    lb = None if host.logit_bias is None else torch.from_numpy(host.logit_bias).to(dev).double()
+    out = torch.zeros(S, cfg.hidden, dtype=torch.float64, device=dev)
+    for t in range(S):
+        sel = [int(e) for e in ids[t] if e >= 0]
+        lg = R[sel] @ X[t]
+        if lb is not None:
+            lg = lg + lb[sel]
+        if cfg.family == FAMILY_QWEN38:
+            w = (lg - lg.max()).exp()
+            w = w / w.sum()
+        else:
+            w = 1.0 / (1.0 + (-lg).exp())
+            w = w / (w.sum() + 1e-20)
+        for j, e in enumerate(sel):
+            out[t] += w[j] * expert64(host.experts[e], X[t], dev)
+        if host.shared is not None:
+            ys = expert64(host.shared, X[t], dev)
+            if host.gate is not None:
+                gv = torch.from_numpy(host.gate).to(dev).double() @ X[t]
+                ys = ys / (1.0 + (-gv).exp())
+            out[t] += ys
+    return out.cpu().numpy()
+
+
+def rel_l2(a, b) -> float:
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    den = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
+
+
+def check_token(gpu, oracle, truth, rtol=1e-5):
+    """The per-token parity rule: the device output is within rtol relative L2 of the reference's
+    (the oracle's sequential-fp32 result); where it is not, the reference itself must be the one
+    off: the device's error against the fp64 truth no larger than the reference's. Returns
+    (device vs oracle, device vs truth, oracle vs truth, passed)."""
+    d = rel_l2(gpu, oracle)
+    eg, eo = rel_l2(gpu, truth), rel_l2(oracle, truth)
+    return d, eg, eo, (d < rtol) or (eg <= eo)

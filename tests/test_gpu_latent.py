@@ -162,6 +162,23 @@ def test_latent_moe_matches_oracle(ctx, orc, proj_kind, S):
     assert rel_l2(situ, normed) > 1e-3
 
 
+# moe_hidden 6144 and 8192: the norm inside the up projection at its widest variants (each wave
+# holds 3 or 4 KB-blocks of the summed row per lane beside the weight fragments)
+@pytest.mark.parametrize("proj_kind", ["mxfp4", "i4g"])
+@pytest.mark.parametrize("MH", [6144, 8192])
+@pytest.mark.parametrize("S", [1, 3])
+def test_latent_moe_wide_norm(ctx, orc, proj_kind, MH, S):
+    import rabbit_amd as R
+    H, I, E, k = 512, 64, 16, 4
+    layer = 70 + (MH == 8192) * 4 + (proj_kind == "i4g") * 2 + (S == 3)
+    L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 8000 + layer, proj_kind, 1.0)
+    x = normal((S, H), layer, 1.0)
+    norm = np.abs(normal(MH, layer + 1, 1.0)) + np.float32(0.5)
+    plain = _run_latent(ctx, R, layer, L, dq, uq, x, S, MH, None, None, None)
+    normed = _run_latent(ctx, R, layer, L, dq, uq, x, S, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
+    assert rel_l2(plain, normed) > 1e-2
+
+
 @pytest.mark.parametrize("misalign", [False, True])
 def test_latent_moe_batch_exact_logits(ctx, orc, misalign):
     # 64 tokens: the router's logits are the reference's sequential folds themselves; a router that
