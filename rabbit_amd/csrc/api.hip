@@ -83,7 +83,7 @@ enum ScratchSlot {
   SC_RREC,
   SC_DJOB,
   SC_DSLOT,
-  SC_D1,
+
   SC_NRM,   // sublayer: the normalised rows
   SC_SUB,   // sublayer: the MoE output before the residual add
   SC_PLN,   // sublayer (host call): post_ln staged
@@ -135,9 +135,8 @@ struct rbt_ctx : rbt::Ctx {
   size_t arena_off[SC_N] = {}, arena_sz[SC_N] = {};
   std::map<uint64_t, PoolEntry> pool;
   std::map<uint32_t, Layer> layers;
-  int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts
+  int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts, [4] gate/up pairs
   int h_flags[8] = {};
-  unsigned *d_sync = nullptr;  // device: epoch and flags of the one-launch router
   // profiling: one row of 5 events per recorded moe_forward_d call
   bool prof = false;
   std::vector<hipEvent_t> ev_free;
@@ -178,7 +177,7 @@ bool kernel_events(const Ctx &base, const void *fn, hipEvent_t *start, hipEvent_
 
 namespace {
 
-constexpr int FLAG_ERR = 0, FLAG_AMB = 1, FLAG_UNIQ = 2, FLAG_NR = 3, FLAG_SYNC = 4, FLAG_N = 8;
+constexpr int FLAG_ERR = 0, FLAG_AMB = 1, FLAG_UNIQ = 2, FLAG_NR = 3, FLAG_GUP = 4, FLAG_N = 8;
 
 int fail(rbt_ctx *c, int code, const char *fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(rbt_ctx *c, int code, const char *fmt, ...) {
@@ -323,12 +322,6 @@ void slot_dims(const rbt_expert_slot *s, size_t *d, size_t *i) {
 int sync_and_check(rbt_ctx *c) {
   HIP_OK(c, hipStreamSynchronize(c->stream));
   HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
-  if (c->h_flags[FLAG_SYNC]) {
-    // a cross-workgroup wait timed out: clear its flag and the sync area for the next call
-    HIP_OK(c, hipMemset(c->d_flags + FLAG_SYNC, 0, sizeof(int)));
-    HIP_OK(c, hipMemset(c->d_sync, 0, rbt::router1_sync_bytes()));
-    return fail(c, RBT_E_HIP, "a cross-workgroup wait on the device timed out");
-  }
   if (c->h_flags[FLAG_ERR]) {
     HIP_OK(c, hipMemset(c->d_flags, 0, sizeof(int)));
     return fail(c, RBT_E_NOT_RESIDENT, "a routed expert is not resident in the pool");
@@ -763,21 +756,21 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool sh_in_select = gu1 && D.has_shared && grp_in_select;
   rbt::SharedGateUp sgu{L.d_shared, x, H, I, nullptr};
   const float *sgate = gated ? D.shared_gate : nullptr;
-  const bool r1 = grp_in_select && rbt::router1_ok(ra, c->num_cu, sh_in_select ? &sgu : nullptr) &&
-                  (uintptr_t)(sgate ? sgate : x) % 16 == 0;
-  // One token on the matrix cores: the selection also writes the down launch's compact job list;
-  // with the one-launch router, a decision that needs exact folds is deferred to the gate/up
-  // launch, the routed pairs then taking up to k + D1_KX slots and the shared expert the one after.
+  // One token on the matrix cores: the down launch takes a compact job list (the winners in rank
+  // order, then the shared expert) and fuses the ordered combine.
   const int kk = std::min(k, E);
   const bool dn1 = gu1 && grp_in_select && rbt::xdown1_ok(kk + (D.has_shared ? 1 : 0), (size_t)I);
+  // ... and with the three-launch decode, the router launch only computes the logits (and streams
+  // the shared expert's gate/up) and every gate/up workgroup selects for itself; a decision that
+  // needs exact folds takes up to k + D1_KX routed slots, the shared expert the one after.
+  const bool r1 = dn1 && rbt::router1_ok(ra, c->num_cu, sh_in_select ? &sgu : nullptr) &&
+                  (uintptr_t)(sgate ? sgate : x) % 16 == 0;
   float *dst = out;
   if (accumulate && !dn1) RBT_TRY(scratch_t(c, SC_SUB, (size_t)S * H, &dst));
-  const bool defer = r1 && dn1;
-  const int sh_slot = defer ? k + rbt::D1_KX : k;
+  const int sh_slot = r1 ? k + rbt::D1_KX : k;
   sgu.hp = reinterpret_cast<__bf16 *>(h) + (size_t)sh_slot * 3 * I;
   RbtExpertDev *djob = nullptr;
   int *dslot = nullptr;
-  rbt::D1Task *d1 = nullptr;
   if (dn1) {
     RBT_TRY(scratch_t(c, SC_DJOB, (size_t)(kk + 1), &djob));
     RBT_TRY(scratch_t(c, SC_DSLOT, (size_t)(kk + 1), &dslot));
@@ -785,16 +778,11 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     ga.down_slot = dslot;
     ga.shared_slot = sh_slot;
   }
-  if (defer) {
-    RBT_TRY(scratch_t(c, SC_D1, 1, &d1));
-    ga.d1 = d1;
-  }
+  float *rec = nullptr;
   if (r1) {
-    // one token: logits, selection and the shared expert's gate/up in one launch
-    float *rec;
+    // one token: router logits, key records and the shared gate
     RBT_TRY(scratch_t(c, SC_RREC, (size_t)E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
-    HIP_OK(c, rbt::launch_router1(*c, ra, sgate, mid, bnd, ids, wts, shs, dflags + FLAG_AMB, &ga,
-                                  sh_in_select ? &sgu : nullptr, c->d_sync, dflags + FLAG_SYNC, rec));
+    HIP_OK(c, rbt::launch_router1(*c, ra, sgate, mid, bnd, shs, rec));
   } else {
     if (rbt::router_exact_ok(S, H) && ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0) {
       // batches: the reference's sequential fp32 logits themselves, then point intervals
@@ -828,9 +816,11 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     if (c->prof) c->t_start = ev[2], c->t_stop = ev[3];
     // every wave of the balanced grid has work; the shared pair is done when it ran in selection;
     // a deferred router decision is settled by the gate/up launch's extra workgroup
-    const hipError_t e2 = defer ? rbt::launch_xgateup1_d1(*c, pjob, d1, x, H, I, hp, ra, ga, ids, wts, dflags + FLAG_AMB)
-                          : gu1 ? rbt::launch_xgateup1(*c, pjob, sh_in_select ? k : npairs, x, H, I, hp)
-                                : rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp);
+    const hipError_t e2 =
+        r1    ? rbt::launch_xgateup1s(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, dflags + FLAG_GUP, I, hp,
+                                      D.has_shared != 0)
+        : gu1 ? rbt::launch_xgateup1(*c, pjob, sh_in_select ? k : npairs, x, H, I, hp)
+              : rbt::launch_xgateup(*c, pjob, ptok, npairs, x, (long)H, H, I, hp);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e2);
     if (c->prof) c->t_start = ev[4], c->t_stop = ev[5];
@@ -863,9 +853,10 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   if (c->prof) {
     HIP_OK(c, hipEventRecord(ev[6], c->stream));
     c->ev_rows.push_back(ev);
-    // one-token decode: the experts each phase streamed (prefill: 0, unknown on the host)
+    // one-token decode: the experts each phase streamed (the three-launch decode counts its gate/up
+    // pairs on the device; prefill: 0, unknown on the host)
     const uint64_t ne = S == 1 ? (uint64_t)npairs : 0;
-    c->ev_experts.push_back({S == 1 ? ne - (sh_in_select ? 1 : 0) : 0, ne});
+    c->ev_experts.push_back({S == 1 && !r1 ? ne - (sh_in_select ? 1 : 0) : 0, ne});
   }
   if (dst != out) HIP_OK(c, rbt::launch_add_rows(*c, out, dst, (size_t)S * H));
   if (ids_out)
@@ -1059,13 +1050,10 @@ int rbt_init(rbt_ctx **out, int device) {
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) what = "hipStreamCreateWithFlags";
   else if ((e = hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMalloc";
   else if ((e = hipMemset(c->d_flags, 0, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMemset";
-  else if ((e = hipMalloc((void **)&c->d_sync, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMalloc";
-  else if ((e = hipMemset(c->d_sync, 0, rbt::router1_sync_bytes())) != hipSuccess) what = "hipMemset";
   // the allocation-free entry point's scratch on this device (the device is current)
   if (!what) c->noalloc = noalloc_base(device, &c->noalloc_err);
   if (what) {
     int rc = init_fail(RBT_E_HIP, what, e);
-    if (c->d_sync) (void)hipFree(c->d_sync);
     if (c->d_flags) (void)hipFree(c->d_flags);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
@@ -1085,7 +1073,6 @@ void rbt_destroy(rbt_ctx *c) {
   for (int i = 0; i < SC_N; i++)
     if (c->scratch[i]) (void)hipFree(c->scratch[i]);
   if (c->d_flags) (void)hipFree(c->d_flags);
-  if (c->d_sync) (void)hipFree(c->d_sync);
   for (auto &r : c->ev_rows)
     for (auto e : r) c->ev_free.push_back(e);
   for (auto &r : c->krecs) {
@@ -1674,9 +1661,11 @@ int rbt_profile_read(rbt_ctx *c, rbt_profile *out, int32_t reset) {
   HIP_OK(c, hipMemcpy(c->h_flags, c->d_flags, FLAG_N * sizeof(int), hipMemcpyDeviceToHost));
   c->acc.ambiguous = (uint64_t)c->h_flags[FLAG_AMB];
   *out = c->acc;
+  out->gateup_experts += (uint64_t)(uint32_t)c->h_flags[FLAG_GUP];  // counted on the device
   if (reset) {
     c->acc = rbt_profile{};
     HIP_OK(c, hipMemset(c->d_flags + FLAG_AMB, 0, sizeof(int)));
+    HIP_OK(c, hipMemset(c->d_flags + FLAG_GUP, 0, sizeof(int)));
   }
   return RBT_OK;
 }

@@ -154,20 +154,18 @@ hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, cons
 bool router_exact_ok(int S, int H);
 hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H, const float *W, int E,
                                       const float *sgate, float *logits);
-// Expert job-table outputs the selection kernel writes itself for a single token (S == 1).
-// One-token decode (router launch -> gate/up launch -> down launch). The router launch writes the
-// routed pairs at slots 0 .. nr-1 of the pair job table (the winners in rank order) and the shared
-// expert at slot `shared_slot`, and the down launch's compact job list: the winners in slot order,
-// then the shared expert, with the pair slot of each (where its h is). When it cannot certify the
-// top-k without the reference's sequential fp32 folds, it defers the decision instead: the routed
-// pairs are the certain winners in midpoint order followed by the undecided candidates, and the
-// gate/up launch's extra workgroup runs the folds while the pairs stream, then writes ids,
-// weights and the down job list.
+// One-token decode on the matrix cores (router launch -> gate/up launch -> down launch). The router
+// launch writes mid / bnd and one key record per expert and streams the shared expert's gate/up;
+// every workgroup of the gate/up launch then selects the top-k from the key records itself. When
+// the certified intervals leave the decision open, the routed pairs are the certain winners in
+// midpoint order followed by the undecided candidates (up to D1_KX beyond top-k), and the gate/up
+// launch's extra workgroup folds the undecided logits exactly while the pairs stream, then writes
+// ids, weights, tok_pair / tok_w and the down launch's job list.
 constexpr int D1_KX = 4;   // routed pair slots beyond top-k for undecided candidates
 constexpr int D1_NC = 32;  // most routed pairs a deferred decision carries
 struct D1Task {
   int nr;       // routed pairs of the call: slots 0 .. nr-1
-  int pending;  // 1: the gate/up launch decides ids, weights and the down job list
+  int pending;  // 1: the decision waits for exact folds
   int pad[2];
   int id[D1_NC];       // expert of slot c
   uint32_t ku[D1_NC];  // its midpoint order key
@@ -182,14 +180,13 @@ struct GroupArgs {
   float *tok_w;
   int *err;
   // one token (all optional): the down launch's job list and pair slots, the shared expert's slot
-  // (default: k), and the deferred-decision task
+  // (default: k)
   RbtExpertDev *down_job = nullptr;
   int *down_slot = nullptr;
   int shared_slot = -1;
-  D1Task *d1 = nullptr;
 };
-// The shared expert's gate/up for a one-token call (balanced body of xgemm), run by the selection
-// launch on the CUs its one selecting workgroup leaves idle. hp: the shared pair's output parts.
+// The shared expert's gate/up for a one-token call (balanced body of xgemm), run by a router launch
+// on the CUs its selection (or its rows) leave free. hp: the shared pair's output parts.
 struct SharedGateUp {
   const RbtExpertDev *dev;
   const float *x;
@@ -199,22 +196,19 @@ struct SharedGateUp {
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr,
                                 const SharedGateUp *sgu = nullptr);
-// One token: logits, selection and the shared expert's gate/up in one launch (num_cu workgroups; rec
-// holds E * ROUTER1_REC_BYTES of scratch
-// that synchronise through `sync`, router1_sync_bytes() of device memory that must hold zeros
-// before the first call and is left consistent by every normal call; a wait that times out sets
-// *err, and the caller must zero `sync` again before the next call).
-size_t router1_sync_bytes();
+// Router launch of the one-token decode (no cross-workgroup waits): mid / bnd of every router row,
+// sh_scale (the shared gate's sigmoid, or 1) and rec (E * ROUTER1_REC_BYTES).
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                          int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs *grp,
-                          const SharedGateUp *sgu, unsigned *sync, int *err, void *rec);
-// One token after launch_router1 with grp->d1: the gate/up of the published routed pairs on num_cu
-// workgroups, plus one workgroup that settles a deferred decision (exact folds of the flagged
-// logits, then ids, weights, tok_pair / tok_w and the down job list).
-hipError_t launch_xgateup1_d1(const Ctx &c, const RbtExpertDev *jobs, const D1Task *T, const float *x, int K, int I,
-                              __bf16 *hp, const RouterArgs &a, const GroupArgs &grp, int32_t *ids, float *wts,
-                              int *stats);
+                          float *sh_scale, void *rec);
+// Gate/up launch of the one-token decode (num_cu workgroups): the selection from rec in every
+// workgroup, the gate/up of the nr routed pairs (slots 0..nr-1, nr <= k + D1_KX) and, with
+// has_shared, of grp.shared_dev at slot nr, into hp (pair slot c at hp + 3 I c), and the routing
+// outputs (ids, wts, grp's tok_pair / tok_w / down_job / down_slot, the shared expert last with its
+// slot). stats counts exact folds; gup (optional) the pairs streamed.
+hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,
+                            const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int *gup,
+                            int I, __bf16 *hp, bool has_shared);
 // Device bytes of the key records launch_router1 writes (per router row).
 constexpr size_t ROUTER1_REC_BYTES = 16;
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);

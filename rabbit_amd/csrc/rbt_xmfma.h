@@ -89,13 +89,45 @@ struct GuLds {
   __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
 };
 
+// The token's activation, thread t's float4 chunks t + 256 j (the first step of the body, issued
+// early by callers that have other work before the body proper).
 template <int NCH>
-__device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
-                                              const float *__restrict__ x, int I, __bf16 *__restrict__ hp, int wg,
-                                              int nwg) {
+__device__ __forceinline__ void xgateup1_load_x(const float *__restrict__ x, float4 (&xv)[NCH / 2]) {
+  const rbt_gf4 *s4 = (const rbt_gf4 *)x;
+#pragma unroll
+  for (int j = 0; j < NCH / 2; j++) xv[j] = s4[threadIdx.x + 256 * j];
+}
+
+// The activation's three bf16 parts (and the zero block) into the body's LDS; the body's first
+// barrier publishes them.
+template <int NCH>
+__device__ __forceinline__ void xgateup1_stage_x(GuLds &L, const float4 (&xv)[NCH / 2]) {
+  constexpr int stride = NCH * 512 + XG_PAD;
+  if (threadIdx.x < 32) L.zb[threadIdx.x] = (__bf16)0.0f;
+#pragma unroll
+  for (int j = 0; j < NCH / 2; j++) {
+    const int q = threadIdx.x + 256 * j;
+    const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      __bf16 hh, mm, ll;
+      split3(e4[e], hh, mm, ll);
+      L.xs[4 * q + e] = hh;
+      L.xs[stride + 4 * q + e] = mm;
+      L.xs[2 * stride + 4 * q + e] = ll;
+    }
+  }
+}
+
+// The body with the activation already in registers (xgateup1_load_x), or, with STAGED, already in
+// LDS (xgateup1_stage_x, xv unused); `jobs` may point at LDS.
+template <int NCH, bool STAGED = false>
+__device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
+                                             const float4 (&xv)[NCH / 2], const float *__restrict__ x, int I,
+                                             __bf16 *__restrict__ hp, int wg, int nwg) {
   // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
   // the first half of the next unit (slots and the unit epilogue are compile-time positions)
-  constexpr int K = NCH * 512, stride = K + XG_PAD, XV = K / 1024, SR = K >> 5, D = NCH / 2;
+  constexpr int K = NCH * 512, stride = K + XG_PAD, SR = K >> 5, D = NCH / 2;
   static_assert(NCH % 2 == 0, "even step count");
   static_assert(K <= 8192, "GuLds holds K <= 8192");
   __bf16 *xs = L.xs;
@@ -106,13 +138,6 @@ __device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__re
   const int tpp = I >> 2;  // 4-row tiles per pair
   const long U = (long)npairs * tpp, NW = 4L * nwg, wi = 4L * wg + w;
   const int u0 = (int)(wi * U / NW), u1 = (int)((wi + 1) * U / NW);
-  // activation: the token's three bf16 parts to LDS (every workgroup)
-  float4 xv[XV];
-  {
-    const rbt_gf4 *s4 = (const rbt_gf4 *)x;
-#pragma unroll
-    for (int j = 0; j < XV; j++) xv[j] = s4[threadIdx.x + 256 * j];
-  }
   // the wave's units span at most two pairs (U / NW < I / 4)
   const int pa = u0 / tpp, pb = min(pa + 1, npairs - 1);
   const RbtExpertDev JA = jobs[pa], JB = jobs[pb];
@@ -153,20 +178,7 @@ __device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__re
       ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * d));
     }
   }
-  if (threadIdx.x < 32) zb[threadIdx.x] = (__bf16)0.0f;
-#pragma unroll
-  for (int j = 0; j < XV; j++) {
-    const int q = threadIdx.x + 256 * j;
-    const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      __bf16 hh, mm, ll;
-      split3(e4[e], hh, mm, ll);
-      xs[4 * q + e] = hh;
-      xs[stride + 4 * q + e] = mm;
-      xs[2 * stride + 4 * q + e] = ll;
-    }
-  }
+  if (!STAGED) xgateup1_stage_x<NCH>(L, xv);
   auto sstore = [&](int buf) {
     *reinterpret_cast<rbt_u4 *>(&sw[w][buf][0][s_row][16 * (lane & 15)]) = sv[0];
     *reinterpret_cast<rbt_u4 *>(&sw[w][buf][1][s_row][16 * (lane & 15)]) = sv[1];
@@ -228,5 +240,15 @@ __device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__re
   }
 }
 
+
+
+template <int NCH>
+__device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
+                                              const float *__restrict__ x, int I, __bf16 *__restrict__ hp, int wg,
+                                              int nwg) {
+  float4 xv[NCH / 2];
+  xgateup1_load_x<NCH>(x, xv);
+  xgateup1_run<NCH>(L, jobs, npairs, xv, x, I, hp, wg, nwg);
+}
 
 }  // namespace rbt

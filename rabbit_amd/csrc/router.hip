@@ -836,13 +836,11 @@ struct GroupOut {
   RbtExpertDev *down_job;  // optional (one token): winners in slot order, then the shared expert
   int *down_slot;          // their pair slots
   int shared_slot;         // pair slot of the shared expert
-  D1Task *d1;              // optional: routed pair count / deferred decision
 };
 
 __host__ __device__ inline GroupOut group_out(const GroupArgs &g, int k) {
   return GroupOut{g.table,    g.shared_dev, g.pair_job, g.pair_tok, g.tok_pair,
-                  g.tok_w,    g.err,        g.down_job, g.down_slot, g.shared_slot >= 0 ? g.shared_slot : k,
-                  g.d1};
+                  g.tok_w,    g.err,        g.down_job, g.down_slot, g.shared_slot >= 0 ? g.shared_slot : k};
 }
 
 // Copy of a job-table entry field by field (a struct temporary ends up in scratch memory).
@@ -1330,10 +1328,6 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
             copy_job(G.down_job + kk, G.shared_dev);
             G.down_slot[kk] = G.shared_slot;
           }
-          if (G.d1) {
-            G.d1->nr = kk;
-            G.d1->pending = 0;
-          }
         }
       }
     }
@@ -1625,32 +1619,23 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
 }
 
 // ------------------------------------------------------------------------------------------------
-// One token, the whole router in one launch (k_router1), one workgroup per CU:
-//  1. every workgroup computes router rows r = nwg-1-b, 2 nwg-1-b, ... with the block variant's
-//     arithmetic (products through padded LDS, per-thread fp64 segments, block scans, the same
-//     bound), the next row's loads in flight while the current one is reduced;
-//  2. each workgroup then counts itself done on a device counter (release); workgroup 0 waits for
-//     the full count (acquire; a bounded spin, whose timeout raises an error flag and skips the
-//     selection so that every wave ends) and runs the selection above;
-//  3. the other workgroups stream the shared expert's gate/up, which does not depend on the
-//     routing. Needs every workgroup resident at once: the grid is one workgroup per CU and the
-//     kernel's LDS admits one per CU.
-// The counter returns to 0 at the end of a normal call (workgroup 0 resets it after the full
-// count), so repeated launches and graph replays need no host reset.
+// One token on the matrix cores, in three launches and with no workgroup waiting for another:
+//  1. k_router1: two (or four) router rows per workgroup with the block variant's arithmetic (fp64
+//     segment sums, block scans, the certified bound), writing mid / bnd and a 16-byte key record
+//     per expert, and the shared-expert gate row (sh_scale). Nothing else: every workgroup's loads
+//     go out at once and the rows' reduction is the whole critical path.
+//  2. k_xgateup1s (num_cu workgroups): every workgroup runs the selection itself from the key
+//     records (identical inputs and code, hence an identical result), so the routing reaches the
+//     streaming workgroups without a cross-workgroup hand-off. Workgroup 0 publishes ids, weights and
+//     the down launch's job list; every workgroup streams its share of the routed pairs' and then
+//     the shared expert's gate/up (pair slot nr: 11 pairs balanced over the grid at C1).
+//     When the certified intervals left the decision open, workgroup 0 instead folds the undecided
+//     logits exactly and decides, while the others stream every candidate.
+//  3. k_xdown1 (xgemm.hip).
 // ------------------------------------------------------------------------------------------------
-constexpr unsigned R1_SPIN_LIMIT = 1u << 24;
-// Sync area: word 0 is the epoch, workgroup b's flag is word R1_FLAG * (1 + b) (own 64-byte line).
-constexpr int R1_FLAG = 16;
-constexpr int R1_MAXWG = 1024;
-constexpr size_t R1_SYNC_BYTES = sizeof(unsigned) * R1_FLAG * (1 + R1_MAXWG);
-// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt = 0 only: expcnt 7 and lgkmcnt 15 are
-// their maxima (no wait), vmcnt bits [3:0] and [15:14] are zero.
-constexpr int RBT_WAIT_VMCNT0 = 0x0F70;
-typedef float rbt_f4v __attribute__((ext_vector_type(4)));  // polls of ~64 cycles: about 0.5 s
 
-// Key record of one expert for the one-launch router: the key interval, the order-preserving bits
-// of the midpoint key and the midpoint logit, computed exactly as the selection's own key setup
-// does from (mid, bnd).
+// Key record of one expert: the key interval, the order-preserving bits of the midpoint key and the
+// midpoint logit, computed exactly as the selection's own key setup does from (mid, bnd).
 struct KeyRec {
   float klo, khi;
   uint32_t ku;
@@ -1676,24 +1661,45 @@ __device__ __forceinline__ KeyRec make_key_rec(const SelParams &P, int e, double
   return r;
 }
 
+// The selection's result in the LDS of one gate/up workgroup: the routed pairs (T: slot c holds
+// expert T.id[c], its midpoint order key and logit, and whether its logit must be folded exactly),
+// their job-table entries, and the general path's outputs when it runs.
+struct PairLds {
+  D1Task T;
+  RbtExpertDev pj[D1_NC + 1];  // the routed pairs, then the shared expert
+  int status;
+  int fb_ids[SEL_MAXK];
+  float fb_w[SEL_MAXK];
+};
+
 // One token, wave 0: the fast path of the selection above from the key records, in registers (DPP
-// reductions, readlane loops over the candidates). The threshold M is the kk-th largest lane
-// maximum, taken by kk rounds of wave maximum that each retire one lane; candidates, ranking, set
-// and order certification are those of the general path. Returns (every lane) 1 when the result is
-// certified without exact recomputation, after writing ids, weights and the job tables; 2 when the
-// decision is deferred to the gate/up launch (task, routed pairs and the shared pair written); 0
-// to leave the call to the general path.
+// reductions, readlane loops over the candidates), into LDS only. The threshold M is the kk-th
+// largest lane maximum, taken by kk rounds of wave maximum that each retire one lane; candidates,
+// ranking, set and order certification are those of the general path. Returns (every lane):
+//  1  certified: the kk winners in rank order at slots 0..kk-1 (L.r_id / L.r_l set as well);
+//  2  deferred: the winners in midpoint rank order, then the candidates that might still win, the
+//     undecided ones flagged for an exact fold (Q.T.pending = 1);
+//  0  the general path is needed (a NaN key, more than SEL_NC candidates, or more undecided
+//     candidates than the pair slots beyond top-k).
+// rv[m]: the key record of expert lane + 64 m (clamped to E - 1; load_key_recs), table: the job
+// table (may be LDS).
 template <int MAXM>
-__device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restrict__ rec,
-                             int32_t *__restrict__ ids, float *__restrict__ wts, const GroupOut &G, int grp) {
+__device__ __forceinline__ void load_key_recs(const KeyRec *__restrict__ rec, int E, float4 (&rv)[MAXM]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int m = 0; m < MAXM; m++) rv[m] = *reinterpret_cast<const float4 *>(rec + min(lane + 64 * m, E - 1));
+}
+
+template <int MAXM>
+__device__ int select_pairs(SelLds &L, PairLds &Q, const SelParams &P, const float4 (&rv)[MAXM],
+                            const RbtExpertDev *__restrict__ table) {
   const int lane = threadIdx.x & 63;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
   uint32_t ku[MAXM];
   float klo[MAXM], khi[MAXM], lm[MAXM];
 #pragma unroll
   for (int m = 0; m < MAXM; m++) {
-    const int e = min(lane + 64 * m, E - 1);  // unconditional (in-bounds) loads
-    const float4 v = *reinterpret_cast<const float4 *>(rec + e);
+    const float4 v = rv[m];
     const bool ok = lane + 64 * m < E;
     klo[m] = ok ? v.x : -INFINITY;
     khi[m] = ok ? v.y : -INFINITY;
@@ -1744,8 +1750,8 @@ __device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restr
   // the candidate's job-table entry, in flight while the selection is certified
   const uint8_t *pf_gd = nullptr, *pf_ud = nullptr, *pf_dd = nullptr;
   const void *pf_gs = nullptr, *pf_us = nullptr, *pf_ds = nullptr;
-  if (grp && cand) {
-    const RbtExpertDev *src = G.table + cid;
+  if (cand) {
+    const RbtExpertDev *src = table + cid;
     pf_gd = src->gd;
     pf_gs = src->gs;
     pf_ud = src->ud;
@@ -1779,11 +1785,25 @@ __device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restr
     const float hj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(chi), j));
     if (iw && !cexact && rj < kk && rj != rank) cflag |= !(rj < rank ? lj > chi : clo > hj);
   }
+  D1Task &T = Q.T;
+  auto task = [&](int slot, int id, uint32_t key, float logit, int flag) {
+    T.id[slot] = id;
+    T.ku[slot] = key;
+    T.lm[slot] = logit;
+    T.flag[slot] = flag;
+  };
+  auto put = [&](int slot) {
+    RbtExpertDev *dst = Q.pj + slot;
+    dst->gd = pf_gd;
+    dst->gs = pf_gs;
+    dst->ud = pf_ud;
+    dst->us = pf_us;
+    dst->dd = pf_dd;
+    dst->ds = pf_ds;
+  };
   if (__ballot(cflag || nflag != 0) != 0) {
-    // Not certain. With a deferred-decision task: the routed pairs are the winners in midpoint
-    // rank order, then the candidates that might still win; the gate/up launch folds the flagged
-    // logits exactly and decides. Otherwise the general path recomputes here.
-    if (!grp || G.d1 == nullptr) return 0;
+    // Not certain: the routed pairs are the winners in midpoint rank order, then the candidates
+    // that might still win; workgroup 0 folds the flagged logits exactly and decides.
     const bool undec = cand && !iw && cflag;
     const unsigned long long um = __ballot(undec);
     const int nuc = __popcll(um);
@@ -1792,22 +1812,6 @@ __device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restr
     for (int m = 0; m < MAXM; m++) nun += __popcll(__ballot((nflag >> m) & 1u));
     const int nr = kk + nuc + nun;
     if (nr > min(k + D1_KX, D1_NC)) return 0;
-    D1Task *T = G.d1;
-    auto task = [&](int slot, int id, uint32_t key, float logit, int flag) {
-      T->id[slot] = id;
-      T->ku[slot] = key;
-      T->lm[slot] = logit;
-      T->flag[slot] = flag;
-    };
-    auto put = [&](int slot) {
-      RbtExpertDev *dst = G.pair_job + slot;
-      dst->gd = pf_gd;
-      dst->gs = pf_gs;
-      dst->ud = pf_ud;
-      dst->us = pf_us;
-      dst->dd = pf_dd;
-      dst->ds = pf_ds;
-    };
     if (iw) {
       task(rank, cid, cku, cl, cflag ? 1 : 0);
       put(rank);
@@ -1817,85 +1821,34 @@ __device__ int select4_fast(SelLds &L, const SelParams &P, const KeyRec *__restr
       task(slot, cid, cku, cl, 1);
       put(slot);
     }
-    int base = kk + nuc;
+    int nb = kk + nuc;
 #pragma unroll
     for (int m = 0; m < MAXM; m++) {
       const bool f = (nflag >> m) & 1u;
       const unsigned long long fb = __ballot(f);
       if (f) {
-        const int slot = base + __popcll(fb & lanemask_lt()), id = lane + 64 * m;
+        const int slot = nb + __popcll(fb & lanemask_lt()), id = lane + 64 * m;
         task(slot, id, ku[m], lm[m], 1);
-        copy_job(G.pair_job + slot, G.table + id);
+        copy_job(Q.pj + slot, table + id);
       }
-      base += __popcll(fb);
+      nb += __popcll(fb);
     }
     if (lane == 0) {
-      T->nr = nr;
-      T->pending = 1;
-      copy_job(G.pair_job + G.shared_slot, G.shared_dev);
+      T.nr = nr;
+      T.pending = 1;
     }
     return 2;
   }
-  // certified: weights in rank order, then the outputs
+  // certified: the winners in rank order
   if (iw) {
     L.r_id[rank] = cid;
     L.r_l[rank] = cl;
+    task(rank, cid, cku, cl, 0);
+    put(rank);
   }
-  __builtin_amdgcn_wave_barrier();
-  winner_weights(L, P, kk);
-  for (int r = lane; r < k; r += 64) {
-    ids[r] = r < kk ? L.r_id[r] : -1;
-    wts[r] = r < kk ? L.s_w[r] : 0.0f;
-  }
-  if (grp) {
-    // single token: pair j = slot j; the shared expert is at G.shared_slot
-    if (iw) {
-      if (pf_gd == nullptr || pf_dd == nullptr) atomicOr(G.err, 1);
-      RbtExpertDev *dst = G.pair_job + rank;
-      dst->gd = pf_gd;
-      dst->gs = pf_gs;
-      dst->ud = pf_ud;
-      dst->us = pf_us;
-      dst->dd = pf_dd;
-      dst->ds = pf_ds;
-      if (G.down_job) {
-        RbtExpertDev *dn = G.down_job + rank;
-        dn->gd = pf_gd;
-        dn->gs = pf_gs;
-        dn->ud = pf_ud;
-        dn->us = pf_us;
-        dn->dd = pf_dd;
-        dn->ds = pf_ds;
-        G.down_slot[rank] = rank;
-      }
-    }
-    for (int r = lane; r <= k; r += 64) {
-      if (r < k) {
-        if (r >= kk) {
-          RbtExpertDev *dst = G.pair_job + r;
-          dst->gd = nullptr;
-          dst->gs = nullptr;
-          dst->ud = nullptr;
-          dst->us = nullptr;
-          dst->dd = nullptr;
-          dst->ds = nullptr;
-        }
-        G.pair_tok[r] = 0;
-        G.tok_pair[r] = r < kk ? r : -1;
-        G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
-      } else {
-        copy_job(G.pair_job + G.shared_slot, G.shared_dev);
-        if (G.shared_slot == k) G.pair_tok[k] = 0;
-        if (G.down_job) {
-          copy_job(G.down_job + kk, G.shared_dev);
-          G.down_slot[kk] = G.shared_slot;
-        }
-        if (G.d1) {
-          G.d1->nr = kk;
-          G.d1->pending = 0;
-        }
-      }
-    }
+  if (lane == 0) {
+    T.nr = kk;
+    T.pending = 0;
   }
   return 1;
 }
@@ -1910,15 +1863,15 @@ struct LgLds {
 };
 
 __device__ __forceinline__ void store_key_rec(KeyRec *dst, const KeyRec &r) {
-  // two device-coherent 8-byte stores (the flag that publishes them waits for both)
   const unsigned long long a = ((unsigned long long)__float_as_uint(r.khi) << 32) | __float_as_uint(r.klo);
   const unsigned long long b = ((unsigned long long)__float_as_uint(r.lm) << 32) | r.ku;
   unsigned long long *d = reinterpret_cast<unsigned long long *>(dst);
-  __hip_atomic_store(d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __hip_atomic_store(d + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  d[0] = a;
+  d[1] = b;
 }
 
-// KP/rec: when KP is set, thread 0 also stores the key records of rows ea and eb (eb < 0: none).
+// KP/rec: when KP is set, the finishing threads also store the key records of rows ea and eb
+// (eb < 0: none).
 __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT_MAXH / 1024],
                                                  const float4 (&wa)[RT_MAXH / 1024],
                                                  const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
@@ -2029,131 +1982,94 @@ __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT
     B = B * (1.0 + 1e-9) + 1e-300;
     double *mo = rowb ? mid_b : mid_a, *bo = rowb ? bnd_b : bnd_a;
     if (mo) {
-      // device-coherent stores (write-through to the device's coherence point): the flag that
-      // follows needs no cache write-back to publish them
-      __hip_atomic_store(mo, tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(bo, B, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *mo = tot;
+      *bo = B;
       const int e = rowb ? eb : ea;
       if (KP && e >= 0) store_key_rec(rec + e, make_key_rec(*KP, e, tot, B));
     }
-    // acknowledged before the barrier below: thread 0's flag, raised after it, then covers both rows
-    __builtin_amdgcn_s_waitcnt(RBT_WAIT_VMCNT0);
   }
   __syncthreads();  // lp and sh are rewritten next
 }
 
-template <int MAXM, int NCH>
+typedef float rbt_f4v __attribute__((ext_vector_type(4)));
+
+// Workgroup b computes RPW router rows: rows RPW b .. RPW b + RPW - 1 of the E router rows followed
+// by the shared-expert gate row (row E, when sgate is given: its fp64 sum gives sh_scale; it has no
+// key record). The rows' loads are issued together, then the rows are reduced two at a time.
+template <int RPW>
 __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
                                                  double *__restrict__ mid, double *__restrict__ bnd,
-                                                 int32_t *__restrict__ ids, float *__restrict__ wts,
-                                                 float *__restrict__ sh_scale, int *__restrict__ stats, GroupOut G,
-                                                 int grp, const RbtExpertDev *__restrict__ shared_dev, int I,
-                                                 __bf16 *__restrict__ hp_shared, unsigned *__restrict__ sync,
-                                                 int *__restrict__ err, KeyRec *__restrict__ rec) {
+                                                 float *__restrict__ sh_scale, KeyRec *__restrict__ rec) {
   constexpr int MC = RT_MAXH / 1024;
-  __shared__ union {
-    LgLds lg;
-    SelLds sel;
-    GuLds gu;
-  } L;
-  __shared__ int go, fast_ok;
-  const int t = threadIdx.x, nwg = gridDim.x, b = blockIdx.x;
+  __shared__ LgLds L;
+  const int t = threadIdx.x, b = blockIdx.x;
   const int H = P.H, E = P.E, nch = H / 1024;
-  // this call's epoch: the value the previous call left (it changes only after every workgroup's
-  // flag is up, so every workgroup reads the same value)
-  const unsigned ep = __hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (sgate == nullptr && b == 0 && t == 0) sh_scale[0] = 1.0f;
+  const int Rn = E + (sgate != nullptr ? 1 : 0), r0 = RPW * b;
+  if (r0 >= Rn) return;
   const float4 *x4 = reinterpret_cast<const float4 *>(P.x);
-  float4 xv[MC], wa[MC], wb[MC], wg[MC];
-  // unconditional loads (chunks past the row repeat its last one): no waits between the rows
-  auto load_row = [&](const float *w, float4(&wv)[MC]) {
-    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+  float4 xv[MC], w[RPW][MC];
+  // unconditional loads (chunks past the row repeat its last one; rows past the end read row 0):
+  // no waits between the rows
+#pragma unroll
+  for (int j = 0; j < RPW; j++) {
+    const int r = r0 + j;
+    const float4 *w4 =
+        reinterpret_cast<const float4 *>(r < E ? P.W + (size_t)r * H : (r == E && sgate != nullptr ? sgate : P.W));
 #pragma unroll
     for (int c = 0; c < MC; c++) {
       const rbt_f4v v =
           __builtin_nontemporal_load(reinterpret_cast<const rbt_f4v *>(w4 + min(c, nch - 1) * 256 + t));
-      wv[c] = make_float4(v[0], v[1], v[2], v[3]);
+      w[j][c] = make_float4(v[0], v[1], v[2], v[3]);
     }
-  };
-  // router rows ra = nwg-1-b and rb = ra + nwg (E <= 2 nwg is checked by the launcher; a missing
-  // row reads a valid one and is not written); the last workgroup also takes the shared-expert
-  // gate row, which the selection does not need
-  const int ra = nwg - 1 - b, rb = ra + nwg;
-  const int rac = min(ra, E - 1), rbc = rb < E ? rb : rac;
-  const bool gate_row = sgate != nullptr && b == nwg - 1;
-  load_row(P.W + (size_t)rac * H, wa);
-  load_row(P.W + (size_t)rbc * H, wb);
-  if (gate_row) load_row(sgate, wg);
+  }
 #pragma unroll
   for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
-  if (ra < E)
-    logits_rows2_blk(L.lg, xv, wa, wb, H, mid + ra, bnd + ra, rb < E ? mid + rb : nullptr, rb < E ? bnd + rb : nullptr,
-                     &P, rec, ra, rb < E ? rb : -1);
-  // selection rows done: raise this workgroup's flag to epoch + 1. Its row results are device-scope
-  // stores made by this thread; waiting for their acknowledgement (vmcnt(0); a store at device
-  // scope is acknowledged once it is coherent there) orders them before the flag, with no L2
-  // write-back.
-  if (t == 0) {
-    __builtin_amdgcn_s_waitcnt(RBT_WAIT_VMCNT0);
-    __hip_atomic_store(sync + R1_FLAG * (1 + b), ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (int j = 0; j < RPW; j += 2) {
+    const int ra = r0 + j, rb = ra + 1;
+    if (ra < Rn)
+      logits_rows2_blk(L, xv, w[j], w[j + 1], H, mid + ra, bnd + ra, rb < Rn ? mid + rb : nullptr,
+                       rb < Rn ? bnd + rb : nullptr, &P, rec, ra < E ? ra : -1, rb < E ? rb : -1);
   }
-  if (gate_row) {
-    logits_rows2_blk(L.lg, xv, wg, wg, H, mid + E, bnd + E, nullptr, nullptr);
-    // gated shared expert: sigmoid of the fp32-rounded gate logit (qwen38/moe.rs:78-83)
-    if (t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
-  } else if (sgate == nullptr && b == nwg - 1 && t == 0) {
-    sh_scale[0] = 1.0f;
-  }
-  if (b == 0) {
-    if (t < 64) {
-      // wave 0 polls every flag (lane l: workgroups l, l + 64, ...) until all show epoch + 1
-      unsigned it = 0;
-      int ok = 1;
-      for (;;) {
-        bool done = true;
-        for (int w = t; w < nwg; w += 64)
-          done &= __hip_atomic_load(sync + R1_FLAG * (1 + w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ep + 1;
-        if (__ballot(!done) == 0) break;
-        __builtin_amdgcn_s_sleep(1);
-        if (++it > R1_SPIN_LIMIT) {
-          ok = 0;
-          break;
-        }
-      }
-      __threadfence();  // acquire: the other workgroups' rows
-      if (t == 0) {
-        // next call's epoch (every workgroup has read this one: its flag is up)
-        if (ok)
-          __hip_atomic_store(sync, ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        else
-          atomicOr(err, 1);
-        go = ok;
-      }
-    }
-    __syncthreads();
-    if (go) {
-      // the register fast path from the key records; anything it cannot certify by itself (an
-      // exact recomputation, many equal keys) goes through the general path from mid/bnd
-      if (t < 64) {
-        const int r = select4_fast<MAXM>(L.sel, P, rec, ids, wts, G, grp);
-        if (t == 0) fast_ok = r;
-      }
-      __syncthreads();
-      if (fast_ok == 0) select3_body<MAXM>(L.sel, P, mid, bnd, ids, wts, nullptr, stats, G, grp, 0);
-    }
-  } else if (shared_dev != nullptr) {
-    xgateup1_body<NCH>(L.gu, shared_dev, 1, P.x, I, hp_shared, b - 1, nwg - 1);
-  }
+  // gated shared expert: sigmoid of the fp32-rounded gate logit (qwen38/moe.rs:78-83); the row's
+  // sum was stored before the last barrier of logits_rows2_blk
+  if (sgate != nullptr && r0 <= E && E < r0 + RPW && t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
 }
 
 // ------------------------------------------------------------------------------------------------
-// Gate/up for one token with the router's decision deferred: workgroups 1 .. num_cu run the balanced
-// gate/up over the routed pairs the router launch published (nr of them, read on the device), and
-// workgroup 0, when a decision is pending, folds the flagged logits as the reference does (the
-// sequential fp32 sum, four waves in parallel), ranks the published candidates with exact keys
-// where they were folded and midpoint keys elsewhere (an unflagged candidate's interval is
-// disjoint from every other candidate's, so its midpoint orders it), and writes ids, weights,
-// tok_pair / tok_w and the down job list.
+// Workgroup 0 of the gate/up launch, after a certified selection: ids, weights, tok_pair / tok_w
+// and the down launch's job list (the winners in rank order at pair slots 0..kk-1, then the shared
+// expert at its slot). Wave 0.
 // ------------------------------------------------------------------------------------------------
+__device__ void publish_certified(SelLds &L, const PairLds &Q, const SelParams &P, const GroupOut &G,
+                                  int32_t *__restrict__ ids, float *__restrict__ wts) {
+  const int lane = threadIdx.x & 63;
+  const int k = P.k, kk = min(P.k, P.E);
+  winner_weights(L, P, kk);
+  for (int r = lane; r <= k; r += 64) {
+    if (r < k) {
+      ids[r] = r < kk ? L.r_id[r] : -1;
+      wts[r] = r < kk ? L.s_w[r] : 0.0f;
+      G.tok_pair[r] = r < kk ? r : -1;
+      G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
+      if (r < kk) {
+        if (Q.pj[r].gd == nullptr || Q.pj[r].dd == nullptr) atomicOr(G.err, 1);
+        copy_job(G.down_job + r, Q.pj + r);
+        G.down_slot[r] = r;
+      }
+    } else {
+      copy_job(G.down_job + kk, G.shared_dev);
+      G.down_slot[kk] = G.shared_slot;
+    }
+  }
+}
+
+// Workgroup 0 after a deferred selection: folds the flagged logits as the reference does (the
+// sequential fp32 sum, four waves in parallel), ranks the candidates with exact keys where they
+// were folded and midpoint keys elsewhere (an unflagged candidate's interval is disjoint from every
+// other candidate's, so its midpoint orders it), and writes ids, weights, tok_pair / tok_w and the
+// down job list.
 __device__ void d1_finish(SelLds &L, float (*fold)[2][1024], const SelParams &P, const D1Task *__restrict__ T,
                           const GroupOut &G, int32_t *__restrict__ ids, float *__restrict__ wts,
                           int *__restrict__ stats) {
@@ -2217,27 +2133,93 @@ __device__ void d1_finish(SelLds &L, float (*fold)[2][1024], const SelParams &P,
   if (lane == 0 && stats && na) atomicAdd(stats, na);
 }
 
-template <int NCH>
-__global__ __launch_bounds__(256) void k_xgateup1f(const RbtExpertDev *__restrict__ jobs, const D1Task *__restrict__ T,
-                                                   const float *__restrict__ x, int I, __bf16 *__restrict__ hp,
-                                                   SelParams P, GroupOut G, int32_t *__restrict__ ids,
-                                                   float *__restrict__ wts, int *__restrict__ stats) {
+// gup (optional) counts the routed pairs the launch streams (for the benchmark's byte accounting).
+constexpr int GU1S_MAXE = 512;  // experts whose job-table entries a workgroup stages in LDS
+template <int MAXM, int NCH>
+__global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__restrict__ rec,
+                                                   const double *__restrict__ mid, const double *__restrict__ bnd,
+                                                   GroupOut G, int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                   int *__restrict__ stats, int *__restrict__ gup, int I,
+                                                   __bf16 *__restrict__ hp, int has_shared) {
   __shared__ union {
     GuLds gu;
-    struct {
-      SelLds sel;
-      __attribute__((aligned(16))) float fold[4][2][1024];  // per wave: exact_logit_lds's blocks
-    } d1;
-  } L;
-  // workgroup 0 (dispatched first) settles a pending decision at raised wave priority (its serial
-  // fold chains then win the issue arbitration of the CU it shares with a gate/up workgroup); the
-  // other num_cu workgroups run the balanced gate/up
-  if (blockIdx.x > 0) {
-    xgateup1_body<NCH>(L.gu, jobs, T->nr, x, I, hp, blockIdx.x - 1, gridDim.x - 1);
-  } else if (T->pending) {
-    __builtin_amdgcn_s_setprio(3);
-    d1_finish(L.d1.sel, L.d1.fold, P, T, G, ids, wts, stats);
+    __attribute__((aligned(16))) float fold[4][2][1024];  // workgroup 0, deferred: exact_logit_lds's blocks
+  } U;
+  __shared__ SelLds S;
+  __shared__ PairLds Q;
+  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[GU1S_MAXE];
+  const int t = threadIdx.x, lane = t & 63;
+  const bool streamer = blockIdx.x > 0;
+  const int E = P.E, kk = min(P.k, P.E);
+  // Everything the selection and the stream need first is in flight together: the key records
+  // (wave 0), the activation, and the whole job table (so a winner's entry is an LDS read).
+  float4 rv[MAXM];
+  if (t < 64) load_key_recs<MAXM>(rec, E, rv);
+  float4 xv[NCH / 2];
+  xgateup1_load_x<NCH>(P.x, xv);
+  {
+    constexpr int TQ = (GU1S_MAXE * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
+    const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
+    const rbt_gu4 *src = (const rbt_gu4 *)G.table;
+    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
+    rbt_u4 tv[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) tv[i] = src[min(t + 256 * i, n4 - 1)];
+#pragma unroll
+    for (int i = 0; i < TQ; i++)
+      if (t + 256 * i < n4) dst[t + 256 * i] = tv[i];
   }
+  xgateup1_stage_x<NCH>(U.gu, xv);
+  __syncthreads();
+  if (t < 64) {
+    const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
+    if (t == 0) Q.status = r;
+  }
+  __syncthreads();
+  const int st = Q.status;
+  // the shared expert streams as the pair after the routed ones: its h lands at pair slot nr
+  GroupOut Gs = G;
+  if (st == 0) {
+    // the general path (exact recomputes until certain), the same in every workgroup; workgroup 0
+    // writes the outputs, the others take the winners as their pairs
+    if (!streamer) {
+      Gs.shared_slot = kk;
+      select3_body<MAXM>(S, P, mid, bnd, ids, wts, nullptr, stats, Gs, 1, 0);
+    } else {
+      select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
+      __syncthreads();
+      if (t < 64) {
+        for (int r = lane; r < kk; r += 64) {
+          Q.T.id[r] = Q.fb_ids[r];
+          copy_job(Q.pj + r, tab + Q.fb_ids[r]);
+        }
+        if (lane == 0) {
+          Q.T.nr = kk;
+          Q.T.pending = 0;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  // A deferred decision: workgroup 0 folds and decides while the others stream every candidate.
+  // Otherwise workgroup 0 publishes the routing (the general path already did) and streams its
+  // share like the rest.
+  const bool pending = st == 2;
+  const int nr = Q.T.nr;
+  Gs.shared_slot = nr;
+  if (!streamer) {
+    if (t == 0 && gup) atomicAdd(gup, nr + has_shared);
+    if (pending) {
+      d1_finish(S, U.fold, P, &Q.T, Gs, ids, wts, stats);  // U.gu's staged activation is not needed
+      return;
+    }
+    if (st == 1 && t < 64) publish_certified(S, Q, P, Gs, ids, wts);
+  }
+  if (has_shared && t == 0) copy_job(Q.pj + nr, G.shared_dev);
+  __syncthreads();
+  // the routed pairs, then the shared expert, balanced over the grid
+  const int wg = pending ? blockIdx.x - 1 : blockIdx.x, nwg = pending ? gridDim.x - 1 : gridDim.x;
+  xgateup1_run<NCH, true>(U.gu, Q.pj, nr + has_shared, xv, P.x, I, hp, wg, nwg);
 }
 
 static SelParams sel_params(const RouterArgs &a) {
@@ -2259,74 +2241,52 @@ static SelParams sel_params(const RouterArgs &a) {
   return P;
 }
 
-hipError_t launch_xgateup1_d1(const Ctx &c, const RbtExpertDev *jobs, const D1Task *T, const float *x, int K, int I,
-                              __bf16 *hp, const RouterArgs &a, const GroupArgs &grp, int32_t *ids, float *wts,
-                              int *stats) {
-  if (I % 4 != 0 || c.num_cu < 2 || !grp.down_job || !grp.down_slot || !T) return hipErrorInvalidValue;
-  const SelParams P = sel_params(a);
-  const GroupOut G = group_out(grp, a.k);
-  const dim3 grid(c.num_cu + 1);
-  if (K == 8192)
-    launch_k(c, k_xgateup1f<16>, grid, dim3(256), jobs, T, x, I, hp, P, G, ids, wts, stats);
-  else if (K == 7168)
-    launch_k(c, k_xgateup1f<14>, grid, dim3(256), jobs, T, x, I, hp, P, G, ids, wts, stats);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
-}
-
-size_t router1_sync_bytes() { return R1_SYNC_BYTES; }
-
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu) {
   const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
-  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 512 && a.k <= SEL_MAXK &&
-         a.H % 1024 == 0 && a.H <= RT_MAXH && aligned && a.E <= 2 * num_cu && num_cu >= 2 &&
-         (sgu == nullptr || sgu->K == a.H) && (sgu == nullptr || a.H == 8192 || a.H == 7168);
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= GU1S_MAXE && a.k + D1_KX <= D1_NC &&
+         (a.H == 8192 || a.H == 7168) && aligned && a.E <= 2 * num_cu && num_cu >= 2 &&
+         (sgu == nullptr || sgu->K == a.H);
 }
 
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                          int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs *grp,
-                          const SharedGateUp *sgu, unsigned *sync, int *err, void *rec_buf) {
+                          float *sh_scale, void *rec_buf) {
   KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
-  if (!router1_ok(a, c.num_cu, sgu) || (sgate && (uintptr_t)sgate % 16 != 0) || c.num_cu > R1_MAXWG)
+  if (!router1_ok(a, c.num_cu, nullptr) || (sgate && (uintptr_t)sgate % 16 != 0)) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  // two rows per workgroup while two workgroups per CU hold them all at once (the rows' reduction
+  // is on the critical path: 9.5 us for 257 x 2 rows at C1's shape against 11.8 us for 129 x 4)
+  const int rn = a.E + (sgate ? 1 : 0);
+  if ((rn + 1) / 2 <= 2 * c.num_cu)  // two workgroups fit on a CU
+    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+  else
+    launch_k(c, k_router1<4>, dim3((rn + 3) / 4), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+  return hipGetLastError();
+}
+
+hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec_buf, const double *mid,
+                            const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int *gup,
+                            int I, __bf16 *hp, bool has_shared) {
+  if (I % 4 != 0 || c.num_cu < 2 || !grp.down_job || !grp.down_slot || !router1_ok(a, c.num_cu, nullptr))
     return hipErrorInvalidValue;
-  SelParams P{};
-  P.family = a.family;
-  P.E = a.E;
-  P.erows = a.erows;
-  P.k = a.k;
-  P.H = a.H;
-  P.S = 1;
-  P.logit_bias = a.logit_bias;
-  P.router_bias = a.router_bias;
-  P.norm_topk = a.norm_topk;
-  P.routed_scale = a.routed_scale;
-  P.n_group = a.n_group;
-  P.topk_group = a.topk_group;
-  P.x = a.x;
-  P.W = a.W;
-  GroupOut G{};
-  int g = 0;
-  if (grp) {
-    G = group_out(*grp, a.k);
-    g = 1;
-  }
-  const RbtExpertDev *sd = sgu ? sgu->dev : nullptr;
-  const int I = sgu ? sgu->I : 0;
-  __bf16 *hp = sgu ? sgu->hp : nullptr;
-  const dim3 grid(c.num_cu), block(256);
+  const SelParams P = sel_params(a);
+  const GroupOut G = group_out(grp, a.k);
+  const KeyRec *rec = reinterpret_cast<const KeyRec *>(rec_buf);
+  const dim3 grid(c.num_cu);
   const bool m4 = a.E <= 256;
-  if (a.H == 7168) {
+#define RBT_GU1S(M, N) \
+  launch_k(c, k_xgateup1s<M, N>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I, hp, (int)has_shared)
+  if (a.H == 8192) {
     if (m4)
-      launch_k(c, k_router1<4, 14>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+      RBT_GU1S(4, 16);
     else
-      launch_k(c, k_router1<8, 14>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+      RBT_GU1S(8, 16);
   } else {
     if (m4)
-      launch_k(c, k_router1<4, 16>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+      RBT_GU1S(4, 14);
     else
-      launch_k(c, k_router1<8, 16>, grid, block, P, sgate, mid, bnd, ids, wts, sh_scale, stats, G, g, sd, I, hp, sync, err, rec);
+      RBT_GU1S(8, 14);
   }
+#undef RBT_GU1S
   return hipGetLastError();
 }
 

@@ -381,7 +381,8 @@ __global__ __launch_bounds__(256) void k_xdown(const RbtExpertDev *__restrict__ 
 // ------------------------------------------------------------------------------------------------
 // down + combine for one token, balanced over the whole chip: one workgroup of XD1_NW waves per CU.
 // Workgroup b owns the 4-row output tiles [T0, T1) (an equal share of H/4) and the units
-// (tile, pair) over them, u = tile * npairs + pair, dealt evenly over its waves. Every pair's h
+// (tile, pair) over them, u = pair * nt + tile (a wave's units are consecutive tiles of one pair:
+// runs of contiguous weight rows), dealt evenly over its waves. Every pair's h
 // parts are staged in LDS once (no per-pair barriers); a wave streams its units' 16-byte code chunks
 // with four units (16 chunks) in flight, block scales for four units at a time through a
 // wave-private LDS window (one 16-byte load per lane), and leaves each unit's four row sums in LDS.
@@ -463,7 +464,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     cp[j] = dummy;
     sp[j] = hb8 + 16 * s_seg;
     if (u < u1) {
-      const int tl = u / npairs, pp = u - tl * npairs;
+      const int pp = u / nt, tl = u - pp * nt;
       const uint8_t *dd = lane_ptr(t_dd, pp);
       const uint8_t *ds = lane_ptr(t_ds, pp);
       if (dd != nullptr && ds != nullptr) {
@@ -516,7 +517,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   // lane pointer of unit u (chunk 0); past the wave's units or for a null job: cached dummy bytes
   auto uptr = [&](int u) -> const uint8_t * {
     if (u >= u1) return dummy;
-    const int tl = u / npairs, pp = u - tl * npairs;
+    const int pp = u / nt, tl = u - pp * nt;
     return plive[pp] ? pd[pp] + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
   };
   // scale window of units ub .. ub+3: lane l holds unit ub + l/16, row (l/4) % 4, bytes 16 (l % 4)
@@ -524,7 +525,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     const int u = ub + s_q;
     const uint8_t *p = hb8 + 16 * s_seg;
     if (u < u1) {
-      const int tl = u / npairs, pp = u - tl * npairs;
+      const int pp = u / nt, tl = u - pp * nt;
       if (plive[pp]) p = ps[pp] + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
     }
     return *(const rbt_gu4 *)p;
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
         ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(np + 256 * c));
       }
       if (u < u1) {
-        const int tl = u / npairs, pp = u - tl * npairs;
+        const int pp = u / nt, tl = u - pp * nt;
         const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[pp]) + boff : reinterpret_cast<const char *>(zb);
         xf4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
