@@ -1381,64 +1381,102 @@ __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, doub
 //   pair_tok[p]   -> token index
 //   tok_pair[t*k + j] -> the t-th token's pairs sorted by unique_experts position
 //   tok_w[t*k + j]    -> matching routing weight
-// One workgroup; thread e handles expert e.
+// One workgroup; thread e handles expert e. The picks (ids, weights) and the per-token pair lists
+// are kept in LDS when they fit (stage != 0): every expert's thread walks all the picks, and the
+// per-token sort is a chain of dependent accesses, each a memory round trip in global memory.
 // ------------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids, const float *__restrict__ wts, int S,
                                                 int k, int E, const RbtExpertDev *__restrict__ table,
                                                 const RbtExpertDev *__restrict__ shared_dev, RbtExpertDev *pair_job,
-                                                int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
+                                                int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq,
+                                                int stage) {
   extern __shared__ int smem[];
+  __shared__ int uniq;
   int *first = smem;       // [E]
   int *cnt = smem + E;     // [E]
   int *off = smem + 2 * E; // [E]
   const int P = S * k;
+  // staged: the picks and the per-token pair lists live in LDS ([P] each)
+  int *sid = smem + 3 * E;
+  float *swt = reinterpret_cast<float *>(smem + 3 * E + P);
+  int *stp = smem + 3 * E + 2 * P;
+  float *stw = reinterpret_cast<float *>(smem + 3 * E + 3 * P);
+  const int32_t *pid = stage ? sid : ids;
+  const float *pwt = stage ? swt : wts;
+  int *tp_all = stage ? stp : tok_pair;
+  float *tw_all = stage ? stw : tok_w;
+  if (threadIdx.x == 0) uniq = 0;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     first[e] = 0x7fffffff;
     cnt[e] = 0;
   }
   // Slots without a pick (grouped routing can select fewer than k) stay empty: null job, no pair.
   for (int p = threadIdx.x; p < P; p += blockDim.x) {
+    if (stage) {
+      sid[p] = ids[p];
+      swt[p] = wts[p];
+    }
     pair_job[p] = RbtExpertDev{};
     pair_tok[p] = 0;
-    tok_pair[p] = -1;
-    tok_w[p] = 0.0f;
+    tp_all[p] = -1;
+    tw_all[p] = 0.0f;
   }
   __syncthreads();
   for (int p = threadIdx.x; p < P; p += blockDim.x) {
-    int e = ids[p];
+    int e = pid[p];
     if (e >= 0 && e < E) {
       atomicMin(&first[e], p);
       atomicAdd(&cnt[e], 1);
     }
   }
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    int o = 0;
-    if (cnt[e] > 0)
-      for (int f = 0; f < E; f++)
-        if (cnt[f] > 0 && first[f] < first[e]) o += cnt[f];
-    off[e] = o;
-  }
+  // off[e]: the picks of the experts first picked before e -- an exclusive prefix sum over the picks
+  // in order of cnt[e] at each expert's first pick (chunks of 1024 picks, wave scans and a carry)
+  __shared__ int wsum[16], carry;
+  if (threadIdx.x == 0) carry = 0;
   __syncthreads();
-  if (threadIdx.x == 0 && nuniq) {
-    int u = 0;
-    for (int e = 0; e < E; e++) u += cnt[e] > 0;
-    *nuniq = u;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int base = 0; base < P; base += 1024) {
+    const int p = base + (int)threadIdx.x;
+    int e = -1, v = 0;
+    if (p < P) {
+      e = pid[p];
+      if (e >= 0 && e < E && first[e] == p) v = cnt[e];
+    }
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int woff = carry, tot = 0;
+    for (int w2 = 0; w2 < 16; w2++) {
+      if (w2 < wave) woff += wsum[w2];
+      tot += wsum[w2];
+    }
+    if (v) {
+      off[e] = woff + incl - v;
+      atomicAdd(&uniq, 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) carry += tot;
+    __syncthreads();
   }
+  if (threadIdx.x == 0 && nuniq) *nuniq = uniq;
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     if (cnt[e] == 0) continue;
     int c = 0;
     RbtExpertDev J = table[e];
     if (J.gd == nullptr || J.dd == nullptr) atomicOr(err, 1);
-    for (int t = 0; t < S; t++) {
-      for (int j = 0; j < k; j++) {
-        if (ids[t * k + j] == e) {
-          int p = off[e] + c++;
-          pair_job[p] = J;
-          pair_tok[p] = t;
-          tok_pair[t * k + j] = p;  // unsorted for now
-          tok_w[t * k + j] = wts[t * k + j];
-        }
+    for (int q = first[e]; q < P; q++) {  // pairs in token order (q = t k + j), from the first pick
+      if (pid[q] == e) {
+        int p = off[e] + c++;
+        pair_job[p] = J;
+        pair_tok[p] = q / k;
+        tp_all[q] = p;  // unsorted for now
+        tw_all[q] = pwt[q];
       }
     }
   }
@@ -1447,8 +1485,8 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
   for (int t = threadIdx.x; t < S; t += blockDim.x) {
     pair_job[P + t] = *shared_dev;
     pair_tok[P + t] = t;
-    int *tp = tok_pair + t * k;
-    float *tw = tok_w + t * k;
+    int *tp = tp_all + t * k;
+    float *tw = tw_all + t * k;
     for (int a = 1; a < k; a++) {
       int cp = tp[a];
       float cw = tw[a];
@@ -1460,6 +1498,13 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
       }
       tp[b] = cp;
       tw[b] = cw;
+    }
+  }
+  if (stage) {
+    __syncthreads();
+    for (int p = threadIdx.x; p < P; p += blockDim.x) {
+      tok_pair[p] = stp[p];
+      tok_w[p] = stw[p];
     }
   }
 }
@@ -1526,11 +1571,18 @@ __global__ void k_group_s1(const int32_t *__restrict__ ids, const float *__restr
 // ------------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_router_logits_tk(const float *__restrict__ x, int S, int H,
+                                                          const float *__restrict__ W, int E,
+                                                          const float *__restrict__ sgate, double *__restrict__ mid,
+                                                          double *__restrict__ bnd, int erows);
+
 hipError_t launch_router_logits(const Ctx &c, const float *x, int S, int H, const float *W, int E, const float *sgate,
                                 double *mid, double *bnd) {
   int erows = E + (sgate ? 1 : 0);
   bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)W % 16 == 0) && (!sgate || (uintptr_t)sgate % 16 == 0);
-  if (H % 1024 == 0 && H <= RT_MAXH && aligned)
+  if (H % 1024 == 0 && H <= RT_MAXH && aligned && S > 1)
+    launch_k(c, k_router_logits_tk, dim3(erows, (S + 3) / 4), dim3(256), x, S, H, W, E, sgate, mid, bnd, erows);
+  else if (H % 1024 == 0 && H <= RT_MAXH && aligned)
     launch_k(c, k_router_logits_b, dim3(erows), dim3(256), x, S, H, W, E, sgate, mid, bnd, erows);
   else if (H % 256 == 0 && H <= RT_MAXH && aligned)
     launch_k(c, k_router_logits_t, dim3(erows), dim3(64), x, S, H, W, E, sgate, mid, bnd, erows);
@@ -1853,12 +1905,13 @@ __device__ int select_pairs(SelLds &L, PairLds &Q, const SelParams &P, const flo
   return 1;
 }
 
-// Two router rows by the whole workgroup at once (one pass, shared scans and sums; per row the
-// block variant's arithmetic, with the cross-lane sums through DPP, which only reorders fp64
+// NR (1 or 2) router rows by the whole workgroup at once (one pass, shared scans and sums; per row
+// the block variant's arithmetic, with the cross-lane sums through DPP, which only reorders fp64
 // additions that the bound's slack covers): xv, wa, wb hold the thread's float4 chunks c * 256 + t
-// of x and of the two rows.
+// of x and of the rows (wb unused when NR is 1).
+template <int NR>
 struct LgLds {
-  __attribute__((aligned(16))) float lp[2][RT_MAXH + 4 * 256];
+  __attribute__((aligned(16))) float lp[NR][RT_MAXH + 4 * 256];
   double sh[16];
 };
 
@@ -1871,13 +1924,15 @@ __device__ __forceinline__ void store_key_rec(KeyRec *dst, const KeyRec &r) {
 }
 
 // KP/rec: when KP is set, the finishing threads also store the key records of rows ea and eb
-// (eb < 0: none).
-__device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT_MAXH / 1024],
-                                                 const float4 (&wa)[RT_MAXH / 1024],
-                                                 const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
-                                                 double *bnd_a, double *mid_b, double *bnd_b,
-                                                 const SelParams *KP = nullptr, KeyRec *rec = nullptr, int ea = -1,
-                                                 int eb = -1) {
+// (-1: none).
+template <int NR>
+__device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)[RT_MAXH / 1024],
+                                                const float4 (&wa)[RT_MAXH / 1024],
+                                                const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
+                                                double *bnd_a, double *mid_b, double *bnd_b,
+                                                const SelParams *KP = nullptr, KeyRec *rec = nullptr, int ea = -1,
+                                                int eb = -1) {
+  static_assert(NR == 1 || NR == 2, "one or two rows");
   const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
   const int seg = H / 256, segp = seg + 4, nch = H / 1024;
   const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
@@ -1887,38 +1942,44 @@ __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT
     if (c < nch) {
       const int j = c * 1024 + 4 * t;
       const int dst = (j / seg) * segp + (j % seg);
-      float4 p, q;
+      float4 p;
       p.x = __fmul_rn(xv[c].x, wa[c].x);
       p.y = __fmul_rn(xv[c].y, wa[c].y);
       p.z = __fmul_rn(xv[c].z, wa[c].z);
       p.w = __fmul_rn(xv[c].w, wa[c].w);
-      q.x = __fmul_rn(xv[c].x, wb[c].x);
-      q.y = __fmul_rn(xv[c].y, wb[c].y);
-      q.z = __fmul_rn(xv[c].z, wb[c].z);
-      q.w = __fmul_rn(xv[c].w, wb[c].w);
       *reinterpret_cast<float4 *>(&L.lp[0][dst]) = p;
-      *reinterpret_cast<float4 *>(&L.lp[1][dst]) = q;
+      if constexpr (NR == 2) {
+        float4 q;
+        q.x = __fmul_rn(xv[c].x, wb[c].x);
+        q.y = __fmul_rn(xv[c].y, wb[c].y);
+        q.z = __fmul_rn(xv[c].z, wb[c].z);
+        q.w = __fmul_rn(xv[c].w, wb[c].w);
+        *reinterpret_cast<float4 *>(&L.lp[NR - 1][dst]) = q;
+      }
     }
   }
   __syncthreads();
-  const float *ma = L.lp[0] + t * segp, *mb = L.lp[1] + t * segp;
+  const float *ma = L.lp[0] + t * segp, *mb = L.lp[NR - 1] + t * segp;
   double la = 0.0, pa = 0.0, lb = 0.0, pb = 0.0;
   for (int q = 0; q < seg; q += 4) {
     const float4 p = *reinterpret_cast<const float4 *>(ma + q);
-    const float4 r = *reinterpret_cast<const float4 *>(mb + q);
     la += (double)p.x;
-    lb += (double)r.x;
     la += (double)p.y;
-    lb += (double)r.y;
     la += (double)p.z;
-    lb += (double)r.z;
     la += (double)p.w;
-    lb += (double)r.w;
     pa += fabs((double)p.x) + fabs((double)p.y) + fabs((double)p.z) + fabs((double)p.w);
-    pb += fabs((double)r.x) + fabs((double)r.y) + fabs((double)r.z) + fabs((double)r.w);
+    if constexpr (NR == 2) {
+      const float4 r = *reinterpret_cast<const float4 *>(mb + q);
+      lb += (double)r.x;
+      lb += (double)r.y;
+      lb += (double)r.z;
+      lb += (double)r.w;
+      pb += fabs((double)r.x) + fabs((double)r.y) + fabs((double)r.z) + fabs((double)r.w);
+    }
   }
-  // exclusive block scan of both segment sums (wave scans, then wave offsets through LDS)
-  const double ia = rbt_wave_scan_d(la), ib = rbt_wave_scan_d(lb);
+  // exclusive block scan of the segment sums (wave scans, then wave offsets through LDS)
+  const double ia = rbt_wave_scan_d(la);
+  const double ib = NR == 2 ? rbt_wave_scan_d(lb) : 0.0;
   if (lane == 63) {
     L.sh[wid] = ia;
     L.sh[4 + wid] = ib;
@@ -1937,28 +1998,32 @@ __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT
   double prea = offa + ia - la, preb = offb + ib - lb, Ta = 0.0, Tb = 0.0;
   for (int q = 0; q < seg; q += 4) {
     const float4 p = *reinterpret_cast<const float4 *>(ma + q);
-    const float4 r = *reinterpret_cast<const float4 *>(mb + q);
     prea += (double)p.x;
-    preb += (double)r.x;
     Ta += fabs(prea);
-    Tb += fabs(preb);
     prea += (double)p.y;
-    preb += (double)r.y;
     Ta += fabs(prea);
-    Tb += fabs(preb);
     prea += (double)p.z;
-    preb += (double)r.z;
     Ta += fabs(prea);
-    Tb += fabs(preb);
     prea += (double)p.w;
-    preb += (double)r.w;
     Ta += fabs(prea);
-    Tb += fabs(preb);
+    if constexpr (NR == 2) {
+      const float4 r = *reinterpret_cast<const float4 *>(mb + q);
+      preb += (double)r.x;
+      Tb += fabs(preb);
+      preb += (double)r.y;
+      Tb += fabs(preb);
+      preb += (double)r.z;
+      Tb += fabs(preb);
+      preb += (double)r.w;
+      Tb += fabs(preb);
+    }
   }
   Ta = rbt_wave_total_d(Ta);
   pa = rbt_wave_total_d(pa);
-  Tb = rbt_wave_total_d(Tb);
-  pb = rbt_wave_total_d(pb);
+  if (NR == 2) {
+    Tb = rbt_wave_total_d(Tb);
+    pb = rbt_wave_total_d(pb);
+  }
   if (lane == 0) {
     L.sh[wid] = Ta;
     L.sh[4 + wid] = pa;
@@ -1967,7 +2032,7 @@ __device__ __forceinline__ void logits_rows2_blk(LgLds &L, const float4 (&xv)[RT
   }
   __syncthreads();
   // row a finishes on thread 0, row b on thread 64 (another wave), in parallel
-  if (t == 0 || t == 64) {
+  if (t == 0 || (NR == 2 && t == 64)) {
     const bool rowb = t == 64;
     const double n = (double)H;
     const double T = rowb ? L.sh[8] + L.sh[9] + L.sh[10] + L.sh[11] : L.sh[0] + L.sh[1] + L.sh[2] + L.sh[3];
@@ -2000,8 +2065,8 @@ template <int RPW>
 __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
                                                  double *__restrict__ mid, double *__restrict__ bnd,
                                                  float *__restrict__ sh_scale, KeyRec *__restrict__ rec) {
-  constexpr int MC = RT_MAXH / 1024;
-  __shared__ LgLds L;
+  constexpr int MC = RT_MAXH / 1024, NR = RPW == 1 ? 1 : 2;
+  __shared__ LgLds<NR> L;
   const int t = threadIdx.x, b = blockIdx.x;
   const int H = P.H, E = P.E, nch = H / 1024;
   if (sgate == nullptr && b == 0 && t == 0) sh_scale[0] = 1.0f;
@@ -2026,15 +2091,45 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
 #pragma unroll
   for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
 #pragma unroll
-  for (int j = 0; j < RPW; j += 2) {
+  for (int j = 0; j < RPW; j += NR) {
     const int ra = r0 + j, rb = ra + 1;
     if (ra < Rn)
-      logits_rows2_blk(L, xv, w[j], w[j + 1], H, mid + ra, bnd + ra, rb < Rn ? mid + rb : nullptr,
-                       rb < Rn ? bnd + rb : nullptr, &P, rec, ra < E ? ra : -1, rb < E ? rb : -1);
+      logits_rows_blk<NR>(L, xv, w[j], w[j + NR - 1], H, mid + ra, bnd + ra, NR == 2 && rb < Rn ? mid + rb : nullptr,
+                          NR == 2 && rb < Rn ? bnd + rb : nullptr, &P, rec, ra < E ? ra : -1,
+                          NR == 2 && rb < E ? rb : -1);
   }
   // gated shared expert: sigmoid of the fp32-rounded gate logit (qwen38/moe.rs:78-83); the row's
-  // sum was stored before the last barrier of logits_rows2_blk
+  // sum was stored before the last barrier of logits_rows_blk
   if (sgate != nullptr && r0 <= E && E < r0 + RPW && t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
+}
+
+// Certified logits of a small batch: workgroup (row, q) computes router row `row` (or the shared
+// gate row, row == E) against tokens 4q .. 4q + 3, two at a time with the two-row arithmetic (the
+// products are the same with the row and the tokens swapped). The row is read once per four tokens.
+__global__ __launch_bounds__(256) void k_router_logits_tk(const float *__restrict__ x, int S, int H,
+                                                          const float *__restrict__ W, int E,
+                                                          const float *__restrict__ sgate, double *__restrict__ mid,
+                                                          double *__restrict__ bnd, int erows) {
+  constexpr int MC = RT_MAXH / 1024;
+  __shared__ LgLds<2> L;
+  const int t = threadIdx.x, row = blockIdx.x, nch = H / 1024;
+  const int s0 = 4 * blockIdx.y;
+  const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
+  float4 wv[MC], xa[MC], xb[MC];
+  auto load = [&](const float4 *p, float4(&v)[MC]) {
+#pragma unroll
+    for (int c = 0; c < MC; c++) v[c] = p[min(c, nch - 1) * 256 + t];
+  };
+  load(w4, wv);
+  for (int s = s0; s < min(S, s0 + 4); s += 2) {
+    const int s1 = min(s + 1, S - 1);
+    load(reinterpret_cast<const float4 *>(x + (size_t)s * H), xa);
+    load(reinterpret_cast<const float4 *>(x + (size_t)s1 * H), xb);
+    const bool two = s + 1 < S;
+    logits_rows_blk<2>(L, wv, xa, xb, H, mid + (size_t)s * erows + row, bnd + (size_t)s * erows + row,
+                       two ? mid + (size_t)(s + 1) * erows + row : nullptr,
+                       two ? bnd + (size_t)(s + 1) * erows + row : nullptr);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -2253,13 +2348,13 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
   KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
   if (!router1_ok(a, c.num_cu, nullptr) || (sgate && (uintptr_t)sgate % 16 != 0)) return hipErrorInvalidValue;
   const SelParams P = sel_params(a);
-  // two rows per workgroup while two workgroups per CU hold them all at once (the rows' reduction
-  // is on the critical path: 9.5 us for 257 x 2 rows at C1's shape against 11.8 us for 129 x 4)
+  // one row per workgroup while the grid fits the chip at once (the rows' reduction is on the
+  // critical path: C1's 513 rows take 9.5 us as 257 x 2 rows, 11.8 us as 129 x 4)
   const int rn = a.E + (sgate ? 1 : 0);
-  if ((rn + 1) / 2 <= 2 * c.num_cu)  // two workgroups fit on a CU
-    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+  if (rn <= 4 * c.num_cu)  // four one-row workgroups fit on a CU
+    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
   else
-    launch_k(c, k_router1<4>, dim3((rn + 3) / 4), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
   return hipGetLastError();
 }
 
@@ -2303,9 +2398,12 @@ hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int 
     launch_k(c, k_group_s1, dim3(1), dim3(((k + 1 + 63) / 64) * 64), ids, wts, k, E, table,
                        shared_dev, pair_job, pair_tok, tok_pair, tok_w, err);
   } else {
-    size_t smem = (size_t)3 * E * sizeof(int);
-    launch_ks(c, k_group, dim3(1), dim3(1024), smem, ids, wts, S, k, E, table, shared_dev, pair_job,
-                       pair_tok, tok_pair, tok_w, err, nuniq);
+    // the picks go to LDS too while they fit (64 KB)
+    const size_t base = (size_t)3 * E * sizeof(int), picks = (size_t)4 * S * k * sizeof(int);
+    const int stage = base + picks <= 65536 ? 1 : 0;
+    const size_t smem = base + (stage ? picks : 0);
+    launch_ks(c, k_group, dim3(1), dim3(1024), (unsigned)smem, ids, wts, S, k, E, table, shared_dev, pair_job,
+              pair_tok, tok_pair, tok_w, err, nuniq, stage);
   }
   return hipGetLastError();
 }
