@@ -50,3 +50,36 @@ def write_safetensors(path, tensors, metadata=None, raw_header=None):
         f.write(len(hb).to_bytes(8, "little"))
         f.write(hb)
         f.write(data)
+
+
+class HipGraph:
+    """A HIP graph captured from a stream (the library's) through the runtime's C API."""
+
+    def __init__(self, stream: int):
+        import ctypes as C
+        self.C = C
+        self.hip = C.CDLL("libamdhip64.so.7")
+        self.stream = C.c_void_p(stream)
+        self.graph, self.exec = C.c_void_p(), C.c_void_p()
+
+    def _ok(self, rc, what):
+        if rc:
+            raise RuntimeError(f"{what} -> {rc}")
+
+    def begin(self):
+        self._ok(self.hip.hipStreamBeginCapture(self.stream, 1), "hipStreamBeginCapture")  # thread-local mode
+
+    def end(self):
+        self._ok(self.hip.hipStreamEndCapture(self.stream, self.C.byref(self.graph)), "hipStreamEndCapture")
+        self._ok(self.hip.hipGraphInstantiate(self.C.byref(self.exec), self.graph, None, None, self.C.c_size_t(0)),
+                 "hipGraphInstantiate")
+
+    def launch(self):
+        self._ok(self.hip.hipGraphLaunch(self.exec, self.stream), "hipGraphLaunch")
+
+    def destroy(self):
+        if self.exec:
+            self.hip.hipGraphExecDestroy(self.exec)
+        if self.graph:
+            self.hip.hipGraphDestroy(self.graph)
+        self.exec = self.graph = self.C.c_void_p()

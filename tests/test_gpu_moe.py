@@ -172,6 +172,47 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
           ", ".join(f"({a:.2e}, {b:.2e}, {c:.2e})" for a, b, c in worst[:4]))
 
 
+@pytest.mark.parametrize("name,ntok", [("c1", 1), ("c3", 8)])
+def test_decode_graph_replays(ctx, orc, name, ntok):
+    """A decode call captured in a HIP graph (as the benchmark replays them) and replayed several
+    times with other inputs, with eager calls and synchronisations between the replays: every
+    replay equals the eager result for its input (no memset node, no state left between calls)."""
+    import rabbit_amd.workloads as W
+    import torch
+    from helpers import HipGraph
+    cfg = W.CONFIGS[name]
+    W.build_layer(ctx, cfg, layer=0, seed=1000)
+    H = cfg.hidden
+    xs = [torch.from_numpy(W.tokens(cfg, ntok, 31 + t)).cuda() for t in range(3)]
+    ref = []
+    for t in range(3):
+        o = torch.empty(ntok * H, dtype=torch.float32, device="cuda")
+        ctx.moe_forward(0, xs[t], ntok, o)
+        ref.append(o.cpu().numpy())
+    xin = xs[0].clone()
+    gout = torch.empty(ntok * H, dtype=torch.float32, device="cuda")
+    ctx.moe_forward(0, xin, ntok, gout)  # scratch sized before the capture
+    torch.cuda.synchronize()
+    g = HipGraph(ctx.stream)
+    g.begin()
+    ctx.moe_forward(0, xin, ntok, gout, sync=False)
+    g.end()
+    try:
+        for rep in range(6):
+            t = rep % 3
+            xin.copy_(xs[t])
+            torch.cuda.synchronize()
+            g.launch()
+            ctx.sync()
+            assert np.array_equal(gout.cpu().numpy(), ref[t]), rep
+            u = (t + 1) % 3
+            o = torch.empty(ntok * H, dtype=torch.float32, device="cuda")
+            ctx.moe_forward(0, xs[u], ntok, o)  # eager work between the replays
+            assert np.array_equal(o.cpu().numpy(), ref[u]), rep
+    finally:
+        g.destroy()
+
+
 # ---- prefill: grouped GEMMs on the matrix cores (bf16 operands, fp32 accumulation) -------------
 PREFILL_RTOL = 1e-2  # bf16-MFMA prefill outputs (x and h rounded to bf16)
 
