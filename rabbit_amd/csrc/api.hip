@@ -688,8 +688,10 @@ int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H
 
 // accumulate: out += the layer's output (x and out must not overlap). The one-token down launch adds
 // in its own store; the other paths write the output to a scratch and add it after.
+// norm_w (the MoE sublayer): the layer's input is rmsnorm_1p(x, norm_w, eps) (qwen38/ops.rs:25-33),
+// computed inside the one-token router launch where it runs, else by a norm launch first.
 int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float *out, int32_t *ids_out,
-                    float *w_out, bool accumulate = false) {
+                    float *w_out, bool accumulate = false, const float *norm_w = nullptr, float eps = 0.0f) {
   auto lit = c->layers.find(layer);
   if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
   Layer &L = lit->second;
@@ -706,6 +708,12 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const int erows = E + (gated ? 1 : 0);
   const int P = S * k;
   const int npairs = P + (D.has_shared ? S : 0);
+  const float *xraw = x;
+  float *xn = nullptr;
+  if (norm_w) {
+    RBT_TRY(scratch_t(c, SC_NRM, (size_t)S * H, &xn));
+    x = xn;  // the layer's input from here on (written before the first launch that reads it)
+  }
 
   double *mid, *bnd;
   int32_t *ids;
@@ -779,10 +787,17 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     ga.shared_slot = sh_slot;
   }
   float *rec = nullptr;
+  // the sublayer's norm: in the one-token router launch (every workgroup normalises the token for its
+  // rows, workgroup 0 writes xn), else as its own launch
+  const bool fold_norm = norm_w && r1 && ((uintptr_t)xraw | (uintptr_t)norm_w) % 16 == 0;
+  if (norm_w && !fold_norm) HIP_OK(c, rbt::launch_rmsnorm(*c, xraw, norm_w, eps, xn, (size_t)S, (size_t)H, true));
   if (r1) {
     // one token: router logits, key records and the shared gate
     RBT_TRY(scratch_t(c, SC_RREC, (size_t)E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
-    HIP_OK(c, rbt::launch_router1(*c, ra, sgate, mid, bnd, shs, rec));
+    rbt::RouterArgs rr = ra;
+    if (fold_norm) rr.x = xraw;
+    HIP_OK(c, rbt::launch_router1(*c, rr, sgate, mid, bnd, shs, rec, fold_norm ? norm_w : nullptr, eps,
+                                  fold_norm ? xn : nullptr));
   } else {
     if (rbt::router_exact_ok(S, H) && ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0) {
       // batches: the reference's sequential fp32 logits themselves, then point intervals
@@ -1542,12 +1557,9 @@ static int moe_sublayer_dev(rbt_ctx *c, uint32_t layer, float *x, size_t s, cons
   if (lit == c->layers.end() || !lit->second.set) return fail(c, RBT_E_INVALID, "layer %u not set", layer);
   if (s == 0) return RBT_OK;
   if (!x || !post_ln) return fail(c, RBT_E_INVALID, "null x or post_ln");
-  const size_t H = lit->second.desc.hidden;
-  float *nrm;
-  RBT_TRY(scratch_t(c, SC_NRM, s * H, &nrm));
-  HIP_OK(c, rbt::launch_rmsnorm(*c, x, post_ln, eps, nrm, s, H, true));
-  // x += layer(nrm): the residual add rides in the layer's last store where it can
-  RBT_TRY(moe_forward_dev(c, layer, nrm, s, x, ids_out, w_out, true));
+  // x += layer(rmsnorm_1p(x)): the norm rides in the one-token router launch and the residual add
+  // in the layer's last store where they can
+  RBT_TRY(moe_forward_dev(c, layer, x, s, x, ids_out, w_out, true, post_ln, eps));
   return RBT_OK;
 }
 

@@ -15,7 +15,10 @@ template <bool ONE_PLUS>
 __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, float eps,
                                                  float *__restrict__ y, int n) {
   // rows up to 256 * R elements stay in registers: the row and the weights are loaded once, all
-  // loads issued together (an element-by-element walk waits on memory once per element)
+  // loads issued together (an element-by-element walk waits on memory once per element). Thread t
+  // holds elements 1024 c + 4 t + e (c < R / 4, e < 4) and sums their squares in that order, the
+  // order the one-token router launch uses when it normalises the token itself (router.hip
+  // norm1p_chunks), so both give the same row bit for bit.
   constexpr int R = 32;
   __shared__ double part[4];
   const float *xr = x + (long)blockIdx.x * n;
@@ -27,7 +30,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
   if (held) {
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      const int i = t + 256 * j;
+      const int i = 1024 * (j >> 2) + 4 * t + (j & 3);
       v[j] = i < n ? xr[i] : 0.0f;
       wv[j] = i < n ? w[i] : 0.0f;
     }
@@ -47,7 +50,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const float *__restrict__ x, co
   if (held) {
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      const int i = t + 256 * j;
+      const int i = 1024 * (j >> 2) + 4 * t + (j & 3);
       const float s = ONE_PLUS ? __fmul_rn(r, __fadd_rn(1.0f, wv[j])) : __fmul_rn(r, wv[j]);
       if (i < n) yr[i] = __fmul_rn(v[j], s);
     }

@@ -197,10 +197,13 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr,
                                 const SharedGateUp *sgu = nullptr);
 // Router launch of the one-token decode (no cross-workgroup waits): mid / bnd of every router row,
-// sh_scale (the shared gate's sigmoid, or 1) and rec (E * ROUTER1_REC_BYTES).
+// sh_scale (the shared gate's sigmoid, or 1) and rec (E * ROUTER1_REC_BYTES). With nw, a.x is the
+// raw token and the rows use rmsnorm_1p(a.x, nw, eps) (bit-identical to launch_rmsnorm's), which
+// the launch also writes to xn.
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                          float *sh_scale, void *rec);
+                          float *sh_scale, void *rec, const float *nw = nullptr, float eps = 0.0f,
+                          float *xn = nullptr);
 // Gate/up launch of the one-token decode (num_cu workgroups): the selection from rec in every
 // workgroup, the gate/up of the nr routed pairs (slots 0..nr-1, nr <= k + D1_KX) and, with
 // has_shared, of grp.shared_dev at slot nr, into hp (pair slot c at hp + 3 I c), and the routing

@@ -2058,22 +2058,69 @@ __device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)
 
 typedef float rbt_f4v __attribute__((ext_vector_type(4)));
 
+// rmsnorm_1p of the token (qwen38/ops.rs:25-33) in the workgroup: r = 1 / sqrt((sum_f64(v^2) / n)
+// as f32 + eps), v[i] *= r * (1 + w[i]), every fp32 operation rounded on its own. The squares are
+// exact in fp64 and summed in the registers' order (thread t: its chunks' elements 1024 c + 4 t ..
+// +3, then the wave totals in fixed order), so every workgroup gets the same r; the sum differs from
+// the reference's sequential one (and from k_rmsnorm's order) in the last fp64 bits only, which
+// change the fp32 mean square only within a few fp64 ulps of an fp32 rounding boundary.
+template <int NR>
+__device__ __forceinline__ void norm1p_chunks(LgLds<NR> &L, float4 (&xv)[RT_MAXH / 1024],
+                                              const float4 (&wv)[RT_MAXH / 1024], int H, float eps) {
+  constexpr int MC = RT_MAXH / 1024;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nch = H / 1024;
+  double acc = 0.0;
+#pragma unroll
+  for (int c = 0; c < MC; c++)
+    if (c < nch) {
+      acc += (double)xv[c].x * (double)xv[c].x;
+      acc += (double)xv[c].y * (double)xv[c].y;
+      acc += (double)xv[c].z * (double)xv[c].z;
+      acc += (double)xv[c].w * (double)xv[c].w;
+    }
+  acc = rbt_wave_total_d(acc);
+  if (lane == 0) L.sh[wave] = acc;
+  __syncthreads();
+  const double ms = (L.sh[0] + L.sh[1]) + (L.sh[2] + L.sh[3]);
+  const float r = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)H), eps)));
+#pragma unroll
+  for (int c = 0; c < MC; c++) {
+    xv[c].x = __fmul_rn(xv[c].x, __fmul_rn(r, __fadd_rn(1.0f, wv[c].x)));
+    xv[c].y = __fmul_rn(xv[c].y, __fmul_rn(r, __fadd_rn(1.0f, wv[c].y)));
+    xv[c].z = __fmul_rn(xv[c].z, __fmul_rn(r, __fadd_rn(1.0f, wv[c].z)));
+    xv[c].w = __fmul_rn(xv[c].w, __fmul_rn(r, __fadd_rn(1.0f, wv[c].w)));
+  }
+  __syncthreads();  // L.sh is the rows' scratch next
+}
+
 // Workgroup b computes RPW router rows: rows RPW b .. RPW b + RPW - 1 of the E router rows followed
 // by the shared-expert gate row (row E, when sgate is given: its fp64 sum gives sh_scale; it has no
 // key record). The rows' loads are issued together, then the rows are reduced two at a time.
+// With nw (the MoE sublayer), P.x is the raw token and every workgroup first normalises it
+// (rmsnorm_1p with weights nw, eps) for its rows; workgroup 0 writes the normalised token to xn.
 template <int RPW>
 __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
                                                  double *__restrict__ mid, double *__restrict__ bnd,
-                                                 float *__restrict__ sh_scale, KeyRec *__restrict__ rec) {
+                                                 float *__restrict__ sh_scale, KeyRec *__restrict__ rec,
+                                                 const float *__restrict__ nw, float eps, float *__restrict__ xn) {
   constexpr int MC = RT_MAXH / 1024, NR = RPW == 1 ? 1 : 2;
   __shared__ LgLds<NR> L;
   const int t = threadIdx.x, b = blockIdx.x;
   const int H = P.H, E = P.E, nch = H / 1024;
   if (sgate == nullptr && b == 0 && t == 0) sh_scale[0] = 1.0f;
   const int Rn = E + (sgate != nullptr ? 1 : 0), r0 = RPW * b;
-  if (r0 >= Rn) return;
+  if (r0 >= Rn && !(nw != nullptr && b == 0)) return;
   const float4 *x4 = reinterpret_cast<const float4 *>(P.x);
-  float4 xv[MC], w[RPW][MC];
+  float4 xv[MC], w[RPW][MC], wv[MC];
+  // the token (and the norm's weights) first: the memory counter retires loads in issue order, so
+  // the norm waits for them only, not for the rows' loads behind them
+#pragma unroll
+  for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
+  if (nw != nullptr) {
+    const float4 *n4 = reinterpret_cast<const float4 *>(nw);
+#pragma unroll
+    for (int c = 0; c < MC; c++) wv[c] = n4[min(c, nch - 1) * 256 + t];
+  }
   // unconditional loads (chunks past the row repeat its last one; rows past the end read row 0):
   // no waits between the rows
 #pragma unroll
@@ -2088,8 +2135,15 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
       w[j][c] = make_float4(v[0], v[1], v[2], v[3]);
     }
   }
+  if (nw != nullptr) {
+    norm1p_chunks<NR>(L, xv, wv, H, eps);
+    if (b == 0) {
 #pragma unroll
-  for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
+      for (int c = 0; c < MC; c++)
+        if (c < nch) reinterpret_cast<float4 *>(xn)[c * 256 + t] = xv[c];
+    }
+    if (r0 >= Rn) return;
+  }
 #pragma unroll
   for (int j = 0; j < RPW; j += NR) {
     const int ra = r0 + j, rb = ra + 1;
@@ -2344,17 +2398,18 @@ bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu) {
 }
 
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                          float *sh_scale, void *rec_buf) {
+                          float *sh_scale, void *rec_buf, const float *nw, float eps, float *xn) {
   KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
   if (!router1_ok(a, c.num_cu, nullptr) || (sgate && (uintptr_t)sgate % 16 != 0)) return hipErrorInvalidValue;
+  if (nw && (!xn || ((uintptr_t)nw | (uintptr_t)xn) % 16 != 0)) return hipErrorInvalidValue;
   const SelParams P = sel_params(a);
   // one row per workgroup while the grid fits the chip at once (the rows' reduction is on the
   // critical path: C1's 513 rows take 9.5 us as 257 x 2 rows, 11.8 us as 129 x 4)
   const int rn = a.E + (sgate ? 1 : 0);
   if (rn <= 4 * c.num_cu)  // four one-row workgroups fit on a CU
-    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn);
   else
-    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec);
+    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn);
   return hipGetLastError();
 }
 

@@ -84,3 +84,26 @@ def test_moe_sublayer_host_buffers(ctx, orc):
     dx = torch.from_numpy(x).cuda()
     ctx.moe_sublayer(0, dx, S, torch.from_numpy(ln).cuda(), 1e-6)
     assert bits_equal(dx.cpu().numpy(), xh)
+
+
+@pytest.mark.parametrize("name,ntok", [("c1", 1), ("c3", 1), ("c1", 2)])
+def test_moe_sublayer_equals_its_composition(ctx, orc, name, ntok):
+    """The sublayer (one token: the norm computed inside the router launch, the residual add in the
+    down launch's store) equals its parts run one by one, bit for bit: rbt_rmsnorm_1p_d, then
+    moe_forward on the normalised rows, then x + out."""
+    import rabbit_amd.workloads as W
+    import torch
+    cfg = W.CONFIGS[name]
+    W.build_layer(ctx, cfg, layer=0, seed=1000)
+    H = cfg.hidden
+    ln = torch.from_numpy(normal(H, 77, 0.1)).cuda()
+    for seed in range(3):
+        x = torch.from_numpy(W.tokens(cfg, ntok, 500 + seed)).cuda()
+        nrm = x.clone()
+        ctx.rmsnorm(nrm, ln, ntok, H, 1e-6, one_plus=True)
+        out = torch.empty(ntok * H, dtype=torch.float32, device="cuda")
+        ctx.moe_forward(0, nrm, ntok, out)
+        exp = (x.reshape(-1) + out).cpu().numpy()
+        got = x.clone()
+        ctx.moe_sublayer(0, got, ntok, ln, 1e-6)
+        assert bits_equal(got.cpu().numpy().ravel(), exp), seed
