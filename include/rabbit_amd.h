@@ -301,6 +301,40 @@ int rbt_moe_sublayer(rbt_ctx *ctx, uint32_t layer, float *x, size_t s, const flo
 int rbt_moe_sublayer_d(rbt_ctx *ctx, uint32_t layer, float *x, size_t s, const float *post_ln, float eps,
                        int32_t *ids_out, float *w_out);
 
+/* ---- token mixers of Qwen 3.8 (one decode token; device buffers) ------------------------------ */
+/* Gated DeltaNet (69 of the 92 layers): the part of qwen38/generate.rs:196-219 gdn_step between
+ * the input projections (in_proj_qkv -> qkv_pre, in_proj_z/a/b -> z, a, b, each an rbt_matmul_qt_d)
+ * and out_proj: ShortConvState::step (kimi_linear/short_conv.rs:58-85) then gdn::step_token
+ * (qwen38/gdn.rs:142-196). conv_state [conv_dim, conv_kernel - 1] (conv_dim = 2 n_k_heads
+ * head_k_dim + n_v_heads head_v_dim) and states [n_v_heads, head_k_dim, head_v_dim] are the layer's
+ * carried state (zero at the start, updated in place: GdnLayerState, KdaState::new kda.rs:99);
+ * qkv_pre [conv_dim], z [n_v_heads head_v_dim], a, b [n_v_heads]; out [n_v_heads head_v_dim].
+ * head_v_dim must divide 256 and head_k_dim be at most 64 * 256 / head_v_dim (RBT_E_UNSUPPORTED
+ * otherwise; Qwen 3.8: 128 x 128). */
+typedef struct {
+    size_t n_v_heads, n_k_heads, head_k_dim, head_v_dim, conv_kernel;
+    const float *conv_weight;  /* [conv_dim, conv_kernel] (conv1d weight, depthwise, no bias) */
+    const float *a_log;        /* [n_v_heads] A_log */
+    const float *dt_bias;      /* [n_v_heads] */
+    const float *norm_weight;  /* [head_v_dim] the gated RMSNorm's weight */
+    float eps;
+} rbt_gdn_desc;
+int rbt_gdn_step_d(rbt_ctx *ctx, const rbt_gdn_desc *desc, float *conv_state, float *states,
+                   const float *qkv_pre, const float *z, const float *a, const float *b, float *out);
+/* GQA attention (23 of the 92 layers): the part of qwen38/generate.rs:226-255 attn_step between the
+ * projections (q_proj -> qg [n_heads, 2 head_dim] as [query, gate] per head, k_proj -> k, v_proj
+ * -> v, each [n_kv_heads head_dim]) and o_proj: split_query_gate (attention.rs:122), norm_heads
+ * (:138), rope_half (:160), KvCache::push (:76) at position pos, attend (:190) over positions
+ * 0..pos, apply_output_gate (:221). k_cache / v_cache [cap, n_kv_heads, head_dim] hold positions
+ * 0..pos-1 (the cache's len is pos). ctx_out [n_heads head_dim]. */
+typedef struct {
+    size_t n_heads, n_kv_heads, head_dim, rope_dim;
+    float theta, attn_scale, eps;
+    const float *q_norm, *k_norm;  /* [head_dim] each, (1 + w) RMSNorm weights */
+} rbt_gqa_desc;
+int rbt_gqa_step_d(rbt_ctx *ctx, const rbt_gqa_desc *desc, float *k_cache, float *v_cache, size_t cap, size_t pos,
+                   const float *qg, const float *k, const float *v, float *ctx_out);
+
 /* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
 typedef struct {
     double router_ms;    /* router logits + top-k selection + grouping (one-token MXFP4 calls: also

@@ -116,6 +116,18 @@ def lib():
         L.orc_rmsnorm_1p.argtypes = [P, P, S, F]
         L.orc_moe_sublayer.restype = I
         L.orc_moe_sublayer.argtypes = [C.POINTER(OrcMoeLayer), P, S, P, F, I, P, P]
+        L.orc_short_conv_step.argtypes = [P, S, S, P, P, P]
+        L.orc_gdn_alpha.restype = F
+        L.orc_gdn_alpha.argtypes = [F, F, F]
+        L.orc_kda_step.argtypes = [P, S, S, P, P, P, F, F, P]
+        L.orc_gdn_prepare_qk.argtypes = [P, P, S]
+        L.orc_gdn_output_gate.argtypes = [P, P, P, S, F]
+        L.orc_gdn_step_token.restype = I
+        L.orc_gdn_step_token.argtypes = [P, S, S, S, P, S, P, P, P, P, P, P, F, P]
+        L.orc_rope_half.argtypes = [P, S, S, F]
+        L.orc_gqa_attend.argtypes = [P, S, P, P, S, S, S, F, P]
+        L.orc_gqa_step.restype = I
+        L.orc_gqa_step.argtypes = [P, P, P, S, S, S, P, P, F, S, F, F, P, P, S, P]
         L.orc_synth_mix64.restype = C.c_uint64
         L.orc_synth_mix64.argtypes = [C.c_uint64]
         L.orc_synth_mxfp4.argtypes = [P, P, S, S, C.c_uint64, C.c_uint32, C.c_uint32]
@@ -315,6 +327,109 @@ def rmsnorm_1p(v, w, eps):
         lib().orc_rmsnorm_1p(_p(row), _p(w), w.size, eps)
         rows[r] = row
     return rows.reshape(v.shape)
+
+
+# --- Qwen 3.8 token mixers (rabbit_oracle_mixers.c) ------------------------------------------
+class GdnState:
+    """One GDN layer's carried state: the short conv's history [conv_dim, kernel - 1] and the
+    per-V-head delta-rule matrices [n_v, d_k, d_v] (kimi_linear/short_conv.rs:17-27,
+    kimi_linear/kda.rs:92-101), all zero at the start."""
+
+    def __init__(self, n_v, n_k, d_k, d_v, kernel=4):
+        self.n_v, self.n_k, self.d_k, self.d_v, self.kernel = n_v, n_k, d_k, d_v, kernel
+        self.key_dim, self.value_dim = n_k * d_k, n_v * d_v
+        self.conv_dim = 2 * self.key_dim + self.value_dim
+        self.conv = np.zeros(self.conv_dim * (kernel - 1), np.float32)
+        self.heads = np.zeros(n_v * d_k * d_v, np.float32)
+
+
+def short_conv_step(state: GdnState, x, weight):
+    """kimi_linear/short_conv.rs:58-85 (updates state.conv); returns the conv output row."""
+    x, weight = _f32(x), _f32(weight)
+    out = np.empty(state.conv_dim, np.float32)
+    lib().orc_short_conv_step(_p(state.conv), state.conv_dim, state.kernel, _p(x), _p(weight), _p(out))
+    return out
+
+
+def gdn_alpha(a_log, a, dt_bias) -> float:
+    return lib().orc_gdn_alpha(a_log, a, dt_bias)
+
+
+def gdn_prepare_qk(q, k):
+    q, k = np.array(q, np.float32, copy=True), np.array(k, np.float32, copy=True)
+    lib().orc_gdn_prepare_qk(_p(q), _p(k), q.size)
+    return q, k
+
+
+def gdn_output_gate(o, norm_weight, z, eps):
+    o = np.array(o, np.float32, copy=True)
+    nw, z = _f32(norm_weight), _f32(z)
+    lib().orc_gdn_output_gate(_p(o), _p(nw), _p(z), o.size, eps)
+    return o
+
+
+def kda_step(s, q, k, v, alpha, beta):
+    """kimi_linear/kda.rs:132-166 for one head; s [d_k, d_v] is updated in place. Returns o."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    assert s.dtype == np.float32 and s.flags["C_CONTIGUOUS"]
+    o = np.empty(v.size, np.float32)
+    lib().orc_kda_step(_p(s), q.size, v.size, _p(q), _p(k), _p(v), alpha, beta, _p(o))
+    return o
+
+
+def gdn_step_token(state: GdnState, qkv, z, a, b, a_log, dt_bias, norm_weight, eps):
+    """qwen38/gdn.rs:142-196 (state.heads updated; qkv is the post-convolution row, not modified)."""
+    qkv = np.array(qkv, dtype=np.float32, copy=True)
+    z, a, b, a_log, dt_bias, nw = (_f32(v) for v in (z, a, b, a_log, dt_bias, norm_weight))
+    out = np.empty(state.value_dim, np.float32)
+    rc = lib().orc_gdn_step_token(_p(state.heads), state.n_v, state.d_k, state.d_v, _p(qkv), state.key_dim,
+                                  _p(z), _p(a), _p(b), _p(a_log), _p(dt_bias), _p(nw), eps, _p(out))
+    if rc:
+        raise ValueError("bad GDN shape")
+    return out
+
+
+def gdn_step(state: GdnState, qkv_pre, conv_weight, z, a, b, a_log, dt_bias, norm_weight, eps):
+    """qwen38/generate.rs:196-219 between the projections: the short conv, then step_token."""
+    return gdn_step_token(state, short_conv_step(state, qkv_pre, conv_weight), z, a, b, a_log, dt_bias,
+                          norm_weight, eps)
+
+
+def rope_half(v, rope_dim, pos, theta):
+    v = np.array(v, dtype=np.float32, copy=True)
+    lib().orc_rope_half(_p(v), rope_dim, pos, theta)
+    return v
+
+
+def gqa_attend(q, k_cache, v_cache, n_kv, head_dim, scale):
+    """qwen38/attention.rs:190-217; k_cache / v_cache [positions, n_kv * head_dim]."""
+    q, kc, vc = _f32(q), _f32(k_cache), _f32(v_cache)
+    positions = kc.size // (n_kv * head_dim)
+    out = np.empty(q.size, np.float32)
+    lib().orc_gqa_attend(_p(q), q.size // head_dim, _p(kc), _p(vc), positions, n_kv, head_dim, scale, _p(out))
+    return out
+
+
+class KvCache:
+    """qwen38/attention.rs:54-82: K and V rows [cap, n_kv * head_dim], positions appended in order."""
+
+    def __init__(self, n_kv, head_dim, cap):
+        self.n_kv, self.head_dim, self.cap, self.len = n_kv, head_dim, cap, 0
+        self.k = np.zeros((cap, n_kv * head_dim), np.float32)
+        self.v = np.zeros((cap, n_kv * head_dim), np.float32)
+
+
+def gqa_step(kv: KvCache, qg, k, v, n_heads, q_norm, k_norm, eps, rope_dim, theta, attn_scale):
+    """qwen38/generate.rs:226-255 between the projections, at position kv.len (appends to kv)."""
+    qg, k, v, qn, kn = (_f32(a) for a in (qg, k, v, q_norm, k_norm))
+    assert kv.len < kv.cap
+    ctx = np.empty(n_heads * kv.head_dim, np.float32)
+    rc = lib().orc_gqa_step(_p(qg), _p(k), _p(v), n_heads, kv.n_kv, kv.head_dim, _p(qn), _p(kn), eps, rope_dim,
+                            theta, attn_scale, _p(kv.k), _p(kv.v), kv.len, _p(ctx))
+    if rc:
+        raise ValueError("bad GQA shape")
+    kv.len += 1
+    return ctx
 
 
 # --- experts and layers ------------------------------------------------------------------------

@@ -162,6 +162,36 @@ void orc_rmsnorm_1p(float *v, const float *w, size_t n, float eps);
 int orc_moe_sublayer(const orc_moe_layer *L, float *x, size_t s, const float *post_ln, float eps, int simd,
                      int32_t *ids_out, float *w_out);
 
+/* --- Qwen 3.8 token mixers (rabbit_oracle_mixers.c) ---------------------------------------- */
+/* kimi_linear/short_conv.rs:58-85: out[c] = sum_t w[c,t] hist[c,t] + w[c,K-1] x[c], then the
+ * per-channel history [d_inner, kernel - 1] shifts in x. weight is [d_inner, kernel]. */
+void orc_short_conv_step(float *history, size_t d_inner, size_t kernel, const float *x, const float *weight,
+                         float *out);
+/* kimi_linear/kda.rs:65-76 (lower_bound None) for one scalar gate. */
+float orc_gdn_alpha(float a_log, float a, float dt_bias);
+/* kimi_linear/kda.rs:132-166 for one head with a broadcast alpha: s [d_k, d_v] updated, o [d_v]. */
+void orc_kda_step(float *s, size_t d_k, size_t d_v, const float *q, const float *k, const float *v, float alpha,
+                  float beta, float *o);
+/* qwen38/gdn.rs:110-118 (q, k of one K head, in place) and :122-128 (one head's output gate). */
+void orc_gdn_prepare_qk(float *q, float *k, size_t d_k);
+void orc_gdn_output_gate(float *o, const float *norm_weight, const float *z, size_t d_v, float eps);
+/* qwen38/gdn.rs:142-196: states [n_v, d_k, d_v] updated; qkv [2 key_dim + n_v d_v] is the
+ * post-convolution row (SiLU applied in place); out [n_v d_v]. Returns -1 on a bad shape. */
+int orc_gdn_step_token(float *states, size_t n_v, size_t d_k, size_t d_v, float *qkv, size_t key_dim,
+                       const float *z, const float *a, const float *b, const float *a_log, const float *dt_bias,
+                       const float *norm_weight, float eps, float *out);
+/* qwen38/attention.rs:160-172, one head in place. */
+void orc_rope_half(float *v, size_t rope_dim, size_t pos, float theta);
+/* qwen38/attention.rs:190-217 over cache positions 0..positions-1 ([positions, n_kv, head_dim]). */
+void orc_gqa_attend(const float *q, size_t n_heads, const float *k_cache, const float *v_cache, size_t positions,
+                    size_t n_kv, size_t head_dim, float scale, float *out);
+/* qwen38/generate.rs:226-255 between the projections: split q|gate per head, (1+w) RMSNorm of the q
+ * and k heads, partial RoPE, push k / v at position pos, attend over positions 0..pos, sigmoid gate.
+ * ctx [n_heads head_dim]. Returns -1 on a bad shape. */
+int orc_gqa_step(const float *qg, const float *k_in, const float *v_in, size_t n_heads, size_t n_kv, size_t head_dim,
+                 const float *q_norm, const float *k_norm, float eps, size_t rope_dim, float theta, float attn_scale,
+                 float *k_cache, float *v_cache, size_t pos, float *ctx);
+
 /* --- synthetic workload generator (shared bit-for-bit with rabbit_amd's device generator) --- */
 uint64_t orc_synth_mix64(uint64_t z);
 void orc_synth_mxfp4(uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,

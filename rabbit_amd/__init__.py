@@ -335,6 +335,33 @@ class Context:
     def synth_i4g(self, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo=0.005, s_hi=0.02):
         self.check(self.lib.rbt_synth_i4g_d(self.h, data_ptr, scale_ptr, rows, cols, gs, seed, s_lo, s_hi))
 
+    # -- token mixers (device tensors) ------------------------------------------------------
+    def gdn_step(self, n_v, n_k, d_k, d_v, conv_weight, a_log, dt_bias, norm_weight, eps, conv_state, states,
+                 qkv_pre, z, a, b, out, kernel=4, sync=True):
+        """rbt_gdn_step_d: one token through a GDN layer's conv + step_token (qwen38/gdn.rs:142);
+        conv_state and states are updated in place."""
+        d = abi.RbtGdnDesc(n_v, n_k, d_k, d_v, kernel, _ptr(conv_weight), _ptr(a_log), _ptr(dt_bias),
+                           _ptr(norm_weight), eps)
+        if sync:
+            self._torch_sync()
+        self.check(self.lib.rbt_gdn_step_d(self.h, C.byref(d), _ptr(conv_state), _ptr(states), _ptr(qkv_pre),
+                                           _ptr(z), _ptr(a), _ptr(b), _ptr(out)))
+        if sync:
+            self.sync()
+        return out
+
+    def gqa_step(self, n_heads, n_kv, head_dim, rope_dim, theta, attn_scale, eps, q_norm, k_norm, k_cache, v_cache,
+                 cap, pos, qg, k, v, out, sync=True):
+        """rbt_gqa_step_d: one token of GQA attention at position pos (qwen38/generate.rs:226-255)."""
+        d = abi.RbtGqaDesc(n_heads, n_kv, head_dim, rope_dim, theta, attn_scale, eps, _ptr(q_norm), _ptr(k_norm))
+        if sync:
+            self._torch_sync()
+        self.check(self.lib.rbt_gqa_step_d(self.h, C.byref(d), _ptr(k_cache), _ptr(v_cache), cap, pos, _ptr(qg),
+                                           _ptr(k), _ptr(v), _ptr(out)))
+        if sync:
+            self.sync()
+        return out
+
     # -- instrumentation --------------------------------------------------------------------
     def profile_enable(self, on: bool = True):
         self.check(self.lib.rbt_profile_enable(self.h, int(on)))

@@ -67,6 +67,18 @@ _P, _S, _I, _F, _U32, _U64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_float, C.c_u
 _CTX = C.c_void_p
 
 
+class RbtGdnDesc(C.Structure):
+    _fields_ = [("n_v_heads", C.c_size_t), ("n_k_heads", C.c_size_t), ("head_k_dim", C.c_size_t),
+                ("head_v_dim", C.c_size_t), ("conv_kernel", C.c_size_t), ("conv_weight", C.c_void_p),
+                ("a_log", C.c_void_p), ("dt_bias", C.c_void_p), ("norm_weight", C.c_void_p), ("eps", C.c_float)]
+
+
+class RbtGqaDesc(C.Structure):
+    _fields_ = [("n_heads", C.c_size_t), ("n_kv_heads", C.c_size_t), ("head_dim", C.c_size_t),
+                ("rope_dim", C.c_size_t), ("theta", C.c_float), ("attn_scale", C.c_float), ("eps", C.c_float),
+                ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
 class RbtKernelStat(C.Structure):
     _fields_ = [("name", C.c_char * 160), ("launches", C.c_uint64), ("total_ms", C.c_double)]
 
@@ -131,6 +143,8 @@ SIGNATURES = {
     "rbt_rmsnorm_1p_d": (_I, [_CTX, _P, _P, _S, _S, _F]),
     "rbt_moe_sublayer": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),
     "rbt_moe_sublayer_d": (_I, [_CTX, _U32, _P, _S, _P, _F, _P, _P]),
+    "rbt_gdn_step_d": (_I, [_CTX, C.POINTER(RbtGdnDesc), _P, _P, _P, _P, _P, _P, _P]),
+    "rbt_gqa_step_d": (_I, [_CTX, C.POINTER(RbtGqaDesc), _P, _P, _S, _S, _P, _P, _P, _P]),
     "rbt_profile_enable": (_I, [_CTX, _I]),
     "rbt_profile_read": (_I, [_CTX, C.POINTER(RbtProfile), _I]),
     "rbt_profile_kernels": (_I, [_CTX, _I]),

@@ -89,6 +89,8 @@ enum ScratchSlot {
   SC_PLN,   // sublayer (host call): post_ln staged
   SC_XL,    // latent MoE: x projected down
   SC_ROUTED,  // latent MoE: summed routed rows
+  SC_MIXA,    // mixers: the GDN conv output / the GQA prepared queries
+  SC_MIXB,    // mixers: the GQA softmax partials
   SC_N
 };
 
@@ -1532,6 +1534,49 @@ int rbt_moe_layer_set(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
 int rbt_moe_layer_set_device(rbt_ctx *c, uint32_t layer, const rbt_moe_layer_desc *d) {
   if (!c) return RBT_E_INVALID;
   return layer_set(c, layer, d, true);
+}
+
+// ---- token mixers (qwen38/gdn.rs, qwen38/attention.rs) ------------------------------------------
+int rbt_gdn_step_d(rbt_ctx *c, const rbt_gdn_desc *d, float *conv_state, float *states, const float *qkv_pre,
+                   const float *z, const float *a, const float *b, float *out) {
+  if (!c || !d) return RBT_E_INVALID;
+  if (!conv_state || !states || !qkv_pre || !z || !a || !b || !out || !d->conv_weight || !d->a_log || !d->dt_bias ||
+      !d->norm_weight)
+    return fail(c, RBT_E_INVALID, "null GDN buffer");
+  const size_t nv = d->n_v_heads, nk = d->n_k_heads, dk = d->head_k_dim, dv = d->head_v_dim, K = d->conv_kernel;
+  if (nv == 0 || nk == 0 || dk == 0 || dv == 0 || K == 0 || nv % nk || nv > (1u << 20) || dk > 4096 || dv > 4096 ||
+      K > 64)
+    return fail(c, RBT_E_INVALID, "bad GDN shape (heads %zu/%zu, dims %zu/%zu, kernel %zu)", nv, nk, dk, dv, K);
+  if (!rbt::gdn_ok((int)nv, (int)nk, (int)dk, (int)dv))
+    return fail(c, RBT_E_UNSUPPORTED, "GDN head dims %zu x %zu: head_v_dim must divide 256 and head_k_dim be at "
+                "most 64 * 256 / head_v_dim", dk, dv);
+  const size_t conv_dim = 2 * nk * dk + nv * dv;
+  float *act;
+  RBT_TRY(scratch_t(c, SC_MIXA, conv_dim, &act));
+  HIP_OK(c, rbt::launch_gdn(*c, conv_state, d->conv_weight, (int)K, states, qkv_pre, z, a, b, d->a_log, d->dt_bias,
+                            d->norm_weight, d->eps, (int)nv, (int)nk, (int)dk, (int)dv, act, out));
+  return RBT_OK;
+}
+
+int rbt_gqa_step_d(rbt_ctx *c, const rbt_gqa_desc *d, float *k_cache, float *v_cache, size_t cap, size_t pos,
+                   const float *qg, const float *k, const float *v, float *ctx_out) {
+  if (!c || !d) return RBT_E_INVALID;
+  if (!k_cache || !v_cache || !qg || !k || !v || !ctx_out || !d->q_norm || !d->k_norm)
+    return fail(c, RBT_E_INVALID, "null GQA buffer");
+  const size_t nh = d->n_heads, nkv = d->n_kv_heads, hd = d->head_dim;
+  if (nh == 0 || nkv == 0 || nh % nkv || hd == 0 || nh > 4096)
+    return fail(c, RBT_E_INVALID, "bad GQA shape (heads %zu over %zu kv heads)", nh, nkv);
+  if (pos >= cap) return fail(c, RBT_E_INVALID, "position %zu is outside the cache (capacity %zu)", pos, cap);
+  if (pos >= (size_t)INT32_MAX) return fail(c, RBT_E_UNSUPPORTED, "position %zu", pos);
+  if (!rbt::gqa_ok((int)nh, (int)nkv, (int)hd, (int)d->rope_dim))
+    return fail(c, RBT_E_UNSUPPORTED, "GQA shape: head_dim %zu (at most 1024), rope_dim %zu, %zu query heads per kv "
+                "head", hd, d->rope_dim, nh / nkv);
+  float *qp, *part;
+  RBT_TRY(scratch_t(c, SC_MIXA, nh * hd, &qp));
+  RBT_TRY(scratch_t(c, SC_MIXB, rbt::gqa_part_floats((int)nh, (int)nkv, (int)hd, (int)pos + 1), &part));
+  HIP_OK(c, rbt::launch_gqa(*c, qg, k, v, (int)nh, (int)nkv, (int)hd, d->q_norm, d->k_norm, d->eps, (int)d->rope_dim,
+                            d->theta, d->attn_scale, (int)pos, k_cache, v_cache, qp, part, ctx_out));
+  return RBT_OK;
 }
 
 int rbt_rmsnorm_d(rbt_ctx *c, float *v, const float *w, size_t s, size_t n, float eps) {

@@ -227,6 +227,20 @@ hipError_t launch_single_rows(const Ctx &c, const int32_t *ids, const float *w, 
 hipError_t launch_accumulate(const Ctx &c, const float *y, int S, int H, const int *pair_tok, const float *pair_w,
                              const int *nr, float *out);
 
+// mixers.hip: Qwen 3.8's token mixers for one token.
+bool gdn_ok(int n_v, int n_k, int d_k, int d_v);
+// act: conv_dim floats of scratch (the conv output after SiLU).
+hipError_t launch_gdn(const Ctx &c, float *conv_hist, const float *conv_w, int K, float *states,
+                      const float *qkv_pre, const float *z, const float *a, const float *b, const float *a_log,
+                      const float *dt_bias, const float *norm_w, float eps, int n_v, int n_k, int d_k, int d_v,
+                      float *act, float *out);
+bool gqa_ok(int n_heads, int n_kv, int hd, int rope_dim);
+// Scratch of the GQA step: qp (n_heads * hd floats) and part (gqa_part_floats).
+size_t gqa_part_floats(int n_heads, int n_kv, int hd, int positions);
+hipError_t launch_gqa(const Ctx &c, const float *qg, const float *k, const float *v, int n_heads, int n_kv, int hd,
+                      const float *qn, const float *kn, float eps, int rope_dim, float theta, float scale, int pos,
+                      float *kc, float *vc, float *qp, float *part, float *ctx);
+
 // synth.hip
 hipError_t launch_synth_mxfp4(const Ctx &c, uint8_t *data, uint8_t *scale, size_t rows, size_t cols, uint64_t seed,
                               uint32_t lo, uint32_t hi);
