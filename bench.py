@@ -855,12 +855,125 @@ def bench_sublayer(args, ctx, hip, cfg):
     ctx.close()
 
 
+def bench_mix(args, ctx, hip):
+    """Qwen 3.8's token mixers, one decode token per call: a Gated DeltaNet layer (128 V heads over 16
+    K heads, 128 x 128 state per head, conv_dim 20480) and a GQA layer (64 query heads over 4 KV
+    heads, head_dim 256) at context length args.context, each graph-replayed with its state carried.
+    Roofline: the bytes each step must move (GDN: the state read and written plus the conv rows;
+    GQA: the cached K and V rows read plus the new row written) over the step's duration."""
+    import torch
+    from oracle import oracle as O
+    rng = np.random.default_rng(args.seed)
+    steps, warm = args.steps, args.warmup
+    # ---- GDN
+    n_v, n_k, d_k, d_v, K = 128, 16, 128, 128, 4
+    conv_dim = 2 * n_k * d_k + n_v * d_v
+    f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    conv_w = f32(rng.standard_normal((conv_dim, K)) * 0.5)
+    a_log, dt = f32(rng.standard_normal(n_v) * 0.5), f32(rng.standard_normal(n_v) * 0.5)
+    nw = f32(1.0 + 0.1 * rng.standard_normal(d_v))
+    conv_st = torch.zeros(conv_dim * (K - 1), dtype=torch.float32, device="cuda")
+    states = torch.zeros(n_v * d_k * d_v, dtype=torch.float32, device="cuda")
+    n = steps + warm
+    xs = f32(rng.standard_normal((n, conv_dim)))
+    zs = f32(rng.standard_normal((n, n_v * d_v)))
+    As, Bs = f32(rng.standard_normal((n, n_v))), f32(rng.standard_normal((n, n_v)))
+    out = torch.empty(n, n_v * d_v, dtype=torch.float32, device="cuda")
+
+    def gdn_call(t):
+        ctx.gdn_step(n_v, n_k, d_k, d_v, conv_w, a_log, dt, nw, 1e-6, conv_st, states, xs[t], zs[t], As[t], Bs[t],
+                     out[t], kernel=K, sync=False)
+
+    for t in range(warm):
+        gdn_call(t)
+    ctx.sync()
+    G = max(1, min(args.graph_tokens, steps))
+    wall, _ = graph_time(hip, ctx, gdn_call, warm, steps, G)
+    gdn_us = wall / steps * 1e6
+    tab = per_call(kernel_table(ctx, lambda: [gdn_call(t) for t in range(warm, n)]), steps)
+    state_b = n_v * d_k * d_v * 4
+    conv_b = conv_dim * (4 * K + 4 * (K - 1) * 2 + 4 + 4)  # weights, history read + written, x, output
+    gdn_bytes = 2 * state_b + conv_b + 2 * n_v * d_v * 4
+    head = next(r for r in tab if r[0] == "k_gdn_head")
+    gdn_rl = {"bound": "hbm", "kernel": "k_gdn_head", "achieved": round(2 * state_b / (head[2] * 1e-6) / 1e9, 1),
+              "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(2 * state_b / (head[2] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+              "bytes_per_launch": 2 * state_b, "launch_us": round(head[2], 3), "traffic": None,
+              "note": "the heads' delta-rule states read and written once per token"}
+    # ---- GQA
+    nh, nkv, hd, rd = 64, 4, 256, 64
+    T = args.context
+    cap = T + steps + warm
+    kc = f32(rng.standard_normal((cap, nkv * hd)))
+    vc = f32(rng.standard_normal((cap, nkv * hd)))
+    qn, kn = f32(0.1 * rng.standard_normal(hd)), f32(0.1 * rng.standard_normal(hd))
+    qgs = f32(rng.standard_normal((n, 2 * nh * hd)))
+    ks, vs = f32(rng.standard_normal((n, nkv * hd))), f32(rng.standard_normal((n, nkv * hd)))
+    ctx_out = torch.empty(n, nh * hd, dtype=torch.float32, device="cuda")
+
+    def gqa_call(t):
+        ctx.gqa_step(nh, nkv, hd, rd, 1e7, 1.0 / 16.0, 1e-6, qn, kn, kc, vc, cap, T + t, qgs[t], ks[t], vs[t],
+                     ctx_out[t], sync=False)
+
+    for t in range(warm):
+        gqa_call(t)
+    ctx.sync()
+    wall, _ = graph_time(hip, ctx, gqa_call, warm, steps, G)
+    gqa_us = wall / steps * 1e6
+    tab2 = per_call(kernel_table(ctx, lambda: [gqa_call(t) for t in range(warm, n)]), steps)
+    kv_b = (T + warm + steps // 2) * nkv * hd * 4 * 2
+    sc = next(r for r in tab2 if r[0] == "k_gqa_chunk")
+    gqa_rl = {"bound": "hbm", "kernel": "k_gqa_chunk", "achieved": round(kv_b / (sc[2] * 1e-6) / 1e9, 1),
+              "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(kv_b / (sc[2] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+              "bytes_per_launch": int(kv_b), "launch_us": round(sc[2], 3), "traffic": None,
+              "note": f"the cached K and V rows of ~{T + warm + steps // 2} positions read once per token"}
+    # ---- CPU: the oracle's restatement (scalar, one thread), a few tokens of each
+    cpu = None
+    if not args.no_cpu:
+        info = cpu_info()
+        st = O.GdnState(n_v, n_k, d_k, d_v, K)
+        cw, al, dtn, nwn = (v.cpu().numpy() for v in (conv_w, a_log, dt, nw))
+        xn, zn, an, bn = (v[:8].cpu().numpy() for v in (xs, zs, As, Bs))
+        t0 = time.perf_counter()
+        for t in range(8):
+            O.gdn_step(st, xn[t], cw, zn[t], an[t], bn[t], al, dtn, nwn, 1e-6)
+        g_cpu = (time.perf_counter() - t0) / 8 * 1e6
+        kv = O.KvCache(nkv, hd, T + 4)
+        kv.k[:T] = kc[:T].cpu().numpy()
+        kv.v[:T] = vc[:T].cpu().numpy()
+        kv.len = T
+        qn_, kn_ = qn.cpu().numpy(), kn.cpu().numpy()
+        t0 = time.perf_counter()
+        for t in range(4):
+            O.gqa_step(kv, qgs[t].cpu().numpy(), ks[t].cpu().numpy(), vs[t].cpu().numpy(), nh, qn_, kn_, 1e-6, rd, 1e7,
+                       1.0 / 16.0)
+        q_cpu = (time.perf_counter() - t0) / 4 * 1e6
+        cpu = cpu_line(g_cpu + q_cpu, None, "us/token (one GDN + one GQA layer)", gdn_bytes + kv_b,
+                       dict(info, threads=1), "port",
+                       f"8 GDN tokens and 4 GQA tokens at context {T}, the oracle's scalar restatement",
+                       {"gdn_us": round(g_cpu, 1), "gqa_us": round(q_cpu, 1)})
+    res = {
+        "metric": "Qwen 3.8 token mixers, decode us/token (one GDN layer + one GQA layer)",
+        "value": round(gdn_us + gqa_us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round((gdn_us + gqa_us) / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "qwen38_mixers", "gdn": f"{n_v}/{n_k} heads, {d_k}x{d_v} state, conv 4",
+                   "gqa": f"{nh}/{nkv} heads x {hd}, rope {rd}", "context": T, "graph_tokens": G},
+        "gdn_us": round(gdn_us, 3), "gqa_us": round(gqa_us, 3),
+        "roofline": gdn_rl, "roofline_gqa": gqa_rl,
+        "kernels": dict(kernels_json(tab), **kernels_json(tab2)),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+    ctx.close()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1024)
     ap.add_argument("--warmup", type=int, default=64)
-    ap.add_argument("--config", default="c1", choices=["c0", "c1", "c2", "c3", "c4", "mm", "k3l", "c1s"])
+    ap.add_argument("--config", default="c1", choices=["c0", "c1", "c2", "c3", "c4", "mm", "k3l", "c1s", "mix"])
+    ap.add_argument("--context", type=int, default=4096, help="mix: GQA context length (cached positions)")
     ap.add_argument("--graph-tokens", type=int, default=64)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
@@ -893,6 +1006,8 @@ def main():
         return bench_sublayer(args, ctx, hip, W.CONFIGS["c1"])
     if args.config == "mm":
         return bench_mm(args, ctx, hip)
+    if args.config == "mix":
+        return bench_mix(args, ctx, hip)
     cfg = W.CONFIGS[args.config]
     if args.config == "k3l":
         return bench_latent(args, ctx, hip, cfg)

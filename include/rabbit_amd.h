@@ -309,8 +309,8 @@ int rbt_moe_sublayer_d(rbt_ctx *ctx, uint32_t layer, float *x, size_t s, const f
  * head_k_dim + n_v_heads head_v_dim) and states [n_v_heads, head_k_dim, head_v_dim] are the layer's
  * carried state (zero at the start, updated in place: GdnLayerState, KdaState::new kda.rs:99);
  * qkv_pre [conv_dim], z [n_v_heads head_v_dim], a, b [n_v_heads]; out [n_v_heads head_v_dim].
- * head_v_dim must divide 256 and head_k_dim be at most 64 * 256 / head_v_dim (RBT_E_UNSUPPORTED
- * otherwise; Qwen 3.8: 128 x 128). */
+ * head_v_dim must be a multiple of 4 dividing 2048 (at most 512) and head_k_dim even and at most
+ * 8192 / head_v_dim (RBT_E_UNSUPPORTED otherwise; Qwen 3.8: 128 x 128); states 16-byte aligned. */
 typedef struct {
     size_t n_v_heads, n_k_heads, head_k_dim, head_v_dim, conv_kernel;
     const float *conv_weight;  /* [conv_dim, conv_kernel] (conv1d weight, depthwise, no bias) */
@@ -326,7 +326,9 @@ int rbt_gdn_step_d(rbt_ctx *ctx, const rbt_gdn_desc *desc, float *conv_state, fl
  * -> v, each [n_kv_heads head_dim]) and o_proj: split_query_gate (attention.rs:122), norm_heads
  * (:138), rope_half (:160), KvCache::push (:76) at position pos, attend (:190) over positions
  * 0..pos, apply_output_gate (:221). k_cache / v_cache [cap, n_kv_heads, head_dim] hold positions
- * 0..pos-1 (the cache's len is pos). ctx_out [n_heads head_dim]. */
+ * 0..pos-1 (the cache's len is pos; 16-byte aligned). ctx_out [n_heads head_dim]. head_dim a
+ * multiple of 64 up to 1024, at most 16 query heads per KV head, pos < 393216 (RBT_E_UNSUPPORTED
+ * otherwise; Qwen 3.8: 64 heads over 4, head_dim 256). */
 typedef struct {
     size_t n_heads, n_kv_heads, head_dim, rope_dim;
     float theta, attn_scale, eps;

@@ -1548,8 +1548,9 @@ int rbt_gdn_step_d(rbt_ctx *c, const rbt_gdn_desc *d, float *conv_state, float *
       K > 64)
     return fail(c, RBT_E_INVALID, "bad GDN shape (heads %zu/%zu, dims %zu/%zu, kernel %zu)", nv, nk, dk, dv, K);
   if (!rbt::gdn_ok((int)nv, (int)nk, (int)dk, (int)dv))
-    return fail(c, RBT_E_UNSUPPORTED, "GDN head dims %zu x %zu: head_v_dim must divide 256 and head_k_dim be at "
-                "most 64 * 256 / head_v_dim", dk, dv);
+    return fail(c, RBT_E_UNSUPPORTED, "GDN head dims %zu x %zu: head_v_dim must be a multiple of 4 dividing 2048 "
+                "(at most 512), head_k_dim even and at most 8192 / head_v_dim", dk, dv);
+  if ((uintptr_t)states % 16) return fail(c, RBT_E_INVALID, "states must be 16-byte aligned");
   const size_t conv_dim = 2 * nk * dk + nv * dv;
   float *act;
   RBT_TRY(scratch_t(c, SC_MIXA, conv_dim, &act));
@@ -1567,10 +1568,11 @@ int rbt_gqa_step_d(rbt_ctx *c, const rbt_gqa_desc *d, float *k_cache, float *v_c
   if (nh == 0 || nkv == 0 || nh % nkv || hd == 0 || nh > 4096)
     return fail(c, RBT_E_INVALID, "bad GQA shape (heads %zu over %zu kv heads)", nh, nkv);
   if (pos >= cap) return fail(c, RBT_E_INVALID, "position %zu is outside the cache (capacity %zu)", pos, cap);
-  if (pos >= (size_t)INT32_MAX) return fail(c, RBT_E_UNSUPPORTED, "position %zu", pos);
+  if (pos >= (size_t)6144 * 64) return fail(c, RBT_E_UNSUPPORTED, "position %zu (at most 393215)", pos);
   if (!rbt::gqa_ok((int)nh, (int)nkv, (int)hd, (int)d->rope_dim))
-    return fail(c, RBT_E_UNSUPPORTED, "GQA shape: head_dim %zu (at most 1024), rope_dim %zu, %zu query heads per kv "
-                "head", hd, d->rope_dim, nh / nkv);
+    return fail(c, RBT_E_UNSUPPORTED, "GQA shape: head_dim %zu (a multiple of 64, at most 1024), rope_dim %zu, %zu "
+                "query heads per kv head (at most 16)", hd, d->rope_dim, nh / nkv);
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache) % 16) return fail(c, RBT_E_INVALID, "caches must be 16-byte aligned");
   float *qp, *part;
   RBT_TRY(scratch_t(c, SC_MIXA, nh * hd, &qp));
   RBT_TRY(scratch_t(c, SC_MIXB, rbt::gqa_part_floats((int)nh, (int)nkv, (int)hd, (int)pos + 1), &part));

@@ -16,9 +16,9 @@
 //                    (attention.rs:122-133), (1 + w) RMSNorm (attention.rs:138-143) and partial
 //                    rotate-half RoPE (attention.rs:160-172); per KV head: the same for k, and k, v
 //                    appended at position pos of the cache [cap, n_kv, head_dim] (attention.rs:76-82).
-//     k_gqa_scores   per (KV head, chunk of 64 positions): the group's query heads' scores, each a
-//                    sequential fp32 dot product over head_dim times the scale (attention.rs:203-206),
-//                    and the chunk's softmax partials: max, sum of exp(s - max), exp-weighted V.
+//     k_gqa_chunk    per (KV head, chunk of 64 positions), on the matrix cores: the group's query
+//                    heads' scores q . k times the scale (attention.rs:203-206) and the chunk's softmax
+//                    partials: max, sum of exp(s - max), exp-weighted V (each K and V row read once).
 //     k_gqa_combine  per query head: the chunks merged (softmax over the whole cache,
 //                    glm52/attention.rs:88-98, attention.rs:207-215), times sigmoid(gate)
 //                    (attention.rs:221-226).
@@ -55,29 +55,39 @@ __global__ __launch_bounds__(256) void k_gdn_conv(float *__restrict__ hist, cons
   y[c] = mx_silu(acc);
 }
 
-constexpr int GDN_MAXR = 64;  // state rows per thread held in registers
+constexpr int GDN_NT = 512;   // threads per head workgroup
+constexpr int GDN_MAXR = 16;  // state rows per thread held in registers (float4 each)
 
-// One V head per workgroup of 256 threads. Thread t owns column j = t % d_v and rows
-// i = g, g + G, ... (g = t / d_v, G = 256 / d_v); d_v divides 256 and d_k <= GDN_MAXR * G.
+// One V head per workgroup of GDN_NT threads. Thread t owns the four columns 4 jq .. 4 jq + 3
+// (jq = t % (d_v / 4)) of rows i = g, g + G, ... (g = t / (d_v / 4), G = GDN_NT / (d_v / 4)); d_v is a
+// multiple of 4 with d_v / 4 dividing GDN_NT and d_v <= GDN_NT, d_k is even and d_k <= GDN_MAXR G. The head's state rows are requested first;
+// q, k, v and the gates are prepared while they arrive.
 // act: the conv output after SiLU, [q (key_dim) | k (key_dim) | v (n_v d_v)].
-__global__ __launch_bounds__(256) void k_gdn_head(float *__restrict__ states, const float *__restrict__ act,
-                                                  int key_dim, int n_v, int n_k, int d_k, int d_v,
-                                                  const float *__restrict__ z, const float *__restrict__ a,
-                                                  const float *__restrict__ b, const float *__restrict__ a_log,
-                                                  const float *__restrict__ dt_bias,
-                                                  const float *__restrict__ norm_w, float eps,
-                                                  float *__restrict__ out) {
+__global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states, const float *__restrict__ act,
+                                                     int key_dim, int n_v, int n_k, int d_k, int d_v,
+                                                     const float *__restrict__ z, const float *__restrict__ a,
+                                                     const float *__restrict__ b, const float *__restrict__ a_log,
+                                                     const float *__restrict__ dt_bias,
+                                                     const float *__restrict__ norm_w, float eps,
+                                                     float *__restrict__ out) {
   extern __shared__ float sm[];
+  const int QN = d_v / 4, G = GDN_NT / QN;
   float *qs = sm, *ks = sm + d_k, *vs = sm + 2 * d_k, *part = sm + 2 * d_k + d_v;  // part [G][d_v]
   __shared__ float coef[4];
   const int h = blockIdx.x, t = threadIdx.x;
   const int kh = h / (n_v / n_k);  // key_head_of (gdn.rs:62-65)
-  const int G = 256 / d_v, j = t % d_v, g = t / d_v;
-  for (int i = t; i < d_k; i += 256) {
+  const int jq = t % QN, g = t / QN;
+  const int nr = g < d_k ? (d_k - g + G - 1) / G : 0;
+  float4 *S4 = reinterpret_cast<float4 *>(states + (long)h * d_k * d_v);
+  float4 s[GDN_MAXR];
+#pragma unroll
+  for (int r = 0; r < GDN_MAXR; r++)
+    if (r < nr) s[r] = S4[(long)(g + G * r) * QN + jq];
+  for (int i = t; i < d_k; i += GDN_NT) {
     qs[i] = act[kh * d_k + i];
     ks[i] = act[key_dim + kh * d_k + i];
   }
-  for (int i = t; i < d_v; i += 256) vs[i] = act[2 * key_dim + h * d_v + i];
+  for (int i = t; i < d_v; i += GDN_NT) vs[i] = act[2 * key_dim + h * d_v + i];
   __syncthreads();
   // prepare_qk (gdn.rs:110-118): l2_norm's sequential f32 sum of squares (kimi_linear/ops.rs:34-40)
   // for q on thread 0 and k on thread 64, the decay and write strength on thread 128
@@ -96,36 +106,49 @@ __global__ __launch_bounds__(256) void k_gdn_head(float *__restrict__ states, co
   __syncthreads();
   const float qscale = __fdiv_rn(1.0f, rbt_sqrt_rn((float)d_k));
   const float sq = coef[0], sk = coef[1], alpha = coef[2], beta = coef[3];
-  // this thread's rows of the state, scaled by alpha (kda.rs:140-144)
-  float *S = states + (long)h * d_k * d_v;
-  const int nr = (d_k - g + G - 1) / G;
-  float s[GDN_MAXR];
+  // S *= alpha (kda.rs:140-144); c[j] = sum_i k_i S[i, j] (kda.rs:146-151)
+  float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < GDN_MAXR; r++)
-    if (r < nr) s[r] = __fmul_rn(S[(long)(g + G * r) * d_v + j], alpha);
-  // c[j] = sum_i k_i S[i, j] (kda.rs:146-151)
-  float c = 0.0f;
-#pragma unroll
-  for (int r = 0; r < GDN_MAXR; r++)
-    if (r < nr) c = __fadd_rn(c, __fmul_rn(__fmul_rn(ks[g + G * r], sk), s[r]));
-  part[g * d_v + j] = c;
+    if (r < nr) {
+      s[r] = make_float4(__fmul_rn(s[r].x, alpha), __fmul_rn(s[r].y, alpha), __fmul_rn(s[r].z, alpha),
+                         __fmul_rn(s[r].w, alpha));
+      const float ki = __fmul_rn(ks[g + G * r], sk);
+      c.x = __fadd_rn(c.x, __fmul_rn(ki, s[r].x));
+      c.y = __fadd_rn(c.y, __fmul_rn(ki, s[r].y));
+      c.z = __fadd_rn(c.z, __fmul_rn(ki, s[r].z));
+      c.w = __fadd_rn(c.w, __fmul_rn(ki, s[r].w));
+    }
+  reinterpret_cast<float4 *>(part)[g * QN + jq] = c;
   __syncthreads();
-  float cj = 0.0f;
-  for (int q = 0; q < G; q++) cj = __fadd_rn(cj, part[q * d_v + j]);
+  float4 cj = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int q = 0; q < G; q++) {
+    const float4 p = reinterpret_cast<const float4 *>(part)[q * QN + jq];
+    cj = make_float4(__fadd_rn(cj.x, p.x), __fadd_rn(cj.y, p.y), __fadd_rn(cj.z, p.z), __fadd_rn(cj.w, p.w));
+  }
   __syncthreads();
   // S[i, j] += (beta k_i) (v_j - c_j) (kda.rs:153-158), then o[j] = sum_i q_i S[i, j] (:160-165)
-  const float dv = __fsub_rn(vs[j], cj);
-  float o = 0.0f;
+  const float4 v4 = reinterpret_cast<const float4 *>(vs)[jq];
+  const float4 dv = make_float4(__fsub_rn(v4.x, cj.x), __fsub_rn(v4.y, cj.y), __fsub_rn(v4.z, cj.z),
+                                __fsub_rn(v4.w, cj.w));
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int r = 0; r < GDN_MAXR; r++)
     if (r < nr) {
       const int i = g + G * r;
-      const float ki = __fmul_rn(ks[i], sk);
-      s[r] = __fadd_rn(s[r], __fmul_rn(__fmul_rn(beta, ki), dv));
-      S[(long)i * d_v + j] = s[r];
-      o = __fadd_rn(o, __fmul_rn(__fmul_rn(__fmul_rn(qs[i], sq), qscale), s[r]));
+      const float bk = __fmul_rn(beta, __fmul_rn(ks[i], sk));
+      s[r].x = __fadd_rn(s[r].x, __fmul_rn(bk, dv.x));
+      s[r].y = __fadd_rn(s[r].y, __fmul_rn(bk, dv.y));
+      s[r].z = __fadd_rn(s[r].z, __fmul_rn(bk, dv.z));
+      s[r].w = __fadd_rn(s[r].w, __fmul_rn(bk, dv.w));
+      S4[(long)i * QN + jq] = s[r];
+      const float qi = __fmul_rn(__fmul_rn(qs[i], sq), qscale);
+      o.x = __fadd_rn(o.x, __fmul_rn(qi, s[r].x));
+      o.y = __fadd_rn(o.y, __fmul_rn(qi, s[r].y));
+      o.z = __fadd_rn(o.z, __fmul_rn(qi, s[r].z));
+      o.w = __fadd_rn(o.w, __fmul_rn(qi, s[r].w));
     }
-  part[g * d_v + j] = o;
+  reinterpret_cast<float4 *>(part)[g * QN + jq] = o;
   __syncthreads();
   if (t < d_v) {
     float oj = 0.0f;
@@ -204,75 +227,162 @@ __global__ __launch_bounds__(256) void k_gqa_prep(const float *__restrict__ qg, 
   }
 }
 
-constexpr int GQA_CHUNK = 64;  // positions per scores workgroup
+constexpr int GQA_CHUNK = 64;  // positions per workgroup (16 per wave)
+constexpr int GQA_MAXREP = 16;  // query heads per KV head (the MFMA tile's rows)
 
-// grid (n_kv, chunks), 256 threads. The n_rep query heads of KV head kvh against positions
-// [c * 64, min(P, c * 64 + 64)): scores into LDS (thread per (head, position), a sequential dot
-// product), then per head m = max, l = sum exp(s - m), acc[d] = sum exp(s - m) v[d].
-// part: [n_kv, chunks, n_rep, 2 + hd] = (m, l, acc).
-__global__ __launch_bounds__(256) void k_gqa_scores(const float *__restrict__ qp, const float *__restrict__ kc,
-                                                    const float *__restrict__ vc, int P, int n_heads, int n_kv, int hd,
-                                                    float scale, float *__restrict__ part) {
-  extern __shared__ float sm[];
+typedef float gq4 __attribute__((ext_vector_type(4)));
+
+// grid (n_kv, chunks), 256 threads. The n_rep (<= 16) query heads of KV head kvh against positions
+// [64 c, min(P, 64 c + 64)), on the matrix cores (v_mfma_f32_16x16x4_f32, fp32 products and sums):
+//   scores  S[head][pos] = (q_head . k_pos) * scale: wave w takes positions 16 w .. 16 w + 15; lane l
+//           (n = l % 16, kq = l / 16) loads 16 bytes of head n's query and of position n's key at
+//           dims 16 g + 4 kq .. +3, and MFMA m of group g uses their component m (A[n][kq], B[kq][n]).
+//   softmax partials per head over the chunk: m = max S, e = exp(S - m) (LDS), l = sum e.
+//   values  O[head][d] = sum_pos e[head][pos] v_pos[d]: wave w takes dims 64 b .. 64 b + 63
+//           (b = w, w + 4, ...) as four strided 16-dim tiles (tile c = dims 64 b + 4 n + c), so lane l's
+//           16-byte load of v_pos[64 b + 4 n .. +3] feeds the four tiles' MFMAs (A[n][kq] = e[n][pos]).
+// part: [n_kv, chunks, n_rep, 4 + hd] = (m, l, -, -, O), rows 16-byte aligned.
+__global__ __launch_bounds__(256) void k_gqa_chunk(const float *__restrict__ qp, const float *__restrict__ kc,
+                                                   const float *__restrict__ vc, int P, int n_heads, int n_kv, int hd,
+                                                   float scale, float *__restrict__ part) {
+  __shared__ float es[GQA_MAXREP][GQA_CHUNK + 4];
+  __shared__ float wm[4][GQA_MAXREP], wl[4][GQA_MAXREP], hm[GQA_MAXREP];
   const int n_rep = n_heads / n_kv, kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
+  const int w = t >> 6, lane = t & 63, n = lane & 15, kq = lane >> 4;
   const int p0 = ch * GQA_CHUNK, np = min(GQA_CHUNK, P - p0);
-  float *qs = sm;                        // [n_rep, hd]
-  float *sc = sm + n_rep * hd;           // [n_rep, GQA_CHUNK]
-  float *st = sc + n_rep * GQA_CHUNK;    // [n_rep, 2]
-  for (int i = t; i < n_rep * hd; i += 256) qs[i] = qp[(long)kvh * n_rep * hd + i];
-  __syncthreads();
   const long kw = (long)n_kv * hd;
-  for (int u = t; u < n_rep * np; u += 256) {
-    const int r = u / np, p = u - r * np;
-    const float *k = kc + (long)(p0 + p) * kw + (long)kvh * hd;
-    const float *q = qs + r * hd;
-    float dot = 0.0f;
-    for (int d = 0; d < hd; d++) dot = __fadd_rn(dot, __fmul_rn(q[d], k[d]));
-    sc[r * GQA_CHUNK + p] = __fmul_rn(dot, scale);
+  const int pl = 16 * w + n;  // this lane's position (B column) within the chunk
+  const bool live = pl < np;
+  const float *qrow = qp + ((long)kvh * n_rep + min(n, n_rep - 1)) * hd + 4 * kq;
+  const float *krow = kc + (long)(p0 + min(pl, np - 1)) * kw + (long)kvh * hd + 4 * kq;
+  gq4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < hd / 16; g++) {
+    const float4 qv = *reinterpret_cast<const float4 *>(qrow + 16 * g);
+    const float4 kv = *reinterpret_cast<const float4 *>(krow + 16 * g);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.x, kv.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.y, kv.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.z, kv.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qv.w, kv.w, acc, 0, 0, 0);
   }
-  __syncthreads();
-  if (t < n_rep) {
-    float m = -1e30f;
-    for (int p = 0; p < np; p++) m = fmaxf(m, sc[t * GQA_CHUNK + p]);
-    float l = 0.0f;
-    for (int p = 0; p < np; p++) {
-      const float e = mx_exp(__fsub_rn(sc[t * GQA_CHUNK + p], m));
-      sc[t * GQA_CHUNK + p] = e;
-      l = __fadd_rn(l, e);
+  // the values of this wave's first dim block, requested before the softmax needs the scores
+  const int nb = hd / 64;
+  float4 vpre[GQA_CHUNK / 4];
+  if (w < nb) {
+    const float *vcol = vc + (long)kvh * hd + 64 * w + 4 * n;
+#pragma unroll
+    for (int st = 0; st < GQA_CHUNK / 4; st++) {
+      const int pp = 4 * st + kq;
+      vpre[st] = pp < np ? *reinterpret_cast<const float4 *>(vcol + (long)(p0 + pp) * kw) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    st[2 * t] = m;
-    st[2 * t + 1] = l;
   }
+  // lane l holds S[4 kq + i][position pl], i = 0..3
+  float sv[4], mx[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    sv[i] = live ? __fmul_rn(acc[i], scale) : -INFINITY;
+    float m = sv[i];
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+    mx[i] = m;
+  }
+  if (n == 0)
+#pragma unroll
+    for (int i = 0; i < 4; i++) wm[w][4 * kq + i] = mx[i];
+  __syncthreads();
+  if (t < GQA_MAXREP) hm[t] = fmaxf(fmaxf(wm[0][t], wm[1][t]), fmaxf(wm[2][t], wm[3][t]));
+  __syncthreads();
+  float ls[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int hh = 4 * kq + i;
+    const float e = live ? mx_exp(__fsub_rn(sv[i], hm[hh])) : 0.0f;
+    es[hh][pl] = e;
+    float l = e;
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) l = __fadd_rn(l, __shfl_xor(l, d, 64));
+    ls[i] = l;
+  }
+  if (n == 0)
+#pragma unroll
+    for (int i = 0; i < 4; i++) wl[w][4 * kq + i] = ls[i];
   __syncthreads();
   const int nch = gridDim.y;
-  for (int u = t; u < n_rep * hd; u += 256) {
-    const int r = u / hd, d = u - r * hd;
-    float acc = 0.0f;
-    for (int p = 0; p < np; p++)
-      acc = __fadd_rn(acc, __fmul_rn(sc[r * GQA_CHUNK + p], vc[(long)(p0 + p) * kw + (long)kvh * hd + d]));
-    float *o = part + ((long)(kvh * nch + ch) * n_rep + r) * (2 + hd);
-    o[2 + d] = acc;
-    if (d == 0) {
-      o[0] = st[2 * r];
-      o[1] = st[2 * r + 1];
+  float *base = part + ((long)(kvh * nch + ch) * n_rep) * (4 + hd);
+  if (t < n_rep) {
+    base[(long)t * (4 + hd)] = hm[t];
+    base[(long)t * (4 + hd) + 1] = __fadd_rn(__fadd_rn(wl[0][t], wl[1][t]), __fadd_rn(wl[2][t], wl[3][t]));
+  }
+  // values: wave w, dim blocks b = w, w + 4, ... (the first one prefetched)
+  for (int b = w; b < nb; b += 4) {
+    gq4 o[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    const float *vcol = vc + (long)kvh * hd + 64 * b + 4 * n;
+#pragma unroll
+    for (int st = 0; st < GQA_CHUNK / 4; st++) {
+      const int pp = 4 * st + kq;
+      const float a = es[n][pp];
+      const float4 vv = b == w ? vpre[st]
+                               : (pp < np ? *reinterpret_cast<const float4 *>(vcol + (long)(p0 + pp) * kw)
+                                          : make_float4(0.f, 0.f, 0.f, 0.f));
+      o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vv.x, o[0], 0, 0, 0);
+      o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vv.y, o[1], 0, 0, 0);
+      o[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vv.z, o[2], 0, 0, 0);
+      o[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, vv.w, o[3], 0, 0, 0);
+    }
+    // lane l holds O[4 kq + i][64 b + 4 n + c] in o[c][i]
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int hh = 4 * kq + i;
+      if (hh < n_rep)
+        *reinterpret_cast<float4 *>(base + (long)hh * (4 + hd) + 4 + 64 * b + 4 * n) =
+            make_float4(o[0][i], o[1][i], o[2][i], o[3][i]);
     }
   }
 }
 
-// One query head per workgroup: the chunks' partials merged, divided by the softmax sum, times
-// sigmoid of the head's gate slice of q_proj's row.
+// One query head per workgroup: the chunks' partials merged (each chunk's O and l scaled by
+// exp(m_c - M), M the largest m_c), divided by the softmax sum, times sigmoid of the head's gate.
 __global__ __launch_bounds__(256) void k_gqa_combine(const float *__restrict__ part, const float *__restrict__ qg,
                                                      int n_heads, int n_kv, int hd, int nch,
                                                      float *__restrict__ ctx) {
-  const int h = blockIdx.x, n_rep = n_heads / n_kv, kvh = h / n_rep, r = h - kvh * n_rep;
-  auto P = [&](int c) { return part + ((long)(kvh * nch + c) * n_rep + r) * (2 + hd); };
-  float M = -1e30f;
-  for (int c = 0; c < nch; c++) M = fmaxf(M, P(c)[0]);
-  float L = 0.0f;
-  for (int c = 0; c < nch; c++) L = __fadd_rn(L, __fmul_rn(P(c)[1], mx_exp(__fsub_rn(P(c)[0], M))));
-  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+  extern __shared__ float fc[];  // [nch] chunk scales, then [nch] scaled sums
+  __shared__ float red[4], tot[2];
+  const int h = blockIdx.x, n_rep = n_heads / n_kv, kvh = h / n_rep, r = h - kvh * n_rep, t = threadIdx.x;
+  const long stride = (long)n_rep * (4 + hd);
+  const float *P0 = part + ((long)kvh * nch * n_rep + r) * (4 + hd);
+  float m = -INFINITY;
+  for (int c = t; c < nch; c += 256) m = fmaxf(m, P0[c * stride]);
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) m = fmaxf(m, __shfl_xor(m, d, 64));
+  if ((t & 63) == 0) red[t >> 6] = m;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float *lc = fc + nch;  // [nch] each chunk's l scaled
+  for (int c = t; c < nch; c += 256) {
+    const float f = mx_exp(__fsub_rn(P0[c * stride], M));
+    fc[c] = f;
+    lc[c] = __fmul_rn(P0[c * stride + 1], f);
+  }
+  __syncthreads();
+  if (t == 0) {
+    float L = 0.0f;
+    for (int c = 0; c < nch; c++) L = __fadd_rn(L, lc[c]);
+    tot[0] = L;
+  }
+  __syncthreads();
+  const float L = tot[0];
+  for (int d = t; d < hd; d += 256) {
+    // the chunks' terms in chunk order; their loads issued four at a time
     float acc = 0.0f;
-    for (int c = 0; c < nch; c++) acc = __fadd_rn(acc, __fmul_rn(P(c)[2 + d], mx_exp(__fsub_rn(P(c)[0], M))));
+    int c = 0;
+    for (; c + 4 <= nch; c += 4) {
+      const float x0 = P0[c * stride + 4 + d], x1 = P0[(c + 1) * stride + 4 + d];
+      const float x2 = P0[(c + 2) * stride + 4 + d], x3 = P0[(c + 3) * stride + 4 + d];
+      acc = __fadd_rn(acc, __fmul_rn(x0, fc[c]));
+      acc = __fadd_rn(acc, __fmul_rn(x1, fc[c + 1]));
+      acc = __fadd_rn(acc, __fmul_rn(x2, fc[c + 2]));
+      acc = __fadd_rn(acc, __fmul_rn(x3, fc[c + 3]));
+    }
+    for (; c < nch; c++) acc = __fadd_rn(acc, __fmul_rn(P0[c * stride + 4 + d], fc[c]));
     const float g = qg[(long)h * 2 * hd + hd + d];
     ctx[(long)h * hd + d] = __fmul_rn(__fdiv_rn(acc, L), mx_sigmoid(g));
   }
@@ -280,8 +390,8 @@ __global__ __launch_bounds__(256) void k_gqa_combine(const float *__restrict__ p
 
 // ---- launchers ----------------------------------------------------------------------------------
 bool gdn_ok(int n_v, int n_k, int d_k, int d_v) {
-  return n_v > 0 && n_k > 0 && n_v % n_k == 0 && d_v > 0 && d_v <= 256 && 256 % d_v == 0 && d_k > 0 &&
-         d_k <= GDN_MAXR * (256 / d_v);
+  return n_v > 0 && n_k > 0 && n_v % n_k == 0 && d_v > 0 && d_v % 4 == 0 && d_v <= GDN_NT &&
+         GDN_NT % (d_v / 4) == 0 && d_k > 0 && d_k % 2 == 0 && d_k <= GDN_MAXR * (GDN_NT / (d_v / 4));
 }
 
 hipError_t launch_gdn(const Ctx &c, float *conv_hist, const float *conv_w, int K, float *states,
@@ -291,33 +401,34 @@ hipError_t launch_gdn(const Ctx &c, float *conv_hist, const float *conv_w, int K
   if (!gdn_ok(n_v, n_k, d_k, d_v) || K < 1) return hipErrorInvalidValue;
   const int key_dim = n_k * d_k, C = 2 * key_dim + n_v * d_v;
   launch_k(c, k_gdn_conv, dim3((C + 255) / 256), dim3(256), conv_hist, qkv_pre, conv_w, C, K, act);
-  const unsigned lds = (unsigned)((2 * d_k + d_v + 256) * sizeof(float));
-  launch_ks(c, k_gdn_head, dim3(n_v), dim3(256), lds, states, (const float *)act, key_dim, n_v, n_k, d_k, d_v, z, a,
+  const unsigned lds = (unsigned)((2 * d_k + d_v + 4 * GDN_NT) * sizeof(float));
+  launch_ks(c, k_gdn_head, dim3(n_v), dim3(GDN_NT), lds, states, (const float *)act, key_dim, n_v, n_k, d_k, d_v, z, a,
             b, a_log, dt_bias, norm_w, eps, out);
   return hipGetLastError();
 }
 
 bool gqa_ok(int n_heads, int n_kv, int hd, int rope_dim) {
-  return n_kv > 0 && n_heads % n_kv == 0 && hd > 0 && hd <= 1024 && rope_dim >= 0 && rope_dim % 2 == 0 &&
-         rope_dim <= hd && (size_t)(n_heads / n_kv) * (hd + GQA_CHUNK + 2) * sizeof(float) <= 64 * 1024;
+  return n_kv > 0 && n_heads % n_kv == 0 && n_heads / n_kv <= GQA_MAXREP && hd > 0 && hd % 64 == 0 &&
+         hd <= 1024 && rope_dim >= 0 && rope_dim % 2 == 0 && rope_dim <= hd;
 }
 
 size_t gqa_part_floats(int n_heads, int n_kv, int hd, int positions) {
   const int nch = (positions + GQA_CHUNK - 1) / GQA_CHUNK;
-  return (size_t)n_kv * nch * (n_heads / n_kv) * (2 + hd);
+  return (size_t)n_kv * nch * (n_heads / n_kv) * (4 + hd);
 }
 
 hipError_t launch_gqa(const Ctx &c, const float *qg, const float *k, const float *v, int n_heads, int n_kv, int hd,
                       const float *qn, const float *kn, float eps, int rope_dim, float theta, float scale, int pos,
                       float *kc, float *vc, float *qp, float *part, float *ctx) {
   if (!gqa_ok(n_heads, n_kv, hd, rope_dim) || pos < 0) return hipErrorInvalidValue;
-  const int P = pos + 1, nch = (P + GQA_CHUNK - 1) / GQA_CHUNK, n_rep = n_heads / n_kv;
+  const int P = pos + 1, nch = (P + GQA_CHUNK - 1) / GQA_CHUNK;
+  if ((size_t)nch * 2 * sizeof(float) > 48 * 1024) return hipErrorInvalidValue;  // the combine's chunk scales
   launch_ks(c, k_gqa_prep, dim3(n_heads + n_kv), dim3(256), (unsigned)(hd * sizeof(float)), qg, k, v, n_heads, n_kv,
             hd, qn, kn, eps, rope_dim, pos, theta, qp, kc, vc);
-  const unsigned lds = (unsigned)(n_rep * (hd + GQA_CHUNK + 2) * sizeof(float));
-  launch_ks(c, k_gqa_scores, dim3(n_kv, nch), dim3(256), lds, (const float *)qp, (const float *)kc,
-            (const float *)vc, P, n_heads, n_kv, hd, scale, part);
-  launch_k(c, k_gqa_combine, dim3(n_heads), dim3(256), (const float *)part, qg, n_heads, n_kv, hd, nch, ctx);
+  launch_k(c, k_gqa_chunk, dim3(n_kv, nch), dim3(256), (const float *)qp, (const float *)kc, (const float *)vc, P,
+           n_heads, n_kv, hd, scale, part);
+  launch_ks(c, k_gqa_combine, dim3(n_heads), dim3(256), (unsigned)(2 * nch * sizeof(float)), (const float *)part, qg,
+            n_heads, n_kv, hd, nch, ctx);
   return hipGetLastError();
 }
 

@@ -107,7 +107,7 @@ def test_mixer_errors(ctx, orc):
     with pytest.raises(R.RbtError) as e:  # position past the cache
         ctx.gqa_step(8, 2, 64, 16, 1e7, 0.125, 1e-6, z, z, z, z, 4, 4, z, z, z, z)
     assert e.value.status == R.abi.RBT_E_INVALID
-    with pytest.raises(R.RbtError) as e:  # head_v_dim 6 does not divide 256
+    with pytest.raises(R.RbtError) as e:  # head_v_dim 6 is not a multiple of 4
         ctx.gdn_step(2, 1, 8, 6, z, z, z, z, 1e-6, z, z, z, z, z, z, z)
     assert e.value.status == R.abi.RBT_E_UNSUPPORTED
     with pytest.raises(R.RbtError) as e:  # V heads not a multiple of K heads
