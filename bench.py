@@ -133,9 +133,9 @@ def kernel_table(ctx, run):
 
 def kernel_role(name: str) -> str:
     """gateup / down / router / proj / other, from the kernel's (possibly mangled) name."""
-    if any(s in name for s in ("xgateup", "pgateup", "decode_gu_act")):
+    if any(s in name for s in ("xgateup", "pgateup", "dgateup", "decode_gu_act")):
         return "gateup"
-    if any(s in name for s in ("xdown", "pdown")):
+    if any(s in name for s in ("xdown", "pdown", "ddown")):
         return "down"
     m = re.search(r"k_decode_gemvILi\d+ELi\d+ELi\d+ELi(\d+)E", name) or \
         re.search(r"k_decode_gemv<\s*\d+,\s*\d+,\s*\d+,\s*(\d+)", name)

@@ -688,6 +688,47 @@ int prefill_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H
   return RBT_OK;
 }
 
+constexpr int DECODE_MAX_S = 16;  // tokens per call up to which MXFP4 layers keep fp32 accuracy
+
+// A few tokens (MXFP4, fp32-accurate): grouped by expert as in prefill, every unique expert's
+// weights streamed once for all its tokens, each token's activation as three exact bf16 parts.
+int decode_grouped_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H, int I, const int32_t *ids,
+                       const float *wts, const float *shs, int *ptok, int *tpair, float *tw, float *h, float *yy,
+                       bool gated, float *out, hipEvent_t *ev) {
+  const rbt_moe_layer_desc &D = L.desc;
+  const int has_shared = D.has_shared ? 1 : 0;
+  const long W = (S + 31) / 32;
+  const long max_tiles = rbt::dgemm_max_tiles(S, k, E, has_shared);
+  const size_t off_pc = align256((size_t)E * W * 4), off_segs = off_pc + align256((size_t)E * W * 4);
+  const size_t off_tiles = off_segs + align256(sizeof(rbt::PSeg) * rbt::PG_MAXE);
+  const size_t off_nt = off_tiles + align256(sizeof(rbt::PTile) * (size_t)max_tiles);
+  void *blk;
+  RBT_TRY(scratch(c, SC_PGRP, off_nt + 256, &blk));
+  char *b = static_cast<char *>(blk);
+  uint32_t *bits = reinterpret_cast<uint32_t *>(b), *pc = reinterpret_cast<uint32_t *>(b + off_pc);
+  rbt::PSeg *segs = reinterpret_cast<rbt::PSeg *>(b + off_segs);
+  rbt::PTile *tiles = reinterpret_cast<rbt::PTile *>(b + off_tiles);
+  int *ntiles = reinterpret_cast<int *>(b + off_nt);
+  __bf16 *xb3;
+  RBT_TRY(scratch_t(c, SC_XB, (size_t)3 * S * H, &xb3));
+  __bf16 *hb3 = reinterpret_cast<__bf16 *>(h);  // [3 (S*k + S), I] bf16 fits the fp32 h scratch (2 I floats per pair)
+  int *dflags = c->d_flags;
+  HIP_OK(c, rbt::launch_pgroup(*c, ids, wts, S, k, E, has_shared, L.d_table, bits, pc, segs, tiles, ntiles, ptok,
+                               tpair, tw, dflags + FLAG_ERR, dflags + FLAG_UNIQ, rbt::PD_TCH));
+  HIP_OK(c, rbt::launch_split3(*c, x, S, H, xb3));
+  if (ev) HIP_OK(c, hipEventRecord(ev[1], c->stream));
+  if (ev) c->t_start = ev[2], c->t_stop = ev[3];
+  const hipError_t e1 = rbt::launch_dgateup(*c, tiles, ntiles, segs, L.d_table, L.d_shared, ptok, xb3, S, H, I, hb3);
+  c->t_start = c->t_stop = nullptr;
+  HIP_OK(c, e1);
+  if (ev) c->t_start = ev[4], c->t_stop = ev[5];
+  const hipError_t e2 = rbt::launch_ddown(*c, tiles, ntiles, segs, L.d_table, L.d_shared, hb3, I, H, yy);
+  c->t_start = c->t_stop = nullptr;
+  HIP_OK(c, e2);
+  HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, has_shared, gated ? 1 : 0, out));
+  return RBT_OK;
+}
+
 // accumulate: out += the layer's output (x and out must not overlap). The one-token down launch adds
 // in its own store; the other paths write the output to a scratch and add it after.
 // norm_w (the MoE sublayer): the layer's input is rmsnorm_1p(x, norm_w, eps) (qwen38/ops.rs:25-33),
@@ -813,10 +854,16 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
                                         grp_in_select ? &ga : nullptr, sh_in_select ? &sgu : nullptr));
   }
-  // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores.
-  const bool grouped = !mfma && S > 1 && (merge || !D.has_shared) &&
+  // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores; a few tokens
+  // (decode batches) as the fp32-accurate grouped decode GEMMs.
+  const bool dgrouped = S > 1 && S <= DECODE_MAX_S && (merge || !D.has_shared) &&
+                        rbt::dgemm_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
+  const bool grouped = !dgrouped && !mfma && S > 1 && (merge || !D.has_shared) &&
                        rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
-  if (grouped) {
+  if (dgrouped) {
+    RBT_TRY(decode_grouped_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, dst,
+                               c->prof ? ev.data() : nullptr));
+  } else if (grouped) {
     RBT_TRY(prefill_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, dst,
                         c->prof ? ev.data() : nullptr));
   } else {

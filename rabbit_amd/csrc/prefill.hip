@@ -80,21 +80,28 @@ __device__ __forceinline__ uint32_t pg_load(const uint32_t *p) {
 // E * ceil(S/32) words each. Outputs:
 //   segs[u]     u < U: unique expert u (first-occurrence order), its pair offset and token count;
 //               u = U (has_shared): the shared expert, pairs [S*k, S*k + S), all tokens.
-//   tiles[i]    (segment, first token of the chunk), *ntiles = count.
+//   tiles[i]    (segment, first token of the chunk of at most tch tokens), *ntiles = count.
 //   pair_tok[p] token of pair p; routed pairs are [0, n_routed) in segment order, tokens
 //               ascending within a segment; the shared pair of token t is S*k + t.
 //   tok_pair / tok_w [t*k + j]: token t's pairs and routing weights sorted by pair index, i.e. in
 //               unique_experts order (-1 / 0 for missing picks, placed last).
+// SMALL (E * ceil(S / 32) <= PG_SMALLW): the token bitmaps and their prefix counts live in LDS
+// (bits / pc unused); otherwise in the global scratch.
+constexpr int PG_SMALLW = 2048;
+template <bool SMALL>
 __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids, const float *__restrict__ wts, int S,
                                                  int k, int E, int has_shared, const RbtExpertDev *__restrict__ table,
-                                                 uint32_t *__restrict__ bits, uint32_t *__restrict__ pc,
+                                                 uint32_t *__restrict__ gbits, uint32_t *__restrict__ gpc,
                                                  PSeg *__restrict__ segs, PTile *__restrict__ tiles,
                                                  int *__restrict__ ntiles, int *__restrict__ pair_tok,
                                                  int *__restrict__ tok_pair, float *__restrict__ tok_w,
-                                                 int *__restrict__ err, int *__restrict__ nuniq) {
+                                                 int *__restrict__ err, int *__restrict__ nuniq, int tch) {
   __shared__ int first[PG_MAXE], cnt[PG_MAXE], rank[PG_MAXE], byrank[PG_MAXE], segoff[PG_MAXE + 1];
+  __shared__ uint32_t lbits[SMALL ? PG_SMALLW : 1], lpc[SMALL ? PG_SMALLW : 1];
   __shared__ int ws[17];
   __shared__ int carry_s;
+  uint32_t *bits = SMALL ? lbits : gbits, *pc = SMALL ? lpc : gpc;
+  auto bload = [&](const uint32_t *q) -> uint32_t { return SMALL ? *q : pg_load(q); };
   const int tid = threadIdx.x;
   const int W = (S + 31) >> 5;
   const int P = S * k;
@@ -103,7 +110,7 @@ __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids
     cnt[e] = 0;
   }
   for (long i = tid; i < (long)E * W; i += 1024) bits[i] = 0u;
-  __threadfence();
+  if (!SMALL) __threadfence();
   __syncthreads();
   // counts, first occurrences, token bitmaps
   for (int p = tid; p < P; p += 1024) {
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids
       if (J.gd == nullptr || J.ud == nullptr || J.dd == nullptr) atomicOr(err, 1);
     }
   }
-  __threadfence();
+  if (!SMALL) __threadfence();
   __syncthreads();
   // rank of each used expert: the number of first occurrences before its own
   if (tid == 0) carry_s = 0;
@@ -158,17 +165,17 @@ __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids
     const int nseg = U + (has_shared ? 1 : 0);
     const int u0 = 2 * tid, u1 = 2 * tid + 1;
     auto seg_cnt = [&](int u) { return u < U ? cnt[byrank[u]] : S; };
-    const int n0 = u0 < nseg ? (seg_cnt(u0) + PF_TCH - 1) / PF_TCH : 0;
-    const int n1 = u1 < nseg ? (seg_cnt(u1) + PF_TCH - 1) / PF_TCH : 0;
+    const int n0 = u0 < nseg ? (seg_cnt(u0) + tch - 1) / tch : 0;
+    const int n1 = u1 < nseg ? (seg_cnt(u1) + tch - 1) / tch : 0;
     int tot;
     const int ex = pg_block_scan(n0 + n1, ws, &tot);
     if (u0 < nseg) {
       segs[u0] = PSeg{u0 < U ? byrank[u0] : -1, u0 < U ? segoff[u0] : P, seg_cnt(u0), 0};
-      for (int c = 0; c < n0; c++) tiles[ex + c] = PTile{u0, c * PF_TCH};
+      for (int c = 0; c < n0; c++) tiles[ex + c] = PTile{u0, c * tch};
     }
     if (u1 < nseg) {
       segs[u1] = PSeg{u1 < U ? byrank[u1] : -1, u1 < U ? segoff[u1] : P, seg_cnt(u1), 0};
-      for (int c = 0; c < n1; c++) tiles[ex + n0 + c] = PTile{u1, c * PF_TCH};
+      for (int c = 0; c < n1; c++) tiles[ex + n0 + c] = PTile{u1, c * tch};
     }
     if (tid == 0) {
       *ntiles = tot;
@@ -181,37 +188,37 @@ __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids
     uint32_t run = 0;
     for (int w = 0; w < W; w++) {
       pc[(long)e * W + w] = run;
-      run += __popc(pg_load(&bits[(long)e * W + w]));
+      run += __popc(bload(&bits[(long)e * W + w]));
     }
   }
-  __threadfence();
+  if (!SMALL) __threadfence();
   __syncthreads();
-  // Pairs, one thread per token. The slot of (t, e) within e's segment is the number of earlier
-  // tokens that picked e. Token t's picks are written in pair order, which is unique_experts order
-  // (segments are in rank order): pick j goes to position #{j' : key(j') < key(j)}, with
-  // key = rank of the expert, and missing picks after every real one in slot order.
-  for (int t = tid; t < S; t += 1024) {
+  // Pairs, one thread per (token, pick). The slot of (t, e) within e's segment is the number of
+  // earlier tokens that picked e. Token t's picks are written in pair order, which is
+  // unique_experts order (segments are in rank order): pick j goes to position
+  // #{j' : key(j') < key(j)}, with key = rank of the expert, and missing picks after every real one
+  // in slot order.
+  for (int p = tid; p < P; p += 1024) {
+    const int t = p / k, j = p - t * k;
     const int32_t *ti = ids + (long)t * k;
-    for (int j = 0; j < k; j++) {
-      const int e = ti[j];
-      const bool v = e >= 0 && e < E;
-      const int kj = v ? rank[e] : E + j;
-      int pos = 0;
-      for (int j2 = 0; j2 < k; j2++) {
-        const int e2 = ti[j2];
-        pos += ((e2 >= 0 && e2 < E) ? rank[e2] : E + j2) < kj;
-      }
-      int pr = -1;
-      if (v) {
-        const long wi = (long)e * W + (t >> 5);
-        const int slot = (int)(pg_load(&pc[wi]) + __popc(pg_load(&bits[wi]) & ((1u << (t & 31)) - 1u)));
-        pr = segoff[rank[e]] + slot;
-        pair_tok[pr] = t;
-      }
-      tok_pair[(long)t * k + pos] = pr;
-      tok_w[(long)t * k + pos] = v ? wts[(long)t * k + j] : 0.0f;
+    const int e = ti[j];
+    const bool v = e >= 0 && e < E;
+    const int kj = v ? rank[e] : E + j;
+    int pos = 0;
+    for (int j2 = 0; j2 < k; j2++) {
+      const int e2 = ti[j2];
+      pos += ((e2 >= 0 && e2 < E) ? rank[e2] : E + j2) < kj;
     }
-    if (has_shared) pair_tok[P + t] = t;
+    int pr = -1;
+    if (v) {
+      const long wi = (long)e * W + (t >> 5);
+      const int slot = (int)(bload(&pc[wi]) + __popc(bload(&bits[wi]) & ((1u << (t & 31)) - 1u)));
+      pr = segoff[rank[e]] + slot;
+      pair_tok[pr] = t;
+    }
+    tok_pair[(long)t * k + pos] = pr;
+    tok_w[(long)t * k + pos] = v ? wts[(long)t * k + j] : 0.0f;
+    if (has_shared && j == 0) pair_tok[P + t] = t;
   }
 }
 
@@ -252,13 +259,13 @@ struct PfTile {
 
 __device__ __forceinline__ PfTile pf_tile(int ti, const PTile *__restrict__ tiles, const PSeg *__restrict__ segs,
                                           const RbtExpertDev *__restrict__ table,
-                                          const RbtExpertDev *__restrict__ shared_dev) {
+                                          const RbtExpertDev *__restrict__ shared_dev, int tch = PF_TCH) {
   PfTile r;
   const PTile T = tiles[ti];
   const PSeg G = segs[T.seg];
   r.J = G.eid >= 0 ? table[G.eid] : *shared_dev;
   r.pbase = G.off + T.c0;
-  r.M = min(PF_TCH, G.cnt - T.c0);
+  r.M = min(tch, G.cnt - T.c0);
   // a missing expert is reported by k_pgroup (error flag); its tiles compute nothing
   r.ok = r.M > 0 && r.J.gd != nullptr && r.J.ud != nullptr && r.J.dd != nullptr;
   return r;
@@ -330,15 +337,24 @@ __device__ __forceinline__ pb8 pf_b(const __bf16 (*buf)[PB_STRIDE], int q, int m
 // One scale load per 4 steps keeps the request count near one per 1 KB of codes, and the group in
 // flight (NM * TILES * 4 KB per wave) covers the memory latency while the current group computes.
 // NM = 2 writes hb = bf16(silu(g) * u), NM = 1 writes y (fp32).
-template <int NM, int NTV, int TILES>
+//
+// DEC (the grouped decode): a 16-column block holds five tokens' three bf16 activation parts
+// (column 3 m + p: token 5 q + m, part p; column 15 unused), so the products are fp32-exact and the
+// epilogue sums each token's three columns (lanes r0, r0 + 1, r0 + 2 of the row group) before the
+// activation: NM = 2 writes h as three bf16 parts (rows 3 pair + part of hb), NM = 1 writes y.
+// rbs: row blocks between a workgroup's consecutive blocks (PF_RBG for prefill, 1 for decode).
+// PG: K steps per group (4 or 8).
+template <int NM, int NTV, int TILES, bool DEC = false, int PG = 4>
 __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&src)[NTV], const uint8_t *const (&a)[NM],
                                         const uint8_t *const (&sc)[NM], long rowb, long rows, int rb0, int per,
                                         int nsteps, int out_cols, __bf16 *__restrict__ hb, float *__restrict__ y,
-                                        __bf16 (*bs)[PF_TCH][PB_STRIDE]) {
-  constexpr int G = 4;  // K steps per group
+                                        __bf16 (*bs)[PF_TCH][PB_STRIDE], int rbs = PF_RBG) {
+  constexpr int G = PG;  // K steps per group
+  constexpr int GS = G / 4;  // 16-byte scale loads per row and group
+  static_assert(G == 4 || G == 8, "groups of 4 or 8 K steps");
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  constexpr int BR = 64 * TILES;                                                 // rows per row block
-  const long blk_a = (long)PF_RBG * BR * rowb, blk_s = (long)PF_RBG * BR * rows;  // between own blocks
+  constexpr int BR = 64 * TILES;                                         // rows per row block
+  const long blk_a = (long)rbs * BR * rowb, blk_s = (long)rbs * BR * rows;  // between own blocks
   const int total = per * nsteps;
   if (total <= 0) return;  // no row block for this workgroup (uniform)
   const uint8_t *pa[NM][TILES], *ps[NM][TILES];
@@ -352,7 +368,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
     }
   // next group to fetch (past the end: the last group again, never used)
   int f_rb = 0, f_s = 0;
-  rbt_u4 nw[G][NM][TILES], ns[NM][TILES];
+  rbt_u4 nw[G][NM][TILES], ns[NM][TILES][GS];
   auto fetch_group = [&]() {
     const int rb = min(f_rb, per - 1);
     const int st = f_rb < per ? f_s : nsteps - G;
@@ -367,7 +383,9 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int t = 0; t < TILES; t++) ns[m][t] = *(const rbt_gu4 *)(ps[m][t] + os);
+      for (int t = 0; t < TILES; t++)
+#pragma unroll
+        for (int h = 0; h < GS; h++) ns[m][t][h] = *(const rbt_gu4 *)(ps[m][t] + os + 16 * h);
     f_s += G;
     if (f_s == nsteps) {
       f_s = 0;
@@ -402,12 +420,13 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       for (int q = 0; q < NTV; q++) acc[m][t][q] = pf4{0.f, 0.f, 0.f, 0.f};
   int c_rb = 0, c_s = 0;  // group being computed
   for (int it0 = 0; it0 < total; it0 += G) {
-    rbt_u4 cw[G][NM][TILES], cs[NM][TILES];
+    rbt_u4 cw[G][NM][TILES], cs[NM][TILES][GS];
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int t = 0; t < TILES; t++) {
-        cs[m][t] = ns[m][t];
+#pragma unroll
+        for (int h = 0; h < GS; h++) cs[m][t][h] = ns[m][t][h];
 #pragma unroll
         for (int d = 0; d < G; d++) cw[d][m][t] = nw[d][m][t];
       }
@@ -427,8 +446,9 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
         for (int m = 0; m < NM; m++)
 #pragma unroll
           for (int t = 0; t < TILES; t++) {
-            const rbt_u4 sv = cs[m][t];
-            const uint32_t sw = d == 0 ? sv.x : d == 1 ? sv.y : d == 2 ? sv.z : sv.w;
+            const rbt_u4 sv = cs[m][t][d >> 2];
+            const int dd = d & 3;
+            const uint32_t sw = dd == 0 ? sv.x : dd == 1 ? sv.y : dd == 2 ? sv.z : sv.w;
             const float scl = pf_e8m0((sw >> (8 * g)) & 0xffu);
             const rbt_u4 c = cw[d][m][t];
             const uint32_t code = k4 == 0 ? c.x : k4 == 1 ? c.y : k4 == 2 ? c.z : c.w;
@@ -444,11 +464,45 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
     if (c_s == nsteps) {  // row block done (wave-uniform)
 #pragma unroll
       for (int t = 0; t < TILES; t++) {
-        const int orow = (rb0 + PF_RBG * c_rb) * BR + 16 * TILES * w + 16 * t + 4 * g;
+        const int orow = (rb0 + rbs * c_rb) * BR + 16 * TILES * w + 16 * t + 4 * g;
 #pragma unroll
         for (int q = 0; q < NTV; q++) {
           const int j = 16 * q + r;
-          if (j < T.M) {
+          if (DEC) {
+            // token 5 q + r / 3 on lanes r = 0, 3, .., 12: its parts hi + mid + lo, in that order
+            pf4 sum[NM];
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+              for (int i = 0; i < 4; i++) {
+                const float v0 = acc[m][t][q][i];
+                const float v1 = __shfl_down(v0, 1, 16), v2 = __shfl_down(v0, 2, 16);
+                sum[m][i] = __fadd_rn(__fadd_rn(v0, v1), v2);
+              }
+            const int tl = 5 * q + r / 3;
+            if (r % 3 == 0 && r < 15 && tl < T.M) {
+              const long pr = T.pbase + tl;
+              if (NM == 2) {
+                pb4 hp[3];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                  const float hv = __fmul_rn(rbt_silu(sum[0][i]), sum[NM - 1][i]);
+                  const __bf16 hh = (__bf16)hv;
+                  const float r1 = __fsub_rn(hv, (float)hh);
+                  const __bf16 mm = (__bf16)r1;
+                  hp[0][i] = hh;
+                  hp[1][i] = mm;
+                  hp[2][i] = (__bf16)__fsub_rn(r1, (float)mm);
+                }
+#pragma unroll
+                for (int p = 0; p < 3; p++)
+                  *reinterpret_cast<pb4 *>(hb + (pr * 3 + p) * out_cols + orow) = hp[p];
+              } else {
+                *reinterpret_cast<float4 *>(y + pr * out_cols + orow) =
+                    float4{sum[0][0], sum[0][1], sum[0][2], sum[0][3]};
+              }
+            }
+          } else if (j < T.M) {
             if (NM == 2) {
               pb4 hv;
 #pragma unroll
@@ -546,6 +600,111 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
 }
 
 // ------------------------------------------------------------------------------------------------
+// grouped decode (a few tokens per call, fp32-accurate): the tile GEMMs above with each token's
+// activation as three bf16 parts hi + mid + lo (split3: exact) in three MFMA columns, five tokens
+// per 16-column block and two blocks per tile (PD_TCH = 10 tokens: the two-block GEMMs keep two
+// workgroups per CU), summed in the epilogue. Every unique expert's
+// weights stream once per call however many of the call's tokens picked it. The work is the
+// (tile, row block) units of all tiles, dealt evenly over a fixed grid (the tile count is on the
+// device), so a handful of experts still fills the chip.
+// ------------------------------------------------------------------------------------------------
+// x [S, H] fp32 -> xb3 [3 S, H] bf16: row 3 t + p is part p of token t.
+__global__ __launch_bounds__(256) void k_split3(const float *__restrict__ x, int S, int H, __bf16 *__restrict__ xb3) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (long)S * H) return;
+  const long t = i / H, c = i - t * H;
+  const float v = x[i];
+  const __bf16 hh = (__bf16)v;
+  const float r1 = __fsub_rn(v, (float)hh);
+  const __bf16 mm = (__bf16)r1;
+  xb3[(3 * t) * H + c] = hh;
+  xb3[(3 * t + 1) * H + c] = mm;
+  xb3[(3 * t + 2) * H + c] = (__bf16)__fsub_rn(r1, (float)mm);
+}
+
+// Row (token part) of virtual column jv of block q in a tile: token 5 q + jv / 3 (clamped to the
+// tile), part jv % 3; column 15 repeats column 0 (its products are never read).
+__device__ __forceinline__ void pd_col(int q, int jv, int M, int &tl, int &part) {
+  if (jv >= 15) jv = 0;
+  tl = min(5 * q + jv / 3, M - 1);
+  part = jv % 3;
+}
+
+// Units u = tile * RB + row block over all tiles, workgroup b taking [b U / nwg, (b + 1) U / nwg):
+// consecutive row blocks of one tile run as one pf_gemm call.
+template <bool GATEUP>
+__device__ __forceinline__ void pd_units(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                         const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
+                                         const RbtExpertDev *__restrict__ shared_dev,
+                                         const int *__restrict__ pair_tok, const __bf16 *__restrict__ src_rows,
+                                         int S, int K, int O, int RB, __bf16 *__restrict__ hb3, float *__restrict__ y,
+                                         __bf16 (*bs)[PF_TCH][PB_STRIDE]) {
+  constexpr int TILES = GATEUP ? 1 : 2;
+  const int U = *ntiles * RB, nwg = gridDim.x, b = blockIdx.x;
+  const int u0 = (int)((long)b * U / nwg), u1 = (int)((long)(b + 1) * U / nwg);
+  const long rowb = K >> 1, rows = K >> 5;
+  const int nsteps = K >> 7;
+  const int jv = threadIdx.x >> 4;
+  for (int u = u0; u < u1;) {
+    const int ti = u / RB, rb0 = u - ti * RB, per = min(u1 - u, RB - rb0);
+    u += per;
+    const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev, PD_TCH);
+    if (!T.ok) continue;  // a missing expert is reported by k_pgroup; its rows compute nothing
+    const int nt = (T.M + 4) / 5;
+    auto src_of = [&](int q) {
+      int tl, part;
+      pd_col(q, jv, T.M, tl, part);
+      long row;
+      if (GATEUP) {
+        const int tok = min(max(pair_tok[T.pbase + tl], 0), S - 1);
+        row = 3L * tok + part;
+      } else {
+        row = 3L * (T.pbase + tl) + part;
+      }
+      return src_rows + row * K + (threadIdx.x & 15) * 8;
+    };
+    const uint8_t *const ga[2] = {T.J.gd, T.J.ud};
+    const uint8_t *const gs[2] = {(const uint8_t *)T.J.gs, (const uint8_t *)T.J.us};
+    const uint8_t *const da[1] = {T.J.dd};
+    const uint8_t *const ds[1] = {(const uint8_t *)T.J.ds};
+#define RBT_PD(NTV_)                                                                                          \
+  {                                                                                                           \
+    const __bf16 *src[NTV_];                                                                                  \
+    for (int q = 0; q < NTV_; q++) src[q] = src_of(q);                                                        \
+    if (GATEUP)                                                                                               \
+      pf_gemm<2, NTV_, TILES, true>(T, src, ga, gs, rowb, rows, rb0, per, nsteps, O, hb3, nullptr, bs, 1);    \
+    else                                                                                                      \
+      pf_gemm<1, NTV_, TILES, true>(T, src, da, ds, rowb, rows, rb0, per, nsteps, O, nullptr, y, bs, 1);      \
+  }
+    if (nt == 1)
+      RBT_PD(1)
+    else
+      RBT_PD(2)
+#undef RBT_PD
+    __syncthreads();  // the next tile's first activation step reuses the LDS buffers
+  }
+}
+
+// Gate/up: hb3 [3 pairs, I] bf16 (h parts). Row blocks of 64 rows (RB = I / 64).
+__global__ __launch_bounds__(256) void k_dgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                                 const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
+                                                 const RbtExpertDev *__restrict__ shared_dev,
+                                                 const int *__restrict__ pair_tok, const __bf16 *__restrict__ xb3,
+                                                 int S, int H, int I, __bf16 *__restrict__ hb3) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
+  pd_units<true>(tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H, I, I / 64, hb3, nullptr, bs);
+}
+
+// Down: y [pairs, H] fp32. Row blocks of 128 rows (RB = H / 128).
+__global__ __launch_bounds__(256) void k_ddown(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
+                                               const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
+                                               const RbtExpertDev *__restrict__ shared_dev,
+                                               const __bf16 *__restrict__ hb3, int I, int H, float *__restrict__ y) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
+  pd_units<false>(tiles, ntiles, segs, table, shared_dev, nullptr, hb3, 0, I, H, H / 128, nullptr, y, bs);
+}
+
+// ------------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------------
 bool prefill_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k) {
@@ -564,10 +723,51 @@ long prefill_max_tiles(int S, int k, int E, int has_shared) {
 
 hipError_t launch_pgroup(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E, int has_shared,
                          const RbtExpertDev *table, uint32_t *bits, uint32_t *pc, PSeg *segs, PTile *tiles,
-                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq) {
-  if (E > PG_MAXE) return hipErrorInvalidValue;
-  launch_k(c, k_pgroup, dim3(1), dim3(1024), ids, wts, S, k, E, has_shared, table, bits, pc, segs,
-                     tiles, ntiles, pair_tok, tok_pair, tok_w, err, nuniq);
+                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq, int tch) {
+  if (E > PG_MAXE || tch < 1) return hipErrorInvalidValue;
+  if ((long)E * ((S + 31) / 32) <= PG_SMALLW)
+    launch_k(c, k_pgroup<true>, dim3(1), dim3(1024), ids, wts, S, k, E, has_shared, table, bits, pc, segs, tiles,
+             ntiles, pair_tok, tok_pair, tok_w, err, nuniq, tch);
+  else
+    launch_k(c, k_pgroup<false>, dim3(1), dim3(1024), ids, wts, S, k, E, has_shared, table, bits, pc, segs, tiles,
+             ntiles, pair_tok, tok_pair, tok_w, err, nuniq, tch);
+  return hipGetLastError();
+}
+
+bool dgemm_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k) {
+  // gate/up: 64-row blocks over I, K groups of 512 columns over H; down: 128-row blocks over H,
+  // K groups of 512 columns over I
+  return kind == RBT_QT_MXFP4 && d % 512 == 0 && i % 512 == 0 && d <= (1u << 20) && i <= (1u << 20) &&
+         n_experts + 1 <= (size_t)PG_MAXE && k <= 64;
+}
+
+long dgemm_max_tiles(int S, int k, int E, int has_shared) {
+  const long P = (long)S * k;
+  const long nseg = std::min<long>(E, P) + (has_shared ? 1 : 0);
+  return nseg + (P + (has_shared ? S : 0) + PD_TCH - 1) / PD_TCH;
+}
+
+hipError_t launch_split3(const Ctx &c, const float *x, int S, int H, __bf16 *xb3) {
+  const long n = (long)S * H;
+  if (n <= 0) return hipSuccess;
+  launch_k(c, k_split3, dim3((unsigned)((n + 255) / 256)), dim3(256), x, S, H, xb3);
+  return hipGetLastError();
+}
+
+hipError_t launch_dgateup(const Ctx &c, const PTile *tiles, const int *ntiles, const PSeg *segs,
+                          const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
+                          const __bf16 *xb3, int S, int H, int I, __bf16 *hb3) {
+  if (H % 512 || I % 64) return hipErrorInvalidValue;
+  launch_k(c, k_dgateup, dim3(c.num_cu), dim3(256), tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H,
+           I, hb3);
+  return hipGetLastError();
+}
+
+hipError_t launch_ddown(const Ctx &c, const PTile *tiles, const int *ntiles, const PSeg *segs,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb3, int I, int H,
+                        float *y) {
+  if (I % 512 || H % 128) return hipErrorInvalidValue;
+  launch_k(c, k_ddown, dim3(2 * c.num_cu), dim3(256), tiles, ntiles, segs, table, shared_dev, hb3, I, H, y);
   return hipGetLastError();
 }
 

@@ -138,7 +138,21 @@ bool prefill_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k);
 long prefill_max_tiles(int S, int k, int E, int has_shared);
 hipError_t launch_pgroup(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E, int has_shared,
                          const RbtExpertDev *table, uint32_t *bits, uint32_t *pc, PSeg *segs, PTile *tiles,
-                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq);
+                         int *ntiles, int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq,
+                         int tch = PF_TCH);
+// Grouped decode (a few tokens, fp32-accurate): tiles of at most PD_TCH tokens from launch_pgroup
+// (tch = PD_TCH), x split into three bf16 parts per token (xb3 [3 S, H]), gate/up -> hb3
+// [3 (pairs), I] bf16 parts, down -> y [pairs, H] fp32; then launch_combine.
+constexpr int PD_TCH = 10;
+bool dgemm_ok(int kind, size_t d, size_t i, size_t n_experts, size_t k);
+long dgemm_max_tiles(int S, int k, int E, int has_shared);
+hipError_t launch_split3(const Ctx &c, const float *x, int S, int H, __bf16 *xb3);
+hipError_t launch_dgateup(const Ctx &c, const PTile *tiles, const int *ntiles, const PSeg *segs,
+                          const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
+                          const __bf16 *xb3, int S, int H, int I, __bf16 *hb3);
+hipError_t launch_ddown(const Ctx &c, const PTile *tiles, const int *ntiles, const PSeg *segs,
+                        const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb3, int I, int H,
+                        float *y);
 hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb);
 hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                           const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,

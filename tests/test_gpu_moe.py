@@ -125,8 +125,9 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
         (tests/f64_truth.py);
       * routing weights within 1e-5 absolute of the oracle's (the device forms them from fp64-summed
         logits; the reference from its fp32 fold);
-      * output identical to the same token through the two-token path (which settles its router
-        decision before gate/up)."""
+      * the same token through the two-token path (which settles its router decision before gate/up
+        and runs the grouped decode GEMMs) passes the same per-token rule and lies within 1e-5 of
+        the one-token output."""
     import rabbit_amd.workloads as W
     from oracle.workload import HostLayer
     from f64_truth import check_token, layer64
@@ -166,7 +167,11 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
                    f"oracle vs fp64 {eo:.3e}"
         assert np.max(np.abs(ws[t] - ew[t])) < 1e-5, (t, np.max(np.abs(ws[t] - ew[t])))
         ctx.moe_forward(0, torch.cat([xt[t:t + 1], xt[t:t + 1]]).contiguous(), 2, o2)
-        assert np.array_equal(outs[t], o2[:cfg.hidden].cpu().numpy()), (t, t in folded)
+        two = o2.cpu().numpy().reshape(2, cfg.hidden)
+        assert np.array_equal(two[0], two[1]), t
+        d2, eg2, eo2, ok2 = check_token(two[0], exp[i], truth[i], RTOL)
+        assert ok2, f"token {t}, two-token path: vs oracle {d2:.3e}, vs fp64 {eg2:.3e}, oracle vs fp64 {eo2:.3e}"
+        assert rel_l2(outs[t], two[0]) < RTOL, (t, rel_l2(outs[t], two[0]))
     worst.sort(reverse=True)
     print("largest per-token (device vs oracle, device vs fp64, oracle vs fp64):",
           ", ".join(f"({a:.2e}, {b:.2e}, {c:.2e})" for a, b, c in worst[:4]))
@@ -218,7 +223,7 @@ PREFILL_RTOL = 1e-2  # bf16-MFMA prefill outputs (x and h rounded to bf16)
 
 
 @pytest.mark.parametrize("family,gated,lb,S,E,k", [
-    (0, True, False, 2, 16, 4),      # smallest batch that takes the grouped path
+    (0, True, False, 17, 16, 4),     # smallest batch that takes the grouped bf16 path
     (0, True, False, 130, 64, 6),    # ragged tiles, segments over 64 tokens (shared: 3 tiles)
     (1, False, False, 97, 32, 8),    # GLM sigmoid routing, ungated shared expert
     (2, False, True, 200, 48, 8),    # K3 routing with Zipf-skewed logits: hot experts span tiles
@@ -244,6 +249,31 @@ def test_moe_prefill_grouped(ctx, orc, family, gated, lb, S, E, k):
     # each token's row on its own: no token's output may depend on the rest of the batch
     for t in (0, S // 2, S - 1):
         assert rel_l2(out.reshape(S, H)[t], exp[t]) < PREFILL_RTOL
+
+
+@pytest.mark.parametrize("family,gated,lb,S,E,k", [
+    (0, True, False, 2, 16, 4),      # smallest batch on the grouped decode GEMMs
+    (0, True, False, 16, 8, 4),      # hot experts and the shared expert span two 10-token tiles
+    (1, False, False, 7, 32, 8),     # GLM sigmoid routing, ungated shared expert
+    (2, False, True, 12, 48, 8),     # K3 routing with Zipf-skewed logits
+])
+def test_moe_decode_grouped(ctx, orc, family, gated, lb, S, E, k):
+    """Decode batches (2..16 tokens, MXFP4): experts grouped as in prefill but every activation as
+    three exact bf16 parts, so the output keeps the fp32 bar (1e-5 relative L2, each token too)."""
+    import rabbit_amd as R
+    H, I = 1024, 512
+    L = _small_layer(ctx, orc, family, R.QT_MXFP4, H, I, E, k, seed=91 + S, gated=gated, logit_bias=lb)
+    x = normal((S, H), 700 + S)
+    exp, eids, ew = L.forward(x, S)
+    out = np.empty(S * H, np.float32)
+    ids = np.empty(S * k, np.int32)
+    w = np.empty(S * k, np.float32)
+    ctx.moe_forward(0, x, S, out, ids, w)
+    assert np.array_equal(ids.reshape(S, k), eids)
+    assert rel_l2(w, ew) < RTOL
+    assert rel_l2(out, exp) < RTOL
+    for t in range(S):
+        assert rel_l2(out.reshape(S, H)[t], exp[t]) < RTOL, t
 
 
 def test_moe_prefill_c4_full(ctx, orc):
