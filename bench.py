@@ -141,7 +141,7 @@ def kernel_role(name: str) -> str:
         re.search(r"k_decode_gemv<\s*\d+,\s*\d+,\s*\d+,\s*(\d+)", name)
     if m:
         return {"0": "down", "1": "gateup", "2": "down", "3": "proj"}[m.group(1)]
-    if "router" in name or "select" in name:
+    if "router" in name or "select" in name or "k_rcert" in name or "k_rcomb" in name:
         return "router"
     return "other"
 
@@ -426,9 +426,11 @@ def bench_prefill(args, ctx, hip, cfg, pool_gb):
     def call(b):
         ctx.moe_forward(0, xs[b], S, out, ids[b], sync=False)
 
+    ctx.profile_read(reset=True)
     for b in range(warm):
         call(b)
     ctx.sync()
+    amb = ctx.profile_read(reset=True)["ambiguous"] / warm  # exact folds of near-threshold experts
     wall, ev_ms = graph_time(hip, ctx, call, warm, steps, steps)
     us_call = wall / steps * 1e6
     log(f"[bench] prefill: {steps} calls of {S} tokens, {us_call:.1f} us/call (events {ev_ms / steps * 1e3:.1f})")
@@ -465,6 +467,7 @@ def bench_prefill(args, ctx, hip, cfg, pool_gb):
                    "n_experts": cfg.n_experts, "topk": k, "shared_expert": cfg.shared, "weights": "mxfp4",
                    "resident_pool_gb": round(pool_gb, 2), "unique_experts_mean": round(U, 1)},
         "us_per_token": round(us_call / S, 3),
+        "router_exact_recomputes": round(amb, 1),
         "roofline": rl,
         "down": down,
         "kernels": kernels_json(rows),

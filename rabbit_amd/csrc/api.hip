@@ -842,7 +842,14 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router1(*c, rr, sgate, mid, bnd, shs, rec, fold_norm ? norm_w : nullptr, eps,
                                   fold_norm ? xn : nullptr));
   } else {
-    if (rbt::router_exact_ok(S, H) && ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0) {
+    const bool al16 = ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0;
+    if (rbt::router_exact_ok(S, H) && rbt::router_bounded_ok(ra) && al16) {
+      // batches: fp64-accurate logits on the matrix cores with a rigorous bound on their distance to
+      // the reference's sequential fp32 fold (the selection folds the ambiguous experts exactly)
+      void *rs;
+      RBT_TRY(scratch(c, SC_RLOG, rbt::router_bounded_scratch(ra, erows), &rs));
+      HIP_OK(c, rbt::launch_router_bounded(*c, ra, sgate, mid, bnd, rs));
+    } else if (rbt::router_exact_ok(S, H) && al16) {
       // batches: the reference's sequential fp32 logits themselves, then point intervals
       float *lg;
       RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * erows, &lg));

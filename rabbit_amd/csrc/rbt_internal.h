@@ -229,6 +229,13 @@ hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec, 
 // Device bytes of the key records launch_router1 writes (per router row).
 constexpr size_t ROUTER1_REC_BYTES = 16;
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);
+// Batched router logits on the matrix cores, certified: mid (fp64-accurate) and a rigorous bound on
+// the distance to the reference's sequential fp32 fold, for launch_router_select (which folds the
+// ambiguous ones exactly). scratch: router_bounded_scratch bytes.
+bool router_bounded_ok(const RouterArgs &a);
+size_t router_bounded_scratch(const RouterArgs &a, int erows);
+hipError_t launch_router_bounded(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
+                                 void *scratch);
 hipError_t launch_group(const Ctx &c, const int32_t *ids, const float *wts, int S, int k, int E,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, RbtExpertDev *pair_job,
                         int *pair_tok, int *tok_pair, float *tok_w, int *err, int *nuniq);

@@ -1606,6 +1606,200 @@ hipError_t launch_router_logits_exact(const Ctx &c, const float *x, int S, int H
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------------
+// Batched router logits on the matrix cores, certified (prefill batches). The selection needs, per
+// (token, router row), a midpoint and a rigorous bound on its distance to the reference's
+// sequential fp32 fold (kernels.rs:113-124); the ambiguous experts are then folded exactly by the
+// selection itself. Here, per 32-column step of a (token, row) pair:
+//   the products run on v_mfma_f32_16x16x4_f32 in two chains of four (columns 8 g + q and
+//   8 g + 4 + q of lane group g), restarted every step; the chains' sum joins an fp64 sum;
+//   sum |x| |w| accumulates over the steps on v_mfma_f32_16x16x32_bf16 from |x| and |w| cut to
+//   bf16 (the same 32 columns, each lane's eight in its natural slot);
+//   the prefix bound collects |sum after the step|: each partial sum S_i of a step lies within
+//   min(|start| + P_<=i, |end| + P_>i) <= (|start| + |end| + P) / 2 of zero (P the step's
+//   sum |x| |w|), so the step's 32 sums total at most 16 (|start| + |end|) + 16 P, and over a part
+//   at most 32 sum_steps |end| + 16 sum |x| |w|.
+// Error model of the matrix cores (addends aligned to the largest and truncated, then one rounding:
+// at most 11 u; measured on MI355X at most 2 u, u = 2^-24): one MFMA output is within
+// 16 u (sum |products| + |accumulator|) of the exact value, so a chain of four is within 64 u of its
+// step's sum |x| |w|; the bf16 magnitude chain of 32 steps reads at least (1 - 64 u)^33 of its
+// exact value; cutting to bf16 loses less than 2^-7 of a value.
+// The reference's fold error is at most u T / (1 - n u), T the sum of its partial sums' magnitudes;
+// its products' rounding is at most u sum |x| |w|.
+// ------------------------------------------------------------------------------------------------
+constexpr int RB_STEP = 32;  // columns per step
+constexpr int RB_WGT = 64;   // tokens and rows per workgroup (four waves of 32 x 32)
+
+struct RbRec {  // one K part of one (token, row): sum, prefix-magnitude sum, sum |xh| |wh|
+  double s;
+  float t, a;
+};
+
+typedef float rbf4 __attribute__((ext_vector_type(4)));
+typedef __bf16 rbh8 __attribute__((ext_vector_type(8)));
+
+// |v| cut to bf16 (toward zero), eight values: the high halves of each pair, sign bits cleared
+__device__ __forceinline__ rbh8 rb_abs8(rbf4 lo, rbf4 hi) {
+  uint4 u;
+  u.x = __builtin_amdgcn_perm(__float_as_uint(lo[1]), __float_as_uint(lo[0]), 0x07060302u) & 0x7fff7fffu;
+  u.y = __builtin_amdgcn_perm(__float_as_uint(lo[3]), __float_as_uint(lo[2]), 0x07060302u) & 0x7fff7fffu;
+  u.z = __builtin_amdgcn_perm(__float_as_uint(hi[1]), __float_as_uint(hi[0]), 0x07060302u) & 0x7fff7fffu;
+  u.w = __builtin_amdgcn_perm(__float_as_uint(hi[3]), __float_as_uint(hi[2]), 0x07060302u) & 0x7fff7fffu;
+  return *reinterpret_cast<rbh8 *>(&u);
+}
+
+// One workgroup: 64 tokens x 64 rows over the columns of K part z (H / ks of them); wave w takes
+// tokens 32 (w >> 1) .. +31 and rows 32 (w & 1) .. +31 as 2 x 2 tiles of 16 x 16. Workgroups are
+// dealt to the eight XCDs in contiguous runs of (token tile, row tile, part) so that one XCD's
+// workgroups share token tiles in its L2. Row E (with sgate) is the shared-expert gate vector; rows
+// and tokens past the ends are computed on clamped inputs and not stored.
+__global__ __launch_bounds__(256) void k_rcert(const float *__restrict__ x, int S, int H,
+                                               const float *__restrict__ W, const float *__restrict__ sgate, int E,
+                                               int erows, int n_t, int n_e, int ks, RbRec *__restrict__ out) {
+  const int nwg = n_t * n_e * ks, run = (nwg + 7) / 8;
+  const int L = (blockIdx.x & 7) * run + (blockIdx.x >> 3);
+  if (L >= nwg) return;
+  const int z = L % ks, et = (L / ks) % n_e, tt = L / (ks * n_e);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int t0 = tt * RB_WGT + 32 * (w >> 1), e0 = et * RB_WGT + 32 * (w & 1);
+  const int kc = H / ks, k0 = z * kc;
+  const float *xp[2], *wp[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    xp[j] = x + (long)min(t0 + 16 * j + r, S - 1) * H + k0 + 8 * g;
+    const int e = min(e0 + 16 * j + r, erows - 1);
+    wp[j] = (e < E ? W + (long)e * H : sgate) + k0 + 8 * g;
+  }
+  // operands of one step: [token or row tile][columns 8 g .. +3, 8 g + 4 .. +7]
+  rbf4 pa[2][2], pb[2][2], qa[2][2], qb[2][2];
+  auto load = [&](rbf4 (&A)[2][2], rbf4 (&B)[2][2], int k) {
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        A[j][h] = *reinterpret_cast<const rbf4 *>(xp[j] + k + 4 * h);
+        B[j][h] = *reinterpret_cast<const rbf4 *>(wp[j] + k + 4 * h);
+      }
+    __builtin_amdgcn_sched_barrier(0);  // keep the loads where they are issued: a full step ahead
+  };
+  double sd[2][2][4], td[2][2][4];
+  rbf4 ab[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      ab[a][b] = rbf4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; i++) sd[a][b][i] = td[a][b][i] = 0.0;
+    }
+  auto step = [&](rbf4 (&A)[2][2], rbf4 (&B)[2][2]) {
+    // opaque operands: the compiler may not reload them here (which would wait on the whole latency)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) asm volatile("" : "+v"(A[j][h]), "+v"(B[j][h]));
+    rbh8 xa[2], wa[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      xa[j] = rb_abs8(A[j][0], A[j][1]);
+      wa[j] = rb_abs8(B[j][0], B[j][1]);
+    }
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        rbf4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = c0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(A[a][0][q], B[b][0][q], c0, 0, 0, 0);
+          c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(A[a][1][q], B[b][1][q], c1, 0, 0, 0);
+        }
+        ab[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[a], wa[b], ab[a][b], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sd[a][b][i] += (double)(c0[i] + c1[i]);
+          td[a][b][i] += fabs(sd[a][b][i]);
+        }
+      }
+  };
+  const int ns = kc / RB_STEP;  // even
+  load(pa, pb, 0);
+  for (int i = 0; i < ns; i += 2) {
+    load(qa, qb, RB_STEP * (i + 1));
+    step(pa, pb);
+    load(pa, pb, RB_STEP * min(i + 2, ns - 2));  // past the end: a step again, unused
+    step(qa, qb);
+  }
+#pragma unroll
+  for (int a = 0; a < 2; a++)
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = t0 + 16 * a + 4 * g + i, e = e0 + 16 * b + r;
+        if (t < S && e < erows) out[((long)z * S + t) * erows + e] = RbRec{sd[a][b][i], (float)td[a][b][i], ab[a][b][i]};
+      }
+}
+
+// mid / bnd [S, erows] from the ks parts, joined in column order: A = sum |x| |w| bound, the prefix
+// bound of a part shifted by the sum before it (and that sum's error), then the fold, product and
+// midpoint errors.
+__global__ __launch_bounds__(256) void k_rcomb(const RbRec *__restrict__ part, int S, int H, int erows, int ks,
+                                               double *__restrict__ mid, double *__restrict__ bnd) {
+  const long idx = (long)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (long)S * erows) return;
+  const double u = 5.9604644775390625e-08, ub = 0.0078125, e64 = 1.1102230246251565e-16, n = (double)H;
+  const double kc = n / ks, steps = kc / RB_STEP;
+  // sum |xh| |wh| (cut values, 32-product MFMA chain over the steps) -> sum |x| |w|
+  const double infl = 1.0 / ((1.0 - ub) * (1.0 - ub) * (1.0 - 64.0 * u * (steps + 1.0))) * (1.0 + 2.0 * u);
+  const double per_mid = 64.01 * u + u * (1.0 + 64.01 * u);  // two chains of four, then their fp32 sum
+  const double per = per_mid + u;                             // + the reference's product rounding
+  double s = 0.0, T = 0.0, A = 0.0;
+  for (int z = 0; z < ks; z++) {
+    const RbRec o = part[(long)z * S * erows + idx];
+    const double az = (double)o.a * infl;
+    const double tz = RB_STEP * (double)o.t * (1.0 + 2.0 * u) + 0.5 * RB_STEP * az + kc * per * az;  // o.t >= 0
+    T += tz + kc * (fabs(s) + per * A);
+    s += o.s;
+    A += az;
+  }
+  double B = u * T * (1.0 + 4.0 * u) / (1.0 - n * u) + per * A + 4.0 * n * e64 * A;
+  B = B * (1.0 + 1e-9) + 1e-28;
+  mid[idx] = s;
+  bnd[idx] = B;
+}
+
+static int router_bounded_ks(const RouterArgs &a, int erows) {
+  const long tiles = (long)((a.S + RB_WGT - 1) / RB_WGT) * ((erows + RB_WGT - 1) / RB_WGT);
+  int ks = 8;
+  while (ks > 1 && (tiles * 4 * (ks / 2) >= 2048 || a.H % (2 * RB_STEP * ks) != 0)) ks /= 2;
+  return ks;
+}
+
+bool router_bounded_ok(const RouterArgs &a) {
+  return a.S >= 1 && a.E >= 1 && a.H % (2 * RB_STEP) == 0 && a.H > 0 && a.n_group <= 1;
+}
+
+size_t router_bounded_scratch(const RouterArgs &a, int erows) {
+  return (size_t)router_bounded_ks(a, erows) * a.S * erows * sizeof(RbRec);
+}
+
+hipError_t launch_router_bounded(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
+                                 void *scratch) {
+  const int erows = a.E + (sgate ? 1 : 0);
+  if (!router_bounded_ok(a)) return hipErrorInvalidValue;
+  if (((uintptr_t)a.x | (uintptr_t)a.W | (uintptr_t)(sgate ? sgate : a.x)) % 16 != 0) return hipErrorInvalidValue;
+  const int ks = router_bounded_ks(a, erows);
+  const int n_t = (a.S + RB_WGT - 1) / RB_WGT, n_e = (erows + RB_WGT - 1) / RB_WGT;
+  const int nwg = n_t * n_e * ks, run = (nwg + 7) / 8;
+  RbRec *part = static_cast<RbRec *>(scratch);
+  launch_k(c, k_rcert, dim3(8 * run), dim3(256), a.x, a.S, a.H, a.W, sgate, a.E, erows, n_t, n_e, ks, part);
+  const long nout = (long)a.S * erows;
+  launch_k(c, k_rcomb, dim3((unsigned)((nout + 255) / 256)), dim3(256), (const RbRec *)part, a.S, a.H, erows, ks,
+           mid, bnd);
+  return hipGetLastError();
+}
+
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp, const SharedGateUp *sgu) {
   SelParams P;
