@@ -327,15 +327,32 @@ __device__ __forceinline__ pb8 pf_b(const __bf16 (*buf)[PB_STRIDE], int q, int m
   return *reinterpret_cast<const pb8 *>(&buf[16 * q + r][32 * g + 8 * m]);
 }
 
+// Weight staging. An MFMA reads 16 rows x 64 bytes per K step, but streams of 16 rows x 64 bytes run
+// at about two thirds of the bandwidth of 4 rows x 256 contiguous bytes on this part. So each
+// wave loads its tiles' K groups (4 steps = 256 bytes per row) as 4 rows x 256 bytes per
+// instruction (lane l: row 4 q + l / 16 of the 16-row tile, bytes 16 (l % 16) .. +15 of the group),
+// writes them to its own LDS area at a PW_STRIDE-byte row stride, and every step reads the MFMA
+// layout back (lane (r, g): row r, bytes 16 (4 d + g) .. +15 of step d). The 272-byte stride puts
+// the 16 rows of a read 4 banks apart, and a wave reads its area only after its own writes, in
+// order, so no barrier is needed.
+constexpr int PW_STRIDE = 256 + 16;       // bytes per staged weight row (one K group)
+constexpr int PW_TILE = 16 * PW_STRIDE;   // bytes per staged 16-row tile
+
+// LDS of one pf_gemm workgroup: the activation double buffer (2 x 16 NTV token rows) then each
+// wave's staged weights (NM TILES tiles).
+constexpr int pf_lds_bytes(int NM, int NTV, int TILES) {
+  return 2 * 16 * NTV * PB_STRIDE * 2 + 4 * NM * TILES * PW_TILE;
+}
+
 // One tile x row-block group. Wave w owns TILES 16-row tiles (16 TILES contiguous rows) of each
 // of NM matrices per row block (gate/up: NM = 2, down: NM = 1); a row block is 64 TILES rows, and
-// the workgroup walks `per` of them: blocks rb0, rb0 + PF_RBG, rb0 + 2 PF_RBG, ...
+// the workgroup walks `per` of them: blocks rb0, rb0 + rbs, rb0 + 2 rbs, ...
 //
-// The weights stream in groups of 4 K steps (512 columns): at the start of a group the wave issues
-// every load of the next group at once, the 16-byte codes of each step and, per 16-row tile, one
-// 16-byte load of its 4 steps' E8M0 bytes (byte 4 s + g of a row is the block of lane group g).
-// One scale load per 4 steps keeps the request count near one per 1 KB of codes, and the group in
-// flight (NM * TILES * 4 KB per wave) covers the memory latency while the current group computes.
+// The weights stream in groups of 4 K steps (512 columns): at the start of a group the wave writes
+// the group loaded a group ago to its LDS area, then issues every load of the next group at once,
+// the codes (4 per tile, see above) and, per 16-row tile, one 16-byte load of its 4 steps' E8M0
+// bytes (byte 4 s + g of a row is the block of lane group g). The group in flight
+// (NM * TILES * 4 KB per wave) covers the memory latency while the current group computes.
 // NM = 2 writes hb = bf16(silu(g) * u), NM = 1 writes y (fp32).
 //
 // DEC (the grouped decode): a 16-column block holds five tokens' three bf16 activation parts
@@ -343,49 +360,47 @@ __device__ __forceinline__ pb8 pf_b(const __bf16 (*buf)[PB_STRIDE], int q, int m
 // epilogue sums each token's three columns (lanes r0, r0 + 1, r0 + 2 of the row group) before the
 // activation: NM = 2 writes h as three bf16 parts (rows 3 pair + part of hb), NM = 1 writes y.
 // rbs: row blocks between a workgroup's consecutive blocks (PF_RBG for prefill, 1 for decode).
-// PG: K steps per group (4 or 8).
-template <int NM, int NTV, int TILES, bool DEC = false, int PG = 4>
+// lds: pf_lds_bytes(NM, NTV, TILES) bytes of LDS.
+template <int NM, int NTV, int TILES, bool DEC = false>
 __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&src)[NTV], const uint8_t *const (&a)[NM],
                                         const uint8_t *const (&sc)[NM], long rowb, long rows, int rb0, int per,
                                         int nsteps, int out_cols, __bf16 *__restrict__ hb, float *__restrict__ y,
-                                        __bf16 (*bs)[PF_TCH][PB_STRIDE], int rbs = PF_RBG) {
-  constexpr int G = PG;  // K steps per group
-  constexpr int GS = G / 4;  // 16-byte scale loads per row and group
-  static_assert(G == 4 || G == 8, "groups of 4 or 8 K steps");
+                                        uint8_t *lds, int rbs = PF_RBG) {
+  constexpr int G = 4;  // K steps per group
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   constexpr int BR = 64 * TILES;                                         // rows per row block
   const long blk_a = (long)rbs * BR * rowb, blk_s = (long)rbs * BR * rows;  // between own blocks
   const int total = per * nsteps;
   if (total <= 0) return;  // no row block for this workgroup (uniform)
+  __bf16(*bs)[16 * NTV][PB_STRIDE] = reinterpret_cast<__bf16(*)[16 * NTV][PB_STRIDE]>(lds);
+  uint8_t *const wl = lds + 2 * 16 * NTV * PB_STRIDE * 2 + w * (NM * TILES * PW_TILE);  // this wave's area
   const uint8_t *pa[NM][TILES], *ps[NM][TILES];
 #pragma unroll
   for (int m = 0; m < NM; m++)
 #pragma unroll
     for (int t = 0; t < TILES; t++) {
-      const long row = (long)rb0 * BR + 16 * TILES * w + 16 * t + r;
-      pa[m][t] = a[m] + row * rowb + 16 * g;
-      ps[m][t] = sc[m] + row * rows;
+      const long row0 = (long)rb0 * BR + 16 * TILES * w + 16 * t;  // first row of the tile
+      pa[m][t] = a[m] + (row0 + (lane >> 4)) * rowb + 16 * (lane & 15);
+      ps[m][t] = sc[m] + (row0 + r) * rows;
     }
   // next group to fetch (past the end: the last group again, never used)
   int f_rb = 0, f_s = 0;
-  rbt_u4 nw[G][NM][TILES], ns[NM][TILES][GS];
+  rbt_u4 nw[NM][TILES][4], ns[NM][TILES];
   auto fetch_group = [&]() {
     const int rb = min(f_rb, per - 1);
     const int st = f_rb < per ? f_s : nsteps - G;
     const long oa = (long)rb * blk_a + 64 * st, os = (long)rb * blk_s + 4 * st;
 #pragma unroll
-    for (int d = 0; d < G; d++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
       for (int m = 0; m < NM; m++)
 #pragma unroll
         for (int t = 0; t < TILES; t++)
-          nw[d][m][t] = __builtin_nontemporal_load((const rbt_gu4 *)(pa[m][t] + oa + 64 * d));
+          nw[m][t][q] = __builtin_nontemporal_load((const rbt_gu4 *)(pa[m][t] + oa + 4 * q * rowb));
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int t = 0; t < TILES; t++)
-#pragma unroll
-        for (int h = 0; h < GS; h++) ns[m][t][h] = *(const rbt_gu4 *)(ps[m][t] + os + 16 * h);
+      for (int t = 0; t < TILES; t++) ns[m][t] = *(const rbt_gu4 *)(ps[m][t] + os);
     f_s += G;
     if (f_s == nsteps) {
       f_s = 0;
@@ -420,15 +435,16 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       for (int q = 0; q < NTV; q++) acc[m][t][q] = pf4{0.f, 0.f, 0.f, 0.f};
   int c_rb = 0, c_s = 0;  // group being computed
   for (int it0 = 0; it0 < total; it0 += G) {
-    rbt_u4 cw[G][NM][TILES], cs[NM][TILES][GS];
+    rbt_u4 cs[NM][TILES];
+    // the group loaded a group ago -> this wave's LDS area (rows at PW_STRIDE)
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int t = 0; t < TILES; t++) {
+        cs[m][t] = ns[m][t];
+        uint8_t *wt = wl + (m * TILES + t) * PW_TILE + (lane >> 4) * PW_STRIDE + 16 * (lane & 15);
 #pragma unroll
-        for (int h = 0; h < GS; h++) cs[m][t][h] = ns[m][t][h];
-#pragma unroll
-        for (int d = 0; d < G; d++) cw[d][m][t] = nw[d][m][t];
+        for (int q = 0; q < 4; q++) *reinterpret_cast<rbt_u4 *>(wt + 4 * q * PW_STRIDE) = nw[m][t][q];
       }
     fetch_group();
 #pragma unroll
@@ -437,6 +453,12 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       // activations of it + 1 (loaded a group ago) -> the other LDS buffer
       pf_stage_store<NTV>(st[(d + 1) % G], bs[buf ^ 1]);
       stage_next(st[(d + 1) % G]);
+      rbt_u4 cw[NM][TILES];
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int t = 0; t < TILES; t++)
+          cw[m][t] = *reinterpret_cast<const rbt_u4 *>(wl + (m * TILES + t) * PW_TILE + r * PW_STRIDE + 16 * (4 * d + g));
 #pragma unroll
       for (int k4 = 0; k4 < 4; k4++) {
         pb8 bv[NTV];
@@ -446,11 +468,10 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
         for (int m = 0; m < NM; m++)
 #pragma unroll
           for (int t = 0; t < TILES; t++) {
-            const rbt_u4 sv = cs[m][t][d >> 2];
-            const int dd = d & 3;
-            const uint32_t sw = dd == 0 ? sv.x : dd == 1 ? sv.y : dd == 2 ? sv.z : sv.w;
+            const rbt_u4 sv = cs[m][t];
+            const uint32_t sw = d == 0 ? sv.x : d == 1 ? sv.y : d == 2 ? sv.z : sv.w;
             const float scl = pf_e8m0((sw >> (8 * g)) & 0xffu);
-            const rbt_u4 c = cw[d][m][t];
+            const rbt_u4 c = cw[m][t];
             const uint32_t code = k4 == 0 ? c.x : k4 == 1 ? c.y : k4 == 2 ? c.z : c.w;
             const pb8 av = pf_fp4x8(code, scl);
 #pragma unroll
@@ -526,13 +547,30 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
 // Gate/up: grid = ntiles_max * PF_RBG workgroups of 256 threads; workgroup (tile, gi) owns rows
 // [gi * I / PF_RBG, (gi + 1) * I / PF_RBG) of gate and of up for the tile's tokens, over all H
 // columns. Output hb[pair, I] = bf16(silu(g) * u) (glm52/moe.rs:33-80 Activation::Silu).
+constexpr int PF_GU_LDS = pf_lds_bytes(2, 1, 2) > pf_lds_bytes(2, 4, 1) ? pf_lds_bytes(2, 1, 2) : pf_lds_bytes(2, 4, 1);
+constexpr int PF_DN_LDS = pf_lds_bytes(1, 1, 4) > pf_lds_bytes(1, 4, 1) ? pf_lds_bytes(1, 1, 4) : pf_lds_bytes(1, 4, 1);
+static_assert(pf_lds_bytes(2, 2, 1) <= PF_GU_LDS && pf_lds_bytes(1, 2, 2) <= PF_DN_LDS, "LDS sizes");
+static_assert(2 * PF_GU_LDS <= 160 * 1024 && 2 * PF_DN_LDS <= 160 * 1024, "two workgroups per CU");
+
+// Workgroup -> (tile, row-block group): the PF_RBG = 8 workgroups of a tile are consecutive
+// dispatch slots of one XCD (workgroups are dealt to the eight XCDs round robin), so the tile's
+// activations come into that XCD's L2 once and its 8 x per row blocks re-read them there.
+// The grid is a multiple of 64 workgroups.
+__device__ __forceinline__ void pf_tile_of_block(int &ti, int &gi) {
+  static_assert(PF_RBG == 8, "eight row-block groups per tile");
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  gi = slot & 7;
+  ti = (slot >> 3) * 8 + xcd;
+}
+
 __global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                  const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                  const RbtExpertDev *__restrict__ shared_dev,
                                                  const int *__restrict__ pair_tok, const __bf16 *__restrict__ xb,
                                                  int S, int H, int I, __bf16 *__restrict__ hb) {
-  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
-  const int ti = blockIdx.x / PF_RBG, gi = blockIdx.x - ti * PF_RBG;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PF_GU_LDS];
+  int ti, gi;
+  pf_tile_of_block(ti, gi);
   if (ti >= *ntiles) return;
   const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
   if (!T.ok) return;
@@ -550,15 +588,15 @@ __global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles
   switch (nt) {
     case 1: {
       const __bf16 *src[1] = {src_of(0)};
-      pf_gemm<2, 1, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, I, hb, nullptr, bs);
+      pf_gemm<2, 1, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, I, hb, nullptr, lds);
     } break;
     case 2: {
       const __bf16 *src[2] = {src_of(0), src_of(1)};
-      pf_gemm<2, 2, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, bs);
+      pf_gemm<2, 2, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, lds);
     } break;
     default: {
       const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
-      pf_gemm<2, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, bs);
+      pf_gemm<2, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, I, hb, nullptr, lds);
     } break;
   }
 }
@@ -569,8 +607,9 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
                                                const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                const RbtExpertDev *__restrict__ shared_dev,
                                                const __bf16 *__restrict__ hb, int I, int H, float *__restrict__ y) {
-  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
-  const int ti = blockIdx.x / PF_RBG, gi = blockIdx.x - ti * PF_RBG;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[PF_DN_LDS];
+  int ti, gi;
+  pf_tile_of_block(ti, gi);
   if (ti >= *ntiles) return;
   const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
   if (!T.ok) return;
@@ -586,15 +625,15 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
   switch (nt) {
     case 1: {
       const __bf16 *src[1] = {src_of(0)};
-      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, bs);
+      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, lds);
     } break;
     case 2: {
       const __bf16 *src[2] = {src_of(0), src_of(1)};
-      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, bs);
+      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, lds);
     } break;
     default: {
       const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
-      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, bs);
+      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, lds);
     } break;
   }
 }
@@ -638,7 +677,7 @@ __device__ __forceinline__ void pd_units(const PTile *__restrict__ tiles, const 
                                          const RbtExpertDev *__restrict__ shared_dev,
                                          const int *__restrict__ pair_tok, const __bf16 *__restrict__ src_rows,
                                          int S, int K, int O, int RB, __bf16 *__restrict__ hb3, float *__restrict__ y,
-                                         __bf16 (*bs)[PF_TCH][PB_STRIDE]) {
+                                         uint8_t *lds) {
   constexpr int TILES = GATEUP ? 1 : 2;
   const int U = *ntiles * RB, nwg = gridDim.x, b = blockIdx.x;
   const int u0 = (int)((long)b * U / nwg), u1 = (int)((long)(b + 1) * U / nwg);
@@ -672,9 +711,9 @@ __device__ __forceinline__ void pd_units(const PTile *__restrict__ tiles, const 
     const __bf16 *src[NTV_];                                                                                  \
     for (int q = 0; q < NTV_; q++) src[q] = src_of(q);                                                        \
     if (GATEUP)                                                                                               \
-      pf_gemm<2, NTV_, TILES, true>(T, src, ga, gs, rowb, rows, rb0, per, nsteps, O, hb3, nullptr, bs, 1);    \
+      pf_gemm<2, NTV_, TILES, true>(T, src, ga, gs, rowb, rows, rb0, per, nsteps, O, hb3, nullptr, lds, 1);   \
     else                                                                                                      \
-      pf_gemm<1, NTV_, TILES, true>(T, src, da, ds, rowb, rows, rb0, per, nsteps, O, nullptr, y, bs, 1);      \
+      pf_gemm<1, NTV_, TILES, true>(T, src, da, ds, rowb, rows, rb0, per, nsteps, O, nullptr, y, lds, 1);     \
   }
     if (nt == 1)
       RBT_PD(1)
@@ -691,8 +730,8 @@ __global__ __launch_bounds__(256) void k_dgateup(const PTile *__restrict__ tiles
                                                  const RbtExpertDev *__restrict__ shared_dev,
                                                  const int *__restrict__ pair_tok, const __bf16 *__restrict__ xb3,
                                                  int S, int H, int I, __bf16 *__restrict__ hb3) {
-  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
-  pd_units<true>(tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H, I, I / 64, hb3, nullptr, bs);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[pf_lds_bytes(2, 2, 1)];
+  pd_units<true>(tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H, I, I / 64, hb3, nullptr, lds);
 }
 
 // Down: y [pairs, H] fp32. Row blocks of 128 rows (RB = H / 128).
@@ -700,8 +739,8 @@ __global__ __launch_bounds__(256) void k_ddown(const PTile *__restrict__ tiles, 
                                                const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                const RbtExpertDev *__restrict__ shared_dev,
                                                const __bf16 *__restrict__ hb3, int I, int H, float *__restrict__ y) {
-  __shared__ __attribute__((aligned(16))) __bf16 bs[2][PF_TCH][PB_STRIDE];
-  pd_units<false>(tiles, ntiles, segs, table, shared_dev, nullptr, hb3, 0, I, H, H / 128, nullptr, y, bs);
+  __shared__ __attribute__((aligned(16))) uint8_t lds[pf_lds_bytes(1, 2, 2)];
+  pd_units<false>(tiles, ntiles, segs, table, shared_dev, nullptr, hb3, 0, I, H, H / 128, nullptr, y, lds);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -782,7 +821,7 @@ hipError_t launch_to_bf16(const Ctx &c, const float *x, long n, __bf16 *xb) {
 hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                           const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
                           const __bf16 *xb, int S, int H, int I, __bf16 *hb) {
-  const long blocks = max_tiles * PF_RBG;
+  const long blocks = (max_tiles + 7) / 8 * 8 * PF_RBG;  // pf_tile_of_block: a multiple of 64
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
   launch_k(c, k_pgateup, dim3((unsigned)blocks), dim3(256), tiles, ntiles, segs, table,
@@ -793,7 +832,7 @@ hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, l
 hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb, int I, int H,
                         float *y) {
-  const long blocks = max_tiles * PF_RBG;
+  const long blocks = (max_tiles + 7) / 8 * 8 * PF_RBG;  // pf_tile_of_block: a multiple of 64
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
   launch_k(c, k_pdown, dim3((unsigned)blocks), dim3(256), tiles, ntiles, segs, table, shared_dev,
