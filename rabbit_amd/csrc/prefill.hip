@@ -87,7 +87,7 @@ __device__ __forceinline__ uint32_t pg_load(const uint32_t *p) {
 //               unique_experts order (-1 / 0 for missing picks, placed last).
 // SMALL (E * ceil(S / 32) <= PG_SMALLW): the token bitmaps and their prefix counts live in LDS
 // (bits / pc unused); otherwise in the global scratch.
-constexpr int PG_SMALLW = 2048;
+constexpr int PG_SMALLW = 8192;  // words: C4 (512 experts x 512 tokens) keeps its bitmaps in LDS
 template <bool SMALL>
 __global__ __launch_bounds__(1024) void k_pgroup(const int32_t *__restrict__ ids, const float *__restrict__ wts, int S,
                                                  int k, int E, int has_shared, const RbtExpertDev *__restrict__ table,
