@@ -339,16 +339,16 @@ int rbt_gqa_step_d(rbt_ctx *ctx, const rbt_gqa_desc *desc, float *k_cache, float
 
 /* ---- instrumentation (no counterpart in the reference: benchmark support) -------------------- */
 typedef struct {
-    double router_ms;    /* router logits + top-k selection + grouping (one-token MXFP4 calls: also
-                            the shared expert's gate/up, which runs in the same launch) */
+    double router_ms;    /* router logits + top-k selection + grouping (one-token MXFP4 calls: the
+                            router launch; the selection itself runs at the start of gate/up) */
     double gateup_ms;    /* gate/up products + silu(g)*u (the experts this phase streams) */
     double down_ms;      /* down products (with the ordered combine where it is fused in) */
     double combine_ms;   /* the separate weighted combine + shared expert; where the combine is
                             fused into the down kernel, only the time to the call's end */
     uint64_t calls;      /* rbt_moe_forward_d calls recorded */
     uint64_t ambiguous;  /* router logits recomputed exactly because of a near-tie */
-    uint64_t gateup_experts; /* one-token calls: experts whose gate/up the gate/up phase streamed (a shared
-                                expert whose gate/up ran inside the router phase is not counted) */
+    uint64_t gateup_experts; /* one-token calls: experts whose gate/up the gate/up phase streamed
+                                (routed pairs, candidates of a deferred decision, the shared expert) */
     uint64_t down_experts;   /* one-token calls: experts whose down the down phase streamed */
 } rbt_profile;
 /* When on, rbt_moe_forward_d records HIP events on the context stream around each phase. */
