@@ -1049,9 +1049,23 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   // one token: the selection writes the pair list itself (pair j = slot j)
   const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
   rbt::GroupArgs ga{table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
-  HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
-                                      grp_in_select ? &ga : nullptr));
-  RBT_TRY(matmul_dev(c, xl, x, &lw->down_proj, s));
+  const rbt_qt &Dp = lw->down_proj;
+  const bool dp_fused = grp_in_select && rbt::router_select_dp_ok(ra, Dp.kind, (int)H, (int)MH) &&
+                        (Dp.kind != RBT_QT_I4_GROUPED || Dp.group_size == 32) &&
+                        ((uintptr_t)Dp.data | (uintptr_t)x) % 16 == 0 && Dp.data && Dp.scale;
+  if (dp_fused) {
+    // one token: the latent down projection streams while the selection runs (one launch)
+    RBT_TRY(check_qt(c, &Dp, "matmul"));
+    RbtExpertDev pj{};
+    pj.dd = (const uint8_t *)Dp.data;
+    pj.ds = Dp.scale;
+    HIP_OK(c, rbt::launch_router_select_dp(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB, ga, pj, Dp.kind,
+                                           (int)H, (int)MH, xl));
+  } else {
+    HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
+                                        grp_in_select ? &ga : nullptr));
+    RBT_TRY(matmul_dev(c, xl, x, &lw->down_proj, s));
+  }
   if (!grp_in_select)
     HIP_OK(c, rbt::launch_group(*c, ids, wts, S, K, (int)E, table, table + E, pjob, ptok, tpair, tw,
                                 dflags + FLAG_ERR, dflags + FLAG_UNIQ));

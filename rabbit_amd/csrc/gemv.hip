@@ -18,336 +18,20 @@
 #include <algorithm>
 
 #include "rbt_device.h"
+#include "rbt_gemv.h"
 #include "rbt_internal.h"
 
 namespace rbt {
-
-// ------------------------------------------------------------------------------------------------
-// MXFP4 block dot: 32 E2M1 codes (one uint4) times 32 activations, scaled by the block's E8M0.
-// ------------------------------------------------------------------------------------------------
-__device__ __forceinline__ float fp4_dword_dot(uint32_t w, float sc, const float *xv, float acc) {
-  rbt_f2 v0 = RBT_FP4X2(w, sc, 0);
-  rbt_f2 v1 = RBT_FP4X2(w, sc, 1);
-  rbt_f2 v2 = RBT_FP4X2(w, sc, 2);
-  rbt_f2 v3 = RBT_FP4X2(w, sc, 3);
-  acc = __builtin_fmaf(xv[0], v0.x, acc);
-  acc = __builtin_fmaf(xv[1], v0.y, acc);
-  acc = __builtin_fmaf(xv[2], v1.x, acc);
-  acc = __builtin_fmaf(xv[3], v1.y, acc);
-  acc = __builtin_fmaf(xv[4], v2.x, acc);
-  acc = __builtin_fmaf(xv[5], v2.y, acc);
-  acc = __builtin_fmaf(xv[6], v3.x, acc);
-  acc = __builtin_fmaf(xv[7], v3.y, acc);
-  return acc;
-}
-
-// Grouped int4: nibble n encodes n-8. Returns sum_k x_k * n_k (unsigned codes); the caller folds in
-// -8 * sum_k x_k and the group scale.
-__device__ __forceinline__ float i4_dword_dot(uint32_t w, const float *xv, float acc) {
-  uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-  acc = __builtin_fmaf(xv[0], (float)(lo & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[1], (float)(hi & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[2], (float)((lo >> 8) & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[3], (float)((hi >> 8) & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[4], (float)((lo >> 16) & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[5], (float)((hi >> 16) & 0xFFu), acc);
-  acc = __builtin_fmaf(xv[6], (float)(lo >> 24), acc);
-  acc = __builtin_fmaf(xv[7], (float)(hi >> 24), acc);
-  return acc;
-}
-
-template <int NB, int LPR>
-__device__ __forceinline__ void load_x_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ x,
-                                             int q, int nblk) {
-  // unconditional loads from a clamped (in-bounds) block, then zeroed: no branches around loads,
-  // so the compiler can count outstanding loads instead of draining them.
-  const rbt_gf4 *xg = (const rbt_gf4 *)x;
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int b = q + LPR * j;
-    const bool ok = b < nblk;
-    const int bb = ok ? b : nblk - 1;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const float4 v = xg[8 * bb + t];
-      xr[j][4 * t + 0] = ok ? v.x : 0.0f;
-      xr[j][4 * t + 1] = ok ? v.y : 0.0f;
-      xr[j][4 * t + 2] = ok ? v.z : 0.0f;
-      xr[j][4 * t + 3] = ok ? v.w : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    float s = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 32; t++) s += xr[j][t];
-    xs[j] = s;
-  }
-}
-
-// rmsnorm of a row held as a whole wave's x slice (64 lanes, blocks q + 64j), in place:
-// r = 1/sqrt((sum_f64(v^2) / n) as f32 + eps), v *= r * w (kimi_linear/ops.rs:46-53), then the
-// block sums again as load_x_slice forms them. The fp64 sum runs in another order than k_rmsnorm's.
-template <int NB>
-__device__ __forceinline__ void norm_x_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ w,
-                                             float eps, int q, int nblk, int n) {
-  // the weights' loads go out first and land while the sum of squares is reduced
-  const rbt_gf4 *wg = (const rbt_gf4 *)w;
-  float4 wv[NB][8];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int bb = min(q + 64 * j, nblk - 1);
-#pragma unroll
-    for (int t = 0; t < 8; t++) wv[j][t] = wg[8 * bb + t];
-  }
-  double acc = 0.0;
-#pragma unroll
-  for (int j = 0; j < NB; j++)
-#pragma unroll
-    for (int t = 0; t < 32; t++) acc += (double)xr[j][t] * (double)xr[j][t];  // zero past the row
-  acc = rbt_wave_total_d(acc);
-  const float r = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(acc / (double)n), eps)));
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const bool ok = q + 64 * j < nblk;
-#pragma unroll
-    for (int t = 0; t < 8; t++) {
-      const float4 v = wv[j][t];
-      xr[j][4 * t + 0] = ok ? __fmul_rn(xr[j][4 * t + 0], __fmul_rn(r, v.x)) : 0.0f;
-      xr[j][4 * t + 1] = ok ? __fmul_rn(xr[j][4 * t + 1], __fmul_rn(r, v.y)) : 0.0f;
-      xr[j][4 * t + 2] = ok ? __fmul_rn(xr[j][4 * t + 2], __fmul_rn(r, v.z)) : 0.0f;
-      xr[j][4 * t + 3] = ok ? __fmul_rn(xr[j][4 * t + 3], __fmul_rn(r, v.w)) : 0.0f;
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    float s = 0.0f;
-#pragma unroll
-    for (int t = 0; t < 32; t++) s += xr[j][t];
-    xs[j] = s;
-  }
-}
-
-
-
-// ------------------------------------------------------------------------------------------------
-// Decode kernel over a job table. Each job u is one expert (or one plain matrix); MODE selects the
-// matrix and the activation:
-//   MODE_DOWN   : y[u*y_stride + r] = down_u[r] . x_u                         (r < rows)
-//   MODE_STACKED: gate_u and up_u as one [2*half, cols] matrix: rows [0, half) are gate's, rows
-//                 [half, 2*half) up's; y[u*y_stride + r] = that row . x_u     (r < rows = 2*half)
-//   MODE_ACT    : like MODE_DOWN, but the activation is built on the fly from a stacked gate/up
-//                 result g|u (2*cols floats): x_k = silu(g_k) * u_k (glm52/moe.rs:33-80).
-// x_u = x + tok(u)*x_stride with tok(u) = x_index[u] (or u when x_index is null).
-// The flattened (job, row) range is split into equal contiguous runs, one per wave. An iteration
-// covers U * (64/LPR) consecutive rows; the next iteration's blocks are loaded before the current
-// one is reduced (double buffering), so a wave keeps two iterations of weight bytes in flight. With
-// U > 1 the host guarantees rows % (U * 64/LPR) == 0 (an iteration never straddles two jobs). A
-// job whose weights are absent (null pointers) yields zeros.
-// ------------------------------------------------------------------------------------------------
-enum { MODE_DOWN = 0, MODE_STACKED = 1, MODE_ACT = 2, MODE_NORM = 3 };  // NORM: MODE_DOWN of rmsnorm(x)
-
-template <int NB, int U>
-struct DecodeFrag {
-  rbt_u4 w[U][NB];
-  uint32_t sb[U][NB];  // E8M0 byte (MXFP4) or f32 bits (I4G)
-};
-
-// Loads the blocks of IPI = U * (64/LPR) consecutive rows starting at `row` (a row pointer into
-// `d`, rows rb bytes apart; scales `sc`, nblk per row). Lane (sub, q) takes rows row + u*RPI + sub.
-// Every load is unconditional (blocks past nblk re-read block nblk-1; block_dots drops them), so
-// the loop body is straight-line and the next iteration's loads stay in flight during this one's
-// arithmetic.
-template <int NB, int LPR, int U, bool I4G>
-__device__ __forceinline__ void frag_load(DecodeFrag<NB, U> &f, const uint8_t *__restrict__ d,
-                                          const uint8_t *__restrict__ sc, int row, int q, int sub, int nblk,
-                                          unsigned rb, int sstride) {
-  constexpr int RPI = RBT_WAVE / LPR;
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    const unsigned r = (unsigned)(row + u * RPI + sub);
-    const rbt_gu4 *rp = (const rbt_gu4 *)(d + (size_t)r * rb);
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int b = q + LPR * j;
-      const int bb = min(b, nblk - 1);
-      f.w[u][j] = __builtin_nontemporal_load(rp + bb);
-      if (I4G)
-        f.sb[u][j] = ((const rbt_gu32 *)sc)[(size_t)r * sstride + bb];
-      else
-        f.sb[u][j] = ((const rbt_gu8 *)sc)[(size_t)r * sstride + bb];
-    }
-  }
-}
-
-// Blocks b = q + LPR*j past nblk hold a re-read of block nblk-1 (frag_load) and contribute nothing.
-template <int NB, int LPR, bool I4G>
-__device__ __forceinline__ float block_dots(const rbt_u4 (&w)[NB], const uint32_t (&sb)[NB], const float (&xr)[NB][32],
-                                            const float (&xs)[NB], int q, int nblk) {
-  float r = 0.0f;
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    float a = 0.0f;
-    if (I4G) {
-      a = i4_dword_dot(w[j].x, &xr[j][0], a);
-      a = i4_dword_dot(w[j].y, &xr[j][8], a);
-      a = i4_dword_dot(w[j].z, &xr[j][16], a);
-      a = i4_dword_dot(w[j].w, &xr[j][24], a);
-      // sum_k x_k (n_k - 8) = sum_k x_k n_k - 8 sum_k x_k, then the group scale.
-      const float t = __builtin_fmaf(__builtin_fmaf(-8.0f, xs[j], a), __uint_as_float(sb[j]), r);
-      r = (q + LPR * j < nblk) ? t : r;
-    } else {
-      const float sc = rbt_e8m0(sb[j]);
-      a = fp4_dword_dot(w[j].x, sc, &xr[j][0], a);
-      a = fp4_dword_dot(w[j].y, sc, &xr[j][8], a);
-      a = fp4_dword_dot(w[j].z, sc, &xr[j][16], a);
-      a = fp4_dword_dot(w[j].w, sc, &xr[j][24], a);
-      r += (q + LPR * j < nblk) ? a : 0.0f;
-    }
-  }
-  return r;
-}
-
-// x slice for MODE_ACT: x_k = silu(g_k) * u_k from a stacked gate/up result. The producer may have
-// split its rows into PARTS column ranges: gu holds PARTS partial gate vectors, then PARTS partial
-// up vectors (cols floats each), summed here.
-template <int PARTS>
-__device__ __forceinline__ float4 sum_parts(const float *__restrict__ p, int cols, int off) {
-  float4 v = *reinterpret_cast<const float4 *>(p + off);
-#pragma unroll
-  for (int h = 1; h < PARTS; h++) {
-    const float4 w = *reinterpret_cast<const float4 *>(p + h * cols + off);
-    v.x += w.x;
-    v.y += w.y;
-    v.z += w.z;
-    v.w += w.w;
-  }
-  return v;
-}
-
-template <int NB, int LPR, int PARTS>
-__device__ __forceinline__ void load_act_slice(float (&xr)[NB][32], float (&xs)[NB], const float *__restrict__ gu,
-                                               int q, int nblk, int cols) {
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    const int b = q + LPR * j;
-    float s = 0.0f;
-    if (b < nblk) {
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const float4 g = sum_parts<PARTS>(gu, cols, 32 * b + 4 * t);
-        const float4 u = sum_parts<PARTS>(gu + PARTS * cols, cols, 32 * b + 4 * t);
-        xr[j][4 * t + 0] = rbt_silu(g.x) * u.x;
-        xr[j][4 * t + 1] = rbt_silu(g.y) * u.y;
-        xr[j][4 * t + 2] = rbt_silu(g.z) * u.z;
-        xr[j][4 * t + 3] = rbt_silu(g.w) * u.w;
-      }
-#pragma unroll
-      for (int t = 0; t < 32; t++) s += xr[j][t];
-    } else {
-#pragma unroll
-      for (int t = 0; t < 32; t++) xr[j][t] = 0.0f;
-    }
-    xs[j] = s;
-  }
-}
-
-template <int NB, int LPR, int U, bool I4G>
-__device__ __forceinline__ void frag_reduce_store(const DecodeFrag<NB, U> &f, const float (&xr)[NB][32],
-                                                  const float (&xs)[NB], float *__restrict__ yrow, int q, int sub,
-                                                  int nblk) {
-  constexpr int RPI = RBT_WAVE / LPR;
-#pragma unroll
-  for (int u = 0; u < U; u++) {
-    float a = block_dots<NB, LPR, I4G>(f.w[u], f.sb[u], xr, xs, q, nblk);
-    a = rbt_group_sum<LPR>(a);
-    if (q == 0) yrow[u * RPI + sub] = a;
-    // one row at a time: keeps the scheduler from decoding every row's nibbles up front, which
-    // would cost 32 registers per block and halve the waves per SIMD.
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
 template <int NB, int LPR, int U, int MODE, bool I4G, int CS, int PARTS>
 __global__ __launch_bounds__(256) void k_decode_gemv(const RbtExpertDev *__restrict__ jobs, RbtExpertDev single,
                                                      int njobs, const int *__restrict__ njobs_dev,
                                                      const float *__restrict__ x, const int *__restrict__ x_index,
                                                      long x_stride, int cols, int rows, float *__restrict__ y,
                                                      long y_stride, const float *__restrict__ nw, float eps) {
-  static_assert(MODE != MODE_NORM || (LPR == 64 && CS == 1), "the norm needs the whole row in one wave");
-  constexpr int RPI = RBT_WAVE / LPR;  // rows side by side in one wave
-  constexpr int IPI = U * RPI;         // rows per iteration
-  const int lane = threadIdx.x & (RBT_WAVE - 1);
-  const int q = lane % LPR, sub = lane / LPR;
-  const int nwaves = gridDim.x * (blockDim.x / RBT_WAVE);
-  const int wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x / RBT_WAVE) + threadIdx.x / RBT_WAVE);
-  int nj = njobs;
-  if (njobs_dev) nj = min(nj, *njobs_dev);
-  // Each logical row of `cols` columns is processed as CS column ranges ("parts"), so a lane's x
-  // slice covers cols/CS columns. A segment is a run of rows of one matrix and one part: per job,
-  // MODE_STACKED has 2*CS segments (gate parts, then up parts), the other modes CS. `rows` counts
-  // logical rows per job (2*half for MODE_STACKED); segment lengths are multiples of IPI.
-  const int seg = MODE == MODE_STACKED ? rows / 2 : rows;
-  const int nseg_job = (rows / seg) * CS;
-  const int total = nj * seg * nseg_job;
-  int per = (total + nwaves - 1) / nwaves;
-  per = ((per + IPI - 1) / IPI) * IPI;
-  int pos = wave * per;
-  if (pos >= total) return;
-  const int end = min(pos + per, total);
-
-  const int pcols = cols / CS;  // columns of one part
-  const int nblk = pcols / 32;
-  const unsigned rb = (unsigned)cols / 2;
-
-  float xr[NB][32];
-  float xs[NB];
-  long cur = -1;
-  DecodeFrag<NB, U> f0, f1;
-
-  while (pos < end) {
-    // one segment: rows [r, r1) of matrix (job, part)
-    const int sidx = pos / seg;
-    const int job = sidx / nseg_job, sj = sidx - job * nseg_job;
-    const int mat = sj / CS, h = sj - mat * CS;  // matrix (gate/up for MODE_STACKED), column part
-    int r = pos - sidx * seg;
-    const int r1 = min(seg, r + (end - pos));
-    pos += r1 - r;
-    const RbtExpertDev J = jobs ? jobs[job] : single;
-    const uint8_t *d = MODE == MODE_STACKED ? (mat ? J.ud : J.gd) : J.dd;
-    const uint8_t *sc = reinterpret_cast<const uint8_t *>(MODE == MODE_STACKED ? (mat ? J.us : J.gs) : J.ds);
-    float *yrow = y + (long)job * y_stride + (long)sj * seg;
-    if (d == nullptr) {
-      for (int rr = r + lane; rr < r1; rr += RBT_WAVE) yrow[rr] = 0.0f;
-      continue;
-    }
-    d += (size_t)h * (pcols / 2);                         // part h of every row
-    sc += (size_t)h * nblk * (I4G ? 4 : 1);
-    // ping-pong over iterations of IPI rows: the next iteration's blocks are in flight while the
-    // current one is reduced. The first weight loads go out before the activation slice is read.
-    frag_load<NB, LPR, U, I4G>(f0, d, sc, r, q, sub, nblk, rb, CS * nblk);
-    const long tok = x_stride == 0 ? 0 : (x_index ? (long)x_index[job] : (long)job);
-    if (tok * CS + h != cur) {
-      if (MODE == MODE_ACT)
-        load_act_slice<NB, LPR, PARTS>(xr, xs, x + tok * x_stride, q, nblk, cols);
-      else
-        load_x_slice<NB, LPR>(xr, xs, x + tok * x_stride + (long)h * pcols, q, nblk);
-      if constexpr (MODE == MODE_NORM) norm_x_slice<NB>(xr, xs, nw, eps, q, nblk, cols);
-      cur = tok * CS + h;
-    }
-    // The prefetch is unconditional: past the segment's last iteration it re-reads that iteration
-    // (rlast), so every load sits in straight-line code.
-    const int rlast = r1 - IPI;
-    while (true) {
-      frag_load<NB, LPR, U, I4G>(f1, d, sc, min(r + IPI, rlast), q, sub, nblk, rb, CS * nblk);
-      frag_reduce_store<NB, LPR, U, I4G>(f0, xr, xs, yrow + r, q, sub, nblk);
-      if (r + IPI >= r1) break;
-      frag_load<NB, LPR, U, I4G>(f0, d, sc, min(r + 2 * IPI, rlast), q, sub, nblk, rb, CS * nblk);
-      frag_reduce_store<NB, LPR, U, I4G>(f1, xr, xs, yrow + r + IPI, q, sub, nblk);
-      r += 2 * IPI;
-      if (r >= r1) break;
-    }
-  }
+  decode_gemv_body<NB, LPR, U, MODE, I4G, CS, PARTS>(jobs, single, njobs, njobs_dev, x, x_index, x_stride, cols,
+                                                     rows, y, y_stride, nw, eps,
+                                                     blockIdx.x * (blockDim.x / RBT_WAVE) + threadIdx.x / RBT_WAVE,
+                                                     gridDim.x * (blockDim.x / RBT_WAVE));
 }
 
 // Activation between the stacked gate/up GEMV and the down GEMV: h[p, k] = act(g, u) with g and

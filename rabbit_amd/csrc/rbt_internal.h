@@ -207,6 +207,13 @@ struct SharedGateUp {
   int K, I;
   __bf16 *hp;
 };
+// One token of the latent MoE: the selection (with the one-token pair list) on workgroup 0 and the
+// latent down projection xl[rows] = proj.dd . x (MXFP4 or grouped int4, 2049..8192 columns) on one
+// workgroup per CU, in one launch.
+bool router_select_dp_ok(const RouterArgs &a, int kind, int cols, int rows);
+hipError_t launch_router_select_dp(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd,
+                                   int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs &grp,
+                                   const RbtExpertDev &proj, int kind, int cols, int rows, float *xl);
 hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd, int32_t *ids,
                                 float *wts, float *sh_scale, int *stats, const GroupArgs *grp = nullptr,
                                 const SharedGateUp *sgu = nullptr);

@@ -23,6 +23,7 @@
 //  3. k_group (several tokens): unique_experts order (glm52/moe.rs:333-344), per-expert token
 //     lists in token order, and per-token pick lists ordered by first occurrence.
 #include "rbt_device.h"
+#include "rbt_gemv.h"
 #include "rbt_internal.h"
 #include "rbt_xmfma.h"
 
@@ -1364,6 +1365,26 @@ __global__ __launch_bounds__(256) void k_router_select3_sh(SelParams P, const do
     xgateup1_body<NCH>(L.gu, shared_dev, 1, x, I, hp_shared, blockIdx.x - 1, gridDim.x - 1);
 }
 
+// One token of the latent MoE: workgroup 0 selects (writing the pair list); the other workgroups,
+// one per CU, run the latent down projection x_latent = down_proj . x (kimi_k3/moe.rs:64-80) as the
+// decode GEMV does, since it does not depend on the routing: it streams while the selection (and
+// any exact fold it needs) runs.
+template <int MAXM, int NB, bool I4G>
+__global__ __launch_bounds__(256) void k_router_select3_dp(SelParams P, const double *__restrict__ mid,
+                                                           const double *__restrict__ bnd, int32_t *__restrict__ ids,
+                                                           float *__restrict__ wts, float *__restrict__ sh_scale,
+                                                           int *__restrict__ stats, GroupOut G, RbtExpertDev proj,
+                                                           int cols, int rows, float *__restrict__ xl) {
+  __shared__ SelLds L;
+  __shared__ float kbuf[4 * 64 * MAXM];
+  if (blockIdx.x == 0)
+    select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, 1, 0, kbuf);
+  else
+    decode_gemv_body<NB, 64, 1, MODE_DOWN, I4G, 1, 1>(nullptr, proj, 1, nullptr, P.x, nullptr, 0, cols, rows, xl, 0,
+                                                      nullptr, 0.0f, (blockIdx.x - 1) * 4 + (threadIdx.x >> 6),
+                                                      (gridDim.x - 1) * 4);
+}
+
 // Routing from precomputed logits (rbt_route_*_topk): the logits are exact inputs, so the
 // interval is a point (bound 0) and the same selection code applies.
 __global__ void k_logits_to_mid(const float *__restrict__ logits, size_t n, double *__restrict__ mid,
@@ -1797,6 +1818,36 @@ hipError_t launch_router_bounded(const Ctx &c, const RouterArgs &a, const float 
   const long nout = (long)a.S * erows;
   launch_k(c, k_rcomb, dim3((unsigned)((nout + 255) / 256)), dim3(256), (const RbRec *)part, a.S, a.H, erows, ks,
            mid, bnd);
+  return hipGetLastError();
+}
+
+static SelParams sel_params(const RouterArgs &a);
+
+bool router_select_dp_ok(const RouterArgs &a, int kind, int cols, int rows) {
+  const int nblk = cols / 32;
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 64 * 16 && rows > 0 &&
+         cols % 32 == 0 && nblk > 64 && nblk <= 256 && (kind == RBT_QT_MXFP4 || kind == RBT_QT_I4_GROUPED);
+}
+
+hipError_t launch_router_select_dp(const Ctx &c, const RouterArgs &a, const double *mid, const double *bnd,
+                                   int32_t *ids, float *wts, float *sh_scale, int *stats, const GroupArgs &grp,
+                                   const RbtExpertDev &proj, int kind, int cols, int rows, float *xl) {
+  if (!router_select_dp_ok(a, kind, cols, rows) || c.num_cu < 1) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  const GroupOut G = group_out(grp, a.k);
+  const int m = (a.E + 63) / 64, nb = (cols / 32 + 63) / 64;
+  const bool i4 = kind == RBT_QT_I4_GROUPED;
+  const dim3 grid(1 + c.num_cu);
+#define RBT_DP(M, NB_)                                                                                               {                                                                                                                    if (i4)                                                                                                              launch_k(c, (k_router_select3_dp<M, NB_, true>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale, stats, G,                proj, cols, rows, xl);                                                                                  else                                                                                                                 launch_k(c, (k_router_select3_dp<M, NB_, false>), grid, dim3(256), P, mid, bnd, ids, wts, sh_scale, stats,                  G, proj, cols, rows, xl);                                                                             }
+#define RBT_DP_NB(M)   { if (nb == 2) RBT_DP(M, 2) else if (nb == 3) RBT_DP(M, 3) else RBT_DP(M, 4) }
+  if (m <= 4)
+    RBT_DP_NB(4)
+  else if (m <= 8)
+    RBT_DP_NB(8)
+  else
+    RBT_DP_NB(16)
+#undef RBT_DP_NB
+#undef RBT_DP
   return hipGetLastError();
 }
 

@@ -204,6 +204,20 @@ def test_latent_moe_k3_dims(ctx, orc):
     _run_latent(ctx, R, 50, L, dq, uq, x, S, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
 
 
+@pytest.mark.parametrize("proj_kind", ["mxfp4", "i4g"])
+def test_latent_moe_k3_dims_one_token(ctx, orc, proj_kind):
+    # one token per call at K3's widths: the latent down projection streams inside the selection's
+    # launch (workgroup 0 selects, the others project); six tokens, each its own call
+    import rabbit_amd as R
+    H, MH, I, E, k = 7168, 3584, 3072, 32, 8
+    layer = 52 + (proj_kind == "i4g")
+    L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 7100 + layer, proj_kind, 0.05)
+    norm = np.abs(normal(MH, 53, 0.2)) + np.float32(0.5)
+    for t in range(6):
+        x = normal((1, H), 600 + t, 0.05)
+        _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
+
+
 def test_latent_moe_identity_projections_equal_routed_forward(ctx, orc):
     # moe_hidden == hidden with identity projections: the latent MoE is the layer's routed forward
     import rabbit_amd as R
