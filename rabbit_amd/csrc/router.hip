@@ -1007,6 +1007,8 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
           kbuf[NE + e] = kh;
           kbuf[2 * NE + e] = lm;
           kbuf[3 * NE + e] = __uint_as_float(u);
+          kbuf[4 * NE + e] = lb[i];  // the biases too: wave 0 reads them from LDS, not memory again
+          kbuf[5 * NE + e] = rb[i];
         }
       }
     }
@@ -1015,8 +1017,8 @@ __device__ __forceinline__ void select3_body(SelLds &L, const SelParams &P, cons
 #pragma unroll
       for (int m = 0; m < MAXM; m++) {
         const int e = min(lane + 64 * m, E - 1);
-        lbv[m] = P.logit_bias ? P.logit_bias[e] : 0.0f;
-        rbv[m] = P.router_bias ? P.router_bias[e] : 0.0f;
+        lbv[m] = kbuf[4 * NE + e];
+        rbv[m] = kbuf[5 * NE + e];
         const bool in = lane + 64 * m < E;
         ku[m] = in ? __float_as_uint(kbuf[3 * NE + e]) : 0u;
         klo[m] = in ? kbuf[e] : -INFINITY;
@@ -1341,7 +1343,7 @@ __global__ __launch_bounds__(256) void k_router_select3(SelParams P, const doubl
                                                         float *__restrict__ wts, float *__restrict__ sh_scale,
                                                         int *__restrict__ stats, GroupOut G, int grp) {
   __shared__ SelLds L;
-  __shared__ float kbuf[4 * 64 * MAXM];
+  __shared__ float kbuf[6 * 64 * MAXM];
   select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, grp, blockIdx.x, kbuf);
 }
 
@@ -1376,7 +1378,7 @@ __global__ __launch_bounds__(256) void k_router_select3_dp(SelParams P, const do
                                                            int *__restrict__ stats, GroupOut G, RbtExpertDev proj,
                                                            int cols, int rows, float *__restrict__ xl) {
   __shared__ SelLds L;
-  __shared__ float kbuf[4 * 64 * MAXM];
+  __shared__ float kbuf[6 * 64 * MAXM];
   if (blockIdx.x == 0)
     select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, G, 1, 0, kbuf);
   else
