@@ -482,7 +482,34 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       __syncthreads();
     }
     c_s += G;
-    if (c_s == nsteps) {  // row block done (wave-uniform)
+    if (!DEC && NM == 1 && c_s == nsteps) {
+      // down, row block done: y leaves in whole cache lines, non-temporal. The wave's 16 NTV tokens x
+      // 16 TILES rows go through its LDS area (idle until the next group's write, which follows in
+      // program order) token-major, then each token's rows are stored as one contiguous run (256
+      // bytes at TILES = 4) instead of 64-byte pieces of 16 rows 32 KB apart. Stores share the
+      // in-order vector memory counter with the weight loads, so their acknowledgements delay the
+      // waits that follow them; streaming stores and one row block per workgroup (PF_DN_RBG) keep that
+      // cost down (k_pdown at C4: 1041 -> 980 us; without any y store it runs in 863 us).
+      constexpr int RW = 16 * TILES, CPT = RW / 4;  // rows per token run, 16-byte chunks in it
+      constexpr int YS = 16 * NTV * (RW * 4 + 16) <= NM * TILES * PW_TILE ? RW * 4 + 16 : RW * 4;
+      static_assert(16 * NTV * YS <= NM * TILES * PW_TILE, "staged y fits the wave's area");
+#pragma unroll
+      for (int t = 0; t < TILES; t++)
+#pragma unroll
+        for (int q = 0; q < NTV; q++) {
+          *reinterpret_cast<pf4 *>(wl + (16 * q + r) * YS + (16 * t + 4 * g) * 4) = acc[0][t][q];
+          acc[0][t][q] = pf4{0.f, 0.f, 0.f, 0.f};
+        }
+      const long row0 = (long)(rb0 + rbs * c_rb) * BR + 16 * TILES * w;
+#pragma unroll
+      for (int k = 0; k < NTV * CPT / 4; k++) {
+        const int c = lane + 64 * k, tok = c / CPT, ch = c - tok * CPT;
+        const pf4 v = *reinterpret_cast<const pf4 *>(wl + tok * YS + 16 * ch);
+        if (tok < T.M) __builtin_nontemporal_store(v, reinterpret_cast<pf4 *>(y + (long)(T.pbase + tok) * out_cols + row0 + 4 * ch));
+      }
+      c_s = 0;
+      ++c_rb;
+    } else if (c_s == nsteps) {  // row block done (wave-uniform)
 #pragma unroll
       for (int t = 0; t < TILES; t++) {
         const int orow = (rb0 + rbs * c_rb) * BR + 16 * TILES * w + 16 * t + 4 * g;
@@ -552,16 +579,19 @@ constexpr int PF_DN_LDS = pf_lds_bytes(1, 1, 4) > pf_lds_bytes(1, 4, 1) ? pf_lds
 static_assert(pf_lds_bytes(2, 2, 1) <= PF_GU_LDS && pf_lds_bytes(1, 2, 2) <= PF_DN_LDS, "LDS sizes");
 static_assert(2 * PF_GU_LDS <= 160 * 1024 && 2 * PF_DN_LDS <= 160 * 1024, "two workgroups per CU");
 
-// Workgroup -> (tile, row-block group): the PF_RBG = 8 workgroups of a tile are consecutive
-// dispatch slots of one XCD (workgroups are dealt to the eight XCDs round robin), so the tile's
-// activations come into that XCD's L2 once and its 8 x per row blocks re-read them there.
-// The grid is a multiple of 64 workgroups.
+// Workgroup -> (tile, row-block group): the RBG workgroups of a tile are consecutive dispatch
+// slots of one XCD (workgroups are dealt to the eight XCDs round robin), so the tile's
+// activations come into that XCD's L2 once and its RBG x per row blocks re-read them there.
+// The grid is a multiple of 8 RBG workgroups.
+template <int RBG = PF_RBG>
 __device__ __forceinline__ void pf_tile_of_block(int &ti, int &gi) {
-  static_assert(PF_RBG == 8, "eight row-block groups per tile");
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  gi = slot & 7;
-  ti = (slot >> 3) * 8 + xcd;
+  gi = slot % RBG;
+  ti = (slot / RBG) * 8 + xcd;
 }
+// Down: 32 workgroups per tile, so that at TILES = 4 (256-row blocks of 8192 rows) each takes one row
+// block and its y stores are its last memory operations.
+constexpr int PF_DN_RBG = 32;
 
 __global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                  const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
@@ -601,21 +631,21 @@ __global__ __launch_bounds__(256) void k_pgateup(const PTile *__restrict__ tiles
   }
 }
 
-// Down: grid = ntiles_max * PF_RBG, 256 threads; workgroup (tile, gi) owns down rows
-// [gi * H / PF_RBG, (gi + 1) * H / PF_RBG) over all I columns; y[pair, H] fp32.
+// Down: grid = ntiles_max * PF_DN_RBG, 256 threads; workgroup (tile, gi) takes the tile's row blocks
+// gi, gi + PF_DN_RBG, .. over all I columns; y[pair, H] fp32.
 __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                const RbtExpertDev *__restrict__ shared_dev,
                                                const __bf16 *__restrict__ hb, int I, int H, float *__restrict__ y) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[PF_DN_LDS];
   int ti, gi;
-  pf_tile_of_block(ti, gi);
+  pf_tile_of_block<PF_DN_RBG>(ti, gi);
   if (ti >= *ntiles) return;
   const PfTile T = pf_tile(ti, tiles, segs, table, shared_dev);
   if (!T.ok) return;
   const int nt = (T.M + 15) >> 4;
   const int nsteps = I >> 7;
-  auto per_of = [&](int br) { return (H / br - gi + PF_RBG - 1) / PF_RBG; };
+  auto per_of = [&](int br) { return (H / br - gi + PF_DN_RBG - 1) / PF_DN_RBG; };
   const long rowb = (long)(I >> 1), rows = (long)(I >> 5);
   const uint8_t *const a[1] = {T.J.dd};
   const uint8_t *const sc[1] = {(const uint8_t *)T.J.ds};
@@ -625,15 +655,15 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
   switch (nt) {
     case 1: {
       const __bf16 *src[1] = {src_of(0)};
-      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, lds);
+      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
     case 2: {
       const __bf16 *src[2] = {src_of(0), src_of(1)};
-      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, lds);
+      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
     default: {
       const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
-      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, lds);
+      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
   }
 }
@@ -832,7 +862,7 @@ hipError_t launch_pgateup(const Ctx &c, const PTile *tiles, const int *ntiles, l
 hipError_t launch_pdown(const Ctx &c, const PTile *tiles, const int *ntiles, long max_tiles, const PSeg *segs,
                         const RbtExpertDev *table, const RbtExpertDev *shared_dev, const __bf16 *hb, int I, int H,
                         float *y) {
-  const long blocks = (max_tiles + 7) / 8 * 8 * PF_RBG;  // pf_tile_of_block: a multiple of 64
+  const long blocks = (max_tiles + 7) / 8 * 8 * PF_DN_RBG;  // pf_tile_of_block
   if (blocks <= 0) return hipSuccess;
   if (blocks > 0x7fffffffL || H % 512 || I % 1024) return hipErrorInvalidValue;
   launch_k(c, k_pdown, dim3((unsigned)blocks), dim3(256), tiles, ntiles, segs, table, shared_dev,
