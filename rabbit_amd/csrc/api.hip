@@ -797,6 +797,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
   const bool merge = D.has_shared && L.shared_kind == L.routed_kind && L.shared_gs == L.routed_gs &&
                      L.shared_inter == (size_t)I;
+  if (merge) ga.shv = L.h_shared;
   // MXFP4 decode shapes run on the matrix cores: gate/up with SiLU, then down with the ordered
   // combine fused in (out written directly).
   const bool mfma = (merge || !D.has_shared) && rbt::xgemm_ok(L.routed_kind, H, I, S, k, D.has_shared) &&

@@ -198,6 +198,9 @@ struct GroupArgs {
   RbtExpertDev *down_job = nullptr;
   int *down_slot = nullptr;
   int shared_slot = -1;
+  // the shared expert's pointers by value (one token: its gate/up loads go out before the routing
+  // is known; all null: not available)
+  RbtExpertDev shv{};
 };
 // The shared expert's gate/up for a one-token call (balanced body of xgemm), run by a router launch
 // on the CUs its selection (or its rows) leave free. hp: the shared pair's output parts.

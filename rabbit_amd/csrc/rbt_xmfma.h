@@ -19,6 +19,14 @@ typedef float xf4 __attribute__((ext_vector_type(4)));
 
 constexpr int XG_PAD = 8;        // bf16 padding between the LDS part rows (bank spread)
 
+// Barrier for LDS hand-offs only: global loads in flight stay in flight (__syncthreads' release
+// fence waits for every outstanding load of the wave first).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // 8 E2M1 codes (one dword) -> 8 bf16, scaled by the block's E8M0 value.
 __device__ __forceinline__ xb8 fp4x8_bf16(uint32_t w, float sc) {
   const xb2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
@@ -87,7 +95,56 @@ struct GuLds {
   __attribute__((aligned(16))) __bf16 xs[3 * (8192 + XG_PAD)];
   __attribute__((aligned(16))) __bf16 zb[32];
   __attribute__((aligned(16))) uint8_t sw[4][2][2][4][256];  // [wave][buffer][matrix][row][byte]
+  float sp[4][4][2];  // [wave][row of the unit][gate, up]: a shared half unit's row sums
 };
+
+// The shared expert's half unit that a wave of the one-token gate/up takes before its routed units:
+// rows 4 su .. 4 su + 3 of the shared gate and up, steps hf D .. hf D + D - 1 (D = NCH / 2, the
+// ring's depth). The shared expert does not depend on the routing, so the caller issues these loads
+// before the selection and they land while it runs. The two halves of a unit belong to waves 2j and
+// 2j + 1 of one workgroup, which leave their row sums in GuLds::sp; the caller adds them after a
+// barrier (xgateup1_sh_combine).
+template <int NCH>
+struct ShHalf {
+  int su = -1, hf = 0;  // su < 0: no half for this wave
+  rbt_u4 ring[NCH / 2][2];
+  rbt_u4 sv[2];  // the lane's scale pieces of the unit (as the body's window loads)
+};
+
+template <int NCH>
+__device__ __forceinline__ void xgateup1_sh_issue(ShHalf<NCH> &s, const RbtExpertDev &J) {
+  constexpr int K = NCH * 512, SR = K >> 5, D = NCH / 2;
+  const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, rho = col >> 2, kap = col & 3;
+  const int s_row = (lane >> 4) & 3, s_off = min(16 * (lane & 15), SR - 16);
+  const long row0 = 4L * s.su;
+  s.sv[0] = *(const rbt_gu4 *)((const uint8_t *)J.gs + (row0 + s_row) * SR + s_off);
+  s.sv[1] = *(const rbt_gu4 *)((const uint8_t *)J.us + (row0 + s_row) * SR + s_off);
+  const long off = (row0 + rho) * (K >> 1) + 64 * kap + 16 * g + 256L * D * s.hf;
+#pragma unroll
+  for (int d = 0; d < D; d++) {
+    s.ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)(J.gd + off + 256 * d));
+    s.ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(J.ud + off + 256 * d));
+  }
+}
+
+// h of the workgroup's shared units [s0, s0 + nsu) from the halves' row sums (after a barrier that
+// follows every wave's half): gate and up are each the first half's sum plus the second's.
+__device__ __forceinline__ void xgateup1_sh_combine(const GuLds &L, int s0, int nsu, int slot, int I,
+                                                    __bf16 *__restrict__ hp) {
+  const int t = threadIdx.x;
+  if (t < 4 * nsu) {
+    const int j = t >> 2, r = t & 3;
+    const float gv = __fadd_rn(L.sp[2 * j][r][0], L.sp[2 * j + 1][r][0]);
+    const float uv = __fadd_rn(L.sp[2 * j][r][1], L.sp[2 * j + 1][r][1]);
+    const float hv = rbt_silu(gv) * uv;
+    __bf16 hh, mm, ll;
+    split3(hv, hh, mm, ll);
+    const long rr = 4L * (s0 + j) + r;
+    hp[((long)slot * 3 + 0) * I + rr] = hh;
+    hp[((long)slot * 3 + 1) * I + rr] = mm;
+    hp[((long)slot * 3 + 2) * I + rr] = ll;
+  }
+}
 
 // The token's activation, thread t's float4 chunks t + 256 j (the first step of the body, issued
 // early by callers that have other work before the body proper).
@@ -121,10 +178,13 @@ __device__ __forceinline__ void xgateup1_stage_x(GuLds &L, const float4 (&xv)[NC
 
 // The body with the activation already in registers (xgateup1_load_x), or, with STAGED, already in
 // LDS (xgateup1_stage_x, xv unused); `jobs` may point at LDS.
-template <int NCH, bool STAGED = false>
+// With SH, a wave whose sh.su >= 0 first multiplies its preloaded shared half unit (scales into
+// window buffer 1, row sums into L.sp) while its first routed unit's loads go out.
+template <int NCH, bool STAGED = false, bool SH = false>
 __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
                                              const float4 (&xv)[NCH / 2], const float *__restrict__ x, int I,
-                                             __bf16 *__restrict__ hp, int wg, int nwg) {
+                                             __bf16 *__restrict__ hp, int wg, int nwg,
+                                             const ShHalf<NCH> *sh = nullptr) {
   // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
   // the first half of the next unit (slots and the unit epilogue are compile-time positions)
   constexpr int K = NCH * 512, stride = K + XG_PAD, SR = K >> 5, D = NCH / 2;
@@ -139,9 +199,14 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
   const long U = (long)npairs * tpp, NW = 4L * nwg, wi = 4L * wg + w;
   const int u0 = (int)(wi * U / NW), u1 = (int)((wi + 1) * U / NW);
   // the wave's units span at most two pairs (U / NW < I / 4)
-  const int pa = u0 / tpp, pb = min(pa + 1, npairs - 1);
-  const RbtExpertDev JA = jobs[pa], JB = jobs[pb];
+  const int pa = min(u0 / tpp, max(npairs - 1, 0)), pb = min(pa + 1, max(npairs - 1, 0));
+  RbtExpertDev JA{}, JB{};
+  if (u1 > u0) {
+    JA = jobs[pa];
+    JB = jobs[pb];
+  }
   const bool live = u1 > u0 && JA.gd != nullptr && JA.ud != nullptr && JB.gd != nullptr && JB.ud != nullptr;
+  const bool shw = SH && sh->su >= 0;  // this wave has a shared half
   // lane pointers of unit u (clamped to the wave's last unit): codes of gate / up at step 0, and the
   // lane's scale piece (16 bytes of row (lane >> 4) & 3, clamped at the row end)
   const int s_row = (lane >> 4) & 3, s_off = min(16 * (lane & 15), SR - 16);
@@ -172,10 +237,12 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
     nxt = uptr(u0 + 1);
     sv[0] = *(const rbt_gu4 *)cur.gs;
     sv[1] = *(const rbt_gu4 *)cur.us;
+    if (!shw) {
 #pragma unroll
-    for (int d = 0; d < D; d++) {
-      ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.g + 256 * d));
-      ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * d));
+      for (int d = 0; d < D; d++) {
+        ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.g + 256 * d));
+        ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * d));
+      }
     }
   }
   if (!STAGED) xgateup1_stage_x<NCH>(L, xv);
@@ -183,6 +250,37 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
     *reinterpret_cast<rbt_u4 *>(&sw[w][buf][0][s_row][16 * (lane & 15)]) = sv[0];
     *reinterpret_cast<rbt_u4 *>(&sw[w][buf][1][s_row][16 * (lane & 15)]) = sv[1];
   };
+  const int bq = col >> 2, bpart = col & 3;
+  const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
+                             : reinterpret_cast<const char *>(zb);
+  const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
+  if (SH && shw) {
+    // the shared half: its scales into window buffer 1 (its loads landed during the selection),
+    // then its steps, each refilled with the same step of the first routed unit
+    *reinterpret_cast<rbt_u4 *>(&sw[w][1][0][s_row][16 * (lane & 15)]) = sh->sv[0];
+    *reinterpret_cast<rbt_u4 *>(&sw[w][1][1][s_row][16 * (lane & 15)]) = sh->sv[1];
+    const uint8_t(*win)[4][256] = sw[w][1];
+    xf4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < D; c++) {
+      const int cs = sh->hf * D + c;
+      const XB B = xb_read(bp + binc * cs);
+      const int sb = 16 * cs + 4 * kap + g;
+      const rbt_u4 cg = sh->ring[c][0], cu = sh->ring[c][1];
+      if (live) {
+        ring[c][0] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.g + 256 * c));
+        ring[c][1] = __builtin_nontemporal_load((const rbt_gu4 *)(cur.u + 256 * c));
+      }
+      xmma_s(cg, xe8m0(win[0][rho][sb]), B, ag);
+      xmma_s(cu, xe8m0(win[1][rho][sb]), B, au);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    const float gv = row_dot(ag, col), uv = row_dot(au, col);
+    if (col == 0) {  // lane 16 g: row g of the unit
+      L.sp[w][g][0] = gv;
+      L.sp[w][g][1] = uv;
+    }
+  }
   if (live) {
     sstore(0);
     sv[0] = *(const rbt_gu4 *)nxt.gs;  // scales of the next unit (the last unit's own, if none)
@@ -197,10 +295,6 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
     }
     return;
   }
-  const int bq = col >> 2, bpart = col & 3;
-  const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
-                             : reinterpret_cast<const char *>(zb);
-  const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
   for (int u = u0; u < u1; u++) {
     const uint8_t(*win)[4][256] = sw[w][(u - u0) & 1];
     xf4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};

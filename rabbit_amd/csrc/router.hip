@@ -1990,7 +1990,7 @@ __device__ __forceinline__ void load_key_recs(const KeyRec *__restrict__ rec, in
 }
 
 template <int MAXM>
-__device__ int select_pairs(SelLds &L, PairLds &Q, const SelParams &P, const float4 (&rv)[MAXM],
+__device__ __forceinline__ int select_pairs(SelLds &L, PairLds &Q, const SelParams &P, const float4 (&rv)[MAXM],
                             const RbtExpertDev *__restrict__ table) {
   const int lane = threadIdx.x & 63;
   const int E = P.E, k = P.k, kk = min(P.k, P.E);
@@ -2438,7 +2438,7 @@ __global__ __launch_bounds__(256) void k_router_logits_tk(const float *__restric
 // and the down launch's job list (the winners in rank order at pair slots 0..kk-1, then the shared
 // expert at its slot). Wave 0.
 // ------------------------------------------------------------------------------------------------
-__device__ void publish_certified(SelLds &L, const PairLds &Q, const SelParams &P, const GroupOut &G,
+__device__ __forceinline__ void publish_certified(SelLds &L, const PairLds &Q, const SelParams &P, const GroupOut &G,
                                   int32_t *__restrict__ ids, float *__restrict__ wts) {
   const int lane = threadIdx.x & 63;
   const int k = P.k, kk = min(P.k, P.E);
@@ -2466,7 +2466,7 @@ __device__ void publish_certified(SelLds &L, const PairLds &Q, const SelParams &
 // were folded and midpoint keys elsewhere (an unflagged candidate's interval is disjoint from every
 // other candidate's, so its midpoint orders it), and writes ids, weights, tok_pair / tok_w and the
 // down job list.
-__device__ void d1_finish(SelLds &L, float (*fold)[2][1024], const SelParams &P, const D1Task *__restrict__ T,
+__device__ __forceinline__ void d1_finish(SelLds &L, float (*fold)[2][1024], const SelParams &P, const D1Task *__restrict__ T,
                           const GroupOut &G, int32_t *__restrict__ ids, float *__restrict__ wts,
                           int *__restrict__ stats) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2536,7 +2536,7 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
                                                    const double *__restrict__ mid, const double *__restrict__ bnd,
                                                    GroupOut G, int32_t *__restrict__ ids, float *__restrict__ wts,
                                                    int *__restrict__ stats, int *__restrict__ gup, int I,
-                                                   __bf16 *__restrict__ hp, int has_shared) {
+                                                   __bf16 *__restrict__ hp, int has_shared, RbtExpertDev shv) {
   __shared__ union {
     GuLds gu;
     __attribute__((aligned(16))) float fold[4][2][1024];  // workgroup 0, deferred: exact_logit_lds's blocks
@@ -2553,25 +2553,44 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   if (t < 64) load_key_recs<MAXM>(rec, E, rv);
   float4 xv[NCH / 2];
   xgateup1_load_x<NCH>(P.x, xv);
+  constexpr int TQ = (GU1S_MAXE * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
+  const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
+  rbt_u4 tv[TQ];
   {
-    constexpr int TQ = (GU1S_MAXE * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
-    const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
     const rbt_gu4 *src = (const rbt_gu4 *)G.table;
-    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
-    rbt_u4 tv[TQ];
 #pragma unroll
     for (int i = 0; i < TQ; i++) tv[i] = src[min(t + 256 * i, n4 - 1)];
+  }
+  {
+    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
 #pragma unroll
     for (int i = 0; i < TQ; i++)
       if (t + 256 * i < n4) dst[t + 256 * i] = tv[i];
   }
   xgateup1_stage_x<NCH>(U.gu, xv);
-  __syncthreads();
+  // The shared expert's gate/up does not depend on the routing: when every workgroup holds at most
+  // two of its 4-row units, each unit is two half units (waves 2j, 2j + 1), whose loads go out now
+  // and land during the selection (issued after the selection's own inputs have landed, which they
+  // would otherwise delay). The routed pairs then balance over the grid without it.
+  const int tpp = I >> 2;
+  const bool shpro = has_shared && shv.gd && shv.ud && shv.gs && shv.us && tpp <= 2 * (int)gridDim.x;
+  const int s0 = shpro ? (int)((long)blockIdx.x * tpp / gridDim.x) : 0;
+  const int nsu = shpro ? (int)((long)(blockIdx.x + 1) * tpp / gridDim.x) - s0 : 0;
+  // Wave 0 selects first: its half goes out after the selection (loads issued ahead of the selection
+  // would hold its issue slots until the memory pipeline has room for all of them).
+  ShHalf<NCH> sh;
+  if ((t >> 6) < 2 * nsu) {
+    sh.su = s0 + (t >> 7);
+    sh.hf = (t >> 6) & 1;
+    if (t >= 64) xgateup1_sh_issue<NCH>(sh, shv);
+  }
+  lds_barrier();  // the staged activation and table (the shared loads stay in flight)
   if (t < 64) {
     const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
     if (t == 0) Q.status = r;
   }
-  __syncthreads();
+  if (t < 64 && sh.su >= 0) xgateup1_sh_issue<NCH>(sh, shv);
+  lds_barrier();
   const int st = Q.status;
   // the shared expert streams as the pair after the routed ones: its h lands at pair slot nr
   GroupOut Gs = G;
@@ -2603,19 +2622,28 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   const bool pending = st == 2;
   const int nr = Q.T.nr;
   Gs.shared_slot = nr;
+  const bool decider = !streamer && pending;  // folds and decides; streams no routed pair
   if (!streamer) {
     if (t == 0 && gup) atomicAdd(gup, nr + has_shared);
-    if (pending) {
-      d1_finish(S, U.fold, P, &Q.T, Gs, ids, wts, stats);  // U.gu's staged activation is not needed
-      return;
-    }
     if (st == 1 && t < 64) publish_certified(S, Q, P, Gs, ids, wts);
   }
-  if (has_shared && t == 0) copy_job(Q.pj + nr, G.shared_dev);
+  if (has_shared && !shpro && t == 0) copy_job(Q.pj + nr, G.shared_dev);
   __syncthreads();
-  // the routed pairs, then the shared expert, balanced over the grid
-  const int wg = pending ? blockIdx.x - 1 : blockIdx.x, nwg = pending ? gridDim.x - 1 : gridDim.x;
-  xgateup1_run<NCH, true>(U.gu, Q.pj, nr + has_shared, xv, P.x, I, hp, wg, nwg);
+  if (!decider || shpro) {
+    // the routed pairs (and the shared expert unless it went out early), balanced over the grid;
+    // the deciding workgroup only multiplies its shared half units
+    const int wg = pending ? blockIdx.x - 1 : blockIdx.x, nwg = pending ? gridDim.x - 1 : gridDim.x;
+    xgateup1_run<NCH, true, true>(U.gu, Q.pj, decider ? 0 : nr + (has_shared && !shpro), xv, P.x, I, hp,
+                                  decider ? 0 : wg, decider ? 1 : nwg, &sh);
+    if (shpro) {
+      __syncthreads();
+      xgateup1_sh_combine(U.gu, s0, nsu, nr, I, hp);
+    }
+  }
+  if (decider) {
+    __syncthreads();
+    d1_finish(S, U.fold, P, &Q.T, Gs, ids, wts, stats);  // U.gu's staged activation is not needed
+  }
 }
 
 static SelParams sel_params(const RouterArgs &a) {
@@ -2671,7 +2699,8 @@ hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec_b
   const dim3 grid(c.num_cu);
   const bool m4 = a.E <= 256;
 #define RBT_GU1S(M, N) \
-  launch_k(c, k_xgateup1s<M, N>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I, hp, (int)has_shared)
+  launch_k(c, k_xgateup1s<M, N>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I, hp, (int)has_shared, \
+           grp.shv)
   if (a.H == 8192) {
     if (m4)
       RBT_GU1S(4, 16);

@@ -397,12 +397,6 @@ constexpr int XD1_NW = 8;    // waves per workgroup
 constexpr int XD1_TPW = 16;  // most 4-row tiles per workgroup
 
 
-// Barrier for LDS hand-offs only: global loads in flight stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 template <int NCH>
 __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__restrict__ jobs,
