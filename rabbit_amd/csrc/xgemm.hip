@@ -427,7 +427,11 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   const int T0 = (int)((long)blockIdx.x * ntile / gridDim.x), T1 = (int)((long)(blockIdx.x + 1) * ntile / gridDim.x);
   const int nt = T1 - T0;
   const int NU = nt * npairs;
-  const int u0 = w * NU / XD1_NW, u1 = (w + 1) * NU / XD1_NW;
+  // Wave w takes units w, w + NW, w + 2 NW, ... (its i-th unit is uu(i)): the eight waves move
+  // through the pairs together, so a window touches the pages of a few experts at a time instead of
+  // every expert's at the start (each new page costs the CU a translation miss).
+  const int nu = NU > w ? (NU - w + XD1_NW - 1) / XD1_NW : 0;
+  auto uu = [&](int i) { return w + XD1_NW * i; };
   const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
   const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
   const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
@@ -450,14 +454,15 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
     return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
   };
-  // First window (units u0 .. u0+3): pointers from the tables' lanes (the pair is wave-uniform).
+  // First window (units 0 .. 3 of the wave): pointers from the tables' lanes (the pair is
+  // wave-uniform).
   const uint8_t *cp[4], *sp[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    const int u = u0 + j;
+    const int u = uu(j);
     cp[j] = dummy;
     sp[j] = hb8 + 16 * s_seg;
-    if (u < u1) {
+    if (j < nu) {
       const int pp = u / nt, tl = u - pp * nt;
       const uint8_t *dd = lane_ptr(t_dd, pp);
       const uint8_t *ds = lane_ptr(t_ds, pp);
@@ -508,18 +513,19 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
       *reinterpret_cast<rbt_u4 *>(&hs[pp][(q / (KD / 8)) * stride + 8 * (q % (KD / 8))]) = hr[i];
     }
   }
-  // lane pointer of unit u (chunk 0); past the wave's units or for a null job: cached dummy bytes
-  auto uptr = [&](int u) -> const uint8_t * {
-    if (u >= u1) return dummy;
-    const int pp = u / nt, tl = u - pp * nt;
+  // lane pointer of the wave's unit i (chunk 0); past its units or for a null job: cached dummy bytes
+  auto uptr = [&](int i) -> const uint8_t * {
+    if (i >= nu) return dummy;
+    const int u = uu(i), pp = u / nt, tl = u - pp * nt;
     return plive[pp] ? pd[pp] + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
   };
-  // scale window of units ub .. ub+3: lane l holds unit ub + l/16, row (l/4) % 4, bytes 16 (l % 4)
-  auto sload = [&](int ub) {
-    const int u = ub + s_q;
+  // scale window of the wave's units ib .. ib+3: lane l holds unit ib + l/16, row (l/4) % 4, bytes
+  // 16 (l % 4)
+  auto sload = [&](int ib) {
+    const int i = ib + s_q;
     const uint8_t *p = hb8 + 16 * s_seg;
-    if (u < u1) {
-      const int pp = u / nt, tl = u - pp * nt;
+    if (i < nu) {
+      const int u = uu(i), pp = u / nt, tl = u - pp * nt;
       if (plive[pp]) p = ps[pp] + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
     }
     return *(const rbt_gu4 *)p;
@@ -529,25 +535,25 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   };
   sstore(0, sv);
   lds_barrier();  // tables, h parts, first scale windows
-  sv = sload(u0 + 4);
+  sv = sload(4);
   const int bq = col >> 2, bpart = col & 3;
   const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
   const int binc = bpart < 3 ? 1024 : 0;
   int buf = 0;
-  for (int ub = u0; ub < u1; ub += 4) {
+  for (int ib = 0; ib < nu; ib += 4) {
     const uint8_t(*win)[4][64] = sw[w][buf];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int u = ub + j;
-      const uint8_t *np = uptr(u + 4);
+      const int i = ib + j;
+      const uint8_t *np = uptr(i + 4);
       rbt_u4 cw[NCH];
 #pragma unroll
       for (int c = 0; c < NCH; c++) {
         cw[c] = ring[j][c];
         ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(np + 256 * c));
       }
-      if (u < u1) {
-        const int pp = u / nt, tl = u - pp * nt;
+      if (i < nu) {
+        const int u = uu(i), pp = u / nt, tl = u - pp * nt;
         const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[pp]) + boff : reinterpret_cast<const char *>(zb);
         xf4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -562,7 +568,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     }
     buf ^= 1;
     sstore(buf, sv);
-    sv = sload(ub + 8);
+    sv = sload(ib + 8);
   }
   __syncthreads();
   if (tid < 4 * nt) {
