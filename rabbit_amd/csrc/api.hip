@@ -1039,6 +1039,34 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   // routing of the full-width x (certified logits, exact folds where the order is not certain)
   rbt::RouterArgs ra{D.family, (int)E, (int)E, K, (int)H, S, D.logit_bias, D.router_bias, D.norm_topk,
                      D.routed_scale, (int)D.n_group, (int)D.topk_group, x, D.router};
+  const rbt_qt &Dp = lw->down_proj;
+  const bool dp_ok = rbt::router_select_dp_ok(ra, Dp.kind, (int)H, (int)MH) &&
+                     (Dp.kind != RBT_QT_I4_GROUPED || Dp.group_size == 32) &&
+                     ((uintptr_t)Dp.data | (uintptr_t)x) % 16 == 0 && Dp.data && Dp.scale;
+  RbtExpertDev none{};
+  if (kind == RBT_QT_MXFP4 && dp_ok && rbt::router1_latent_ok(ra, c->num_cu, (int)MH, (int)I) &&
+      rbt::decode_shape_ok(I, kind, gs)) {
+    // One token, MXFP4 experts, as the plain layer's decode: the router rows' key records; the
+    // latent down projection; the selection in every workgroup of the gate/up launch (matrix cores,
+    // act fused, h in fp32); the down GEMV over the winners' job list (h rows at their pair slots);
+    // then the ordered combine and the up projection below.
+    RBT_TRY(check_qt(c, &Dp, "matmul"));
+    float *rec;
+    RbtExpertDev *djob;
+    int *dslot;
+    RBT_TRY(scratch_t(c, SC_RREC, E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
+    RBT_TRY(scratch_t(c, SC_DJOB, (size_t)(K + 1), &djob));
+    RBT_TRY(scratch_t(c, SC_DSLOT, (size_t)(K + 1), &dslot));
+    rbt::GroupArgs ga{table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
+    ga.down_job = djob;
+    ga.down_slot = dslot;
+    HIP_OK(c, rbt::launch_router1_latent(*c, ra, mid, bnd, shs, rec, (int)MH, (int)I));
+    RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
+    HIP_OK(c, rbt::launch_xgateup1s_latent(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, nullptr, xl, (int)MH,
+                                           (int)I, h, act));
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, djob, none, K, nullptr, h, dslot, (long)I, (int)I,
+                                 (int)MH, yy, (long)MH));
+  } else {
   if (rbt::router_exact_ok(S, (int)H) && ((uintptr_t)x | (uintptr_t)D.router) % 16 == 0) {
     float *lg;
     RBT_TRY(scratch_t(c, SC_RLOG, (size_t)S * E, &lg));
@@ -1050,10 +1078,7 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   // one token: the selection writes the pair list itself (pair j = slot j)
   const bool grp_in_select = S == 1 && !(D.n_group > 1 && D.family != RBT_FAMILY_QWEN38);
   rbt::GroupArgs ga{table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
-  const rbt_qt &Dp = lw->down_proj;
-  const bool dp_fused = grp_in_select && rbt::router_select_dp_ok(ra, Dp.kind, (int)H, (int)MH) &&
-                        (Dp.kind != RBT_QT_I4_GROUPED || Dp.group_size == 32) &&
-                        ((uintptr_t)Dp.data | (uintptr_t)x) % 16 == 0 && Dp.data && Dp.scale;
+  const bool dp_fused = grp_in_select && dp_ok;
   if (dp_fused) {
     // one token: the latent down projection streams while the selection runs (one launch)
     RBT_TRY(check_qt(c, &Dp, "matmul"));
@@ -1070,8 +1095,8 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   if (!grp_in_select)
     HIP_OK(c, rbt::launch_group(*c, ids, wts, S, K, (int)E, table, table + E, pjob, ptok, tpair, tw,
                                 dflags + FLAG_ERR, dflags + FLAG_UNIQ));
-  RbtExpertDev none{};
   RBT_TRY(expert_pairs(c, kind, gs, pjob, none, P, nullptr, xl, ptok, MH, I, h, yy, nullptr, act));
+  }
   HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
   const rbt_qt &U = lw->up_proj;
   if (lw->norm && U.kind != RBT_QT_F32 && rbt::decode_shape_ok(MH, U.kind, U.group_size) &&

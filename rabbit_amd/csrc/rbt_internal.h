@@ -236,6 +236,16 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
 hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,
                             const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int *gup,
                             int I, __bf16 *hp, bool has_shared);
+// K3's latent MoE, one token: the router rows' key records (one row per workgroup), then, after the
+// latent down projection, the selection and the experts' gate/up with act on the matrix cores over
+// x_latent (moe_hidden 3584), h in fp32 (pair slot c at h + I c); ga's down job list, slots,
+// tok_pair and tok_w as launch_xgateup1s writes them.
+bool router1_latent_ok(const RouterArgs &a, int num_cu, int mh, int I);
+hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                                 void *rec, int mh, int I);
+hipError_t launch_xgateup1s_latent(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,
+                                   const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats,
+                                   int *gup, const float *xl, int mh, int I, float *h, const RbtAct &act);
 // Device bytes of the key records launch_router1 writes (per router row).
 constexpr size_t ROUTER1_REC_BYTES = 16;
 hipError_t launch_logits_to_mid(const Ctx &c, const float *logits, size_t n, double *mid, double *bnd);

@@ -107,12 +107,13 @@ struct GuLds {
 template <int NCH>
 struct ShHalf {
   int su = -1, hf = 0;  // su < 0: no half for this wave
-  rbt_u4 ring[NCH / 2][2];
+  rbt_u4 ring[NCH % 2 == 0 ? NCH / 2 : 1][2];
   rbt_u4 sv[2];  // the lane's scale pieces of the unit (as the body's window loads)
 };
 
 template <int NCH>
 __device__ __forceinline__ void xgateup1_sh_issue(ShHalf<NCH> &s, const RbtExpertDev &J) {
+  static_assert(NCH % 2 == 0, "half units need an even step count");
   constexpr int K = NCH * 512, SR = K >> 5, D = NCH / 2;
   const int lane = threadIdx.x & 63, g = lane >> 4, col = lane & 15, rho = col >> 2, kap = col & 3;
   const int s_row = (lane >> 4) & 3, s_off = min(16 * (lane & 15), SR - 16);
@@ -149,21 +150,25 @@ __device__ __forceinline__ void xgateup1_sh_combine(const GuLds &L, int s0, int 
 // The token's activation, thread t's float4 chunks t + 256 j (the first step of the body, issued
 // early by callers that have other work before the body proper).
 template <int NCH>
-__device__ __forceinline__ void xgateup1_load_x(const float *__restrict__ x, float4 (&xv)[NCH / 2]) {
+constexpr int xg_nv() { return (NCH * 128 + 255) / 256; }  // float4 chunks of K = 512 NCH values per thread
+
+template <int NCH>
+__device__ __forceinline__ void xgateup1_load_x(const float *__restrict__ x, float4 (&xv)[xg_nv<NCH>()]) {
   const rbt_gf4 *s4 = (const rbt_gf4 *)x;
 #pragma unroll
-  for (int j = 0; j < NCH / 2; j++) xv[j] = s4[threadIdx.x + 256 * j];
+  for (int j = 0; j < xg_nv<NCH>(); j++) xv[j] = s4[min((int)threadIdx.x + 256 * j, NCH * 128 - 1)];
 }
 
 // The activation's three bf16 parts (and the zero block) into the body's LDS; the body's first
 // barrier publishes them.
 template <int NCH>
-__device__ __forceinline__ void xgateup1_stage_x(GuLds &L, const float4 (&xv)[NCH / 2]) {
+__device__ __forceinline__ void xgateup1_stage_x(GuLds &L, const float4 (&xv)[xg_nv<NCH>()]) {
   constexpr int stride = NCH * 512 + XG_PAD;
   if (threadIdx.x < 32) L.zb[threadIdx.x] = (__bf16)0.0f;
 #pragma unroll
-  for (int j = 0; j < NCH / 2; j++) {
+  for (int j = 0; j < xg_nv<NCH>(); j++) {
     const int q = threadIdx.x + 256 * j;
+    if (q >= NCH * 128) break;
     const float e4[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -179,16 +184,18 @@ __device__ __forceinline__ void xgateup1_stage_x(GuLds &L, const float4 (&xv)[NC
 // The body with the activation already in registers (xgateup1_load_x), or, with STAGED, already in
 // LDS (xgateup1_stage_x, xv unused); `jobs` may point at LDS.
 // With SH, a wave whose sh.su >= 0 first multiplies its preloaded shared half unit (scales into
-// window buffer 1, row sums into L.sp) while its first routed unit's loads go out.
-template <int NCH, bool STAGED = false, bool SH = false>
+// window buffer 1, row sums into L.sp) while its first routed unit's loads go out. h = act(g, u)
+// (rbt_act: SiLU by default); with HF32 it is stored as one fp32 value per row (pair p's rows at
+// hp + 2 I p as floats) instead of three bf16 parts.
+template <int NCH, bool STAGED = false, bool SH = false, bool HF32 = false>
 __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
-                                             const float4 (&xv)[NCH / 2], const float *__restrict__ x, int I,
+                                             const float4 (&xv)[xg_nv<NCH>()], const float *__restrict__ x, int I,
                                              __bf16 *__restrict__ hp, int wg, int nwg,
-                                             const ShHalf<NCH> *sh = nullptr) {
+                                             const ShHalf<NCH> *sh = nullptr, const RbtAct &act = RbtAct{}) {
   // ring depth: half a unit, so step c < D prefetches step c + D of the same unit and step c >= D
   // the first half of the next unit (slots and the unit epilogue are compile-time positions)
-  constexpr int K = NCH * 512, stride = K + XG_PAD, SR = K >> 5, D = NCH / 2;
-  static_assert(NCH % 2 == 0, "even step count");
+  // (an odd step count keeps a whole unit in flight)
+  constexpr int K = NCH * 512, stride = K + XG_PAD, SR = K >> 5, D = NCH % 2 == 0 ? NCH / 2 : NCH;
   static_assert(K <= 8192, "GuLds holds K <= 8192");
   __bf16 *xs = L.xs;
   __bf16 *zb = L.zb;
@@ -254,7 +261,7 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
   const char *bp = bpart < 3 ? reinterpret_cast<const char *>(xs + bpart * stride + 128 * bq + 32 * g)
                              : reinterpret_cast<const char *>(zb);
   const int binc = bpart < 3 ? 1024 : 0;  // bytes per step (512 bf16)
-  if (SH && shw) {
+  if constexpr (SH && NCH % 2 == 0) if (shw) {
     // the shared half: its scales into window buffer 1 (its loads landed during the selection),
     // then its steps, each refilled with the same step of the first routed unit
     *reinterpret_cast<rbt_u4 *>(&sw[w][1][0][s_row][16 * (lane & 15)]) = sh->sv[0];
@@ -291,7 +298,11 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
     // a missing expert is reported by the grouping (error flag); zero this wave's rows of h
     for (int u = u0; u < u1; u++) {
       const int pp = u / tpp;
-      if (lane < 12) hp[((long)pp * 3 + lane / 4) * I + 4L * (u - pp * tpp) + (lane & 3)] = (__bf16)0.0f;
+      if (HF32) {
+        if (lane < 4) reinterpret_cast<float *>(hp)[(long)pp * I + 4L * (u - pp * tpp) + lane] = 0.0f;
+      } else if (lane < 12) {
+        hp[((long)pp * 3 + lane / 4) * I + 4L * (u - pp * tpp) + (lane & 3)] = (__bf16)0.0f;
+      }
     }
     return;
   }
@@ -304,9 +315,9 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
       const XB B = xb_read(bp + binc * c);
       const int sb = 16 * c + 4 * kap + g;
       const rbt_u4 cg = ring[d][0], cu = ring[d][1];
-      // refill: step c + D of this unit, or step c - D of the next one
-      const uint8_t *rg = c < D ? cur.g + 256 * (c + D) : nxt.g + 256 * (c - D);
-      const uint8_t *ru = c < D ? cur.u + 256 * (c + D) : nxt.u + 256 * (c - D);
+      // refill: step c + D of this unit, or of the next one past the unit's end
+      const uint8_t *rg = c + D < NCH ? cur.g + 256 * (c + D) : nxt.g + 256 * (c + D - NCH);
+      const uint8_t *ru = c + D < NCH ? cur.u + 256 * (c + D) : nxt.u + 256 * (c + D - NCH);
       ring[d][0] = __builtin_nontemporal_load((const rbt_gu4 *)rg);
       ring[d][1] = __builtin_nontemporal_load((const rbt_gu4 *)ru);
       xmma_s(cg, xe8m0(win[0][rho][sb]), B, ag);
@@ -317,13 +328,17 @@ __device__ __forceinline__ void xgateup1_run(GuLds &L, const RbtExpertDev *__res
     const float gv = row_dot(ag, col), uv = row_dot(au, col);
     const int pp = u / tpp;
     if (col == 0) {  // lane 16*g: row 4 t + g of the unit's pair
-      const float hv = rbt_silu(gv) * uv;
-      __bf16 hh, mm, ll;
-      split3(hv, hh, mm, ll);
+      const float hv = rbt_act(act, gv, uv);
       const long rr = 4L * (u - pp * tpp) + g;
-      hp[((long)pp * 3 + 0) * I + rr] = hh;
-      hp[((long)pp * 3 + 1) * I + rr] = mm;
-      hp[((long)pp * 3 + 2) * I + rr] = ll;
+      if (HF32) {
+        reinterpret_cast<float *>(hp)[(long)pp * I + rr] = hv;
+      } else {
+        __bf16 hh, mm, ll;
+        split3(hv, hh, mm, ll);
+        hp[((long)pp * 3 + 0) * I + rr] = hh;
+        hp[((long)pp * 3 + 1) * I + rr] = mm;
+        hp[((long)pp * 3 + 2) * I + rr] = ll;
+      }
     }
     // next unit's scales into the other window, then look one unit further ahead
     sstore((u + 1 - u0) & 1);
@@ -340,7 +355,7 @@ template <int NCH>
 __device__ __forceinline__ void xgateup1_body(GuLds &L, const RbtExpertDev *__restrict__ jobs, int npairs,
                                               const float *__restrict__ x, int I, __bf16 *__restrict__ hp, int wg,
                                               int nwg) {
-  float4 xv[NCH / 2];
+  float4 xv[xg_nv<NCH>()];
   xgateup1_load_x<NCH>(x, xv);
   xgateup1_run<NCH>(L, jobs, npairs, xv, x, I, hp, wg, nwg);
 }

@@ -2346,13 +2346,13 @@ __device__ __forceinline__ void norm1p_chunks(LgLds<NR> &L, float4 (&xv)[RT_MAXH
 // With nw (the MoE sublayer), P.x is the raw token and every workgroup first normalises it
 // (rmsnorm_1p with weights nw, eps) for its rows; workgroup 0 writes the normalised token to xn.
 template <int RPW>
-__global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
-                                                 double *__restrict__ mid, double *__restrict__ bnd,
-                                                 float *__restrict__ sh_scale, KeyRec *__restrict__ rec,
-                                                 const float *__restrict__ nw, float eps, float *__restrict__ xn) {
+__device__ __forceinline__ void router1_body(LgLds<RPW == 1 ? 1 : 2> &L, const SelParams &P,
+                                             const float *__restrict__ sgate, double *__restrict__ mid,
+                                             double *__restrict__ bnd, float *__restrict__ sh_scale,
+                                             KeyRec *__restrict__ rec, const float *__restrict__ nw, float eps,
+                                             float *__restrict__ xn, int b) {
   constexpr int MC = RT_MAXH / 1024, NR = RPW == 1 ? 1 : 2;
-  __shared__ LgLds<NR> L;
-  const int t = threadIdx.x, b = blockIdx.x;
+  const int t = threadIdx.x;
   const int H = P.H, E = P.E, nch = H / 1024;
   if (sgate == nullptr && b == 0 && t == 0) sh_scale[0] = 1.0f;
   const int Rn = E + (sgate != nullptr ? 1 : 0), r0 = RPW * b;
@@ -2402,6 +2402,15 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
   // gated shared expert: sigmoid of the fp32-rounded gate logit (qwen38/moe.rs:78-83); the row's
   // sum was stored before the last barrier of logits_rows_blk
   if (sgate != nullptr && r0 <= E && E < r0 + RPW && t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
+}
+
+template <int RPW>
+__global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
+                                                 double *__restrict__ mid, double *__restrict__ bnd,
+                                                 float *__restrict__ sh_scale, KeyRec *__restrict__ rec,
+                                                 const float *__restrict__ nw, float eps, float *__restrict__ xn) {
+  __shared__ LgLds<RPW == 1 ? 1 : 2> L;
+  router1_body<RPW>(L, P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn, blockIdx.x);
 }
 
 // Certified logits of a small batch: workgroup (row, q) computes router row `row` (or the shared
@@ -2530,20 +2539,23 @@ __device__ __forceinline__ void d1_finish(SelLds &L, float (*fold)[2][1024], con
 }
 
 // gup (optional) counts the routed pairs the launch streams (for the benchmark's byte accounting).
-constexpr int GU1S_MAXE = 512;  // experts whose job-table entries a workgroup stages in LDS
-template <int MAXM, int NCH>
+// xg: the gate/up activation (K = 512 NCH values; the router's own token in a plain layer, the
+// latent token in K3's latent MoE); h = act(g, u), as three bf16 parts or (HF32) fp32.
+// A workgroup stages the job-table entries of up to 64 MAXM experts in LDS.
+template <int MAXM, int NCH, bool HF32>
 __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__restrict__ rec,
                                                    const double *__restrict__ mid, const double *__restrict__ bnd,
                                                    GroupOut G, int32_t *__restrict__ ids, float *__restrict__ wts,
                                                    int *__restrict__ stats, int *__restrict__ gup, int I,
-                                                   __bf16 *__restrict__ hp, int has_shared, RbtExpertDev shv) {
+                                                   __bf16 *__restrict__ hp, int has_shared, RbtExpertDev shv,
+                                                   const float *__restrict__ xg, RbtAct act) {
   __shared__ union {
     GuLds gu;
     __attribute__((aligned(16))) float fold[4][2][1024];  // workgroup 0, deferred: exact_logit_lds's blocks
   } U;
   __shared__ SelLds S;
   __shared__ PairLds Q;
-  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[GU1S_MAXE];
+  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[64 * MAXM];
   const int t = threadIdx.x, lane = t & 63;
   const bool streamer = blockIdx.x > 0;
   const int E = P.E, kk = min(P.k, P.E);
@@ -2551,9 +2563,9 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   // (wave 0), the activation, and the whole job table (so a winner's entry is an LDS read).
   float4 rv[MAXM];
   if (t < 64) load_key_recs<MAXM>(rec, E, rv);
-  float4 xv[NCH / 2];
-  xgateup1_load_x<NCH>(P.x, xv);
-  constexpr int TQ = (GU1S_MAXE * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
+  float4 xv[xg_nv<NCH>()];
+  xgateup1_load_x<NCH>(xg, xv);
+  constexpr int TQ = (64 * MAXM * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
   const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
   rbt_u4 tv[TQ];
   {
@@ -2573,7 +2585,8 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   // and land during the selection (issued after the selection's own inputs have landed, which they
   // would otherwise delay). The routed pairs then balance over the grid without it.
   const int tpp = I >> 2;
-  const bool shpro = has_shared && shv.gd && shv.ud && shv.gs && shv.us && tpp <= 2 * (int)gridDim.x;
+  const bool shpro = NCH % 2 == 0 && !HF32 && has_shared && shv.gd && shv.ud && shv.gs && shv.us &&
+                     tpp <= 2 * (int)gridDim.x;
   const int s0 = shpro ? (int)((long)blockIdx.x * tpp / gridDim.x) : 0;
   const int nsu = shpro ? (int)((long)(blockIdx.x + 1) * tpp / gridDim.x) - s0 : 0;
   // Wave 0 selects first: its half goes out after the selection (loads issued ahead of the selection
@@ -2582,14 +2595,16 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   if ((t >> 6) < 2 * nsu) {
     sh.su = s0 + (t >> 7);
     sh.hf = (t >> 6) & 1;
-    if (t >= 64) xgateup1_sh_issue<NCH>(sh, shv);
+    if constexpr (NCH % 2 == 0)
+      if (t >= 64) xgateup1_sh_issue<NCH>(sh, shv);
   }
   lds_barrier();  // the staged activation and table (the shared loads stay in flight)
   if (t < 64) {
     const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
     if (t == 0) Q.status = r;
   }
-  if (t < 64 && sh.su >= 0) xgateup1_sh_issue<NCH>(sh, shv);
+  if constexpr (NCH % 2 == 0)
+    if (t < 64 && sh.su >= 0) xgateup1_sh_issue<NCH>(sh, shv);
   lds_barrier();
   const int st = Q.status;
   // the shared expert streams as the pair after the routed ones: its h lands at pair slot nr
@@ -2633,8 +2648,8 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
     // the routed pairs (and the shared expert unless it went out early), balanced over the grid;
     // the deciding workgroup only multiplies its shared half units
     const int wg = pending ? blockIdx.x - 1 : blockIdx.x, nwg = pending ? gridDim.x - 1 : gridDim.x;
-    xgateup1_run<NCH, true, true>(U.gu, Q.pj, decider ? 0 : nr + (has_shared && !shpro), xv, P.x, I, hp,
-                                  decider ? 0 : wg, decider ? 1 : nwg, &sh);
+    xgateup1_run<NCH, true, true, HF32>(U.gu, Q.pj, decider ? 0 : nr + (has_shared && !shpro), xv, xg, I, hp,
+                                        decider ? 0 : wg, decider ? 1 : nwg, &sh, act);
     if (shpro) {
       __syncthreads();
       xgateup1_sh_combine(U.gu, s0, nsu, nr, I, hp);
@@ -2667,7 +2682,7 @@ static SelParams sel_params(const RouterArgs &a) {
 
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu) {
   const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
-  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= GU1S_MAXE && a.k + D1_KX <= D1_NC &&
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 512 && a.k + D1_KX <= D1_NC &&
          (a.H == 8192 || a.H == 7168) && aligned && a.E <= 2 * num_cu && num_cu >= 2 &&
          (sgu == nullptr || sgu->K == a.H);
 }
@@ -2688,6 +2703,15 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
   return hipGetLastError();
 }
 
+hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                                 void *rec_buf, int mh, int I) {
+  if (!router1_latent_ok(a, c.num_cu, mh, I)) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  launch_k(c, k_router1<1>, dim3(a.E), dim3(256), P, nullptr, mid, bnd, sh_scale, reinterpret_cast<KeyRec *>(rec_buf),
+           nullptr, 0.0f, nullptr);
+  return hipGetLastError();
+}
+
 hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec_buf, const double *mid,
                             const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int *gup,
                             int I, __bf16 *hp, bool has_shared) {
@@ -2698,9 +2722,10 @@ hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec_b
   const KeyRec *rec = reinterpret_cast<const KeyRec *>(rec_buf);
   const dim3 grid(c.num_cu);
   const bool m4 = a.E <= 256;
-#define RBT_GU1S(M, N) \
-  launch_k(c, k_xgateup1s<M, N>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I, hp, (int)has_shared, \
-           grp.shv)
+  const RbtAct act{};
+#define RBT_GU1S(M, N)                                                                                              \
+  launch_k(c, k_xgateup1s<M, N, false>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I, hp,          \
+           (int)has_shared, grp.shv, a.x, act)
   if (a.H == 8192) {
     if (m4)
       RBT_GU1S(4, 16);
@@ -2713,6 +2738,26 @@ hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec_b
       RBT_GU1S(8, 14);
   }
 #undef RBT_GU1S
+  return hipGetLastError();
+}
+
+bool router1_latent_ok(const RouterArgs &a, int num_cu, int mh, int I) {
+  const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 1024 && a.E <= 4 * num_cu &&
+         a.k + D1_KX <= D1_NC && (a.H == 8192 || a.H == 7168) && aligned && num_cu >= 2 && mh == 3584 &&
+         I % 4 == 0 && (long)a.k * (I / 4) >= 4L * num_cu;
+}
+
+hipError_t launch_xgateup1s_latent(const Ctx &c, const RouterArgs &a, const void *rec_buf, const double *mid,
+                                   const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats,
+                                   int *gup, const float *xl, int mh, int I, float *h, const RbtAct &act) {
+  if (!grp.down_job || !grp.down_slot || !router1_latent_ok(a, c.num_cu, mh, I) || (uintptr_t)xl % 16 != 0)
+    return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  const GroupOut G = group_out(grp, a.k);
+  const KeyRec *rec = reinterpret_cast<const KeyRec *>(rec_buf);
+  launch_k(c, k_xgateup1s<16, 7, true>, dim3(c.num_cu), dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I,
+           reinterpret_cast<__bf16 *>(h), 0, RbtExpertDev{}, xl, act);
   return hipGetLastError();
 }
 
