@@ -1061,7 +1061,10 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
     ga.down_job = djob;
     ga.down_slot = dslot;
     HIP_OK(c, rbt::launch_router1_latent(*c, ra, mid, bnd, shs, rec, (int)MH, (int)I));
-    RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
+    if (rbt::proj1_ok(Dp.kind, Dp.group_size, (int)H, (int)MH, c->num_cu))
+      HIP_OK(c, rbt::launch_proj1(*c, Dp.kind, Dp.group_size, Dp.data, Dp.scale, x, (int)H, (int)MH, xl));
+    else
+      RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
     HIP_OK(c, rbt::launch_xgateup1s_latent(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, nullptr, xl, (int)MH,
                                            (int)I, h, act));
     HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, djob, none, K, nullptr, h, dslot, (long)I, (int)I,
@@ -1099,7 +1102,13 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   }
   HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
   const rbt_qt &U = lw->up_proj;
-  if (lw->norm && U.kind != RBT_QT_F32 && rbt::decode_shape_ok(MH, U.kind, U.group_size) &&
+  if (S == 1 && rbt::proj1_ok(U.kind, U.group_size, (int)MH, (int)H, c->num_cu) &&
+      ((uintptr_t)U.data | (uintptr_t)(lw->norm ? lw->norm : routed)) % 16 == 0) {
+    // one token: the up projection with x staged per workgroup (the norm folded in)
+    RBT_TRY(check_qt(c, &U, "matmul"));
+    HIP_OK(c, rbt::launch_proj1(*c, U.kind, U.group_size, U.data, U.scale, routed, (int)MH, (int)H, out, lw->norm,
+                                lw->eps));
+  } else if (lw->norm && U.kind != RBT_QT_F32 && rbt::decode_shape_ok(MH, U.kind, U.group_size) &&
       ((uintptr_t)U.data | (uintptr_t)lw->norm) % 16 == 0) {
     // the norm of each summed row inside the up projection's waves, which read the whole row
     RBT_TRY(check_qt(c, &U, "matmul"));

@@ -79,6 +79,14 @@ __device__ __forceinline__ float rbt_dpp_add(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// Barrier for LDS hand-offs only: global loads in flight stay in flight (__syncthreads' release
+// fence waits for every outstanding load of the wave first).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Sum over aligned groups of WIDTH lanes (WIDTH a power of two <= 64). Within a 16-lane row the
 // butterfly runs on DPP (quad_perm xor 1, xor 2, row_half_mirror, row_mirror); every lane of the
 // group ends with the sum for WIDTH <= 32. For WIDTH = 64 the total is valid in lanes 0..31.

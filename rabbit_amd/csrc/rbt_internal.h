@@ -92,6 +92,11 @@ hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const
 // h[p, k] = act(sum of gate parts, sum of up parts) for the stacked producer's output.
 hipError_t launch_swiglu(const Ctx &c, const float *gu, long gu_stride, int half, int npairs, const int *npairs_dev,
                          int parts, float *h, const RbtAct &act = RbtAct{});
+// One token through one MXFP4 or grouped-int4 (groups of 32) matrix of 2048..8192 columns, x staged
+// in LDS per workgroup (a projection); with nw, x is rmsnorm(x) * nw first (DECODE_NORM).
+bool proj1_ok(int kind, size_t gs, int cols, int rows, int num_cu);
+hipError_t launch_proj1(const Ctx &c, int kind, size_t gs, const void *data, const void *scale, const float *x,
+                        int cols, int rows, float *y, const float *nw = nullptr, float eps = 0.0f);
 // Column parts the stacked gate/up kernel splits a row of `cols` columns into; its output per job
 // is 2 * parts vectors of `half` floats (gate parts, then up parts).
 int decode_parts(int cols);

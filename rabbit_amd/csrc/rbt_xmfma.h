@@ -19,14 +19,6 @@ typedef float xf4 __attribute__((ext_vector_type(4)));
 
 constexpr int XG_PAD = 8;        // bf16 padding between the LDS part rows (bank spread)
 
-// Barrier for LDS hand-offs only: global loads in flight stay in flight (__syncthreads' release
-// fence waits for every outstanding load of the wave first).
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // 8 E2M1 codes (one dword) -> 8 bf16, scaled by the block's E8M0 value.
 __device__ __forceinline__ xb8 fp4x8_bf16(uint32_t w, float sc) {
   const xb2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
