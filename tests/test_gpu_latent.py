@@ -218,6 +218,52 @@ def test_latent_moe_k3_dims_one_token(ctx, orc, proj_kind):
         _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
 
 
+def test_latent_moe_k3_graph_replays(ctx, orc):
+    # one token at K3's widths (the key-record router, the selection in the gate/up launch) captured
+    # in a HIP graph as the benchmark replays it, and replayed with other inputs, eager calls between
+    # the replays: every replay equals the eager result
+    import rabbit_amd as R
+    import torch
+    from helpers import HipGraph
+    H, MH, I, E, k = 7168, 3584, 3072, 32, 8
+    layer = 54
+    L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 7300, "i4g", 0.05)
+    norm = torch.from_numpy(np.abs(normal(MH, 55, 0.2)) + np.float32(0.5)).cuda()
+    dqd, uqd, act = _dev_qt(R, dq), _dev_qt(R, uq), R.situ(4.0, 25.0)
+    xs = [torch.from_numpy(normal((1, H), 700 + t, 0.05)).cuda() for t in range(3)]
+
+    def call(x, out, sync=True):
+        ctx.latent_moe(layer, MH, dqd, uqd, x, 1, out, norm=norm, eps=1e-5, activation=act, sync=sync)
+
+    ref = []
+    for t in range(3):
+        o = torch.empty(H, device="cuda")
+        call(xs[t], o)
+        ref.append(o.cpu().numpy())
+    xin = xs[0].clone()
+    gout = torch.empty(H, device="cuda")
+    call(xin, gout)  # scratch sized before the capture
+    torch.cuda.synchronize()
+    g = HipGraph(ctx.stream)
+    g.begin()
+    call(xin, gout, sync=False)
+    g.end()
+    try:
+        for rep in range(6):
+            t = rep % 3
+            xin.copy_(xs[t])
+            torch.cuda.synchronize()
+            g.launch()
+            ctx.sync()
+            assert np.array_equal(gout.cpu().numpy(), ref[t]), rep
+            u = (t + 1) % 3
+            o = torch.empty(H, device="cuda")
+            call(xs[u], o)
+            assert np.array_equal(o.cpu().numpy(), ref[u]), rep
+    finally:
+        g.destroy()
+
+
 def test_latent_moe_identity_projections_equal_routed_forward(ctx, orc):
     # moe_hidden == hidden with identity projections: the latent MoE is the layer's routed forward
     import rabbit_amd as R
