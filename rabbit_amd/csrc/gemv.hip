@@ -57,11 +57,11 @@ __global__ __launch_bounds__(256) void k_swiglu(const float *__restrict__ gu, lo
   }
 }
 
-// Gate/up and the activation in one pass, for rows of 2049..4096 columns (one token per pair, one
+// Gate/up and the activation in one pass, for rows of 2049..6144 columns (one token per pair, one
 // column part): a wave takes a contiguous run of (pair, r) items; for each it streams gate row r and
 // up row r of the pair's expert, reduces both as k_decode_gemv does (block_dots, the wave sum), and
 // lane 0 writes h[p, r] = act(g, u). Below 4096 columns the g and u values are the stacked kernel's,
-// so h is bit-identical to k_decode_gemv (stacked) + k_swiglu; at exactly 4096 columns the stacked
+// so h is bit-identical to k_decode_gemv (stacked) + k_swiglu; from 4096 columns on the stacked
 // kernel sums two column parts (g0 + g1) where this one reduces the whole row, so the two agree
 // only within the fp32 accumulation tolerance there. The gate|up scratch and one launch are saved.
 // Two items in flight per wave.
@@ -168,7 +168,8 @@ __global__ __launch_bounds__(256) void k_decode_gu_act(const RbtExpertDev *__res
 }
 
 bool gu_act_ok(size_t cols, int kind, size_t gs) {
-  return decode_shape_ok(cols, kind, gs) && cols > 2048 && cols <= 4096;
+  // (8192 columns would take four blocks per lane: 256 registers, one wave per SIMD)
+  return decode_shape_ok(cols, kind, gs) && cols > 2048 && cols <= 6144;
 }
 
 hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
@@ -176,16 +177,27 @@ hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const
                          float *h, const RbtAct &act) {
   const long total = (long)njobs * I;
   if (total <= 0) return hipSuccess;
-  if (total >= (1L << 31) || cols > 4096 || cols % 32 != 0) return hipErrorInvalidValue;
+  if (total >= (1L << 31) || cols > 8192 || cols % 32 != 0) return hipErrorInvalidValue;
   long waves = (long)c.num_cu * 8;
   if (waves > total) waves = total;
   const int blocks = (int)((waves + 3) / 4);
-  if (kind == RBT_QT_I4_GROUPED)
-    launch_k(c, k_decode_gu_act<2, true>, dim3(blocks), dim3(256), jobs, single, njobs, njobs_dev, x, x_index,
-             x_stride, cols, I, act, h);
+  const int nb = (cols / 32 + 63) / 64;  // blocks per lane: 2 up to 4096 columns, 3 to 6144, 4 beyond
+#define RBT_GUA(NB_)                                                                                              \
+  {                                                                                                               \
+    if (kind == RBT_QT_I4_GROUPED)                                                                                \
+      launch_k(c, k_decode_gu_act<NB_, true>, dim3(blocks), dim3(256), jobs, single, njobs, njobs_dev, x, x_index, \
+               x_stride, cols, I, act, h);                                                                        \
+    else                                                                                                          \
+      launch_k(c, k_decode_gu_act<NB_, false>, dim3(blocks), dim3(256), jobs, single, njobs, njobs_dev, x,        \
+               x_index, x_stride, cols, I, act, h);                                                               \
+  }
+  if (nb <= 2)
+    RBT_GUA(2)
+  else if (nb == 3)
+    RBT_GUA(3)
   else
-    launch_k(c, k_decode_gu_act<2, false>, dim3(blocks), dim3(256), jobs, single, njobs, njobs_dev, x, x_index,
-             x_stride, cols, I, act, h);
+    RBT_GUA(4)
+#undef RBT_GUA
   return hipGetLastError();
 }
 

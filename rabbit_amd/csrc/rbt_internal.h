@@ -82,9 +82,9 @@ hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *j
                          int njobs, const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols,
                          int rows, float *y, long y_stride, int parts = 1, const float *nw = nullptr,
                          float eps = 0.0f);
-// Gate/up and the activation in one pass into h [njobs, I] (rows of 2049..4096 columns, the shapes
+// Gate/up and the activation in one pass into h [njobs, I] (rows of 2049..6144 columns, the shapes
 // decode_shape_ok accepts): bit-identical to the stacked decode + launch_swiglu below 4096 columns,
-// within the fp32 accumulation tolerance at 4096 (where the stacked decode splits the row in two).
+// within the fp32 accumulation tolerance from 4096 on (where the stacked decode splits the row in two).
 bool gu_act_ok(size_t cols, int kind, size_t gs);
 hipError_t launch_gu_act(const Ctx &c, int kind, const RbtExpertDev *jobs, const RbtExpertDev &single, int njobs,
                          const int *njobs_dev, const float *x, const int *x_index, long x_stride, int cols, int I,
