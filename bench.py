@@ -133,7 +133,7 @@ def kernel_table(ctx, run):
 
 def kernel_role(name: str) -> str:
     """gateup / down / router / proj / other, from the kernel's (possibly mangled) name."""
-    if any(s in name for s in ("xgateup", "pgateup", "dgateup", "decode_gu_act")):
+    if any(s in name for s in ("xgateup", "pgateup", "dgateup", "decode_gu_act", "gu1s_gemv")):
         return "gateup"
     if any(s in name for s in ("xdown", "pdown", "ddown")):
         return "down"

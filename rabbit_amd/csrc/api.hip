@@ -835,6 +835,28 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   // rows, workgroup 0 writes xn), else as its own launch
   const bool fold_norm = norm_w && r1 && ((uintptr_t)xraw | (uintptr_t)norm_w) % 16 == 0;
   if (norm_w && !fold_norm) HIP_OK(c, rbt::launch_rmsnorm(*c, xraw, norm_w, eps, xn, (size_t)S, (size_t)H, true));
+  // One token off the matrix cores (grouped int4, or MXFP4 shapes they do not take): the same three
+  // launches with the decode GEMVs. The router rows' key records; the selection in every workgroup of
+  // the fused gate/up + activation GEMV (routed pairs, then the shared expert); the down GEMV over the
+  // published job list (winners in rank order, then the shared expert); the ordered combine.
+  const bool g1 = S == 1 && !mfma && grp_in_select && (merge || !D.has_shared) && kk == k && !c->prof &&
+                  rbt::gu1s_gemv_ok(ra, c->num_cu, L.routed_kind, L.routed_gs, I) &&
+                  rbt::decode_shape_ok(I, L.routed_kind, L.routed_gs) && (uintptr_t)(sgate ? sgate : x) % 16 == 0;
+  if (g1) {
+    RBT_TRY(scratch_t(c, SC_RREC, (size_t)E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
+    RBT_TRY(scratch_t(c, SC_DJOB, (size_t)(kk + 1), &djob));
+    RBT_TRY(scratch_t(c, SC_DSLOT, (size_t)(kk + 1), &dslot));
+    ga.down_job = djob;
+    ga.down_slot = dslot;
+    ga.shared_slot = k + rbt::D1_KX;
+    RbtExpertDev none{};
+    HIP_OK(c, rbt::launch_router1_any(*c, ra, mid, bnd, shs, sgate, rec));
+    HIP_OK(c, rbt::launch_gu1s_gemv(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, L.routed_kind,
+                                    L.routed_gs, I, h, D.has_shared != 0));
+    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, L.routed_kind, djob, none, kk + (D.has_shared ? 1 : 0),
+                                 nullptr, h, dslot, (long)I, I, H, yy, (long)H));
+    HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, dst));
+  } else {
   if (r1) {
     // one token: router logits, key records and the shared gate
     RBT_TRY(scratch_t(c, SC_RREC, (size_t)E * rbt::ROUTER1_REC_BYTES / sizeof(float), &rec));
@@ -920,6 +942,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     }
     if (c->prof) HIP_OK(c, hipEventRecord(ev[5], c->stream));
     HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, dst));
+  }
   }
   }
   if (c->prof) {

@@ -347,4 +347,115 @@ __device__ __forceinline__ void decode_gemv_body(const RbtExpertDev *__restrict_
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// Gate/up and the activation in one pass, for rows of 2049..6144 columns (one token per pair, one
+// column part): a wave takes a contiguous run of (pair, r) items; for each it streams gate row r and
+// up row r of the pair's expert, reduces both as k_decode_gemv does (block_dots, the wave sum), and
+// lane 0 writes h[p, r] = act(g, u). Below 4096 columns the g and u values are the stacked kernel's,
+// so h is bit-identical to k_decode_gemv (stacked) + k_swiglu; from 4096 columns on the stacked
+// kernel sums two column parts (g0 + g1) where this one reduces the whole row, so the two agree
+// only within the fp32 accumulation tolerance there. The gate|up scratch and one launch are saved.
+// Two items in flight per wave.
+template <int NB, bool I4G>
+__device__ __forceinline__ void frag_load_gu(DecodeFrag<NB, 2> &f, const RbtExpertDev &J, int row, int q, int nblk,
+                                             unsigned rb) {
+#pragma unroll
+  for (int m = 0; m < 2; m++) {
+    const uint8_t *d = m ? J.ud : J.gd;
+    const uint8_t *sc = reinterpret_cast<const uint8_t *>(m ? J.us : J.gs);
+    const rbt_gu4 *rp = (const rbt_gu4 *)(d + (size_t)row * rb);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const int bb = min(q + 64 * j, nblk - 1);
+      f.w[m][j] = __builtin_nontemporal_load(rp + bb);
+      if (I4G)
+        f.sb[m][j] = ((const rbt_gu32 *)sc)[(size_t)row * nblk + bb];
+      else
+        f.sb[m][j] = ((const rbt_gu8 *)sc)[(size_t)row * nblk + bb];
+    }
+  }
+}
+
+// The wave's gate and up sums of one row, as values uniform across the wave (lane 0's total, which
+// is what the stacked kernel stores).
+template <int NB, bool I4G>
+__device__ __forceinline__ void frag_gu_sums(const DecodeFrag<NB, 2> &f, const float (&xr)[NB][32],
+                                             const float (&xs)[NB], int q, int nblk, float &g, float &u) {
+  g = block_dots<NB, 64, I4G>(f.w[0], f.sb[0], xr, xs, q, nblk);
+  g = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rbt_group_sum<64>(g)), 0));
+  __builtin_amdgcn_sched_barrier(0);
+  u = block_dots<NB, 64, I4G>(f.w[1], f.sb[1], xr, xs, q, nblk);
+  u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rbt_group_sum<64>(u)), 0));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// The wave `wave_in` of `nwaves` (the kernel's grid, or the part of a grid that runs it beside other
+// work): its contiguous run of (pair, row) items. `jobs` may point at LDS.
+template <int NB, bool I4G>
+__device__ __forceinline__ void gu_act_body(const RbtExpertDev *__restrict__ jobs, RbtExpertDev single, int njobs,
+                                            const int *__restrict__ njobs_dev, const float *__restrict__ x,
+                                            const int *__restrict__ x_index, long x_stride, int cols, int I,
+                                            const RbtAct &act, float *__restrict__ h, int wave_in, int nwaves) {
+  const int q = threadIdx.x & (RBT_WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(wave_in);
+  int nj = njobs;
+  if (njobs_dev) nj = min(nj, *njobs_dev);
+  const int total = nj * I;
+  const int per = (total + nwaves - 1) / nwaves;
+  int pos = wave * per;
+  if (pos >= total) return;
+  const int end = min(pos + per, total);
+  const int nblk = cols / 32;
+  const unsigned rb = (unsigned)cols / 2;
+  float xr[NB][32];
+  float xs[NB];
+  long cur = -1;
+  DecodeFrag<NB, 2> f0, f1;
+  while (pos < end) {
+    // one run: rows [r, r1) of pair `job`
+    const int job = pos / I;
+    int r = pos - job * I;
+    const int r1 = min(I, r + (end - pos));
+    pos += r1 - r;
+    const RbtExpertDev J = jobs ? jobs[job] : single;
+    float *hrow = h + (long)job * I;
+    if (J.gd == nullptr || J.ud == nullptr) {  // no expert: g = u = 0, act(0, 0) = 0
+      for (int rr = r + q; rr < r1; rr += RBT_WAVE) hrow[rr] = 0.0f;
+      continue;
+    }
+    frag_load_gu<NB, I4G>(f0, J, r, q, nblk, rb);
+    const long tok = x_stride == 0 ? 0 : (x_index ? (long)x_index[job] : (long)job);
+    if (tok != cur) {
+      load_x_slice<NB, 64>(xr, xs, x + tok * x_stride, q, nblk);
+      cur = tok;
+    }
+    // rows' sums collect in lane (row - wb) of a 64-row window; the activation then runs once per
+    // window on all lanes (on one lane per row it would serialise the whole wave)
+    int wb = r;
+    float gk = 0.0f, uk = 0.0f;
+    auto take = [&](const DecodeFrag<NB, 2> &f, int rr) {
+      float g, u;
+      frag_gu_sums<NB, I4G>(f, xr, xs, q, nblk, g, u);
+      if (q == rr - wb) {
+        gk = g;
+        uk = u;
+      }
+      if (rr - wb == RBT_WAVE - 1 || rr + 1 == r1) {
+        if (q <= rr - wb) hrow[wb + q] = rbt_act(act, gk, uk);
+        wb = rr + 1;
+      }
+    };
+    const int rlast = r1 - 1;
+    while (true) {
+      frag_load_gu<NB, I4G>(f1, J, min(r + 1, rlast), q, nblk, rb);
+      take(f0, r);
+      if (r + 1 >= r1) break;
+      frag_load_gu<NB, I4G>(f0, J, min(r + 2, rlast), q, nblk, rb);
+      take(f1, r + 1);
+      r += 2;
+      if (r >= r1) break;
+    }
+  }
+}
+
 }  // namespace rbt

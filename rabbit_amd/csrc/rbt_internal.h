@@ -246,6 +246,16 @@ hipError_t launch_xgateup1s(const Ctx &c, const RouterArgs &a, const void *rec, 
 // x_latent (moe_hidden 3584), h in fp32 (pair slot c at h + I c); ga's down job list, slots,
 // tok_pair and tok_w as launch_xgateup1s writes them.
 bool router1_latent_ok(const RouterArgs &a, int num_cu, int mh, int I);
+// One token through the decode GEMVs (grouped int4 and the other non-matrix-core shapes):
+// launch_router1_any writes the key records (and the shared gate), launch_gu1s_gemv selects in every
+// workgroup and runs the fused gate/up + activation GEMV over the routed pairs and the shared expert
+// (h in fp32 at the pair slots; ga's down job list, slots, tok_pair and tok_w as launch_xgateup1s).
+bool gu1s_gemv_ok(const RouterArgs &a, int num_cu, int kind, size_t gs, int I);
+hipError_t launch_router1_any(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                              const float *sgate, void *rec);
+hipError_t launch_gu1s_gemv(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,
+                            const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int kind,
+                            size_t gs, int I, float *h, bool has_shared);
 hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
                                  void *rec, int mh, int I);
 hipError_t launch_xgateup1s_latent(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,

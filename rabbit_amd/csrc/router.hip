@@ -2661,6 +2661,83 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   }
 }
 
+// One token through the decode GEMVs (grouped int4, or any format the matrix-core kernels do not
+// take), as the three-launch decode does it on the matrix cores: every workgroup selects from the
+// key records (k_router1), workgroup 0 publishes the routing and the down job list, and the grid's
+// waves run the fused gate/up + activation GEMV over the routed pairs and the shared expert (the
+// pair after them), h in fp32 at the pairs' slots. A deferred decision: workgroup 0 folds and decides
+// while the other workgroups stream every candidate.
+template <int MAXM, int NB, bool I4G>
+__global__ __launch_bounds__(256) void k_gu1s_gemv(SelParams P, const KeyRec *__restrict__ rec,
+                                                   const double *__restrict__ mid, const double *__restrict__ bnd,
+                                                   GroupOut G, int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                   int *__restrict__ stats, int I, float *__restrict__ h,
+                                                   int has_shared, RbtAct act) {
+  __shared__ __attribute__((aligned(16))) float fold[4][2][1024];  // workgroup 0, deferred
+  __shared__ SelLds S;
+  __shared__ PairLds Q;
+  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[64 * MAXM];
+  const int t = threadIdx.x, lane = t & 63;
+  const bool streamer = blockIdx.x > 0;
+  const int E = P.E, kk = min(P.k, P.E);
+  float4 rv[MAXM];
+  if (t < 64) load_key_recs<MAXM>(rec, E, rv);
+  {
+    constexpr int TQ = (64 * MAXM * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
+    const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
+    const rbt_gu4 *src = (const rbt_gu4 *)G.table;
+    rbt_u4 tv[TQ];
+#pragma unroll
+    for (int i = 0; i < TQ; i++) tv[i] = src[min(t + 256 * i, n4 - 1)];
+    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
+#pragma unroll
+    for (int i = 0; i < TQ; i++)
+      if (t + 256 * i < n4) dst[t + 256 * i] = tv[i];
+  }
+  lds_barrier();
+  if (t < 64) {
+    const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
+    if (t == 0) Q.status = r;
+  }
+  lds_barrier();
+  const int st = Q.status;
+  GroupOut Gs = G;
+  if (st == 0) {
+    if (!streamer) {
+      Gs.shared_slot = kk;
+      select3_body<MAXM>(S, P, mid, bnd, ids, wts, nullptr, stats, Gs, 1, 0);
+    } else {
+      select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
+      __syncthreads();
+      if (t < 64) {
+        for (int r = lane; r < kk; r += 64) {
+          Q.T.id[r] = Q.fb_ids[r];
+          copy_job(Q.pj + r, tab + Q.fb_ids[r]);
+        }
+        if (lane == 0) {
+          Q.T.nr = kk;
+          Q.T.pending = 0;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  const bool pending = st == 2;
+  const int nr = Q.T.nr;
+  Gs.shared_slot = nr;
+  const bool decider = !streamer && pending;
+  if (!streamer && st == 1 && t < 64) publish_certified(S, Q, P, Gs, ids, wts);
+  if (has_shared && t == 0) copy_job(Q.pj + nr, G.shared_dev);
+  __syncthreads();
+  if (!decider) {
+    const int wg = pending ? blockIdx.x - 1 : blockIdx.x, nwg = pending ? gridDim.x - 1 : gridDim.x;
+    gu_act_body<NB, I4G>(Q.pj, RbtExpertDev{}, nr + has_shared, nullptr, P.x, nullptr, 0, P.H, I, act, h,
+                         wg * 4 + (t >> 6), nwg * 4);
+  } else {
+    d1_finish(S, fold, P, &Q.T, Gs, ids, wts, stats);
+  }
+}
+
 static SelParams sel_params(const RouterArgs &a) {
   SelParams P{};
   P.family = a.family;
@@ -2758,6 +2835,58 @@ hipError_t launch_xgateup1s_latent(const Ctx &c, const RouterArgs &a, const void
   const KeyRec *rec = reinterpret_cast<const KeyRec *>(rec_buf);
   launch_k(c, k_xgateup1s<16, 7, true>, dim3(c.num_cu), dim3(256), P, rec, mid, bnd, G, ids, wts, stats, gup, I,
            reinterpret_cast<__bf16 *>(h), 0, RbtExpertDev{}, xl, act);
+  return hipGetLastError();
+}
+
+bool gu1s_gemv_ok(const RouterArgs &a, int num_cu, int kind, size_t gs, int I) {
+  const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
+  return a.S == 1 && !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38) && a.E <= 512 && a.E <= 4 * num_cu &&
+         a.k + D1_KX <= D1_NC && a.H % 1024 == 0 && a.H <= RT_MAXH && aligned && num_cu >= 2 &&
+         gu_act_ok(a.H, kind, gs) && I > 0;
+}
+
+hipError_t launch_gu1s_gemv(const Ctx &c, const RouterArgs &a, const void *rec_buf, const double *mid,
+                            const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int kind,
+                            size_t gs, int I, float *h, bool has_shared) {
+  if (!grp.down_job || !grp.down_slot || !gu1s_gemv_ok(a, c.num_cu, kind, gs, I)) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  const GroupOut G = group_out(grp, a.k);
+  const KeyRec *rec = reinterpret_cast<const KeyRec *>(rec_buf);
+  const dim3 grid(c.num_cu);
+  const RbtAct act{};
+  const bool i4 = kind == RBT_QT_I4_GROUPED, m4 = a.E <= 256;
+  const int nb = (a.H / 32 + 63) / 64;
+#define RBT_G1(M, NB_)                                                                                          \
+  {                                                                                                             \
+    if (i4)                                                                                                     \
+      launch_k(c, k_gu1s_gemv<M, NB_, true>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, I, h,        \
+               (int)has_shared, act);                                                                           \
+    else                                                                                                        \
+      launch_k(c, k_gu1s_gemv<M, NB_, false>, grid, dim3(256), P, rec, mid, bnd, G, ids, wts, stats, I, h,       \
+               (int)has_shared, act);                                                                           \
+  }
+  if (nb <= 2) {
+    if (m4) RBT_G1(4, 2) else RBT_G1(8, 2)
+  } else {
+    if (m4) RBT_G1(4, 3) else RBT_G1(8, 3)
+  }
+#undef RBT_G1
+  return hipGetLastError();
+}
+
+hipError_t launch_router1_any(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                              const float *sgate, void *rec_buf) {
+  if (a.S != 1 || a.H % 1024 != 0 || a.H > RT_MAXH || ((uintptr_t)a.x | (uintptr_t)a.W) % 16 != 0 ||
+      (sgate && (uintptr_t)sgate % 16 != 0))
+    return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
+  const int rn = a.E + (sgate ? 1 : 0);
+  if (rn <= 4 * c.num_cu)
+    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr);
+  else
+    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f,
+             nullptr);
   return hipGetLastError();
 }
 
