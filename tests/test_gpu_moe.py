@@ -115,8 +115,10 @@ def test_moe_forward_full_config(ctx, orc, name, ntok):
         assert ok, (t, d, eg, eo)
 
 
-def test_router_ids_exact_over_many_tokens(ctx, orc):
-    """C1 one-token calls (the three-launch decode): ids bit-exact against the sequential fp32 fold
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_router_ids_exact_over_many_tokens(ctx, orc, name):
+    """One-token calls (the three-launch decode: C1 on the matrix cores, C2's grouped int4 on the
+    decode GEMVs): ids bit-exact against the sequential fp32 fold
     over many tokens. For the tokens whose router decision needed exact folds (settled inside the
     gate/up launch while the candidates stream) plus a sample of certified ones, every token on its
     own (one token is one decode call):
@@ -132,7 +134,7 @@ def test_router_ids_exact_over_many_tokens(ctx, orc):
     from oracle.workload import HostLayer
     from f64_truth import check_token, layer64
     import torch
-    cfg = W.CONFIGS["c1"]
+    cfg = W.CONFIGS[name]
     ntok = 256
     W.build_layer(ctx, cfg, layer=0, seed=1000)
     host = HostLayer(cfg, 1000)
