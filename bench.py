@@ -255,10 +255,12 @@ def cpu_line(us_warm, us_cold, unit, bytes_per_unit, info, kind, sample, extra=N
     return res
 
 
-def cpu_baseline_layer(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token, simd=True):
+def cpu_baseline_layer(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token, simd=True, post_ln=None,
+                       eps=1e-6):
     """The oracle's restated reference kernels on the same layer and tokens, one token per call.
     Experts the tokens route to are regenerated on the host first (not timed); each token runs warm
-    (right after that) and cold (after an eviction)."""
+    (right after that) and cold (after an eviction). With post_ln: the MoE sublayer
+    x + moe_forward(rmsnorm_1p(x, post_ln)) (qwen38/generate.rs:397-413)."""
     from oracle import oracle as O
     from oracle.workload import HostLayer
     info = cpu_info()
@@ -272,15 +274,21 @@ def cpu_baseline_layer(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token, 
         xt = x_tokens[t:t + S]
         if xt.shape[0] < S:
             break
-        ids, _ = host.route(xt)
+        if post_ln is not None:
+            from oracle import oracle as Oc
+            ids, _ = host.route(np.stack([Oc.rmsnorm_1p(r, post_ln, eps) for r in xt]))
+        else:
+            ids, _ = host.route(xt)
         host.ensure(ids)
         lay = host._layer()
+        run = (lambda: lay.sublayer(xt, S, post_ln, eps, simd=simd)[0]) if post_ln is not None else \
+            (lambda: lay.forward(xt, S, simd=simd)[0])
         t0 = time.perf_counter()
-        out, _, _ = lay.forward(xt, S, simd=simd)
+        out = run()
         warm += time.perf_counter() - t0
         ev()
         t0 = time.perf_counter()
-        lay.forward(xt, S, simd=simd)
+        run()
         cold += time.perf_counter() - t0
         outs.append(out)
         done += S
@@ -289,8 +297,9 @@ def cpu_baseline_layer(cfg, seed, x_tokens, budget_s, gpu_out, bytes_per_token, 
         if len(host.experts) > 160:  # bound host memory (~4 GB of regenerated experts)
             host.experts.clear()
     per = lambda v: v / done * 1e6  # noqa: E731
-    sample = (f"{done} tokens of {cfg.name} ({S} per call: router + {cfg.topk} routed"
-              f"{' + shared' if cfg.shared else ''} experts), {tier} tier of the reference's kernels restated "
+    sample = (f"{done} tokens of {cfg.name} ({S} per call: {'rmsnorm_1p + ' if post_ln is not None else ''}"
+              f"router + {cfg.topk} routed{' + shared' if cfg.shared else ''} experts"
+              f"{' + residual' if post_ln is not None else ''}), {tier} tier of the reference's kernels restated "
               f"in C, rows in parallel on {info['threads']} threads")
     res = cpu_line(per(warm), per(cold), "us/token", bytes_per_token, info, "port", sample)
     g = gpu_out[:done].astype(np.float64).ravel()
@@ -842,6 +851,24 @@ def bench_sublayer(args, ctx, hip, cfg):
     sw, _ = graph_time(hip, ctx, sub_call, warm, steps, G)
     layer_us, sub_us = lw / steps * 1e6, sw / steps * 1e6
     log(f"[bench] sublayer {sub_us:.2f} us/token, layer alone {layer_us:.2f}")
+    tab = kernel_table(ctx, lambda: [sub_call(t) for t in range(warm, ntok)])
+    rows = per_call(tab, steps)
+    gu_bytes = (cfg.topk + (1 if cfg.shared else 0)) * 2 * expert_matrix_bytes(cfg, cfg.inter, H)
+    rl = roofline(rows, "gateup", gu_bytes, "c1",
+                  note=f"algorithmic bytes: gate+up weights of the {cfg.topk} routed experts and the shared one")
+    cpu = None
+    if not args.no_cpu:
+        # the CPU port on fresh copies of a few tokens, the device sublayer on the same copies
+        ncpu = min(16, ntok)
+        x0 = W.tokens(cfg, ncpu, args.seed + 77)
+        xd = torch.from_numpy(x0.copy()).cuda()
+        for t in range(ncpu):
+            ctx.moe_sublayer(0, xd[t], 1, ln, 1e-6, sync=False)
+        ctx.sync()
+        bpt = (cfg.topk + (1 if cfg.shared else 0)) * 3 * expert_matrix_bytes(cfg, cfg.inter, H) + \
+            (cfg.n_experts + 1) * H * 4
+        cpu = cpu_baseline_layer(cfg, args.seed, x0, args.cpu_budget, xd.cpu().numpy(), bpt,
+                                 post_ln=ln.cpu().numpy(), eps=1e-6)
     res = {
         "metric": "MoE sublayer decode us/token (rmsnorm_1p + MoE layer + residual add), MXFP4",
         "value": round(sub_us, 3), "unit": "us/token", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -852,7 +879,9 @@ def bench_sublayer(args, ctx, hip, cfg):
                    "resident_pool_gb": round(pool_gb, 2), "graph_tokens": G},
         "layer_us_per_token": round(layer_us, 3),
         "norm_and_residual_us": round(sub_us - layer_us, 3),
-        "cpu_baseline": None,
+        "roofline": rl,
+        "kernels": kernels_json(rows),
+        "cpu_baseline": cpu,
     }
     print(json.dumps(res), flush=True)
     ctx.close()
