@@ -2522,7 +2522,9 @@ __device__ __forceinline__ void d1_finish(SelLds &L, float (*fold)[2][1024], con
     if (r < k) {
       ids[r] = r < kk ? L.r_id[r] : -1;
       wts[r] = r < kk ? L.s_w[r] : 0.0f;
-      G.tok_pair[r] = r < kk ? L.q_id[r] : -1;
+      // the consumers of the job list (the down launches, the combine) index their rows by rank,
+      // not by the winner's gate/up slot (down_slot)
+      G.tok_pair[r] = r < kk ? r : -1;
       G.tok_w[r] = r < kk ? L.s_w[r] : 0.0f;
       if (r < kk) {
         const RbtExpertDev *src = G.table + L.r_id[r];

@@ -34,6 +34,32 @@ def bits_equal(a, b) -> bool:
     return bool(np.all(same | both_nan))
 
 
+def boundary_router(E: int, H: int, k: int, x: np.ndarray):
+    """A router whose last top-k place only the sequential fp32 fold decides (kernels.rs:113-124).
+
+    Experts a = 1 and b = 2 have the same exact logit 1 + 2^-18 (a: 1 then sixty-four 2^-24 terms;
+    b: the sixty-four 2^-24 terms then 1), so any sum taken more accurately than the fold ties them
+    and orders a (the lower id) first. The fold gives a exactly 1 (each 2^-24 after the leading 1 is
+    half an ulp and rounds to even) and b 1 + 2^-18 (its small terms add exactly before the 1), so b
+    takes the last place. k - 1 experts (ids 3, 6, 9, ...) rank above both with logits 1.5 + j/16;
+    every other expert's logit is 0. x (one token, changed in place) gets ones in its first 65
+    entries, the only ones the rows use. Returns (router [E, H], a, b, the k - 1 higher ids)."""
+    m = 64
+    x[:m + 1] = 1.0
+    router = np.zeros((E, H), np.float32)
+    d = np.float32(2.0 ** -24)
+    hi = [3 + 3 * j for j in range(k - 1)]
+    assert hi[-1] < E
+    for j, e in enumerate(hi):
+        router[e, 0] = np.float32(1.5 + j / 16)
+    a, b = 1, 2
+    router[a, 0] = 1.0
+    router[a, 1:m + 1] = d
+    router[b, :m] = d
+    router[b, m] = 1.0
+    return router, a, b, hi
+
+
 def write_safetensors(path, tensors, metadata=None, raw_header=None):
     """Writes a safetensors file: tensors is a list of (name, dtype, shape, bytes) in data order.
     raw_header (bytes), when given, replaces the JSON header (for malformed-header tests)."""

@@ -218,6 +218,29 @@ def test_latent_moe_k3_dims_one_token(ctx, orc, proj_kind):
         _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
 
 
+def test_latent_moe_k3_folded_boundary_winner(ctx, orc):
+    # one token at K3's widths whose last top-k place only the exact folds decide
+    # (helpers.boundary_router, no correction bias): the winner comes from the first undecided
+    # gate/up slot, and the down GEMV and the combine take its row by rank
+    import rabbit_amd as R
+    import torch
+    from helpers import boundary_router
+    H, MH, I, E, k, layer = 7168, 3584, 3072, 32, 8, 54
+    L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 7300, "i4g", 0.05)
+    x = normal((1, H), 610, 0.05)
+    router, a, b, _ = boundary_router(E, H, k, x[0])
+    bias = np.zeros(E, np.float32)
+    L = orc.MoeLayer(orc.FAMILY_GLM52, H, I, E, k, router, L.experts, router_bias=bias, norm_topk=False)
+    t_router, t_bias = torch.from_numpy(router).cuda(), torch.from_numpy(bias).cuda()
+    ctx.moe_layer_set(layer, R.FAMILY_GLM52, H, I, E, k, t_router, router_bias=t_bias, norm_topk=False)
+    torch.cuda.synchronize()
+    norm = np.abs(normal(MH, 55, 0.2)) + np.float32(0.5)
+    ctx.profile_read(reset=True)
+    got = _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
+    assert ctx.profile_read(reset=True)["ambiguous"], "the router decision did not need exact folds"
+    assert np.all(np.isfinite(got))
+
+
 def test_latent_moe_k3_graph_replays(ctx, orc):
     # one token at K3's widths (the key-record router, the selection in the gate/up launch) captured
     # in a HIP graph as the benchmark replays it, and replayed with other inputs, eager calls between

@@ -179,6 +179,45 @@ def test_router_ids_exact_over_many_tokens(ctx, orc, name):
           ", ".join(f"({a:.2e}, {b:.2e}, {c:.2e})" for a, b, c in worst[:4]))
 
 
+@pytest.mark.parametrize("name", ["c1", "c2"])
+def test_folded_boundary_winner(ctx, orc, name):
+    """One token whose last top-k place only the exact folds decide (helpers.boundary_router): the
+    midpoint order puts expert a at rank k-1 and expert b in the first undecided gate/up slot (k);
+    the folds give the place to b. ids and weights as the oracle's, and the output within the
+    per-token rule: the down launch and the combine take b's row by its rank, not by its slot."""
+    import rabbit_amd.workloads as W
+    from oracle.workload import HostLayer
+    from f64_truth import check_token, layer64
+    from helpers import boundary_router
+    import torch
+    cfg = W.CONFIGS[name]
+    info = W.build_layer(ctx, cfg, layer=0, seed=1000)
+    host = HostLayer(cfg, 1000)
+    x = W.tokens(cfg, 1, 777)
+    router, a, b, hi = boundary_router(cfg.n_experts, cfg.hidden, cfg.topk, x[0])
+    host.router = router
+    t_router = torch.from_numpy(router).cuda()
+    t_gate = torch.from_numpy(info["shared_gate"]).cuda() if info["shared_gate"] is not None else None
+    t_lb = torch.from_numpy(info["logit_bias"]).cuda() if info["logit_bias"] is not None else None
+    ctx.moe_layer_set(0, cfg.family, cfg.hidden, cfg.inter, cfg.n_experts, cfg.topk, t_router, shared=info["shared"],
+                      shared_gate=t_gate, logit_bias=t_lb, norm_topk=True, routed_scale=1.0)
+    torch.cuda.synchronize()
+    eids, ew = host.route(x)
+    assert b in eids[0] and a not in eids[0]
+    out = torch.empty(cfg.hidden, dtype=torch.float32, device="cuda")
+    ids = torch.empty(cfg.topk, dtype=torch.int32, device="cuda")
+    w = torch.empty(cfg.topk, dtype=torch.float32, device="cuda")
+    ctx.profile_read(reset=True)
+    ctx.moe_forward(0, torch.from_numpy(x).cuda(), 1, out, ids, w)
+    assert ctx.profile_read(reset=True)["ambiguous"], "the router decision did not need exact folds"
+    assert np.array_equal(ids.cpu().numpy(), eids[0])
+    assert np.max(np.abs(w.cpu().numpy() - ew[0])) < 1e-5
+    exp, _, _ = host.forward(x)
+    truth = layer64(host, x, eids)
+    d, eg, eo, ok = check_token(out.cpu().numpy(), exp[0], truth[0], RTOL)
+    assert ok, f"device vs oracle {d:.3e}, device vs fp64 {eg:.3e}, oracle vs fp64 {eo:.3e}"
+
+
 @pytest.mark.parametrize("name,ntok", [("c1", 1), ("c3", 8)])
 def test_decode_graph_replays(ctx, orc, name, ntok):
     """A decode call captured in a HIP graph (as the benchmark replays them) and replayed several

@@ -242,6 +242,22 @@ def test_glm_norm_topk_sums_to_routed_scale(orc):
     assert abs(float(w.sum()) - k["routed_scale"]) < k["tol"]
 
 
+def test_boundary_router_is_decided_by_the_fold(orc):
+    """helpers.boundary_router: the oracle's logits of experts a and b are the fold's (1 and
+    1 + 2^-18) while their exact sums tie, and b, not a, takes the last of the k places under both
+    selection rules (the GPU tests use it to reach a router decision that only exact folds settle)."""
+    from helpers import boundary_router
+    E, H, k = 64, 1024, 8
+    x = np.random.default_rng(5).standard_normal(H).astype(np.float32)
+    router, a, b, hi = boundary_router(E, H, k, x)
+    logits = orc.matmul(x, router.ravel(), 1, H, E).ravel()
+    assert logits[a] == np.float32(1.0) and logits[b] == np.float32(1.0 + 2.0 ** -18)
+    exact = router.astype(np.float64) @ x.astype(np.float64)
+    assert exact[a] == exact[b] == 1.0 + 2.0 ** -18
+    for ids, _ in (orc.route_softmax(logits, k), orc.route_sigmoid(logits, k, norm_topk=True)):
+        assert sorted(ids) == sorted(hi + [b]) and a not in list(ids)
+
+
 def test_glm_grouped_kats(orc):
     for c in KATS["glm_grouped"]["cases"]:
         # The KATs rank raw choice values; sigmoid is strictly monotone on them, so feeding the
