@@ -921,7 +921,9 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     // one token: the balanced down over the compact job list (all pairs' h in LDS); batches: a grid
     // of row blocks
     const hipError_t e3 =
-        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out, accumulate)
+        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out, accumulate,
+                                 D.has_shared ? L.h_shared.dd : nullptr,
+                                 D.has_shared ? (const uint8_t *)L.h_shared.ds : nullptr)
             : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, dst);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e3);

@@ -117,10 +117,13 @@ hipError_t launch_xgateup1(const Ctx &c, const RbtExpertDev *jobs, int npairs, c
 // pairs are the kk winners in slot order (down_job[j], h at pair slot down_slot[j], weight
 // tok_w[j]) and, with has_shared, the shared expert (down_job[kk], h at down_slot[kk]).
 // accumulate: out += the combined row instead of out = (one rounding, as x[i] += tmp[i]).
+// sh_dd/sh_ds: the shared expert's down weights and scales (the same as down_job[kk]'s), or null;
+// given, its tiles go first and their first loads are issued before the job table is read.
 bool xdown1_ok(int npairs, size_t i);
 hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
                          int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
-                         float *out, bool accumulate = false);
+                         float *out, bool accumulate = false, const uint8_t *sh_dd = nullptr,
+                         const uint8_t *sh_ds = nullptr);
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);

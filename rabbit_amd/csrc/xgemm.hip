@@ -404,10 +404,16 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
                                                         const __bf16 *__restrict__ hp, int H,
                                                         const float *__restrict__ tok_w,
                                                         const float *__restrict__ sh_scale, int has_shared,
-                                                        int gated, float *__restrict__ out, int accumulate) {
+                                                        int gated, float *__restrict__ out, int accumulate,
+                                                        const uint8_t *__restrict__ sh_dd,
+                                                        const uint8_t *__restrict__ sh_ds) {
   // pairs: the kk winners in slot order (jobs[j], h at pair slot slots[j], weight tok_w[j]), then
   // the shared expert (jobs[kk], h at slots[kk], weight sh_scale when gated, else 1)
   const int npairs = kk + (has_shared ? 1 : 0);
+  // With the shared expert's pointers given (sh_dd, sh_ds), the waves take it first: its first
+  // window goes out at entry, before the pair tables land (the combine keeps the pair order).
+  const bool shf = has_shared && sh_dd != nullptr && sh_ds != nullptr;
+  auto pp_of = [&](int q) { return shf ? (q == 0 ? npairs - 1 : q - 1) : q; };  // pair of processing slot q
   constexpr int KD = NCH * 512, stride = KD + XG_PAD, SRD = KD >> 5;
   constexpr int PPP = 3 * KD / 8;                                  // 16-byte pieces of one pair's parts
   constexpr int HI = (XD1_NP * PPP + 64 * XD1_NW - 1) / (64 * XD1_NW);  // pieces per thread
@@ -435,6 +441,14 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
   const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
   const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
+  rbt_u4 ring[4][NCH];
+  const bool early = shf && nu > 0 && uu(0) < nt;  // the wave's first unit is a shared-expert tile
+  if (early) {
+    const uint8_t *c0 = sh_dd + (long)(4 * (T0 + uu(0)) + rho) * (KD >> 1) + 64 * kap + 16 * g;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) ring[0][c] = __builtin_nontemporal_load((const rbt_gu4 *)(c0 + 256 * c));
+  }
+  __builtin_amdgcn_sched_barrier(0);
   // Prologue. vmcnt counts loads in issue order, so everything the staging barrier waits for (the h
   // parts, the pair tables, the first scale window) is issued before the first window's weights:
   // the h pieces come from L2 while the weights (128 KB per CU, all CUs at once) take the HBM's time,
@@ -463,9 +477,10 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     cp[j] = dummy;
     sp[j] = hb8 + 16 * s_seg;
     if (j < nu) {
-      const int pp = u / nt, tl = u - pp * nt;
-      const uint8_t *dd = lane_ptr(t_dd, pp);
-      const uint8_t *ds = lane_ptr(t_ds, pp);
+      const int q = u / nt, pp = pp_of(q), tl = u - q * nt;
+      const bool shq = shf && q == 0;
+      const uint8_t *dd = shq ? sh_dd : lane_ptr(t_dd, pp);
+      const uint8_t *ds = shq ? sh_ds : lane_ptr(t_ds, pp);
       if (dd != nullptr && ds != nullptr) {
         cp[j] = dd + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g;
         sp[j] = ds + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
@@ -489,11 +504,12 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   }
   rbt_u4 sv = *(const rbt_gu4 *)(s_q == 0 ? sp[0] : s_q == 1 ? sp[1] : s_q == 2 ? sp[2] : sp[3]);
   __builtin_amdgcn_sched_barrier(0);
-  rbt_u4 ring[4][NCH];
 #pragma unroll
   for (int j = 0; j < 4; j++)
+    if (j > 0 || !early) {
 #pragma unroll
-    for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp[j] + 256 * c));
+      for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp[j] + 256 * c));
+    }
   __builtin_amdgcn_sched_barrier(0);
   if (tid < 32) zb[tid] = (__bf16)0.0f;
   if (w == 0 && lane < npairs) {
@@ -516,7 +532,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   // lane pointer of the wave's unit i (chunk 0); past its units or for a null job: cached dummy bytes
   auto uptr = [&](int i) -> const uint8_t * {
     if (i >= nu) return dummy;
-    const int u = uu(i), pp = u / nt, tl = u - pp * nt;
+    const int u = uu(i), q = u / nt, pp = pp_of(q), tl = u - q * nt;
     return plive[pp] ? pd[pp] + (long)(4 * (T0 + tl) + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
   };
   // scale window of the wave's units ib .. ib+3: lane l holds unit ib + l/16, row (l/4) % 4, bytes
@@ -525,7 +541,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
     const int i = ib + s_q;
     const uint8_t *p = hb8 + 16 * s_seg;
     if (i < nu) {
-      const int u = uu(i), pp = u / nt, tl = u - pp * nt;
+      const int u = uu(i), q = u / nt, pp = pp_of(q), tl = u - q * nt;
       if (plive[pp]) p = ps[pp] + (long)(4 * (T0 + tl) + s_row) * SRD + 16 * s_seg;
     }
     return *(const rbt_gu4 *)p;
@@ -553,7 +569,7 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
         ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(np + 256 * c));
       }
       if (i < nu) {
-        const int u = uu(i), pp = u / nt, tl = u - pp * nt;
+        const int u = uu(i), q = u / nt, pp = pp_of(q), tl = u - q * nt;
         const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[pp]) + boff : reinterpret_cast<const char *>(zb);
         xf4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -585,12 +601,13 @@ bool xdown1_ok(int npairs, size_t i) { return i == 2048 && npairs >= 1 && npairs
 
 hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
                          int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
-                         float *out, bool accumulate) {
+                         float *out, bool accumulate, const uint8_t *sh_dd,
+                         const uint8_t *sh_ds) {
   const int grid = c.num_cu;
   if (!xdown1_ok(kk + (has_shared ? 1 : 0), I) || H % 4 != 0 || grid <= 0 || (H / 4 + grid - 1) / grid > XD1_TPW)
     return hipErrorInvalidValue;
   launch_k(c, k_xdown1<4>, dim3(grid), dim3(64 * XD1_NW), down_job, down_slot, kk, hp, H, tok_w, sh_scale,
-           has_shared, gated, out, (int)accumulate);
+           has_shared, gated, out, (int)accumulate, sh_dd, sh_ds);
   return hipGetLastError();
 }
 
