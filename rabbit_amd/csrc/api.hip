@@ -838,7 +838,8 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
   // One token off the matrix cores (grouped int4, or MXFP4 shapes they do not take): the same three
   // launches with the decode GEMVs. The router rows' key records; the selection in every workgroup of
   // the fused gate/up + activation GEMV (routed pairs, then the shared expert); the down GEMV over the
-  // published job list (winners in rank order, then the shared expert); the ordered combine.
+  // published job list (winners in rank order, then the shared expert) with the ordered combine fused
+  // (or the two launches where the fused kernel does not take the shape).
   const bool g1 = S == 1 && !mfma && grp_in_select && (merge || !D.has_shared) && kk == k && !c->prof &&
                   rbt::gu1s_gemv_ok(ra, c->num_cu, L.routed_kind, L.routed_gs, I) &&
                   rbt::decode_shape_ok(I, L.routed_kind, L.routed_gs) && (uintptr_t)(sgate ? sgate : x) % 16 == 0;
@@ -853,9 +854,14 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router1_any(*c, ra, mid, bnd, shs, sgate, rec));
     HIP_OK(c, rbt::launch_gu1s_gemv(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, L.routed_kind,
                                     L.routed_gs, I, h, D.has_shared != 0));
-    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, L.routed_kind, djob, none, kk + (D.has_shared ? 1 : 0),
-                                 nullptr, h, dslot, (long)I, I, H, yy, (long)H));
-    HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, dst));
+    if (rbt::down1c_ok(L.routed_kind, L.routed_gs, kk + (D.has_shared ? 1 : 0), I, H, c->num_cu)) {
+      HIP_OK(c, rbt::launch_down1c(*c, L.routed_kind, L.routed_gs, djob, dslot, kk, D.has_shared, h, (long)I, I, H,
+                                   tw, shs, gated, dst));
+    } else {
+      HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, L.routed_kind, djob, none, kk + (D.has_shared ? 1 : 0),
+                                   nullptr, h, dslot, (long)I, I, H, yy, (long)H));
+      HIP_OK(c, rbt::launch_combine(*c, yy, S, k, H, tpair, tw, shs, D.has_shared, gated, dst));
+    }
   } else {
   if (r1) {
     // one token: router logits, key records and the shared gate
@@ -1069,12 +1075,13 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
                      (Dp.kind != RBT_QT_I4_GROUPED || Dp.group_size == 32) &&
                      ((uintptr_t)Dp.data | (uintptr_t)x) % 16 == 0 && Dp.data && Dp.scale;
   RbtExpertDev none{};
+  bool combined = false;  // the down launch wrote the combined rows (routed) itself
   if (kind == RBT_QT_MXFP4 && dp_ok && rbt::router1_latent_ok(ra, c->num_cu, (int)MH, (int)I) &&
       rbt::decode_shape_ok(I, kind, gs)) {
     // One token, MXFP4 experts, as the plain layer's decode: the router rows' key records; the
     // latent down projection; the selection in every workgroup of the gate/up launch (matrix cores,
-    // act fused, h in fp32); the down GEMV over the winners' job list (h rows at their pair slots);
-    // then the ordered combine and the up projection below.
+    // act fused, h in fp32); the down GEMV over the winners' job list (h rows at their pair slots)
+    // with the ordered combine fused; then the up projection below.
     RBT_TRY(check_qt(c, &Dp, "matmul"));
     float *rec;
     RbtExpertDev *djob;
@@ -1092,8 +1099,14 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
       RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
     HIP_OK(c, rbt::launch_xgateup1s_latent(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, nullptr, xl, (int)MH,
                                            (int)I, h, act));
-    HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, djob, none, K, nullptr, h, dslot, (long)I, (int)I,
-                                 (int)MH, yy, (long)MH));
+    if (rbt::down1c_ok(kind, gs, K, (int)I, (int)MH, c->num_cu)) {
+      HIP_OK(c, rbt::launch_down1c(*c, kind, gs, djob, dslot, K, 0, h, (long)I, (int)I, (int)MH, tw, nullptr, 0,
+                                   routed));
+      combined = true;
+    } else {
+      HIP_OK(c, rbt::launch_decode(*c, rbt::DECODE_DOWN, kind, djob, none, K, nullptr, h, dslot, (long)I, (int)I,
+                                   (int)MH, yy, (long)MH));
+    }
   } else {
   if (rbt::router_exact_ok(S, (int)H) && ((uintptr_t)x | (uintptr_t)D.router) % 16 == 0) {
     float *lg;
@@ -1125,7 +1138,7 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
                                 dflags + FLAG_ERR, dflags + FLAG_UNIQ));
   RBT_TRY(expert_pairs(c, kind, gs, pjob, none, P, nullptr, xl, ptok, MH, I, h, yy, nullptr, act));
   }
-  HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
+  if (!combined) HIP_OK(c, rbt::launch_combine(*c, yy, S, K, (int)MH, tpair, tw, shs, 0, 0, routed));
   const rbt_qt &U = lw->up_proj;
   if (S == 1 && rbt::proj1_ok(U.kind, U.group_size, (int)MH, (int)H, c->num_cu) &&
       ((uintptr_t)U.data | (uintptr_t)(lw->norm ? lw->norm : routed)) % 16 == 0) {

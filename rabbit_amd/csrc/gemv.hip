@@ -540,6 +540,128 @@ hipError_t launch_decode(const Ctx &c, int mode, int kind, const RbtExpertDev *j
 #undef RBT_MODE
 }
 
+// ------------------------------------------------------------------------------------------------
+// One token: the down GEMV over a rank-ordered job list (the kk winners, then the shared expert)
+// with the ordered combine fused. Workgroup b owns output rows [R0, R1) (whole iterations of IPI
+// rows) of every job; its waves deal out the (job, row) items job-major in equal contiguous runs, so
+// a wave reloads its x slice (the job's h row, at slots[job]) once per job of its run. Each row is
+// computed as k_decode_gemv computes it (same blocks per lane, same reductions: bit-identical row
+// sums). The sums land in LDS; thread r then combines row R0 + r in rank order with separate
+// roundings, as k_combine does (acc = 0, acc += w_j y_j, then + the shared row, scaled by
+// sh_scale[0] when gated; glm52/moe.rs:508-512, qwen38/generate.rs:303-349), and writes it. The
+// combine's launch and its re-read of every row sum are saved.
+// ------------------------------------------------------------------------------------------------
+constexpr int DC_MAXJ = 33, DC_MAXR = 64;
+
+template <int NB, int LPR, int U, int NW, bool I4G>
+__global__ __launch_bounds__(64 * NW) void k_down1c(const RbtExpertDev *__restrict__ jobs,
+                                                       const int *__restrict__ slots, int kk, int has_shared,
+                                                       const float *__restrict__ h, long h_stride, int cols,
+                                                       int rows, const float *__restrict__ tok_w,
+                                                       const float *__restrict__ sh_scale, int gated,
+                                                       float *__restrict__ out) {
+  constexpr int RPI = RBT_WAVE / LPR, IPI = U * RPI;
+  __shared__ float ys[DC_MAXJ][DC_MAXR];
+  const int nj = kk + (has_shared ? 1 : 0);
+  const int lane = threadIdx.x & (RBT_WAVE - 1), q = lane % LPR, sub = lane / LPR;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int ntile = rows / IPI;
+  const int T0 = (int)((long)blockIdx.x * ntile / gridDim.x), T1 = (int)((long)(blockIdx.x + 1) * ntile / gridDim.x);
+  const int R0 = T0 * IPI, nr = (T1 - T0) * IPI;
+  const int total = nj * nr;
+  int per = (total + NW - 1) / NW;
+  per = ((per + IPI - 1) / IPI) * IPI;
+  int pos = w * per;
+  const int end = min(pos + per, total);
+  const int nblk = cols / 32;
+  const unsigned rb = (unsigned)cols / 2;
+  float xr[NB][32];
+  float xs[NB];
+  DecodeFrag<NB, U> f0, f1;
+  while (pos < end) {
+    // one job's rows [r, r1) of the workgroup's block
+    const int job = pos / nr;
+    int r = pos - job * nr;
+    const int r1 = min(nr, r + (end - pos));
+    pos += r1 - r;
+    const RbtExpertDev J = jobs[job];
+    const uint8_t *d = J.dd;
+    const uint8_t *sc = reinterpret_cast<const uint8_t *>(J.ds);
+    float *yrow = ys[job];
+    if (d == nullptr) {
+      for (int rr = r + lane; rr < r1; rr += RBT_WAVE) yrow[rr] = 0.0f;
+      continue;
+    }
+    // the first weights go out before the x slice is read; then ping-pong as k_decode_gemv
+    frag_load<NB, LPR, U, I4G>(f0, d, sc, R0 + r, q, sub, nblk, rb, nblk);
+    load_x_slice<NB, LPR>(xr, xs, h + (long)slots[job] * h_stride, q, nblk);
+    const int rlast = r1 - IPI;
+    while (true) {
+      frag_load<NB, LPR, U, I4G>(f1, d, sc, R0 + min(r + IPI, rlast), q, sub, nblk, rb, nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f0, xr, xs, yrow + r, q, sub, nblk);
+      if (r + IPI >= r1) break;
+      frag_load<NB, LPR, U, I4G>(f0, d, sc, R0 + min(r + 2 * IPI, rlast), q, sub, nblk, rb, nblk);
+      frag_reduce_store<NB, LPR, U, I4G>(f1, xr, xs, yrow + r + IPI, q, sub, nblk);
+      r += 2 * IPI;
+      if (r >= r1) break;
+    }
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < nr) {
+    float acc = 0.0f;
+    for (int j = 0; j < kk; j++) acc = __fadd_rn(acc, __fmul_rn(tok_w[j], ys[j][t]));
+    if (has_shared) {
+      float sh = ys[kk][t];
+      if (gated) sh = __fmul_rn(sh, sh_scale[0]);
+      acc = __fadd_rn(acc, sh);
+    }
+    out[R0 + t] = acc;
+  }
+}
+
+// Blocks per lane as k_decode_gemv's MODE_DOWN takes them for these columns (so the sums are the
+// same bits; the rows per iteration do not change them): 1025..2048 columns one block per lane, in
+// 8 waves with 4 rows per iteration (C2's inter 2048: 18.6 us against 19.9 in 16 waves); 2049..4096
+// two, in 16 waves with one row per iteration (K3's 3584 x 3072: 23.1 us against 24.5 with 2 rows,
+// whose 16-wave build spills, and 24.4 in 8 waves with 2 rows). Returns the rows per iteration.
+static int down1c_ipi(int cols) {
+  const int nblk = cols / 32;
+  return nblk > 32 && nblk <= 64 ? 4 : nblk > 64 && nblk <= 128 ? 1 : 0;
+}
+
+bool down1c_ok(int kind, size_t gs, int njobs, int cols, int rows, int num_cu) {
+  if (!decode_shape_ok((size_t)cols, kind, gs) || njobs < 1 || njobs > DC_MAXJ || num_cu <= 0) return false;
+  const int ipi = down1c_ipi(cols);
+  if (ipi == 0 || rows <= 0 || rows % ipi != 0) return false;
+  const int ntile = rows / ipi;
+  return (long)ipi * ((ntile + num_cu - 1) / num_cu) <= DC_MAXR;
+}
+
+hipError_t launch_down1c(const Ctx &c, int kind, size_t gs, const RbtExpertDev *jobs, const int *slots, int kk,
+                         int has_shared, const float *h, long h_stride, int cols, int rows, const float *tok_w,
+                         const float *sh_scale, int gated, float *out) {
+  const int nj = kk + (has_shared ? 1 : 0);
+  if (!down1c_ok(kind, gs, nj, cols, rows, c.num_cu) || (gated && !sh_scale)) return hipErrorInvalidValue;
+  const bool i4 = kind == RBT_QT_I4_GROUPED;
+  const dim3 grid(c.num_cu);
+#define RBT_DC(NB, U, NW)                                                                                           \
+  {                                                                                                                 \
+    if (i4)                                                                                                         \
+      launch_k(c, k_down1c<NB, 64, U, NW, true>, grid, dim3(64 * NW), jobs, slots, kk, has_shared, h, h_stride,     \
+               cols, rows, tok_w, sh_scale, gated, out);                                                            \
+    else                                                                                                            \
+      launch_k(c, k_down1c<NB, 64, U, NW, false>, grid, dim3(64 * NW), jobs, slots, kk, has_shared, h, h_stride,    \
+               cols, rows, tok_w, sh_scale, gated, out);                                                            \
+  }
+  if (down1c_ipi(cols) == 4)
+    RBT_DC(1, 4, 8)
+  else
+    RBT_DC(2, 1, 16)
+#undef RBT_DC
+  return hipGetLastError();
+}
+
 hipError_t launch_pair_generic(const Ctx &c, bool gateup, int kind, size_t gs, const RbtExpertDev *jobs,
                                const RbtExpertDev &single, int njobs, const int *njobs_dev, const float *x,
                                const int *x_index, long x_stride, int cols, int rows, float *y, long y_stride,

@@ -66,6 +66,15 @@ hipError_t launch_rmsnorm(const Ctx &c, const float *x, const float *w, float ep
 hipError_t launch_add_rows(const Ctx &c, float *x, const float *t, size_t n);
 
 // gemv.hip
+// One token: the down GEMV over the job list jobs[0 .. kk + has_shared) (the winners in rank
+// order, then the shared expert; h rows at h + slots[j] * h_stride) with the ordered combine fused:
+// out[r] = sum_j w_j y_j in rank order, then + the shared row (times sh_scale[0] when gated), the
+// rounding sequence of launch_combine; the row sums are the bits of launch_decode's MODE_DOWN.
+// One workgroup per CU. cols 1025..4096 (MXFP4 or grouped int4 with groups of 32).
+bool down1c_ok(int kind, size_t gs, int njobs, int cols, int rows, int num_cu);
+hipError_t launch_down1c(const Ctx &c, int kind, size_t gs, const RbtExpertDev *jobs, const int *slots, int kk,
+                         int has_shared, const float *h, long h_stride, int cols, int rows, const float *tok_w,
+                         const float *sh_scale, int gated, float *out);
 hipError_t launch_generic(const Ctx &c, int kind, float *y, const float *x, const void *data, const void *scale,
                           size_t gs, size_t s, size_t i, size_t o);
 hipError_t launch_dequant(const Ctx &c, float *out, int kind, const void *data, const void *scale, size_t cols,
