@@ -1092,11 +1092,17 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
     rbt::GroupArgs ga{table, table + E, pjob, ptok, tpair, tw, dflags + FLAG_ERR};
     ga.down_job = djob;
     ga.down_slot = dslot;
-    HIP_OK(c, rbt::launch_router1_latent(*c, ra, mid, bnd, shs, rec, (int)MH, (int)I));
-    if (rbt::proj1_ok(Dp.kind, Dp.group_size, (int)H, (int)MH, c->num_cu))
-      HIP_OK(c, rbt::launch_proj1(*c, Dp.kind, Dp.group_size, Dp.data, Dp.scale, x, (int)H, (int)MH, xl));
-    else
-      RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
+    if (rbt::router1_proj_ok(ra, c->num_cu, (int)MH, (int)I, Dp.kind, Dp.group_size)) {
+      // the router rows and the latent down projection in one launch
+      HIP_OK(c, rbt::launch_router1_proj(*c, ra, mid, bnd, shs, rec, (int)MH, (int)I, Dp.kind, Dp.group_size,
+                                         Dp.data, Dp.scale, xl));
+    } else {
+      HIP_OK(c, rbt::launch_router1_latent(*c, ra, mid, bnd, shs, rec, (int)MH, (int)I));
+      if (rbt::proj1_ok(Dp.kind, Dp.group_size, (int)H, (int)MH, c->num_cu))
+        HIP_OK(c, rbt::launch_proj1(*c, Dp.kind, Dp.group_size, Dp.data, Dp.scale, x, (int)H, (int)MH, xl));
+      else
+        RBT_TRY(matmul_dev(c, xl, x, &Dp, s));
+    }
     HIP_OK(c, rbt::launch_xgateup1s_latent(*c, ra, rec, mid, bnd, ga, ids, wts, dflags + FLAG_AMB, nullptr, xl, (int)MH,
                                            (int)I, h, act));
     if (rbt::down1c_ok(kind, gs, K, (int)I, (int)MH, c->num_cu)) {

@@ -352,133 +352,16 @@ static hipError_t launch_decode_k(const Ctx &c, const RbtExpertDev *jobs, const 
 
 int decode_parts(int cols) { return long_split(cols); }
 
-// ------------------------------------------------------------------------------------------------
-// One token through one matrix (a projection of up to 8192 columns, MXFP4 or grouped int4 with
-// groups of 32). The decode GEMV above keeps a slice of x per wave in registers, which at one
-// matrix of long rows means every wave reloads all of x for two or three rows and runs at one
-// wave per SIMD. Here each workgroup stages x once in LDS (32-value blocks padded to 36 floats, so
-// lanes reading consecutive blocks hit distinct banks) and each wave holds only its rows' weights:
-// a wave's (at most PJ_RW) rows go out as one batch of loads at kernel entry, ahead of the staging.
-// Per row the lane arithmetic is block_dots' (blocks q + 64 j, the same fused multiply-adds and
-// -8 fold) and the wave sum rbt_group_sum<64>; the block sums of x for the fold are added as a
-// tree. NORM: x is first replaced by rmsnorm(x) * nw (norm_x_slice's arithmetic; the fp64 sum of
-// squares is formed over the workgroup, in another order).
-// ------------------------------------------------------------------------------------------------
-constexpr int PJ_MAXC = 8192, PJ_RW = 4, PJ_NW = 8;  // columns, rows per wave, waves per workgroup
+// k_proj1: one token through one matrix (proj1_body, rbt_gemv.h), one workgroup per CU.
+constexpr int PJ_NW = 8;  // waves per workgroup of k_proj1
 
 template <bool I4G, bool NORM, int NB>
 __global__ __launch_bounds__(64 * PJ_NW) void k_proj1(const uint8_t *__restrict__ d, const uint8_t *__restrict__ sc,
                                                       const float *__restrict__ x, int cols, int rows,
                                                       float *__restrict__ y, const float *__restrict__ nw,
                                                       float eps) {
-  __shared__ __attribute__((aligned(16))) float xs[PJ_MAXC / 32 * 36];
-  __shared__ float bsum[PJ_MAXC / 32];
-  __shared__ double red[PJ_NW];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int nblk = cols / 32;
-  const long NW = (long)gridDim.x * PJ_NW, wi = (long)blockIdx.x * PJ_NW + w;
-  const int r0 = (int)(wi * rows / NW), r1 = (int)((wi + 1) * rows / NW);
-  const unsigned rb = (unsigned)cols / 2;
-  // the wave's rows (clamped: a wave without rows re-reads row 0 and stores nothing)
-  rbt_u4 wr[PJ_RW][NB];
-  uint32_t sb[PJ_RW][NB];
-#pragma unroll
-  for (int u = 0; u < PJ_RW; u++) {
-    const int r = r1 > r0 ? min(r0 + u, r1 - 1) : 0;
-    const rbt_gu4 *rp = (const rbt_gu4 *)(d + (size_t)r * rb);
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int bb = min(lane + 64 * j, nblk - 1);
-      wr[u][j] = __builtin_nontemporal_load(rp + bb);
-      sb[u][j] = I4G ? ((const rbt_gu32 *)sc)[(size_t)r * nblk + bb] : ((const rbt_gu8 *)sc)[(size_t)r * nblk + bb];
-    }
-  }
-  // x into LDS, one float4 per thread and step (with the norm: after scaling), and for grouped int4
-  // the 32-value block sums (chunk sums added over the block's eight lanes). Barriers here are
-  // LDS-only: the weights stay in flight.
-  constexpr int XV = PJ_MAXC / 4 / (64 * PJ_NW);
-  const int n4 = cols / 4;
-  float4 xv4[XV];
-  double sq = 0.0;
-  auto put = [&](int i, const float4 &v) {
-    *reinterpret_cast<float4 *>(&xs[(i >> 3) * 36 + 4 * (i & 7)]) = v;
-    if (I4G) {
-      const float bsv = rbt_group_sum<8>(__fadd_rn(__fadd_rn(__fadd_rn(v.x, v.y), v.z), v.w));
-      if ((i & 7) == 0) bsum[i >> 3] = bsv;
-    }
-  };
-#pragma unroll
-  for (int k = 0; k < XV; k++) {
-    const int i = t + 64 * PJ_NW * k;
-    if (i < n4) {
-      const float4 v = ((const rbt_gf4 *)x)[i];
-      xv4[k] = v;
-      if (NORM)
-        sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-      else
-        put(i, v);
-    }
-  }
-  if (NORM) {
-    sq = rbt_wave_total_d(sq);
-    if (lane == 0) red[w] = sq;
-    lds_barrier();
-    double tot = 0.0;
-#pragma unroll
-    for (int i = 0; i < PJ_NW; i++) tot += red[i];
-    const float r = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(tot / (double)cols), eps)));
-#pragma unroll
-    for (int k = 0; k < XV; k++) {
-      const int i = t + 64 * PJ_NW * k;
-      if (i < n4) {
-        const float4 g = ((const rbt_gf4 *)nw)[i];
-        float4 v = xv4[k];
-        v.x = __fmul_rn(v.x, __fmul_rn(r, g.x));
-        v.y = __fmul_rn(v.y, __fmul_rn(r, g.y));
-        v.z = __fmul_rn(v.z, __fmul_rn(r, g.z));
-        v.w = __fmul_rn(v.w, __fmul_rn(r, g.w));
-        put(i, v);
-      }
-    }
-  }
-  lds_barrier();
-#pragma unroll
-  for (int u = 0; u < PJ_RW; u++) {
-    if (r0 + u >= r1) break;
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int b = lane + 64 * j;
-      const int bb = min(b, nblk - 1);
-      float xv[32];
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        const float4 v = *reinterpret_cast<const float4 *>(&xs[bb * 36 + 4 * k]);
-        xv[4 * k] = v.x;
-        xv[4 * k + 1] = v.y;
-        xv[4 * k + 2] = v.z;
-        xv[4 * k + 3] = v.w;
-      }
-      float a = 0.0f;
-      if (I4G) {
-        a = i4_dword_dot(wr[u][j].x, &xv[0], a);
-        a = i4_dword_dot(wr[u][j].y, &xv[8], a);
-        a = i4_dword_dot(wr[u][j].z, &xv[16], a);
-        a = i4_dword_dot(wr[u][j].w, &xv[24], a);
-        const float tt = __builtin_fmaf(__builtin_fmaf(-8.0f, bsum[bb], a), __uint_as_float(sb[u][j]), acc);
-        acc = b < nblk ? tt : acc;
-      } else {
-        const float scv = rbt_e8m0(sb[u][j]);
-        a = fp4_dword_dot(wr[u][j].x, scv, &xv[0], a);
-        a = fp4_dword_dot(wr[u][j].y, scv, &xv[8], a);
-        a = fp4_dword_dot(wr[u][j].z, scv, &xv[16], a);
-        a = fp4_dword_dot(wr[u][j].w, scv, &xv[24], a);
-        acc += b < nblk ? a : 0.0f;
-      }
-    }
-    acc = rbt_group_sum<64>(acc);
-    if (lane == 0) y[r0 + u] = acc;
-  }
+  __shared__ PjLds L;
+  proj1_body<I4G, NORM, NB, PJ_NW>(L, d, sc, x, cols, rows, y, nw, eps, blockIdx.x, gridDim.x);
 }
 
 bool proj1_ok(int kind, size_t gs, int cols, int rows, int num_cu) {

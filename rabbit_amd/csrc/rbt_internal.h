@@ -268,6 +268,12 @@ hipError_t launch_router1_any(const Ctx &c, const RouterArgs &a, double *mid, do
 hipError_t launch_gu1s_gemv(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,
                             const double *bnd, const GroupArgs &grp, int32_t *ids, float *wts, int *stats, int kind,
                             size_t gs, int I, float *h, bool has_shared);
+// The router rows of launch_router1_latent and the latent down projection xl = Dp . x (Dp: mh rows
+// of a.H columns, MXFP4 or grouped int4 with groups of 32; launch_proj1's arithmetic) in one launch.
+bool router1_proj_ok(const RouterArgs &a, int num_cu, int mh, int I, int kind, size_t gs);
+hipError_t launch_router1_proj(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                               void *rec_buf, int mh, int I, int kind, size_t gs, const void *data, const void *scale,
+                               float *xl);
 hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
                                  void *rec, int mh, int I);
 hipError_t launch_xgateup1s_latent(const Ctx &c, const RouterArgs &a, const void *rec, const double *mid,

@@ -2413,6 +2413,26 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
   router1_body<RPW>(L, P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn, blockIdx.x);
 }
 
+// One token of K3's latent MoE: the router rows' key records (router1_body, workgroups npj ..
+// npj + E - 1) and the latent down projection xl = Dp . x (proj1_body, workgroups 0 .. npj - 1, four
+// waves of at most two rows each) in one launch. Both read only the token, and each alone is bound by its latency
+// (router rows 10 us for 26 MB, the projection 8 us for 16 MB), not by HBM.
+union RouterProjLds {
+  LgLds<1> lg;
+  PjLds pj;
+};
+template <bool I4G, int NB>
+__global__ __launch_bounds__(256) void k_router1_proj(SelParams P, double *__restrict__ mid, double *__restrict__ bnd,
+                                                      float *__restrict__ sh_scale, KeyRec *__restrict__ rec,
+                                                      const uint8_t *__restrict__ pd, const uint8_t *__restrict__ ps,
+                                                      int mh, float *__restrict__ xl, int npj) {
+  __shared__ RouterProjLds U;
+  if ((int)blockIdx.x < npj)
+    proj1_body<I4G, false, NB, 4, 2>(U.pj, pd, ps, P.x, P.H, mh, xl, nullptr, 0.0f, blockIdx.x, npj);
+  else
+    router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x - npj);
+}
+
 // Certified logits of a small batch: workgroup (row, q) computes router row `row` (or the shared
 // gate row, row == E) against tokens 4q .. 4q + 3, two at a time with the two-row arithmetic (the
 // products are the same with the row and the tokens swapped). The row is read once per four tokens.
@@ -2788,6 +2808,30 @@ hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid,
   const SelParams P = sel_params(a);
   launch_k(c, k_router1<1>, dim3(a.E), dim3(256), P, nullptr, mid, bnd, sh_scale, reinterpret_cast<KeyRec *>(rec_buf),
            nullptr, 0.0f, nullptr);
+  return hipGetLastError();
+}
+
+bool router1_proj_ok(const RouterArgs &a, int num_cu, int mh, int I, int kind, size_t gs) {
+  const bool fmt = kind == RBT_QT_MXFP4 || (kind == RBT_QT_I4_GROUPED && gs == 32);
+  return fmt && router1_latent_ok(a, num_cu, mh, I) && a.H % 32 == 0 && a.H <= PJ_MAXC &&
+         (long)mh <= 2L * 4 * (2 * num_cu);
+}
+
+hipError_t launch_router1_proj(const Ctx &c, const RouterArgs &a, double *mid, double *bnd, float *sh_scale,
+                               void *rec_buf, int mh, int I, int kind, size_t gs, const void *data, const void *scale,
+                               float *xl) {
+  if (!router1_proj_ok(a, c.num_cu, mh, I, kind, gs) || ((uintptr_t)data | (uintptr_t)xl) % 16 != 0)
+    return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  const int npj = 2 * c.num_cu;  // 8 waves per CU, two rows each
+  const dim3 grid(npj + a.E), block(256);
+  KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
+  const uint8_t *pd = (const uint8_t *)data, *ps = (const uint8_t *)scale;
+  // hidden 7168 or 8192: four 32-value blocks per lane
+  if (kind == RBT_QT_I4_GROUPED)
+    launch_k(c, k_router1_proj<true, 4>, grid, block, P, mid, bnd, sh_scale, rec, pd, ps, mh, xl, npj);
+  else
+    launch_k(c, k_router1_proj<false, 4>, grid, block, P, mid, bnd, sh_scale, rec, pd, ps, mh, xl, npj);
   return hipGetLastError();
 }
 
