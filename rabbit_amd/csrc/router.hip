@@ -2413,10 +2413,11 @@ __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__res
   router1_body<RPW>(L, P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn, blockIdx.x);
 }
 
-// One token of K3's latent MoE: the router rows' key records (router1_body, workgroups npj ..
-// npj + E - 1) and the latent down projection xl = Dp . x (proj1_body, workgroups 0 .. npj - 1, four
-// waves of at most two rows each) in one launch. Both read only the token, and each alone is bound by its latency
-// (router rows 10 us for 26 MB, the projection 8 us for 16 MB), not by HBM.
+// One token of K3's latent MoE: the router rows' key records (router1_body, workgroups 0 .. E - 1)
+// and the latent down projection xl = Dp . x (proj1_body, workgroups E .. E + npj - 1, four waves of
+// at most two rows each) in one launch. Both read only the token, and each alone is bound by its
+// latency (router rows 10 us for 26 MB, the projection 8 us for 16 MB), not by HBM: together 15.4
+// us (the projection's workgroups first: 15.9).
 union RouterProjLds {
   LgLds<1> lg;
   PjLds pj;
@@ -2427,10 +2428,10 @@ __global__ __launch_bounds__(256) void k_router1_proj(SelParams P, double *__res
                                                       const uint8_t *__restrict__ pd, const uint8_t *__restrict__ ps,
                                                       int mh, float *__restrict__ xl, int npj) {
   __shared__ RouterProjLds U;
-  if ((int)blockIdx.x < npj)
-    proj1_body<I4G, false, NB, 4, 2>(U.pj, pd, ps, P.x, P.H, mh, xl, nullptr, 0.0f, blockIdx.x, npj);
+  if ((int)blockIdx.x >= P.E)
+    proj1_body<I4G, false, NB, 4, 2>(U.pj, pd, ps, P.x, P.H, mh, xl, nullptr, 0.0f, blockIdx.x - P.E, npj);
   else
-    router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x - npj);
+    router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x);
 }
 
 // Certified logits of a small batch: workgroup (row, q) computes router row `row` (or the shared
