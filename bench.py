@@ -135,8 +135,10 @@ def kernel_role(name: str) -> str:
     """gateup / down / router / proj / other, from the kernel's (possibly mangled) name."""
     if any(s in name for s in ("xgateup", "pgateup", "dgateup", "decode_gu_act", "gu1s_gemv")):
         return "gateup"
-    if any(s in name for s in ("xdown", "pdown", "ddown")):
+    if any(s in name for s in ("xdown", "pdown", "ddown", "down1c")):
         return "down"
+    if "proj1" in name and "router" not in name:
+        return "proj"
     m = re.search(r"k_decode_gemvILi\d+ELi\d+ELi\d+ELi(\d+)E", name) or \
         re.search(r"k_decode_gemv<\s*\d+,\s*\d+,\s*\d+,\s*(\d+)", name)
     if m:
