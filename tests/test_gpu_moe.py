@@ -218,7 +218,7 @@ def test_folded_boundary_winner(ctx, orc, name):
     assert ok, f"device vs oracle {d:.3e}, device vs fp64 {eg:.3e}, oracle vs fp64 {eo:.3e}"
 
 
-@pytest.mark.parametrize("name,ntok", [("c1", 1), ("c3", 8)])
+@pytest.mark.parametrize("name,ntok", [("c1", 1), ("c2", 1), ("c3", 8)])
 def test_decode_graph_replays(ctx, orc, name, ntok):
     """A decode call captured in a HIP graph (as the benchmark replays them) and replayed several
     times with other inputs, with eager calls and synchronisations between the replays: every
