@@ -491,6 +491,14 @@ __device__ __forceinline__ void proj1_body(PjLds &L, const uint8_t *__restrict__
   const long NWT = (long)nwg * NW, wi = (long)wg * NW + w;
   const int r0 = (int)(wi * rows / NWT), r1 = (int)((wi + 1) * rows / NWT);
   const unsigned rb = (unsigned)cols / 2;
+  // x first (one float4 per thread and step): the memory counter retires loads in issue order, so
+  // the staging below waits for x only, not for the weights issued after it
+  constexpr int XV = PJ_MAXC / 4 / (64 * NW);
+  const int n4 = cols / 4;
+  float4 xv4[XV];
+#pragma unroll
+  for (int k = 0; k < XV; k++) xv4[k] = ((const rbt_gf4 *)x)[min(t + 64 * NW * k, n4 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
   // the wave's rows (clamped: a wave without rows re-reads row 0 and stores nothing)
   rbt_u4 wr[RW][NB];
   uint32_t sb[RW][NB];
@@ -505,12 +513,9 @@ __device__ __forceinline__ void proj1_body(PjLds &L, const uint8_t *__restrict__
       sb[u][j] = I4G ? ((const rbt_gu32 *)sc)[(size_t)r * nblk + bb] : ((const rbt_gu8 *)sc)[(size_t)r * nblk + bb];
     }
   }
-  // x into LDS, one float4 per thread and step (with the norm: after scaling), and for grouped int4
-  // the 32-value block sums (chunk sums added over the block's eight lanes). Barriers here are
-  // LDS-only: the weights stay in flight.
-  constexpr int XV = PJ_MAXC / 4 / (64 * NW);
-  const int n4 = cols / 4;
-  float4 xv4[XV];
+  __builtin_amdgcn_sched_barrier(0);
+  // x into LDS (with the norm: after scaling), and for grouped int4 the 32-value block sums (chunk
+  // sums added over the block's eight lanes). Barriers here are LDS-only: the weights stay in flight.
   double sq = 0.0;
   auto put = [&](int i, const float4 &v) {
     *reinterpret_cast<float4 *>(&xs[(i >> 3) * 36 + 4 * (i & 7)]) = v;
@@ -523,8 +528,7 @@ __device__ __forceinline__ void proj1_body(PjLds &L, const uint8_t *__restrict__
   for (int k = 0; k < XV; k++) {
     const int i = t + 64 * NW * k;
     if (i < n4) {
-      const float4 v = ((const rbt_gf4 *)x)[i];
-      xv4[k] = v;
+      const float4 v = xv4[k];
       if (NORM)
         sq += (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
       else
