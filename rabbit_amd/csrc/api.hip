@@ -1058,12 +1058,14 @@ static int latent_moe_dev(rbt_ctx *c, uint32_t layer, const rbt_latent_moe_desc 
   RBT_TRY(scratch_t(c, SC_IDS, (size_t)P, &ids));
   RBT_TRY(scratch_t(c, SC_WTS, (size_t)P, &wts));
   RBT_TRY(scratch_t(c, SC_SHS, (size_t)S, &shs));
-  RBT_TRY(scratch_t(c, SC_PJOB, (size_t)(P + S), &pjob));
-  RBT_TRY(scratch_t(c, SC_PTOK, (size_t)(P + S), &ptok));
+  // one token may stream k + D1_KX routed pairs (a deferred router decision), each with its h row
+  const size_t pslots = S == 1 ? std::max((size_t)(P + S), (size_t)(K + rbt::D1_KX + 1)) : (size_t)(P + S);
+  RBT_TRY(scratch_t(c, SC_PJOB, pslots, &pjob));
+  RBT_TRY(scratch_t(c, SC_PTOK, pslots, &ptok));
   RBT_TRY(scratch_t(c, SC_TPAIR, (size_t)P, &tpair));
   RBT_TRY(scratch_t(c, SC_TW, (size_t)P, &tw));
   RBT_TRY(scratch_t(c, SC_XL, (size_t)S * MH, &xl));
-  RBT_TRY(scratch_t(c, SC_H, (size_t)P * I * 2, &h));
+  RBT_TRY(scratch_t(c, SC_H, pslots * I * 2, &h));
   RBT_TRY(scratch_t(c, SC_YY, (size_t)P * MH, &yy));
   RBT_TRY(scratch_t(c, SC_ROUTED, (size_t)S * MH, &routed));
   int *dflags = c->d_flags;

@@ -2561,6 +2561,28 @@ __device__ __forceinline__ void d1_finish(SelLds &L, float (*fold)[2][1024], con
   if (lane == 0 && stats && na) atomicAdd(stats, na);
 }
 
+// After the general selection (select3_body, the same in every workgroup), the workgroup's routed
+// pairs: the winners in rank order (L.r_id, left by wave 0 in every workgroup, the publishing one
+// included), their job-table entries from the staged table, nr = kk, nothing pending. Ends with a
+// workgroup barrier.
+__device__ __forceinline__ void fallback_pairs(const SelLds &L, PairLds &Q, const RbtExpertDev *__restrict__ tab,
+                                               int kk) {
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 64) {
+    for (int r = t; r < kk; r += 64) {
+      const int e = L.r_id[r];
+      Q.T.id[r] = e;
+      copy_job(Q.pj + r, tab + e);
+    }
+    if (t == 0) {
+      Q.T.nr = kk;
+      Q.T.pending = 0;
+    }
+  }
+  __syncthreads();
+}
+
 // gup (optional) counts the routed pairs the launch streams (for the benchmark's byte accounting).
 // xg: the gate/up activation (K = 512 NCH values; the router's own token in a plain layer, the
 // latent token in K3's latent MoE); h = act(g, u), as three bf16 parts or (HF32) fp32.
@@ -2640,19 +2662,8 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
       select3_body<MAXM>(S, P, mid, bnd, ids, wts, nullptr, stats, Gs, 1, 0);
     } else {
       select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
-      __syncthreads();
-      if (t < 64) {
-        for (int r = lane; r < kk; r += 64) {
-          Q.T.id[r] = Q.fb_ids[r];
-          copy_job(Q.pj + r, tab + Q.fb_ids[r]);
-        }
-        if (lane == 0) {
-          Q.T.nr = kk;
-          Q.T.pending = 0;
-        }
-      }
     }
-    __syncthreads();
+    fallback_pairs(S, Q, tab, kk);
   }
   // A deferred decision: workgroup 0 folds and decides while the others stream every candidate.
   // Otherwise workgroup 0 publishes the routing (the general path already did) and streams its
@@ -2731,19 +2742,8 @@ __global__ __launch_bounds__(256) void k_gu1s_gemv(SelParams P, const KeyRec *__
       select3_body<MAXM>(S, P, mid, bnd, ids, wts, nullptr, stats, Gs, 1, 0);
     } else {
       select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
-      __syncthreads();
-      if (t < 64) {
-        for (int r = lane; r < kk; r += 64) {
-          Q.T.id[r] = Q.fb_ids[r];
-          copy_job(Q.pj + r, tab + Q.fb_ids[r]);
-        }
-        if (lane == 0) {
-          Q.T.nr = kk;
-          Q.T.pending = 0;
-        }
-      }
     }
-    __syncthreads();
+    fallback_pairs(S, Q, tab, kk);
   }
   const bool pending = st == 2;
   const int nr = Q.T.nr;

@@ -102,11 +102,19 @@ def rel_l2(a, b) -> float:
     return float(np.linalg.norm(a - b) / (den if den > 0 else 1.0))
 
 
-def check_token(gpu, oracle, truth, rtol=1e-5):
+# Ceiling of the device-vs-oracle distance for a token that passes only because the oracle is the
+# one farther from the fp64 truth. The oracle's 8192-term sequential fp32 folds put it up to about
+# 1.4e-5 from the device on single tokens at hidden 8192 (largest over 1024 one-token calls: 1.44e-5);
+# twice the north_star's 1e-5 bounds that with margin and still fails a real device error.
+FALLBACK_CAP = 2e-5
+
+
+def check_token(gpu, oracle, truth, rtol=1e-5, cap=FALLBACK_CAP):
     """The per-token parity rule: the device output is within rtol relative L2 of the reference's
     (the oracle's sequential-fp32 result); where it is not, the reference itself must be the one
-    off: the device's error against the fp64 truth no larger than the reference's. Returns
-    (device vs oracle, device vs truth, oracle vs truth, passed)."""
+    off: the device's error against the fp64 truth no larger than the reference's, and the device
+    still within `cap` of the oracle. Returns (device vs oracle, device vs truth, oracle vs truth,
+    passed)."""
     d = rel_l2(gpu, oracle)
     eg, eo = rel_l2(gpu, truth), rel_l2(oracle, truth)
-    return d, eg, eo, (d < rtol) or (eg <= eo)
+    return d, eg, eo, (d < rtol) or (eg <= eo and d < cap)

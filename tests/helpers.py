@@ -60,6 +60,37 @@ def boundary_router(E: int, H: int, k: int, x: np.ndarray):
     return router, a, b, hi
 
 
+def tied_boundary_router(E: int, H: int, k: int, x: np.ndarray, n_tied: int = 5):
+    """A router whose last top-k place n_tied experts contest with the same exact logit 1 + 2^-18:
+    tied expert i has 1.0 at position p_i = 64 i / (n_tied - 1) of its first 65 entries and 2^-24
+    at the other 64. Any sum more accurate than the fold ties them (midpoint order: lower id
+    first); the sequential fp32 fold (kernels.rs:113-124) adds the p_i small terms exactly, then
+    the 1 (exact for even p_i), and every later 2^-24 is half an ulp that rounds to even, so it gives
+    1 + 2^-23 m_i with m_i = p_i / 2 rounded up to even. The fold thus ranks the tied experts in
+    the opposite order to their ids: the highest id takes the place. k - 1 experts (ids 3, 6, 9,
+    ...) rank above with logits 1.5 + j/16; every other logit is 0. x (one token, changed in place)
+    gets ones in its first 65 entries. Returns (router [E, H], tied ids, their fold values, the
+    k - 1 higher ids)."""
+    m = 64
+    x[:m + 1] = 1.0
+    router = np.zeros((E, H), np.float32)
+    d = np.float32(2.0 ** -24)
+    hi = [3 + 3 * j for j in range(k - 1)]
+    tied = [e for e in range(1, E) if e % 3 != 0][:n_tied]
+    assert hi[-1] < E and len(tied) == n_tied
+    for j, e in enumerate(hi):
+        router[e, 0] = np.float32(1.5 + j / 16)
+    folds = []
+    for i, e in enumerate(tied):
+        p = m * i // (n_tied - 1)
+        router[e, :m + 1] = d
+        router[e, p] = 1.0
+        mi = p // 2 + (p // 2) % 2 if p % 2 == 0 else None
+        assert mi is not None, "positions must be even"
+        folds.append(np.float32(1.0 + mi * 2.0 ** -23))
+    return router, tied, folds, hi
+
+
 def write_safetensors(path, tensors, metadata=None, raw_header=None):
     """Writes a safetensors file: tensors is a list of (name, dtype, shape, bytes) in data order.
     raw_header (bytes), when given, replaces the JSON header (for malformed-header tests)."""

@@ -41,3 +41,19 @@ def test_layer64_matches_the_oracle_layer(orc, family, kind, gated):
     for t in range(3):
         err = rel_l2(exp[t], truth[t])
         assert err < 2e-6, (t, err)
+
+
+def test_check_token_rule_and_its_ceiling():
+    """check_token: within 1e-5 of the oracle passes; farther passes only while the oracle is the
+    one farther from the fp64 truth and the device stays within the 2e-5 ceiling."""
+    from f64_truth import check_token
+    rng = np.random.default_rng(3)
+    truth = rng.standard_normal(4096)
+    u = rng.standard_normal(4096)
+    u /= np.linalg.norm(u) / np.linalg.norm(truth)  # |u| = |truth|: an offset c * u is c relative
+    assert check_token(truth + 5e-6 * u, truth, truth)[3]                 # within 1e-5 of the oracle
+    assert check_token(truth, truth + 1.5e-5 * u, truth)[3]               # the oracle is the one off
+    assert not check_token(truth + 1.5e-5 * u, truth, truth)[3]           # the device is the one off
+    # both 1.2e-5 from the truth on opposite sides: 2.4e-5 apart, over the ceiling
+    assert not check_token(truth - 1.2e-5 * u, truth + 1.2e-5 * u, truth)[3]
+    assert check_token(truth - 0.9e-5 * u, truth + 0.9e-5 * u, truth)[3]  # 1.8e-5 apart: under it

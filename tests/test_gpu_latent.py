@@ -218,17 +218,23 @@ def test_latent_moe_k3_dims_one_token(ctx, orc, proj_kind):
         _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
 
 
-def test_latent_moe_k3_folded_boundary_winner(ctx, orc):
-    # one token at K3's widths whose last top-k place only the exact folds decide
-    # (helpers.boundary_router, no correction bias): the winner comes from the first undecided
-    # gate/up slot, and the down GEMV and the combine take its row by rank
+@pytest.mark.parametrize("k,tied", [(8, False), (2, True)])
+def test_latent_moe_k3_folded_boundary_winner(ctx, orc, k, tied):
+    # one token at K3's widths whose last top-k place only the exact folds decide (no correction
+    # bias): helpers.boundary_router (two experts), the winner from the first undecided gate/up slot;
+    # or at top-2 helpers.tied_boundary_router (five experts): k + 4 = 6 routed pairs stream, three
+    # times top-k, each with its h row. The down GEMV and the combine take the winner's row by rank.
     import rabbit_amd as R
     import torch
-    from helpers import boundary_router
-    H, MH, I, E, k, layer = 7168, 3584, 3072, 32, 8, 54
+    from helpers import boundary_router, tied_boundary_router
+    H, MH, I, E, layer = 7168, 3584, 3072, 32, 54 + 10 * tied
     L, dq, uq, _ = _latent_case(ctx, orc, layer, H, MH, I, E, k, 7300, "i4g", 0.05)
     x = normal((1, H), 610, 0.05)
-    router, a, b, _ = boundary_router(E, H, k, x[0])
+    if tied:
+        router, cands, _, _ = tied_boundary_router(E, H, k, x[0])
+        b = cands[-1]
+    else:
+        router, a, b, _ = boundary_router(E, H, k, x[0])
     bias = np.zeros(E, np.float32)
     L = orc.MoeLayer(orc.FAMILY_GLM52, H, I, E, k, router, L.experts, router_bias=bias, norm_topk=False)
     t_router, t_bias = torch.from_numpy(router).cuda(), torch.from_numpy(bias).cuda()
@@ -239,6 +245,11 @@ def test_latent_moe_k3_folded_boundary_winner(ctx, orc):
     got = _run_latent(ctx, R, layer, L, dq, uq, x, 1, MH, norm, orc.situ(4.0, 25.0), R.situ(4.0, 25.0))
     assert ctx.profile_read(reset=True)["ambiguous"], "the router decision did not need exact folds"
     assert np.all(np.isfinite(got))
+    ids = torch.empty(k, dtype=torch.int32, device="cuda")
+    ctx.latent_moe(layer, MH, _dev_qt(R, dq), _dev_qt(R, uq), torch.from_numpy(x).cuda(), 1,
+                   torch.empty(H, device="cuda"), norm=torch.from_numpy(norm).cuda(), eps=1e-5,
+                   activation=R.situ(4.0, 25.0), ids_out=ids)
+    assert b in list(ids.cpu().numpy())
 
 
 def test_latent_moe_k3_graph_replays(ctx, orc):

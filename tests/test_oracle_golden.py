@@ -258,6 +258,24 @@ def test_boundary_router_is_decided_by_the_fold(orc):
         assert sorted(ids) == sorted(hi + [b]) and a not in list(ids)
 
 
+@pytest.mark.parametrize("k", [2, 10])
+def test_tied_boundary_router_is_decided_by_the_fold(orc, k):
+    """helpers.tied_boundary_router: the five tied experts' exact sums are equal, the oracle's
+    logits are the predicted folds 1 + 2^-23 m_i (all distinct), and the tied expert with the
+    largest fold (the highest id, which the midpoint order ranks last) takes the last of the k
+    places under both selection rules."""
+    from helpers import tied_boundary_router
+    E, H = 64, 1024
+    x = np.random.default_rng(6).standard_normal(H).astype(np.float32)
+    router, tied, folds, hi = tied_boundary_router(E, H, k, x)
+    logits = orc.matmul(x, router.ravel(), 1, H, E).ravel()
+    assert [logits[e] for e in tied] == folds and len(set(folds)) == len(folds)
+    exact = router.astype(np.float64) @ x.astype(np.float64)
+    assert all(exact[e] == 1.0 + 2.0 ** -18 for e in tied)
+    for ids, _ in (orc.route_softmax(logits, k), orc.route_sigmoid(logits, k, norm_topk=True)):
+        assert sorted(ids) == sorted(hi + [tied[-1]])
+
+
 def test_glm_grouped_kats(orc):
     for c in KATS["glm_grouped"]["cases"]:
         # The KATs rank raw choice values; sigmoid is strictly monotone on them, so feeding the
