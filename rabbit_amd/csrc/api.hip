@@ -137,7 +137,9 @@ struct rbt_ctx : rbt::Ctx {
   size_t arena_off[SC_N] = {}, arena_sz[SC_N] = {};
   std::map<uint64_t, PoolEntry> pool;
   std::map<uint32_t, Layer> layers;
-  int *d_flags = nullptr;  // device: [0] error flag, [1] ambiguity count, [2] unique experts, [4] gate/up pairs
+  // device: [0] error flag, [1] ambiguity count, [2] unique experts, [4] gate/up pairs; then the
+  // arrival counters (d_cnt)
+  int *d_flags = nullptr;
   int h_flags[8] = {};
   // profiling: one row of 5 events per recorded moe_forward_d call
   bool prof = false;
@@ -926,11 +928,15 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     if (c->prof) c->t_start = ev[4], c->t_stop = ev[5];
     // one token: the balanced down over the compact job list (all pairs' h in LDS); batches: a grid
     // of row blocks
+    const uint8_t *sh_dd = D.has_shared ? L.h_shared.dd : nullptr;
+    const uint8_t *sh_ds = D.has_shared ? (const uint8_t *)L.h_shared.ds : nullptr;
     const hipError_t e3 =
-        dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out, accumulate,
-                                 D.has_shared ? L.h_shared.dd : nullptr,
-                                 D.has_shared ? (const uint8_t *)L.h_shared.ds : nullptr)
-            : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, dst);
+        dn1 && rbt::xdown2_ok(kk + (D.has_shared ? 1 : 0), (size_t)I, H, c->num_cu)
+            ? rbt::launch_xdown2(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, yy, out, accumulate,
+                                 sh_dd, sh_ds)
+        : dn1 ? rbt::launch_xdown1(*c, djob, dslot, kk, hp, I, H, tw, shs, D.has_shared, gated, out, accumulate,
+                                   sh_dd, sh_ds)
+              : rbt::launch_xdown(*c, pjob, npairs, hp, I, H, S, k, ptok, tpair, tw, shs, D.has_shared, gated, dst);
     c->t_start = c->t_stop = nullptr;
     HIP_OK(c, e3);
   } else {
@@ -1214,8 +1220,9 @@ int rbt_init(rbt_ctx **out, int device) {
     c->num_cu = prop.multiProcessorCount;
   const char *what = nullptr;
   if ((e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) what = "hipStreamCreateWithFlags";
-  else if ((e = hipMalloc((void **)&c->d_flags, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMalloc";
-  else if ((e = hipMemset(c->d_flags, 0, FLAG_N * sizeof(int))) != hipSuccess) what = "hipMemset";
+  else if ((e = hipMalloc((void **)&c->d_flags, (FLAG_N + rbt::CNT_N) * sizeof(int))) != hipSuccess) what = "hipMalloc";
+  else if ((e = hipMemset(c->d_flags, 0, (FLAG_N + rbt::CNT_N) * sizeof(int))) != hipSuccess) what = "hipMemset";
+  if (!what) c->d_cnt = reinterpret_cast<unsigned *>(c->d_flags + FLAG_N);
   // the allocation-free entry point's scratch on this device (the device is current)
   if (!what) c->noalloc = noalloc_base(device, &c->noalloc_err);
   if (what) {

@@ -23,7 +23,11 @@ struct Ctx {
   // Per-kernel profiling: when set, every launch records a start/end event pair of its own
   // (kernel_events in api.hip hands them out and files them under the kernel).
   bool kprof = false;
+  // Arrival counters (CNT_N, device memory, zeroed at creation): a kernel that counts arrivals on
+  // them returns each to 0 before it ends.
+  unsigned *d_cnt = nullptr;
 };
+constexpr int CNT_N = 1024;
 
 // Events for one profiled launch of `fn` (false when none could be created: the launch is untimed).
 bool kernel_events(const Ctx &c, const void *fn, hipEvent_t *start, hipEvent_t *stop);
@@ -133,6 +137,13 @@ hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *
                          int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
                          float *out, bool accumulate = false, const uint8_t *sh_dd = nullptr,
                          const uint8_t *sh_ds = nullptr);
+// One token, pair-major: the same pair list's down products as contiguous runs of 4-row tiles per
+// wave (a workgroup stages the h of at most two pairs), each pair's rows into yy[j * H + r] (j in
+// the pair list's order), then the ordered combine (k_combine1) into out.
+bool xdown2_ok(int npairs, size_t i, int H, int num_cu);
+hipError_t launch_xdown2(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
+                         int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+                         float *yy, float *out, bool accumulate, const uint8_t *sh_dd, const uint8_t *sh_ds);
 hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, const __bf16 *hp, int I, int H, int S,
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);

@@ -2635,15 +2635,16 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   const int s0 = shpro ? (int)((long)blockIdx.x * tpp / gridDim.x) : 0;
   const int nsu = shpro ? (int)((long)(blockIdx.x + 1) * tpp / gridDim.x) - s0 : 0;
   // Wave 0 selects first: its half goes out after the selection (loads issued ahead of the selection
-  // would hold its issue slots until the memory pipeline has room for all of them).
+  // would hold its issue slots until the memory pipeline has room for all of them). Waves 1-3 issue
+  // theirs after the staging barrier, so that the selection does not wait for those issues.
   ShHalf<NCH> sh;
   if ((t >> 6) < 2 * nsu) {
     sh.su = s0 + (t >> 7);
     sh.hf = (t >> 6) & 1;
-    if constexpr (NCH % 2 == 0)
-      if (t >= 64) xgateup1_sh_issue<NCH>(sh, shv);
   }
-  lds_barrier();  // the staged activation and table (the shared loads stay in flight)
+  lds_barrier();  // the staged activation and table
+  if constexpr (NCH % 2 == 0)
+    if (t >= 64 && sh.su >= 0) xgateup1_sh_issue<NCH>(sh, shv);
   if (t < 64) {
     const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
     if (t == 0) Q.status = r;

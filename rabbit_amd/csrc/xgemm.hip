@@ -597,6 +597,331 @@ __global__ __launch_bounds__(64 * XD1_NW) void k_xdown1(const RbtExpertDev *__re
   }
 }
 
+// ------------------------------------------------------------------------------------------------
+// down for one token, pair-major: the U = npairs * H/4 units (pair q, 4-row output tile) in pair
+// order are dealt as contiguous runs over every wave of the grid (wave i of NW: units
+// [i U / NW, (i + 1) U / NW)). A wave streams consecutive 4 KB tiles of one expert's down rows and a
+// workgroup's run (XD2_NW waves x U / NW units, 352 KB at C1) covers at most two experts, so the
+// workgroup stages the h parts of at most two pairs (24 KB of LDS, against all eleven pairs' 135 KB
+// when a workgroup owns output rows of every pair) and touches few pages. Each unit's four row sums
+// go to yy[pair][row]; k_combine1 then forms the ordered combine over the pairs.
+// Processing order: with the shared expert's down pointers given (sh_dd, sh_ds), the shared expert
+// is processed first (q = 0), so the waves whose run lies in it issue their first window from kernel
+// arguments, before the pair tables land (its h slot still comes from the table); yy keeps the pair
+// list's order (the winners, then the shared expert at npairs - 1).
+// ------------------------------------------------------------------------------------------------
+constexpr int XD2_NW = 8;     // waves per workgroup
+constexpr int XD2_NP = 2;     // pairs whose h a workgroup stages
+constexpr int XD2_TB = 16;    // output tiles per block of the fused combine (64 rows)
+constexpr int XD2_MAXB = 32;  // blocks one workgroup can complete
+constexpr int XC1_MAXP = 64;  // pairs of the combine
+constexpr bool XD2_FUSED = true;  // the combine in the down launch (else k_combine1)
+
+template <int NCH, bool FC>
+__global__ __launch_bounds__(64 * XD2_NW) void k_xdown2(const RbtExpertDev *__restrict__ jobs,
+                                                        const int *__restrict__ slots, int npairs,
+                                                        const __bf16 *__restrict__ hp, int H,
+                                                        float *__restrict__ yy, const uint8_t *__restrict__ sh_dd,
+                                                        const uint8_t *__restrict__ sh_ds, int kk, int gated,
+                                                        const float *__restrict__ tok_w,
+                                                        const float *__restrict__ sh_scale, float *__restrict__ out,
+                                                        int accumulate, unsigned *__restrict__ cnt) {
+  constexpr int KD = NCH * 512, stride = KD + XG_PAD, SRD = KD >> 5;
+  constexpr int PPP = 3 * KD / 8;                                        // 16-byte pieces of one pair's parts
+  constexpr int HI = (XD2_NP * PPP + 64 * XD2_NW - 1) / (64 * XD2_NW);  // pieces per thread
+  static_assert(NCH == 4 && SRD == 64, "a unit is 4 rows x 4 chunks with 64 scale bytes per row");
+  __shared__ __attribute__((aligned(16))) __bf16 hs[XD2_NP][3 * stride];
+  __shared__ __attribute__((aligned(16))) uint8_t sw[XD2_NW][2][4][4][64];  // [wave][buffer][unit][row][byte]
+  __shared__ __attribute__((aligned(16))) __bf16 zb[32];
+  __shared__ float pw[XC1_MAXP];  // FC: the combine's pair weights and liveness
+  __shared__ int plive[XC1_MAXP];
+  __shared__ int lastb[XD2_MAXB], nlast;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rho = col >> 2, kap = col & 3;
+  const int nt = H >> 2;
+  const bool shf = sh_dd != nullptr && sh_ds != nullptr;
+  // FC: pair j's liveness and combine weight, loaded by lane j of wave 1 now (independent loads, no
+  // waits) and put in LDS after the stream
+  uint64_t f_dd = 0, f_ds = 0;
+  float f_w = 0.0f, f_s = 0.0f;
+  if (FC && w == 1) {
+    const int jl = min(lane, npairs - 1);
+    f_dd = reinterpret_cast<uint64_t>(jobs[jl].dd);
+    f_ds = reinterpret_cast<uint64_t>(jobs[jl].ds);
+    f_w = tok_w[min(jl, max(kk - 1, 0))];
+    f_s = sh_scale[0];
+  }
+  if (FC && tid == 0) nlast = 0;
+  // pair-list index of processing pair q
+  auto pl_of = [&](int q) { return shf ? (q == 0 ? npairs - 1 : q - 1) : q; };
+  const long U = (long)npairs * nt, NWT = (long)gridDim.x * XD2_NW, wi = (long)blockIdx.x * XD2_NW + w;
+  const int u0 = (int)(wi * U / NWT), nu = (int)((wi + 1) * U / NWT) - u0;
+  const int b0 = (int)((long)blockIdx.x * XD2_NW * U / NWT);
+  const int b1 = (int)((long)(blockIdx.x + 1) * XD2_NW * U / NWT);
+  const int qa = b0 / nt, qb = min(max(b1 - 1, b0) / nt, npairs - 1);  // the workgroup's pairs (qb <= qa + 1)
+  const uint8_t *hb8 = reinterpret_cast<const uint8_t *>(hp);
+  const uint8_t *dummy = hb8 + 64 * kap + 16 * g;
+  const int s_q = lane >> 4, s_row = (lane >> 2) & 3, s_seg = lane & 3;
+  // The workgroup's two pairs (local 0 = qa, 1 = qb): down pointers and h slots, from the kernel
+  // arguments for the shared expert, else from the tables (lane l loads local pair l & 1).
+  const uint8_t *pdd[XD2_NP], *pds[XD2_NP];
+  int pslot[XD2_NP];
+  {
+    const int ql = min(qa + (lane & 1), qb), pl = pl_of(ql);
+    const bool tab = !(shf && ql == 0);
+    // the three table loads unconditionally (one trip to memory), then the choice
+    const uint8_t *j_dd = jobs[pl].dd;
+    const uint8_t *j_ds = (const uint8_t *)jobs[pl].ds;
+    const int t_slot = slots[pl];  // the shared expert's h slot is decided on the device (after the routed pairs)
+    const uint8_t *t_dd = tab ? j_dd : sh_dd;
+    const uint8_t *t_ds = tab ? j_ds : sh_ds;
+    auto lane_ptr = [](const uint8_t *p, int l) -> const uint8_t * {
+      const uint64_t v = reinterpret_cast<uint64_t>(p);
+      const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l);
+      const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+      return reinterpret_cast<const uint8_t *>(((uint64_t)hi << 32) | lo);
+    };
+#pragma unroll
+    for (int i = 0; i < XD2_NP; i++) {
+      pdd[i] = lane_ptr(t_dd, i);
+      pds[i] = lane_ptr(t_ds, i);
+      pslot[i] = __builtin_amdgcn_readlane(t_slot, i);
+    }
+  }
+  const bool live[XD2_NP] = {pdd[0] != nullptr && pds[0] != nullptr, pdd[1] != nullptr && pds[1] != nullptr};
+  // lane pointers of the wave's unit i: codes at chunk 0, and its piece of the scale window
+  auto uptr = [&](int i) -> const uint8_t * {
+    if (i >= nu) return dummy;
+    const int u = u0 + i, q = u / nt, tl = u - q * nt, lq = q - qa;
+    const uint8_t *dd = lq == 0 ? pdd[0] : pdd[1];
+    return (lq == 0 ? live[0] : live[1]) ? dd + (long)(4 * tl + rho) * (KD >> 1) + 64 * kap + 16 * g : dummy;
+  };
+  auto sload = [&](int ib) {
+    const int i = ib + s_q;
+    const uint8_t *p = hb8 + 16 * s_seg;
+    if (i < nu) {
+      const int u = u0 + i, q = u / nt, tl = u - q * nt, lq = q - qa;
+      if (lq == 0 ? live[0] : live[1]) p = (lq == 0 ? pds[0] : pds[1]) + (long)(4 * tl + s_row) * SRD + 16 * s_seg;
+    }
+    return *(const rbt_gu4 *)p;
+  };
+  // h parts of the workgroup's pairs first (vmcnt counts loads in issue order: waiting for them then
+  // does not mean waiting for the weights issued after them)
+  const int npc = (qb - qa + 1) * PPP;
+  rbt_u4 hr[HI];
+#pragma unroll
+  for (int i = 0; i < HI; i++) {
+    const int e = min(tid + 64 * XD2_NW * i, npc - 1), lq = e / PPP;
+    const long slot = lq == 0 ? pslot[0] : pslot[1];
+    hr[i] = *(const rbt_gu4 *)(hp + 8L * (slot * PPP + (e - lq * PPP)));
+  }
+  rbt_u4 sv = sload(0);
+  rbt_u4 ring[4][NCH];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint8_t *cp = uptr(j);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(cp + 256 * c));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid < 32) zb[tid] = (__bf16)0.0f;
+#pragma unroll
+  for (int i = 0; i < HI; i++) {
+    const int e = tid + 64 * XD2_NW * i;
+    if (e < npc) {
+      const int lq = e / PPP, r = e - lq * PPP;
+      *reinterpret_cast<rbt_u4 *>(&hs[lq][(r / (KD / 8)) * stride + 8 * (r % (KD / 8))]) = hr[i];
+    }
+  }
+  auto sstore = [&](int buf, const rbt_u4 &v) {
+    *reinterpret_cast<rbt_u4 *>(&sw[w][buf][s_q][s_row][16 * s_seg]) = v;
+  };
+  sstore(0, sv);
+  lds_barrier();  // h parts, first scale windows
+  sv = sload(4);
+  const int bq = col >> 2, bpart = col & 3;
+  const int boff = bpart < 3 ? 2 * (bpart * stride + 128 * bq + 32 * g) : -1;
+  const int binc = bpart < 3 ? 1024 : 0;
+  int buf = 0;
+  for (int ib = 0; ib < nu; ib += 4) {
+    const uint8_t(*win)[4][64] = sw[w][buf];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int i = ib + j;
+      const uint8_t *np = uptr(i + 4);
+      rbt_u4 cw[NCH];
+#pragma unroll
+      for (int c = 0; c < NCH; c++) {
+        cw[c] = ring[j][c];
+        ring[j][c] = __builtin_nontemporal_load((const rbt_gu4 *)(np + 256 * c));
+      }
+      if (i < nu) {
+        const int u = u0 + i, q = u / nt, tl = u - q * nt, lq = q - qa;
+        const char *bp = boff >= 0 ? reinterpret_cast<const char *>(hs[lq]) + boff : reinterpret_cast<const char *>(zb);
+        xf4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+          const XB B = xb_read(bp + binc * c);
+          xmma_s(cw[c], xe8m0(win[j][rho][16 * c + 4 * kap + g]), B, acc);
+        }
+        const float y = row_dot(acc, col);
+        if (col == 0) {
+          const float yv = (lq == 0 ? live[0] : live[1]) ? y : 0.0f;
+          float *dst = yy + (long)pl_of(q) * H + 4 * tl + g;
+          if constexpr (FC)
+            __hip_atomic_store(dst, yv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // at the device's coherence point
+          else
+            *dst = yv;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    buf ^= 1;
+    sstore(buf, sv);
+    sv = sload(ib + 8);
+  }
+  if constexpr (FC) {
+    // The ordered combine by the last contributor of each block of XD2_TB output tiles: the
+    // workgroup adds the tiles it wrote to the block's arrival counter once its rows of yy are
+    // complete; the workgroup that completes npairs x (the block's tiles) combines the block and
+    // returns the counter to 0. No workgroup waits for another. The rows of yy, the counters and
+    // the combine's reads are device-scope atomic accesses, performed at the device's point of
+    // coherence (no cache of one XCD holds them), so no cache-wide write-back or invalidate is
+    // needed: a row store completes (vmcnt 0) before the counter add that announces it, and the
+    // combine reads after its add has seen every announcement.
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's rows of yy are complete
+    if (w == 1 && lane < npairs) {
+      asm volatile("" : "+v"(f_dd), "+v"(f_ds), "+v"(f_w), "+v"(f_s));  // used here, so waited for here
+      plive[lane] = f_dd != 0 && f_ds != 0;
+      pw[lane] = lane < kk ? f_w : (gated ? f_s : 1.0f);
+    }
+    __syncthreads();
+    // the workgroup's segments: pair qa's tiles [ta0, ta1), then pair qb's [0, tb1) when qb > qa
+    const int ta0 = b0 - qa * nt, ta1 = min(b1, (qa + 1) * nt) - qa * nt, tb1 = qb > qa ? b1 - qb * nt : 0;
+    const int na = ta1 > ta0 ? (ta1 - 1) / XD2_TB - ta0 / XD2_TB + 1 : 0;
+    const int nb = tb1 > 0 ? (tb1 - 1) / XD2_TB + 1 : 0;
+    if (tid < na + nb) {
+      const bool sa = tid < na;
+      const int blk = sa ? ta0 / XD2_TB + tid : tid - na;
+      const int lo = max(blk * XD2_TB, sa ? ta0 : 0), hi = min((blk + 1) * XD2_TB, sa ? ta1 : tb1);
+      const unsigned n = (unsigned)(hi - lo);
+      const unsigned tgt = (unsigned)npairs * (unsigned)(min((blk + 1) * XD2_TB, nt) - blk * XD2_TB);
+      const unsigned old = __hip_atomic_fetch_add(&cnt[blk], n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old + n == tgt) lastb[atomicAdd(&nlast, 1)] = blk;
+    }
+    __syncthreads();
+    const int nl = nlast;
+    if (nl > 0) {
+      constexpr int RB = 4 * XD2_TB;  // rows per block
+      for (int i0 = 0; i0 < nl; i0 += 64 * XD2_NW / RB) {
+        const int i = i0 + tid / RB;
+        if (i < nl) {
+          const int r = lastb[i] * RB + tid % RB;
+          if (r < H) {
+            constexpr int CH = 16;  // the rows of 16 pairs in flight at once
+            float o = 0.0f;
+            for (int j0 = 0; j0 < npairs; j0 += CH) {
+              float v[CH];
+#pragma unroll
+              for (int u = 0; u < CH; u++)
+                v[u] = __hip_atomic_load(yy + (long)min(j0 + u, npairs - 1) * H + r, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+              for (int u = 0; u < CH; u++)
+                if (j0 + u < npairs && plive[j0 + u]) o = __fadd_rn(o, __fmul_rn(pw[j0 + u], v[u]));
+            }
+            if (accumulate) o = __fadd_rn(out[r], o);
+            out[r] = o;
+          }
+        }
+      }
+      if (tid < nl) __hip_atomic_store(&cnt[lastb[tid]], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// The ordered combine of one token over the pair list of the down launch (yy rows: the kk winners
+// in rank order, then the shared expert):
+//   out[r] = (...(w_0 y_0[r] + w_1 y_1[r]) + ...) + s y_s[r]   (s: the shared gate when gated, else 1)
+// with separate roundings, the reference's order (qwen38/generate.rs:303-349); a pair whose job is
+// null (reported through the error flag) is left out. With accumulate, out[r] + (that) in one
+// rounding (x += layer(x), qwen38/generate.rs:411-413).
+
+__global__ __launch_bounds__(256) void k_combine1(const float *__restrict__ yy, const RbtExpertDev *__restrict__ jobs,
+                                                  int kk, int has_shared, int gated,
+                                                  const float *__restrict__ tok_w,
+                                                  const float *__restrict__ sh_scale, int H,
+                                                  float *__restrict__ out, int accumulate) {
+  // the rows and the pair tables go out together (lane l of every wave reads pair l's entry)
+  const int npairs = kk + (has_shared ? 1 : 0);
+  const int lane = threadIdx.x & 63;
+  const int r = min((int)(blockIdx.x * 256 + threadIdx.x), H - 1);
+  constexpr int CH = 16;
+  float o = 0.0f;
+  for (int j0 = 0; j0 < npairs; j0 += 64) {
+    const int jl = min(j0 + lane, npairs - 1);
+    const int lv = jobs[jl].dd != nullptr && jobs[jl].ds != nullptr;
+    const float lw = jl < kk ? tok_w[jl] : (gated ? sh_scale[0] : 1.0f);
+    for (int j1 = j0; j1 < min(j0 + 64, npairs); j1 += CH) {
+      float v[CH];
+#pragma unroll
+      for (int u = 0; u < CH; u++) v[u] = yy[(long)min(j1 + u, npairs - 1) * H + r];
+#pragma unroll
+      for (int u = 0; u < CH; u++) {
+        const int j = j1 + u;
+        const int live = __builtin_amdgcn_readlane(lv, min(j - j0, 63));
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lw), min(j - j0, 63)));
+        if (j < npairs && live) o = __fadd_rn(o, __fmul_rn(wj, v[u]));
+      }
+    }
+  }
+  if ((int)(blockIdx.x * 256 + threadIdx.x) >= H) return;
+  if (accumulate) o = __fadd_rn(out[r], o);
+  out[r] = o;
+}
+
+bool xdown2_ok(int npairs, size_t i, int H, int num_cu) {
+  if (i != 2048 || H % 4 != 0 || num_cu <= 0 || npairs < 1 || npairs > XC1_MAXP) return false;
+  const long U = (long)npairs * (H / 4), per = (U + num_cu - 1) / num_cu;
+  // a workgroup's run spans at most two pairs; the fused combine's blocks: its counters, and the
+  // blocks a workgroup can complete
+  return per <= H / 4 && (H / 4 + XD2_TB - 1) / XD2_TB <= CNT_N && per / XD2_TB + 4 <= XD2_MAXB;
+}
+
+hipError_t launch_xdown2(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
+                         int I, int H, const float *tok_w, const float *sh_scale, int has_shared, int gated,
+                         float *yy, float *out, bool accumulate, const uint8_t *sh_dd, const uint8_t *sh_ds) {
+  const int npairs = kk + (has_shared ? 1 : 0);
+  if (!xdown2_ok(npairs, (size_t)I, H, c.num_cu)) return hipErrorInvalidValue;
+  const bool shf = has_shared && sh_dd != nullptr && sh_ds != nullptr;
+  // phase events: the start at the down kernel's start, the end after the combine (the context is
+  // the one the caller holds: per-kernel profiling files events under it)
+  Ctx &m = const_cast<Ctx &>(c);
+  const hipEvent_t ts = c.t_start, te = c.t_stop;
+  m.t_stop = nullptr;
+  if (XD2_FUSED && c.d_cnt) {
+    m.t_stop = te;
+    launch_k(c, k_xdown2<4, true>, dim3(c.num_cu), dim3(64 * XD2_NW), down_job, down_slot, npairs, hp, H, yy,
+             shf ? sh_dd : nullptr, shf ? sh_ds : nullptr, kk, gated, tok_w, sh_scale, out, (int)accumulate, c.d_cnt);
+    return hipGetLastError();
+  }
+  launch_k(c, k_xdown2<4, false>, dim3(c.num_cu), dim3(64 * XD2_NW), down_job, down_slot, npairs, hp, H, yy,
+           shf ? sh_dd : nullptr, shf ? sh_ds : nullptr, kk, gated, tok_w, sh_scale, out, (int)accumulate,
+           (unsigned *)nullptr);
+  m.t_start = nullptr;
+  launch_k(c, k_combine1, dim3((H + 255) / 256), dim3(256), (const float *)yy, down_job, kk, has_shared, gated, tok_w,
+           sh_scale, H, out, (int)accumulate);
+  m.t_start = ts;
+  m.t_stop = te;
+  if (te) {
+    const hipError_t e = hipEventRecord(te, c.stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipGetLastError();
+}
+
 bool xdown1_ok(int npairs, size_t i) { return i == 2048 && npairs >= 1 && npairs <= XD1_NP; }
 
 hipError_t launch_xdown1(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
