@@ -394,6 +394,12 @@ int matmul_dev(rbt_ctx *c, float *y, const float *x, const rbt_qt *w, size_t s) 
   if (s > (1u << 24)) return fail(c, RBT_E_INVALID, "token count %zu too large", s);
   const size_t i = w->cols, o = w->rows;
   bool aligned = ((uintptr_t)w->data % 16 == 0) && ((uintptr_t)x % 16 == 0);
+  if (w->kind == RBT_QT_MXFP4 && s == 1 && aligned && (uintptr_t)w->scale % 4 == 0 &&
+      rbt::xgemv1_ok(i, o, c->num_cu)) {
+    // one token on the matrix cores, the whole matrix in flight at once
+    HIP_OK(c, rbt::launch_xgemv1(*c, (const uint8_t *)w->data, (const uint8_t *)w->scale, x, (int)i, (int)o, y));
+    return RBT_OK;
+  }
   if (w->kind != RBT_QT_F32 && aligned && rbt::decode_shape_ok(i, w->kind, w->group_size)) {
     RbtExpertDev one{};
     one.dd = (const uint8_t *)w->data;
@@ -1016,6 +1022,16 @@ int apply_single_dev(rbt_ctx *c, const rbt_expert_slot *slot, const int32_t *ids
   int kind;
   size_t gs;
   RBT_TRY(slot_view(c, slot, d, i, &v, &kind, &gs));
+  if (s == 1 && kind == RBT_QT_MXFP4 && k <= 64 && rbt::xexpert1_ok(d, i, c->num_cu) &&
+      ((uintptr_t)x | (uintptr_t)v.gd | (uintptr_t)v.ud | (uintptr_t)v.dd) % 16 == 0 &&
+      ((uintptr_t)v.gs | (uintptr_t)v.us | (uintptr_t)v.ds) % 4 == 0) {
+    // one token: gate/up + act and down + the weighted add, two launches on the matrix cores
+    float *hs;
+    RBT_TRY(scratch_t(c, SC_H, 2 * i, &hs));  // three bf16 parts of h (1.5 i floats)
+    HIP_OK(c, rbt::launch_xexpert1(*c, v, x, (int)d, (int)i, ids, w, (int)k, (int)slot->eid,
+                                   reinterpret_cast<__bf16 *>(hs), out, act));
+    return RBT_OK;
+  }
   int *ptok, *nr;
   float *pw, *h, *yy;
   RBT_TRY(scratch_t(c, SC_PTOK, s, &ptok));

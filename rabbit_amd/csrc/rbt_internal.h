@@ -148,6 +148,17 @@ hipError_t launch_xdown(const Ctx &c, const RbtExpertDev *jobs, int npairs, cons
                         int k, const int *tok, const int *tok_pair, const float *tok_w, const float *sh_scale,
                         int has_shared, int gated, float *out);
 
+// xgemv1.hip: one token, MXFP4, on the matrix cores with every load issued at entry.
+// y[O] = W[O, I] . x (matmul_mxfp4 for s = 1), I a multiple of 512 (4, 7, 8, 14 or 16 steps).
+bool xgemv1_ok(size_t cols, size_t rows, int num_cu);
+hipError_t launch_xgemv1(const Ctx &c, const uint8_t *data, const uint8_t *scale, const float *x, int I, int O,
+                         float *y);
+// apply_single_expert for one token (d = 8192 or 7168, i = 2048): when ids[0..k) holds eid, out +=
+// w * down(act(gate . x, up . x)) with w its first matching weight; hp: 3 * i bf16 of scratch.
+bool xexpert1_ok(size_t d, size_t i, int num_cu);
+hipError_t launch_xexpert1(const Ctx &c, const RbtExpertDev &J, const float *x, int d, int i, const int32_t *ids,
+                           const float *wts, int k, int eid, __bf16 *hp, float *out, const RbtAct &act);
+
 // prefill.hip: MXFP4 prefill as grouped GEMMs on the matrix cores.
 constexpr int PG_MAXE = 2048;  // segments (unique experts + shared) per call
 constexpr int PF_TCH = 64;     // tokens per GEMM tile

@@ -95,6 +95,48 @@ def test_decode_gemv_scale_byte_zero(ctx, orc):
     assert np.array_equal(_np(y), (hq.dense()[:, 5].astype(np.float64) * 2.0 ** 100).astype(np.float32))
 
 
+# ---- one token on the matrix cores (k_xgemv1): exact weights, scale byte 0, benchmark shapes -----
+@pytest.mark.parametrize("rows,cols", [(64, 8192), (3072, 3584), (8192, 2048)])
+def test_one_token_matmul_reads_exact_weights(ctx, orc, rows, cols):
+    """One token per call (the single-token matrix-core path): a one-hot activation reads back one
+    weight column bit for bit (the E2M1 x E8M0 decode and the three-part split of x are exact)."""
+    import torch
+    hq = orc.synth_mxfp4(rows, cols, seed=13 + rows, exp_lo=100, exp_hi=140)
+    dense = hq.dense()
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    for k in (0, 1, 31, 32, 511, 512, cols - 1):
+        x = np.zeros((1, cols), np.float32)
+        x[0, k] = 1.0
+        ctx.matmul_mxfp4(y, _t(x), _t(hq.data), _t(hq.scale), 1, cols, rows)
+        assert np.array_equal(_np(y), dense[:, k]), k
+
+
+def test_one_token_matmul_scale_byte_zero(ctx, orc):
+    # E8M0 byte 0 is the subnormal 2^-127 (quant.rs:391-396) on the single-token path too
+    import torch
+    rows, cols = 64, 2048
+    hq = orc.synth_mxfp4(rows, cols, seed=14, exp_lo=0, exp_hi=0)
+    x = np.zeros((1, cols), np.float32)
+    x[0, 5] = 2.0 ** 100
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.matmul_mxfp4(y, _t(x), _t(hq.data), _t(hq.scale), 1, cols, rows)
+    assert np.array_equal(_np(y), (hq.dense()[:, 5].astype(np.float64) * 2.0 ** 100).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,cols", [(3072, 3584), (4096, 4096), (2048, 8192), (8192, 2048), (2048, 7168),
+                                       (7168, 2048)])
+def test_one_token_matmul_parity(ctx, orc, rows, cols):
+    """matmul_mxfp4 for one token at the reference's micro-benchmark shapes (benches/kernels.rs:
+    209-240, 310-343) and C0's matrices: within 1e-5 of the scalar tier."""
+    import torch
+    hq = orc.synth_mxfp4(rows, cols, seed=rows * 3 + cols)
+    x = normal((1, cols), seed=rows)
+    exp = orc.matmul_mxfp4_scalar(x, hq.data, hq.scale, 1, cols, rows)
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    ctx.matmul_mxfp4(y, _t(x), _t(hq.data), _t(hq.scale), 1, cols, rows)
+    assert rel_l2(_np(y), exp) < RTOL
+
+
 # ---- matmul parity ------------------------------------------------------------------------------
 @pytest.mark.parametrize("rows,cols,s", [(2048, 8192, 1), (8192, 2048, 1), (2048, 6144, 1), (7168, 2048, 1),
                                          (2048, 7168, 1), (300, 8192, 3), (64, 96, 2)])
@@ -225,6 +267,35 @@ def test_apply_single_expert_c0(ctx, orc):
     out2 = np.zeros(H, np.float32)
     ctx.apply_single_expert(fused, ids, w, 1, 1, x, H, I, out2)
     assert bits_equal(out, out2)
+
+
+@pytest.mark.parametrize("H", [8192, 7168])
+def test_apply_single_expert_one_token_routing(ctx, orc, H):
+    """One token, k = 3 (the single-token matrix-core path): the expert's first matching slot gives
+    the weight (glm52/moe.rs:465-470), out accumulates onto what it held; a token that did not pick
+    the expert leaves out untouched; Situ runs on this path too."""
+    import rabbit_amd as R
+    I = 2048
+    g, u, dn = orc.synth_mxfp4(I, H, 21), orc.synth_mxfp4(I, H, 22), orc.synth_mxfp4(H, I, 23)
+    slot = orc.Slot(7, dn, gate=g, up=u)
+    rs = R.Slot(7, R.QT.mxfp4(dn.data, dn.scale, H, I), gate=R.QT.mxfp4(g.data, g.scale, I, H),
+                up=R.QT.mxfp4(u.data, u.scale, I, H))
+    x = normal((1, H), 24)
+    base = normal((1, H), 25).ravel()
+    ids = np.array([[3, 7, 7]], np.int32)
+    w = np.array([[0.5, -0.75, 2.0]], np.float32)
+    exp = orc.apply_single_expert(slot, ids, w, x, H, I, base.copy())
+    out = base.copy()
+    ctx.apply_single_expert(rs, ids, w, 1, 3, x, H, I, out)
+    assert rel_l2(out - base, exp - base) < RTOL
+    miss = base.copy()
+    ctx.apply_single_expert(rs, np.array([[1, 2, 3]], np.int32), w, 1, 3, x, H, I, miss)
+    assert np.array_equal(miss, base)
+    xs = normal((1, H), 26, 0.5)
+    exp_s = orc.apply_single_expert(slot, ids, w, xs, H, I, np.zeros(H, np.float32), act=orc.situ(4.0, 25.0))
+    out_s = np.zeros(H, np.float32)
+    ctx.apply_single_expert(rs, ids, w, 1, 3, xs, H, I, out_s, activation=R.situ(4.0, 25.0))
+    assert rel_l2(out_s, exp_s) < RTOL
 
 
 def test_apply_single_expert_multi_token_accumulates(ctx, orc):
