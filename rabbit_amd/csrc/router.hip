@@ -189,6 +189,12 @@ __global__ __launch_bounds__(256) void k_router_logits_w(const float *__restrict
 // lane and a single wave scan give every prefix sum S_j. The segment stride is padded by 4 floats
 // so the 16-byte LDS reads of neighbouring lanes fall in different banks.
 constexpr int RT_MAXH = 8192;
+// LDS stride of a thread's segment of seg products (seg a multiple of 4): every thread reads its
+// segment with 16-byte loads, which are conflict-free when the stride in 16-byte units is odd (an even
+// stride puts neighbouring lanes on the same banks: at seg = 28 the plain seg + 4 = 32 dwords maps all
+// 64 lanes onto two bank groups).
+__device__ __forceinline__ int rt_segp(int seg) { return ((seg >> 2) & 1) ? seg : seg + 4; }
+
 
 __global__ __launch_bounds__(64) void k_router_logits_t(const float *__restrict__ x, int S, int H,
                                                         const float *__restrict__ W, int E,
@@ -199,7 +205,7 @@ __global__ __launch_bounds__(64) void k_router_logits_t(const float *__restrict_
   const int row = blockIdx.x;
   const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
   const int seg = H / 64;      // elements per lane segment
-  const int segp = seg + 4;    // padded segment stride in LDS
+  const int segp = rt_segp(seg);  // padded segment stride in LDS
   const int nch = H / 256;     // coalesced chunks (one float4 per lane)
   const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
   const double e64 = 1.1102230246251565e-16;  // 2^-53
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(256) void k_router_logits_b(const float *__restrict
   const int row = blockIdx.x;
   const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
   const int seg = H / 256;   // elements per thread segment
-  const int segp = seg + 4;  // padded stride
+  const int segp = rt_segp(seg);  // padded stride
   const int nch = H / 1024;  // coalesced chunks (one float4 per thread)
   const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
   const double e64 = 1.1102230246251565e-16;  // 2^-53
@@ -2171,19 +2177,16 @@ __device__ __forceinline__ void store_key_rec(KeyRec *dst, const KeyRec &r) {
 }
 
 // KP/rec: when KP is set, the finishing threads also store the key records of rows ea and eb
-// (-1: none).
+// (-1: none), row b's at rec_b + eb when rec_b is given (two tokens of one router row).
+// logits_rows_blk in two phases: the products into LDS (the inputs are dead after it), then the
+// sums, the scan, the bound and the outputs.
 template <int NR>
-__device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)[RT_MAXH / 1024],
-                                                const float4 (&wa)[RT_MAXH / 1024],
-                                                const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
-                                                double *bnd_a, double *mid_b, double *bnd_b,
-                                                const SelParams *KP = nullptr, KeyRec *rec = nullptr, int ea = -1,
-                                                int eb = -1) {
+__device__ __forceinline__ void logits_rows_store(LgLds<NR> &L, const float4 (&xv)[RT_MAXH / 1024],
+                                                  const float4 (&wa)[RT_MAXH / 1024],
+                                                  const float4 (&wb)[RT_MAXH / 1024], int H) {
   static_assert(NR == 1 || NR == 2, "one or two rows");
-  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
-  const int seg = H / 256, segp = seg + 4, nch = H / 1024;
-  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
-  const double e64 = 1.1102230246251565e-16;  // 2^-53
+  const int t = threadIdx.x;
+  const int seg = H / 256, segp = rt_segp(seg), nch = H / 1024;
 #pragma unroll
   for (int c = 0; c < RT_MAXH / 1024; c++) {
     if (c < nch) {
@@ -2205,6 +2208,17 @@ __device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)
       }
     }
   }
+}
+
+template <int NR>
+__device__ __forceinline__ void logits_rows_finish(LgLds<NR> &L, int H, double *mid_a, double *bnd_a, double *mid_b,
+                                                   double *bnd_b, const SelParams *KP = nullptr,
+                                                   KeyRec *rec = nullptr, int ea = -1, int eb = -1,
+                                                   KeyRec *rec_b = nullptr) {
+  const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+  const int seg = H / 256, segp = rt_segp(seg);
+  const double u1 = 5.9604648328104515e-08;   // u/(1-u), u = 2^-24 (rounded up)
+  const double e64 = 1.1102230246251565e-16;  // 2^-53
   __syncthreads();
   const float *ma = L.lp[0] + t * segp, *mb = L.lp[NR - 1] + t * segp;
   double la = 0.0, pa = 0.0, lb = 0.0, pb = 0.0;
@@ -2297,10 +2311,21 @@ __device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)
       *mo = tot;
       *bo = B;
       const int e = rowb ? eb : ea;
-      if (KP && e >= 0) store_key_rec(rec + e, make_key_rec(*KP, e, tot, B));
+      if (KP && e >= 0) store_key_rec((rowb && rec_b ? rec_b : rec) + e, make_key_rec(*KP, e, tot, B));
     }
   }
   __syncthreads();  // lp and sh are rewritten next
+}
+
+template <int NR>
+__device__ __forceinline__ void logits_rows_blk(LgLds<NR> &L, const float4 (&xv)[RT_MAXH / 1024],
+                                                const float4 (&wa)[RT_MAXH / 1024],
+                                                const float4 (&wb)[RT_MAXH / 1024], int H, double *mid_a,
+                                                double *bnd_a, double *mid_b, double *bnd_b,
+                                                const SelParams *KP = nullptr, KeyRec *rec = nullptr, int ea = -1,
+                                                int eb = -1, KeyRec *rec_b = nullptr) {
+  logits_rows_store<NR>(L, xv, wa, wb, H);
+  logits_rows_finish<NR>(L, H, mid_a, bnd_a, mid_b, bnd_b, KP, rec, ea, eb, rec_b);
 }
 
 typedef float rbt_f4v __attribute__((ext_vector_type(4)));
@@ -2432,6 +2457,89 @@ __global__ __launch_bounds__(256) void k_router1_proj(SelParams P, double *__res
     proj1_body<I4G, false, NB, 4, 2>(U.pj, pd, ps, P.x, P.H, mh, xl, nullptr, 0.0f, blockIdx.x - P.E, npj);
   else
     router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x);
+}
+
+// Certified logits of a decode batch (2..RB_TOK tokens per workgroup): workgroup (row, q) reads
+// router row `row` (or the shared gate row, row == E) once and computes it against tokens
+// RB_TOK q .. RB_TOK q + RB_TOK - 1, two at a time with the two-row arithmetic (the products are the
+// same with the row and the tokens swapped), the next two tokens' loads in flight meanwhile.
+constexpr int RB_TOK = 8;
+__global__ __launch_bounds__(256) void k_router_logits_t8(const float *__restrict__ x, int S, int H,
+                                                          const float *__restrict__ W, int E,
+                                                          const float *__restrict__ sgate, double *__restrict__ mid,
+                                                          double *__restrict__ bnd, int erows) {
+  constexpr int MC = RT_MAXH / 1024;
+  __shared__ LgLds<2> L;
+  const int t = threadIdx.x, row = blockIdx.x, nch = H / 1024;
+  const int s0 = RB_TOK * blockIdx.y, s1 = min(S, s0 + RB_TOK);
+  const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
+  float4 wv[MC], xa[MC], xb[MC];
+  auto load = [&](const float4 *p, float4(&v)[MC]) {
+#pragma unroll
+    for (int c = 0; c < MC; c++) v[c] = p[min(c, nch - 1) * 256 + t];
+  };
+  auto tok = [&](int s) { return reinterpret_cast<const float4 *>(x + (size_t)min(s, S - 1) * H); };
+  load(tok(s0), xa);
+  load(tok(s0 + 1), xb);
+  load(w4, wv);
+  for (int s = s0; s < s1; s += 2) {
+    logits_rows_store<2>(L, wv, xa, xb, H);
+    if (s + 2 < s1) {  // the next two tokens' loads go out while this pair is reduced
+      load(tok(s + 2), xa);
+      load(tok(s + 3), xb);
+    }
+    const bool two = s + 1 < s1;
+    logits_rows_finish<2>(L, H, mid + (size_t)s * erows + row, bnd + (size_t)s * erows + row,
+                          two ? mid + (size_t)(s + 1) * erows + row : nullptr,
+                          two ? bnd + (size_t)(s + 1) * erows + row : nullptr);
+  }
+}
+
+// The selection of a decode batch, one workgroup per token: the four waves form the token's key
+// records from its intervals (sel_keys: three fp64 sigmoids per expert for the sigmoid families),
+// then wave 0 runs the one-token fast path (select_pairs); when it certifies, the winners' weights
+// and ids; otherwise (an open decision, ties beyond the candidate window, NaN keys) the general
+// path from the intervals, exact folds included (select3_body). Writes ids / wts / sh_scale of the
+// token as k_router_select3 does.
+template <int MAXM>
+__global__ __launch_bounds__(256) void k_router_select_rec(SelParams P, const double *__restrict__ mid,
+                                                           const double *__restrict__ bnd,
+                                                           const RbtExpertDev *__restrict__ table,
+                                                           int32_t *__restrict__ ids, float *__restrict__ wts,
+                                                           float *__restrict__ sh_scale, int *__restrict__ stats) {
+  __shared__ SelLds L;
+  __shared__ PairLds Q;
+  __shared__ __attribute__((aligned(16))) float4 kr[64 * MAXM];
+  __shared__ float kbuf[6 * 64 * MAXM];
+  const int s = blockIdx.x, t = threadIdx.x, lane = t & 63;
+  const int E = P.E, k = P.k, kk = min(P.k, P.E);
+  const double *ms = mid + (size_t)s * P.erows, *bs = bnd + (size_t)s * P.erows;
+  for (int e = t; e < E; e += 256) {
+    const float lb = P.logit_bias ? P.logit_bias[e] : 0.0f;
+    const float rb = P.router_bias ? P.router_bias[e] : 0.0f;
+    float lm, kl, kh;
+    uint32_t u;
+    sel_keys(P, ms[e], bs[e], lb, rb, lm, u, kl, kh);
+    kr[e] = make_float4(kl, kh, __uint_as_float(u), lm);
+  }
+  __syncthreads();
+  if (t < 64) {
+    float4 rv[MAXM];
+#pragma unroll
+    for (int m = 0; m < MAXM; m++) rv[m] = kr[min(lane + 64 * m, E - 1)];
+    const int r = select_pairs<MAXM>(L, Q, P, rv, table);
+    if (r == 1) {
+      winner_weights(L, P, kk);
+      for (int j = lane; j < k; j += 64) {
+        ids[(size_t)s * k + j] = j < kk ? L.r_id[j] : -1;
+        wts[(size_t)s * k + j] = j < kk ? L.s_w[j] : 0.0f;
+      }
+      if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
+    }
+    if (lane == 0) Q.status = r;
+  }
+  __syncthreads();
+  if (Q.status != 1) select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, GroupOut{}, 0, s, kbuf);
 }
 
 // Certified logits of a small batch: workgroup (row, q) computes router row `row` (or the shared
@@ -2779,6 +2887,31 @@ static SelParams sel_params(const RouterArgs &a) {
   P.x = a.x;
   P.W = a.W;
   return P;
+}
+
+bool router_batch_ok(const RouterArgs &a) {
+  const bool aligned = ((uintptr_t)a.x % 16 == 0) && ((uintptr_t)a.W % 16 == 0);
+  return a.S >= 2 && a.H % 1024 == 0 && a.H <= RT_MAXH && aligned && a.E <= 1024 && a.k <= SEL_MAXK &&
+         !(a.n_group > 1 && a.family != RBT_FAMILY_QWEN38);
+}
+
+hipError_t launch_router_batch(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
+                               const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats) {
+  if (!router_batch_ok(a) || (sgate && (uintptr_t)sgate % 16 != 0) || !table) return hipErrorInvalidValue;
+  const SelParams P = sel_params(a);
+  launch_k(c, k_router_logits_t8, dim3(a.erows, (a.S + RB_TOK - 1) / RB_TOK), dim3(256), a.x, a.S, a.H, a.W, a.E,
+           sgate, mid, bnd, a.erows);
+  const int m = (a.E + 63) / 64;
+  if (m <= 4)
+    launch_k(c, k_router_select_rec<4>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table, ids,
+             wts, sh_scale, stats);
+  else if (m <= 8)
+    launch_k(c, k_router_select_rec<8>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table, ids,
+             wts, sh_scale, stats);
+  else
+    launch_k(c, k_router_select_rec<16>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table,
+             ids, wts, sh_scale, stats);
+  return hipGetLastError();
 }
 
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu) {
