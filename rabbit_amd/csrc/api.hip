@@ -879,7 +879,7 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router1(*c, rr, sgate, mid, bnd, shs, rec, fold_norm ? norm_w : nullptr, eps,
                                   fold_norm ? xn : nullptr));
   } else if (!rbt::router_exact_ok(S, H) && rbt::router_batch_ok(ra) && (uintptr_t)(sgate ? sgate : x) % 16 == 0) {
-    // a decode batch: the router read once per 8 tokens, then the per-token selection
+    // a decode batch: certified intervals for every (row, token), then the per-token selection
     HIP_OK(c, rbt::launch_router_batch(*c, ra, sgate, mid, bnd, L.d_table, ids, wts, shs, dflags + FLAG_AMB));
   } else {
     const bool al16 = ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0;

@@ -265,10 +265,10 @@ hipError_t launch_router_select(const Ctx &c, const RouterArgs &a, const double 
 // the launch also writes to xn.
 bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
 // A decode batch (2+ tokens, hidden a multiple of 1024 up to 8192, up to 1024 experts, no grouped
-// routing): certified intervals (mid/bnd as launch_router_logits) with every router row read once
-// per 8 tokens, then one selection workgroup per token (keys formed by the whole workgroup, the
-// one-token fast path, the general path where it does not certify). table: the layer's job table
-// (the fast path reads winners' entries).
+// routing): certified intervals (mid/bnd as launch_router_logits), one (row, token) per workgroup,
+// then one selection workgroup per token (keys formed by the whole workgroup, the one-token fast
+// path, the general path where it does not certify). table: the layer's job table (the fast path
+// reads winners' entries).
 bool router_batch_ok(const RouterArgs &a);
 hipError_t launch_router_batch(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
                                const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats);

@@ -2459,40 +2459,26 @@ __global__ __launch_bounds__(256) void k_router1_proj(SelParams P, double *__res
     router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x);
 }
 
-// Certified logits of a decode batch (2..RB_TOK tokens per workgroup): workgroup (row, q) reads
-// router row `row` (or the shared gate row, row == E) once and computes it against tokens
-// RB_TOK q .. RB_TOK q + RB_TOK - 1, two at a time with the two-row arithmetic (the products are the
-// same with the row and the tokens swapped), the next two tokens' loads in flight meanwhile.
-constexpr int RB_TOK = 8;
-__global__ __launch_bounds__(256) void k_router_logits_t8(const float *__restrict__ x, int S, int H,
+// Certified logits of a decode batch, one (row, token) per workgroup: a smaller LDS footprint than
+// the two-at-a-time form, so four workgroups share a CU; the row is read from HBM once and its
+// other tokens' reads hit L2 when the router's row count is a multiple of the XCD count (the grid's
+// tokens of one row are then dispatched to one XCD).
+__global__ __launch_bounds__(256) void k_router_logits_t1(const float *__restrict__ x, int S, int H,
                                                           const float *__restrict__ W, int E,
                                                           const float *__restrict__ sgate, double *__restrict__ mid,
                                                           double *__restrict__ bnd, int erows) {
   constexpr int MC = RT_MAXH / 1024;
-  __shared__ LgLds<2> L;
-  const int t = threadIdx.x, row = blockIdx.x, nch = H / 1024;
-  const int s0 = RB_TOK * blockIdx.y, s1 = min(S, s0 + RB_TOK);
+  __shared__ LgLds<1> L;
+  const int t = threadIdx.x, row = blockIdx.x, s = blockIdx.y, nch = H / 1024;
   const float4 *w4 = reinterpret_cast<const float4 *>(row < E ? W + (size_t)row * H : sgate);
-  float4 wv[MC], xa[MC], xb[MC];
-  auto load = [&](const float4 *p, float4(&v)[MC]) {
+  const float4 *x4 = reinterpret_cast<const float4 *>(x + (size_t)s * H);
+  float4 wv[MC], xv[MC];
 #pragma unroll
-    for (int c = 0; c < MC; c++) v[c] = p[min(c, nch - 1) * 256 + t];
-  };
-  auto tok = [&](int s) { return reinterpret_cast<const float4 *>(x + (size_t)min(s, S - 1) * H); };
-  load(tok(s0), xa);
-  load(tok(s0 + 1), xb);
-  load(w4, wv);
-  for (int s = s0; s < s1; s += 2) {
-    logits_rows_store<2>(L, wv, xa, xb, H);
-    if (s + 2 < s1) {  // the next two tokens' loads go out while this pair is reduced
-      load(tok(s + 2), xa);
-      load(tok(s + 3), xb);
-    }
-    const bool two = s + 1 < s1;
-    logits_rows_finish<2>(L, H, mid + (size_t)s * erows + row, bnd + (size_t)s * erows + row,
-                          two ? mid + (size_t)(s + 1) * erows + row : nullptr,
-                          two ? bnd + (size_t)(s + 1) * erows + row : nullptr);
-  }
+  for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
+#pragma unroll
+  for (int c = 0; c < MC; c++) wv[c] = w4[min(c, nch - 1) * 256 + t];
+  logits_rows_blk<1>(L, wv, xv, xv, H, mid + (size_t)s * erows + row, bnd + (size_t)s * erows + row, nullptr,
+                     nullptr);
 }
 
 // The selection of a decode batch, one workgroup per token: the four waves form the token's key
@@ -2899,8 +2885,7 @@ hipError_t launch_router_batch(const Ctx &c, const RouterArgs &a, const float *s
                                const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats) {
   if (!router_batch_ok(a) || (sgate && (uintptr_t)sgate % 16 != 0) || !table) return hipErrorInvalidValue;
   const SelParams P = sel_params(a);
-  launch_k(c, k_router_logits_t8, dim3(a.erows, (a.S + RB_TOK - 1) / RB_TOK), dim3(256), a.x, a.S, a.H, a.W, a.E,
-           sgate, mid, bnd, a.erows);
+  launch_k(c, k_router_logits_t1, dim3(a.erows, a.S), dim3(256), a.x, a.S, a.H, a.W, a.E, sgate, mid, bnd, a.erows);
   const int m = (a.E + 63) / 64;
   if (m <= 4)
     launch_k(c, k_router_select_rec<4>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table, ids,
