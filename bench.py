@@ -133,6 +133,12 @@ def kernel_table(ctx, run):
 
 def kernel_role(name: str) -> str:
     """gateup / down / router / proj / other, from the kernel's (possibly mangled) name."""
+    # k_xgemv1<NCH, KS, GU, PIN>: GU is the one-token expert's gate/up, PIN its down
+    m = re.search(r"k_xgemv1ILi\d+ELi\d+ELb([01])ELb([01])E", name) or \
+        re.search(r"k_xgemv1<\s*\d+,\s*\d+,\s*(true|false),\s*(true|false)", name)
+    if m:
+        gu, pin = m.group(1) in ("1", "true"), m.group(2) in ("1", "true")
+        return "gateup" if gu else ("down" if pin else "other")
     if any(s in name for s in ("xgateup", "pgateup", "dgateup", "decode_gu_act", "gu1s_gemv")):
         return "gateup"
     if any(s in name for s in ("xdown", "pdown", "ddown", "down1c")):
@@ -415,8 +421,8 @@ def bench_layer(args, ctx, hip, cfg, pool_gb):
         "router_exact_recomputes": int(prof["ambiguous"]),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
 # ---- prefill (c4) ------------------------------------------------------------------------------
@@ -468,7 +474,10 @@ def bench_prefill(args, ctx, hip, cfg, pool_gb):
                 "mfma_util": round(dn_flops / (dn[2] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline_prefill(cfg, args.seed, xs[warm].cpu().numpy(), nexp * (per_gu + per_dn))
+        call(warm)  # the sampled call once more, its output kept for the comparison
+        ctx.sync()
+        cpu = cpu_baseline_prefill(cfg, args.seed, xs[warm].cpu().numpy(), nexp * (per_gu + per_dn),
+                                   gpu_out=out.cpu().numpy())
     res = {
         "metric": "MoE-layer prefill us/call (512 tokens) + grouped-GEMM HBM GB/s and MFMA utilisation, MXFP4",
         "value": round(us_call, 1), "unit": "us/call", "n_gpus": 1, "steps": steps, "warmup": warm,
@@ -484,15 +493,15 @@ def bench_prefill(args, ctx, hip, cfg, pool_gb):
         "kernels": kernels_json(rows),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
-def cpu_baseline_prefill(cfg, seed, x, bytes_per_call):
+def cpu_baseline_prefill(cfg, seed, x, bytes_per_call, gpu_out=None):
     """The whole 512-token call on the host (the oracle's SIMD tier, the reference's order: every
     unique expert once over its tokens, the shared expert, the combine), experts generated first
-    (not timed). One call; its working set (every expert, 13.7 GB) is far past any cache, so warm
-    and cold coincide and one run is reported."""
+    (not timed), warm (right after generation) and cold (256 MiB written first). gpu_out: the device
+    output of the same call, for rel_l2_vs_gpu (bf16 prefill against the fp32 reference order)."""
     from oracle import oracle as O
     from oracle.workload import HostLayer
     info = cpu_info()
@@ -505,13 +514,23 @@ def cpu_baseline_prefill(cfg, seed, x, bytes_per_call):
     gen_s = time.perf_counter() - t0
     lay = host._layer()
     t0 = time.perf_counter()
-    lay.forward(x, S, simd=True)
+    out, _, _ = lay.forward(x, S, simd=True)
     us = (time.perf_counter() - t0) * 1e6
-    log(f"[bench] cpu prefill: {us / 1e3:.0f} ms per call ({len(host.experts)} experts generated in {gen_s:.0f} s)")
-    return cpu_line(us, None, "us/call", bytes_per_call, info, "port",
-                    f"one {S}-token call of {cfg.name} ({len(host.experts)} unique experts + shared), "
-                    f"{simd_tier(O)} tier of the reference's matmul_mxfp4 restated in C, rows in parallel on "
-                    f"{info['threads']} threads")
+    Evictor()()  # cold: 256 MiB written first (the reference's cold benchmark, benches/kernels.rs:355-383)
+    t0 = time.perf_counter()
+    lay.forward(x, S, simd=True)
+    us_cold = (time.perf_counter() - t0) * 1e6
+    log(f"[bench] cpu prefill: {us / 1e3:.0f} ms per call warm, {us_cold / 1e3:.0f} cold "
+        f"({len(host.experts)} experts generated in {gen_s:.0f} s)")
+    res = cpu_line(us, us_cold, "us/call", bytes_per_call, info, "port",
+                   f"one {S}-token call of {cfg.name} ({len(host.experts)} unique experts + shared), warm and "
+                   f"cold, {simd_tier(O)} tier of the reference's matmul_mxfp4 restated in C, rows in parallel on "
+                   f"{info['threads']} threads")
+    if gpu_out is not None:
+        g = np.asarray(gpu_out, np.float64).ravel()
+        c = np.asarray(out, np.float64).ravel()
+        res["rel_l2_vs_gpu"] = float(np.linalg.norm(g - c) / np.linalg.norm(c))
+    return res
 
 
 # ---- one expert (c0) and bare matrices (mm) ------------------------------------------------------
@@ -611,8 +630,8 @@ def bench_c0(args, ctx, hip, cfg):
         "kernels": kernels_json(rows),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
 def bench_mm(args, ctx, hip):
@@ -711,8 +730,8 @@ def bench_mm(args, ctx, hip):
                                    f"written before each call",
                          "cpu": info},
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
 # ---- K3 latent MoE (k3l) and the sublayer (c1s) -------------------------------------------------
@@ -817,8 +836,8 @@ def bench_latent(args, ctx, hip, cfg):
         "kernels": kernels_json(rows),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
 def bench_sublayer(args, ctx, hip, cfg):
@@ -885,8 +904,8 @@ def bench_sublayer(args, ctx, hip, cfg):
         "kernels": kernels_json(rows),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
 
 
 def bench_mix(args, ctx, hip):
@@ -997,8 +1016,40 @@ def bench_mix(args, ctx, hip):
         "kernels": dict(kernels_json(tab), **kernels_json(tab2)),
         "cpu_baseline": cpu,
     }
-    print(json.dumps(res), flush=True)
     ctx.close()
+    return res
+
+
+def run_config(args, name, hip):
+    """One configuration's result dict (its own context: the pool of one config at a time)."""
+    import rabbit_amd as R
+    import rabbit_amd.workloads as W
+    ctx = R.Context(0)
+    if name == "c1s":
+        return bench_sublayer(args, ctx, hip, W.CONFIGS["c1"])
+    if name == "mm":
+        return bench_mm(args, ctx, hip)
+    if name == "mix":
+        return bench_mix(args, ctx, hip)
+    cfg = W.CONFIGS[name]
+    if name == "k3l":
+        return bench_latent(args, ctx, hip, cfg)
+    if name == "c0":
+        return bench_c0(args, ctx, hip, cfg)
+    t0 = time.perf_counter()
+    W.build_layer(ctx, cfg, layer=0, seed=args.seed)
+    pool_gb = ctx.pool_resident_bytes() / 1e9
+    log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
+    if name == "c4":
+        return bench_prefill(args, ctx, hip, cfg, pool_gb)
+    return bench_layer(args, ctx, hip, cfg, pool_gb)
+
+
+# The other BASELINE configurations, run after the headline line (C1) of a default run, each with a
+# bounded step count of its own and a short CPU-baseline budget: (name, steps, warmup).
+SUB_CONFIGS = [("c0", 128, 16), ("c2", 128, 16), ("c3", 128, 16), ("c4", 8, 2)]
+SUB_KEYS = ("metric", "value", "unit", "steps", "warmup", "dtype", "config", "roofline", "expert_gemv", "call",
+            "us_per_token", "down", "router_exact_recomputes", "cpu_baseline")
 
 
 def main():
@@ -1011,6 +1062,8 @@ def main():
     ap.add_argument("--graph-tokens", type=int, default=64)
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline work")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sub", action="store_true",
+                    help="c1: the headline line only (no c0/c2/c3/c4 sub-results)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a 1 GiB device copy first (reference kernel for the FETCH/WRITE counters)")
     ap.add_argument("--seed", type=int, default=1000)
@@ -1022,8 +1075,6 @@ def main():
         sys.exit(2)
 
     import torch
-    import rabbit_amd as R
-    import rabbit_amd.workloads as W
 
     torch.zeros(1, device="cuda")
     if args.calibrate_copy:
@@ -1034,26 +1085,21 @@ def main():
         b.copy_(a)
         torch.cuda.synchronize()
         del a, b
-    ctx = R.Context(0)
     hip = hip_runtime()
-    if args.config == "c1s":
-        return bench_sublayer(args, ctx, hip, W.CONFIGS["c1"])
-    if args.config == "mm":
-        return bench_mm(args, ctx, hip)
-    if args.config == "mix":
-        return bench_mix(args, ctx, hip)
-    cfg = W.CONFIGS[args.config]
-    if args.config == "k3l":
-        return bench_latent(args, ctx, hip, cfg)
-    if args.config == "c0":
-        return bench_c0(args, ctx, hip, cfg)
-    t0 = time.perf_counter()
-    W.build_layer(ctx, cfg, layer=0, seed=args.seed)
-    pool_gb = ctx.pool_resident_bytes() / 1e9
-    log(f"[bench] {cfg.name}: {cfg.n_experts} experts resident ({pool_gb:.2f} GB) in {time.perf_counter() - t0:.1f}s")
-    if args.config == "c4":
-        return bench_prefill(args, ctx, hip, cfg, pool_gb)
-    return bench_layer(args, ctx, hip, cfg, pool_gb)
+    res = run_config(args, args.config, hip)
+    if args.config == "c1" and not args.no_sub:
+        # compact lines of the other configurations beside the headline (each its own pool)
+        subs = {}
+        for name, steps, warm in SUB_CONFIGS:
+            t0 = time.perf_counter()
+            sa = argparse.Namespace(**vars(args))
+            sa.steps, sa.warmup, sa.cpu_budget = steps, warm, min(args.cpu_budget, 4.0)
+            torch.cuda.empty_cache()
+            r = run_config(sa, name, hip)
+            subs[name] = {k: r[k] for k in SUB_KEYS if k in r}
+            log(f"[bench] sub-result {name}: {r['value']} {r['unit']} ({time.perf_counter() - t0:.1f} s)")
+        res["configs"] = subs
+    print(json.dumps(res), flush=True)
 
 
 if __name__ == "__main__":
