@@ -2657,7 +2657,7 @@ __device__ __forceinline__ void d1_finish(SelLds &L, float (*fold)[2][1024], con
 
 // After the general selection (select3_body, the same in every workgroup), the workgroup's routed
 // pairs: the winners in rank order (L.r_id, left by wave 0 in every workgroup, the publishing one
-// included), their job-table entries from the staged table, nr = kk, nothing pending. Ends with a
+// included), their job-table entries, nr = kk, nothing pending. Ends with a
 // workgroup barrier.
 __device__ __forceinline__ void fallback_pairs(const SelLds &L, PairLds &Q, const RbtExpertDev *__restrict__ tab,
                                                int kk) {
@@ -2694,30 +2694,15 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
   } U;
   __shared__ SelLds S;
   __shared__ PairLds Q;
-  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[64 * MAXM];
   const int t = threadIdx.x, lane = t & 63;
   const bool streamer = blockIdx.x > 0;
   const int E = P.E, kk = min(P.k, P.E);
-  // Everything the selection and the stream need first is in flight together: the key records
-  // (wave 0), the activation, and the whole job table (so a winner's entry is an LDS read).
+  // The key records (wave 0) and the activation are in flight together; the selection loads each
+  // candidate's job-table entry while it certifies.
   float4 rv[MAXM];
   if (t < 64) load_key_recs<MAXM>(rec, E, rv);
   float4 xv[xg_nv<NCH>()];
   xgateup1_load_x<NCH>(xg, xv);
-  constexpr int TQ = (64 * MAXM * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
-  const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
-  rbt_u4 tv[TQ];
-  {
-    const rbt_gu4 *src = (const rbt_gu4 *)G.table;
-#pragma unroll
-    for (int i = 0; i < TQ; i++) tv[i] = src[min(t + 256 * i, n4 - 1)];
-  }
-  {
-    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
-#pragma unroll
-    for (int i = 0; i < TQ; i++)
-      if (t + 256 * i < n4) dst[t + 256 * i] = tv[i];
-  }
   xgateup1_stage_x<NCH>(U.gu, xv);
   // The shared expert's gate/up does not depend on the routing: when every workgroup holds at most
   // two of its 4-row units, each unit is two half units (waves 2j, 2j + 1), whose loads go out now
@@ -2736,11 +2721,11 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
     sh.su = s0 + (t >> 7);
     sh.hf = (t >> 6) & 1;
   }
-  lds_barrier();  // the staged activation and table
+  lds_barrier();  // the staged activation
   if constexpr (NCH % 2 == 0)
     if (t >= 64 && sh.su >= 0) xgateup1_sh_issue<NCH>(sh, shv);
   if (t < 64) {
-    const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
+    const int r = select_pairs<MAXM>(S, Q, P, rv, G.table);
     if (t == 0) Q.status = r;
   }
   if constexpr (NCH % 2 == 0)
@@ -2758,7 +2743,7 @@ __global__ __launch_bounds__(256) void k_xgateup1s(SelParams P, const KeyRec *__
     } else {
       select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
     }
-    fallback_pairs(S, Q, tab, kk);
+    fallback_pairs(S, Q, G.table, kk);
   }
   // A deferred decision: workgroup 0 folds and decides while the others stream every candidate.
   // Otherwise workgroup 0 publishes the routing (the general path already did) and streams its
@@ -2805,27 +2790,13 @@ __global__ __launch_bounds__(256) void k_gu1s_gemv(SelParams P, const KeyRec *__
   __shared__ __attribute__((aligned(16))) float fold[4][2][1024];  // workgroup 0, deferred
   __shared__ SelLds S;
   __shared__ PairLds Q;
-  __shared__ __attribute__((aligned(16))) RbtExpertDev tab[64 * MAXM];
   const int t = threadIdx.x, lane = t & 63;
   const bool streamer = blockIdx.x > 0;
   const int E = P.E, kk = min(P.k, P.E);
   float4 rv[MAXM];
   if (t < 64) load_key_recs<MAXM>(rec, E, rv);
-  {
-    constexpr int TQ = (64 * MAXM * (int)sizeof(RbtExpertDev) / 16 + 255) / 256;
-    const int n4 = E * (int)sizeof(RbtExpertDev) / 16;
-    const rbt_gu4 *src = (const rbt_gu4 *)G.table;
-    rbt_u4 tv[TQ];
-#pragma unroll
-    for (int i = 0; i < TQ; i++) tv[i] = src[min(t + 256 * i, n4 - 1)];
-    rbt_u4 *dst = reinterpret_cast<rbt_u4 *>(tab);
-#pragma unroll
-    for (int i = 0; i < TQ; i++)
-      if (t + 256 * i < n4) dst[t + 256 * i] = tv[i];
-  }
-  lds_barrier();
   if (t < 64) {
-    const int r = select_pairs<MAXM>(S, Q, P, rv, tab);
+    const int r = select_pairs<MAXM>(S, Q, P, rv, G.table);
     if (t == 0) Q.status = r;
   }
   lds_barrier();
@@ -2838,7 +2809,7 @@ __global__ __launch_bounds__(256) void k_gu1s_gemv(SelParams P, const KeyRec *__
     } else {
       select3_body<MAXM>(S, P, mid, bnd, Q.fb_ids, Q.fb_w, nullptr, nullptr, G, 0, 0);
     }
-    fallback_pairs(S, Q, tab, kk);
+    fallback_pairs(S, Q, G.table, kk);
   }
   const bool pending = st == 2;
   const int nr = Q.T.nr;
