@@ -2014,13 +2014,16 @@ __device__ __forceinline__ int select_pairs(SelLds &L, PairLds &Q, const SelPara
   uint32_t cur = 0;
 #pragma unroll
   for (int m = 0; m < MAXM; m++) cur = max(cur, ku[m]);
+  // M: the kk-th largest of the lanes' largest keys (with multiplicity), found bit by bit as the
+  // largest value that at least kk of them reach; every expert at or above it is a candidate (at
+  // least kk of them, so every winner is one)
   uint32_t M = 0;
-  for (int r = 0; r < kk; r++) {
-    M = rbt_wave_max_u(cur);
-    const unsigned long long hit = __ballot(cur == M);
-    if (lane == __ffsll((unsigned long long)hit) - 1) cur = 0;
+#pragma unroll
+  for (int b = 31; b >= 0; b--) {
+    const uint32_t c = M | (1u << b);
+    if (__popcll(__ballot(cur >= c)) >= kk) M = c;
   }
-  if (M == 0) return 0;  // a key maps to 0 (a NaN)
+  if (M == 0) return 0;  // a key maps to 0 (a NaN), or fewer than kk experts
   int nc = 0;
 #pragma unroll
   for (int m = 0; m < MAXM; m++) nc += __popcll(__ballot(ku[m] >= M));
@@ -2083,12 +2086,27 @@ __device__ __forceinline__ int select_pairs(SelLds &L, PairLds &Q, const SelPara
     if (!((cm >> m) & 1u) && ku[m] != 0 && klo[m] != khi[m] && khi[m] >= lo_sel) nflag |= 1u << m;
   const bool cexact = clo == chi;
   bool cflag = cand && !cexact && (iw ? clo <= hi_uns : chi >= lo_sel);
-  // order: every pair of winners strictly ordered, or both exact
-  for (int j = 0; j < nc; j++) {
-    const int rj = __builtin_amdgcn_readlane(rank, j);
-    const float lj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(clo), j));
-    const float hj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(chi), j));
-    if (iw && !cexact && rj < kk && rj != rank) cflag |= !(rj < rank ? lj > chi : clo > hj);
+  // order: every pair of winners strictly ordered, or both exact. The winners are ranked by their
+  // midpoint keys, which their intervals hold, so that holds iff it holds for each winner and the
+  // next one in rank order; only when some adjacent pair fails does the pairwise scan run, which
+  // flags every non-exact winner that overlaps another.
+  if (iw) {
+    L.r_lo[rank] = clo;
+    L.r_hi[rank] = chi;
+  }
+  __builtin_amdgcn_wave_barrier();
+  bool bad = false;
+  if (iw && rank + 1 < kk) {
+    const float nlo = L.r_lo[rank + 1], nhi = L.r_hi[rank + 1];
+    bad = !(cexact && nlo == nhi) && !(clo > nhi);
+  }
+  if (__ballot(bad) != 0) {
+    for (int j = 0; j < nc; j++) {
+      const int rj = __builtin_amdgcn_readlane(rank, j);
+      const float lj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(clo), j));
+      const float hj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(chi), j));
+      if (iw && !cexact && rj < kk && rj != rank) cflag |= !(rj < rank ? lj > chi : clo > hj);
+    }
   }
   D1Task &T = Q.T;
   auto task = [&](int slot, int id, uint32_t key, float logit, int flag) {
