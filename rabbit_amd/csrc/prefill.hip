@@ -754,7 +754,10 @@ __device__ __forceinline__ void pd_units(const PTile *__restrict__ tiles, const 
   }
 }
 
-// Gate/up: hb3 [3 pairs, I] bf16 (h parts). Row blocks of 64 rows (RB = I / 64).
+// Gate/up: hb3 [3 pairs, I] bf16 (h parts). Row blocks of 64 rows (RB = I / 64). Three workgroups
+// per CU (52 KB of LDS, four waves each): a workgroup keeps one K group of its rows in flight, so
+// the chip's loads in flight grow with the workgroups per CU (C3: 90 -> 79 us per call against one
+// per CU; two per CU balance no better than one).
 __global__ __launch_bounds__(256) void k_dgateup(const PTile *__restrict__ tiles, const int *__restrict__ ntiles,
                                                  const PSeg *__restrict__ segs, const RbtExpertDev *__restrict__ table,
                                                  const RbtExpertDev *__restrict__ shared_dev,
@@ -827,7 +830,7 @@ hipError_t launch_dgateup(const Ctx &c, const PTile *tiles, const int *ntiles, c
                           const RbtExpertDev *table, const RbtExpertDev *shared_dev, const int *pair_tok,
                           const __bf16 *xb3, int S, int H, int I, __bf16 *hb3) {
   if (H % 512 || I % 64) return hipErrorInvalidValue;
-  launch_k(c, k_dgateup, dim3(c.num_cu), dim3(256), tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H,
+  launch_k(c, k_dgateup, dim3(3 * c.num_cu), dim3(256), tiles, ntiles, segs, table, shared_dev, pair_tok, xb3, S, H,
            I, hb3);
   return hipGetLastError();
 }
