@@ -614,6 +614,7 @@ constexpr int XD2_NW = 8;     // waves per workgroup
 constexpr int XD2_NP = 2;     // pairs whose h a workgroup stages
 constexpr int XD2_TB = 16;    // output tiles per block of the fused combine (64 rows)
 constexpr int XD2_MAXB = 32;  // blocks one workgroup can complete
+constexpr int XD2_MAXU = (XD2_MAXB - 4) * XD2_TB;  // most units of one workgroup (xdown2_ok)
 constexpr int XC1_MAXP = 64;  // pairs of the combine
 constexpr bool XD2_FUSED = true;  // the combine in the down launch (else k_combine1)
 
@@ -636,6 +637,7 @@ __global__ __launch_bounds__(64 * XD2_NW) void k_xdown2(const RbtExpertDev *__re
   __shared__ float pw[XC1_MAXP];  // FC: the combine's pair weights and liveness
   __shared__ int plive[XC1_MAXP];
   __shared__ int lastb[XD2_MAXB], nlast;
+  __shared__ float yl[FC ? 4 * XD2_MAXU : 1];  // FC: the row sums of the workgroup's units [b0, b1)
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, col = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rho = col >> 2, kap = col & 3;
@@ -769,11 +771,10 @@ __global__ __launch_bounds__(64 * XD2_NW) void k_xdown2(const RbtExpertDev *__re
         const float y = row_dot(acc, col);
         if (col == 0) {
           const float yv = (lq == 0 ? live[0] : live[1]) ? y : 0.0f;
-          float *dst = yy + (long)pl_of(q) * H + 4 * tl + g;
           if constexpr (FC)
-            __hip_atomic_store(dst, yv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // at the device's coherence point
+            yl[4 * (u - b0) + g] = yv;  // written to yy in one pass after the stream
           else
-            *dst = yv;
+            yy[(long)pl_of(q) * H + 4 * tl + g] = yv;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -791,7 +792,15 @@ __global__ __launch_bounds__(64 * XD2_NW) void k_xdown2(const RbtExpertDev *__re
     // coherence (no cache of one XCD holds them), so no cache-wide write-back or invalidate is
     // needed: a row store completes (vmcnt 0) before the counter add that announces it, and the
     // combine reads after its add has seen every announcement.
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's rows of yy are complete
+    // The workgroup's rows of yy leave in one coalesced pass (device-scope stores inside the stream
+    // loop, one per unit, slowed the weight stream by about a tenth).
+    __syncthreads();
+    for (int e = tid; e < 4 * (b1 - b0); e += 64 * XD2_NW) {
+      const int u = b0 + (e >> 2), q = u / nt, tl = u - q * nt;
+      __hip_atomic_store(yy + (long)pl_of(q) * H + 4 * tl + (e & 3), yl[e], __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);  // at the device's coherence point
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's rows of yy are complete
     if (w == 1 && lane < npairs) {
       asm volatile("" : "+v"(f_dd), "+v"(f_ds), "+v"(f_w), "+v"(f_s));  // used here, so waited for here
       plive[lane] = f_dd != 0 && f_ds != 0;
@@ -887,7 +896,7 @@ bool xdown2_ok(int npairs, size_t i, int H, int num_cu) {
   const long U = (long)npairs * (H / 4), per = (U + num_cu - 1) / num_cu;
   // a workgroup's run spans at most two pairs; the fused combine's blocks: its counters, and the
   // blocks a workgroup can complete
-  return per <= H / 4 && (H / 4 + XD2_TB - 1) / XD2_TB <= CNT_N && per / XD2_TB + 4 <= XD2_MAXB;
+  return per <= H / 4 && per <= XD2_MAXU && (H / 4 + XD2_TB - 1) / XD2_TB <= CNT_N && per / XD2_TB + 4 <= XD2_MAXB;
 }
 
 hipError_t launch_xdown2(const Ctx &c, const RbtExpertDev *down_job, const int *down_slot, int kk, const __bf16 *hp,
