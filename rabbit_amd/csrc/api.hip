@@ -700,9 +700,10 @@ constexpr int DECODE_MAX_S = 16;  // tokens per call up to which MXFP4 layers ke
 
 // A few tokens (MXFP4, fp32-accurate): grouped by expert as in prefill, every unique expert's
 // weights streamed once for all its tokens, each token's activation as three exact bf16 parts.
+// xb3: the tokens' three-part split when the router launch already wrote it (else null: split here).
 int decode_grouped_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E, int H, int I, const int32_t *ids,
                        const float *wts, const float *shs, int *ptok, int *tpair, float *tw, float *h, float *yy,
-                       bool gated, float *out, hipEvent_t *ev) {
+                       bool gated, float *out, hipEvent_t *ev, __bf16 *xb3_done = nullptr) {
   const rbt_moe_layer_desc &D = L.desc;
   const int has_shared = D.has_shared ? 1 : 0;
   const long W = (S + 31) / 32;
@@ -717,13 +718,13 @@ int decode_grouped_dev(rbt_ctx *c, Layer &L, const float *x, int S, int k, int E
   rbt::PSeg *segs = reinterpret_cast<rbt::PSeg *>(b + off_segs);
   rbt::PTile *tiles = reinterpret_cast<rbt::PTile *>(b + off_tiles);
   int *ntiles = reinterpret_cast<int *>(b + off_nt);
-  __bf16 *xb3;
-  RBT_TRY(scratch_t(c, SC_XB, (size_t)3 * S * H, &xb3));
+  __bf16 *xb3 = xb3_done;
+  if (!xb3) RBT_TRY(scratch_t(c, SC_XB, (size_t)3 * S * H, &xb3));
   __bf16 *hb3 = reinterpret_cast<__bf16 *>(h);  // [3 (S*k + S), I] bf16 fits the fp32 h scratch (2 I floats per pair)
   int *dflags = c->d_flags;
   HIP_OK(c, rbt::launch_pgroup(*c, ids, wts, S, k, E, has_shared, L.d_table, bits, pc, segs, tiles, ntiles, ptok,
                                tpair, tw, dflags + FLAG_ERR, dflags + FLAG_UNIQ, rbt::PD_TCH));
-  HIP_OK(c, rbt::launch_split3(*c, x, S, H, xb3));
+  if (!xb3_done) HIP_OK(c, rbt::launch_split3(*c, x, S, H, xb3));
   if (ev) HIP_OK(c, hipEventRecord(ev[1], c->stream));
   if (ev) c->t_start = ev[2], c->t_stop = ev[3];
   const hipError_t e1 = rbt::launch_dgateup(*c, tiles, ntiles, segs, L.d_table, L.d_shared, ptok, xb3, S, H, I, hb3);
@@ -839,6 +840,11 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     ga.shared_slot = sh_slot;
   }
   float *rec = nullptr;
+  // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores; a few tokens
+  // (decode batches) as the fp32-accurate grouped decode GEMMs.
+  const bool dgrouped = S > 1 && S <= DECODE_MAX_S && (merge || !D.has_shared) &&
+                        rbt::dgemm_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
+  __bf16 *xb3_sel = nullptr;  // the split the batch router's selection writes
   // the sublayer's norm: in the one-token router launch (every workgroup normalises the token for its
   // rows, workgroup 0 writes xn), else as its own launch
   const bool fold_norm = norm_w && r1 && ((uintptr_t)xraw | (uintptr_t)norm_w) % 16 == 0;
@@ -879,8 +885,10 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router1(*c, rr, sgate, mid, bnd, shs, rec, fold_norm ? norm_w : nullptr, eps,
                                   fold_norm ? xn : nullptr));
   } else if (!rbt::router_exact_ok(S, H) && rbt::router_batch_ok(ra) && (uintptr_t)(sgate ? sgate : x) % 16 == 0) {
-    // a decode batch: certified intervals for every (row, token), then the per-token selection
-    HIP_OK(c, rbt::launch_router_batch(*c, ra, sgate, mid, bnd, L.d_table, ids, wts, shs, dflags + FLAG_AMB));
+    // a decode batch: certified intervals for every (row, token), then the per-token selection (whose
+    // idle waves split the tokens for the grouped decode GEMMs)
+    if (dgrouped && (uintptr_t)x % 16 == 0 && H % 4 == 0) RBT_TRY(scratch_t(c, SC_XB, (size_t)3 * S * H, &xb3_sel));
+    HIP_OK(c, rbt::launch_router_batch(*c, ra, sgate, mid, bnd, L.d_table, ids, wts, shs, dflags + FLAG_AMB, xb3_sel));
   } else {
     const bool al16 = ((uintptr_t)x | (uintptr_t)D.router | (uintptr_t)(sgate ? sgate : x)) % 16 == 0;
     if (rbt::router_exact_ok(S, H) && rbt::router_bounded_ok(ra) && al16) {
@@ -901,15 +909,11 @@ int moe_forward_dev(rbt_ctx *c, uint32_t layer, const float *x, size_t s, float 
     HIP_OK(c, rbt::launch_router_select(*c, ra, mid, bnd, ids, wts, shs, dflags + FLAG_AMB,
                                         grp_in_select ? &ga : nullptr, sh_in_select ? &sgu : nullptr));
   }
-  // Larger MXFP4 batches (prefill) run as grouped GEMMs on the matrix cores; a few tokens
-  // (decode batches) as the fp32-accurate grouped decode GEMMs.
-  const bool dgrouped = S > 1 && S <= DECODE_MAX_S && (merge || !D.has_shared) &&
-                        rbt::dgemm_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
   const bool grouped = !dgrouped && !mfma && S > 1 && (merge || !D.has_shared) &&
                        rbt::prefill_ok(L.routed_kind, H, I, (size_t)E, (size_t)k);
   if (dgrouped) {
     RBT_TRY(decode_grouped_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, dst,
-                               c->prof ? ev.data() : nullptr));
+                               c->prof ? ev.data() : nullptr, xb3_sel));
   } else if (grouped) {
     RBT_TRY(prefill_dev(c, L, x, S, k, E, H, I, ids, wts, shs, ptok, tpair, tw, h, yy, gated, dst,
                         c->prof ? ev.data() : nullptr));

@@ -270,8 +270,11 @@ bool router1_ok(const RouterArgs &a, int num_cu, const SharedGateUp *sgu);
 // path, the general path where it does not certify). table: the layer's job table (the fast path
 // reads winners' entries).
 bool router_batch_ok(const RouterArgs &a);
+// xb3 (optional, [3 S, H] bf16): the tokens' exact three-part bf16 split, written by the selection
+// launch's idle waves (the grouped decode GEMMs' activation)
 hipError_t launch_router_batch(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                               const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats);
+                               const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats,
+                               __bf16 *xb3 = nullptr);
 hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
                           float *sh_scale, void *rec, const float *nw = nullptr, float eps = 0.0f,
                           float *xn = nullptr);

@@ -2510,7 +2510,8 @@ __global__ __launch_bounds__(256) void k_router_select_rec(SelParams P, const do
                                                            const double *__restrict__ bnd,
                                                            const RbtExpertDev *__restrict__ table,
                                                            int32_t *__restrict__ ids, float *__restrict__ wts,
-                                                           float *__restrict__ sh_scale, int *__restrict__ stats) {
+                                                           float *__restrict__ sh_scale, int *__restrict__ stats,
+                                                           __bf16 *__restrict__ xb3) {
   __shared__ SelLds L;
   __shared__ PairLds Q;
   __shared__ __attribute__((aligned(16))) float4 kr[64 * MAXM];
@@ -2541,6 +2542,23 @@ __global__ __launch_bounds__(256) void k_router_select_rec(SelParams P, const do
       if (lane == 0 && sh_scale) sh_scale[s] = (P.erows > E) ? sigmoid_ref(__double2float_rn(ms[E])) : 1.0f;
     }
     if (lane == 0) Q.status = r;
+  } else if (xb3 != nullptr) {
+    // waves 1-3 meanwhile: the token's three exact bf16 parts for the grouped decode GEMMs (x = hi +
+    // mid + lo, each the bf16 rounding of the remainder; rows 3 s + part of xb3)
+    const int H = P.H;
+    const float4 *x4 = reinterpret_cast<const float4 *>(P.x + (size_t)s * H);
+    __bf16 *o0 = xb3 + (size_t)(3 * s) * H, *o1 = o0 + H, *o2 = o1 + H;
+    for (int q = t - 64; q < H / 4; q += 192) {
+      const float4 v = x4[q];
+      const float e4[4] = {v.x, v.y, v.z, v.w};
+      __bf16 hh[4], mm[4], ll[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) split3(e4[e], hh[e], mm[e], ll[e]);
+      typedef __bf16 b4v __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<b4v *>(o0 + 4 * q) = b4v{hh[0], hh[1], hh[2], hh[3]};
+      *reinterpret_cast<b4v *>(o1 + 4 * q) = b4v{mm[0], mm[1], mm[2], mm[3]};
+      *reinterpret_cast<b4v *>(o2 + 4 * q) = b4v{ll[0], ll[1], ll[2], ll[3]};
+    }
   }
   __syncthreads();
   if (Q.status != 1) select3_body<MAXM, true>(L, P, mid, bnd, ids, wts, sh_scale, stats, GroupOut{}, 0, s, kbuf);
@@ -2871,20 +2889,22 @@ bool router_batch_ok(const RouterArgs &a) {
 }
 
 hipError_t launch_router_batch(const Ctx &c, const RouterArgs &a, const float *sgate, double *mid, double *bnd,
-                               const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats) {
+                               const RbtExpertDev *table, int32_t *ids, float *wts, float *sh_scale, int *stats,
+                               __bf16 *xb3) {
   if (!router_batch_ok(a) || (sgate && (uintptr_t)sgate % 16 != 0) || !table) return hipErrorInvalidValue;
+  if (xb3 && ((uintptr_t)a.x % 16 != 0 || (uintptr_t)xb3 % 8 != 0 || a.H % 4 != 0)) return hipErrorInvalidValue;
   const SelParams P = sel_params(a);
   launch_k(c, k_router_logits_t1, dim3(a.erows, a.S), dim3(256), a.x, a.S, a.H, a.W, a.E, sgate, mid, bnd, a.erows);
   const int m = (a.E + 63) / 64;
   if (m <= 4)
     launch_k(c, k_router_select_rec<4>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table, ids,
-             wts, sh_scale, stats);
+             wts, sh_scale, stats, xb3);
   else if (m <= 8)
     launch_k(c, k_router_select_rec<8>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table, ids,
-             wts, sh_scale, stats);
+             wts, sh_scale, stats, xb3);
   else
     launch_k(c, k_router_select_rec<16>, dim3(a.S), dim3(256), P, (const double *)mid, (const double *)bnd, table,
-             ids, wts, sh_scale, stats);
+             ids, wts, sh_scale, stats, xb3);
   return hipGetLastError();
 }
 
