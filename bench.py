@@ -1094,6 +1094,7 @@ def main():
             t0 = time.perf_counter()
             sa = argparse.Namespace(**vars(args))
             sa.steps, sa.warmup, sa.cpu_budget = steps, warm, min(args.cpu_budget, 4.0)
+            sa.config = name  # its own metric name and traffic file
             torch.cuda.empty_cache()
             r = run_config(sa, name, hip)
             subs[name] = {k: r[k] for k in SUB_KEYS if k in r}
