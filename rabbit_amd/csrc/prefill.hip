@@ -361,7 +361,7 @@ constexpr int pf_lds_bytes(int NM, int NTV, int TILES) {
 // activation: NM = 2 writes h as three bf16 parts (rows 3 pair + part of hb), NM = 1 writes y.
 // rbs: row blocks between a workgroup's consecutive blocks (PF_RBG for prefill, 1 for decode).
 // lds: pf_lds_bytes(NM, NTV, TILES) bytes of LDS.
-template <int NM, int NTV, int TILES, bool DEC = false>
+template <int NM, int NTV, int TILES, bool DEC = false, bool SL = false>
 __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&src)[NTV], const uint8_t *const (&a)[NM],
                                         const uint8_t *const (&sc)[NM], long rowb, long rows, int rb0, int per,
                                         int nsteps, int out_cols, __bf16 *__restrict__ hb, float *__restrict__ y,
@@ -374,7 +374,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
   if (total <= 0) return;  // no row block for this workgroup (uniform)
   __bf16(*bs)[16 * NTV][PB_STRIDE] = reinterpret_cast<__bf16(*)[16 * NTV][PB_STRIDE]>(lds);
   uint8_t *const wl = lds + 2 * 16 * NTV * PB_STRIDE * 2 + w * (NM * TILES * PW_TILE);  // this wave's area
-  const uint8_t *pa[NM][TILES], *ps[NM][TILES];
+  const uint8_t *pa[NM][TILES], *ps[NM][TILES], *pl[NM][TILES];
 #pragma unroll
   for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -382,7 +382,21 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       const long row0 = (long)rb0 * BR + 16 * TILES * w + 16 * t;  // first row of the tile
       pa[m][t] = a[m] + (row0 + (lane >> 4)) * rowb + 16 * (lane & 15);
       ps[m][t] = sc[m] + (row0 + r) * rows;
+      pl[m][t] = sc[m] + (row0 + (lane >> 2)) * rows + 16 * (lane & 3);
     }
+  // Scale lines: when a row's E8M0 bytes are 64 (K = 2048: four groups), one 16-byte load per lane
+  // and tile (row lane / 4, bytes 16 (lane % 4) .. +15) reads the tile's 16 rows x 64 bytes of the
+  // row block as whole lines, and each group's 16 bytes reach their MFMA lanes by shuffles. Loading
+  // each group's 16 bytes of a row on its own touched every 128-byte line four times, a group
+  // apart, and the weights streaming through the XCD's L2 in between evicted it: four fetches.
+  const bool sline = SL && rows == 64 && nsteps == 4 * G;  // SL: the down GEMMs
+  rbt_u4 sl[NM][TILES];
+  auto sl_load = [&](int rb) {
+#pragma unroll
+    for (int m = 0; m < NM; m++)
+#pragma unroll
+      for (int t = 0; t < TILES; t++) sl[m][t] = *(const rbt_gu4 *)(pl[m][t] + (long)rb * blk_s);
+  };
   // next group to fetch (past the end: the last group again, never used)
   int f_rb = 0, f_s = 0;
   rbt_u4 nw[NM][TILES][4], ns[NM][TILES];
@@ -397,10 +411,12 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
 #pragma unroll
         for (int t = 0; t < TILES; t++)
           nw[m][t][q] = __builtin_nontemporal_load((const rbt_gu4 *)(pa[m][t] + oa + 4 * q * rowb));
+    if (!sline) {
 #pragma unroll
-    for (int m = 0; m < NM; m++)
+      for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int t = 0; t < TILES; t++) ns[m][t] = *(const rbt_gu4 *)(ps[m][t] + os);
+        for (int t = 0; t < TILES; t++) ns[m][t] = *(const rbt_gu4 *)(ps[m][t] + os);
+    }
     f_s += G;
     if (f_s == nsteps) {
       f_s = 0;
@@ -422,6 +438,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
     pf_stage_load<NTV>(s0, src, 0);
 #pragma unroll
     for (int d = 0; d < G; d++) stage_next(st[(d + 1) % G]);
+    if (sline) sl_load(0);
     fetch_group();
     pf_stage_store<NTV>(s0, bs[0]);
   }
@@ -436,12 +453,24 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
   int c_rb = 0, c_s = 0;  // group being computed
   for (int it0 = 0; it0 < total; it0 += G) {
     rbt_u4 cs[NM][TILES];
+    if (sline) {
+      // this group's 16 bytes of row r: lane 4 r + group holds them; the next row block's line
+      // goes out once the last group's bytes are taken
+      const int gq = c_s / G, src = 4 * r + gq;
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+#pragma unroll
+        for (int t = 0; t < TILES; t++)
+          cs[m][t] = rbt_u4{(uint32_t)__shfl((int)sl[m][t].x, src, 64), (uint32_t)__shfl((int)sl[m][t].y, src, 64),
+                            (uint32_t)__shfl((int)sl[m][t].z, src, 64), (uint32_t)__shfl((int)sl[m][t].w, src, 64)};
+      if (gq == 3 && c_rb + 1 < per) sl_load(c_rb + 1);
+    }
     // the group loaded a group ago -> this wave's LDS area (rows at PW_STRIDE)
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
       for (int t = 0; t < TILES; t++) {
-        cs[m][t] = ns[m][t];
+        if (!sline) cs[m][t] = ns[m][t];
         uint8_t *wt = wl + (m * TILES + t) * PW_TILE + (lane >> 4) * PW_STRIDE + 16 * (lane & 15);
 #pragma unroll
         for (int q = 0; q < 4; q++) *reinterpret_cast<rbt_u4 *>(wt + 4 * q * PW_STRIDE) = nw[m][t][q];
@@ -655,15 +684,15 @@ __global__ __launch_bounds__(256) void k_pdown(const PTile *__restrict__ tiles, 
   switch (nt) {
     case 1: {
       const __bf16 *src[1] = {src_of(0)};
-      pf_gemm<1, 1, 4>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, lds, PF_DN_RBG);
+      pf_gemm<1, 1, 4, false, true>(T, src, a, sc, rowb, rows, gi, per_of(256), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
     case 2: {
       const __bf16 *src[2] = {src_of(0), src_of(1)};
-      pf_gemm<1, 2, 2>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, lds, PF_DN_RBG);
+      pf_gemm<1, 2, 2, false, true>(T, src, a, sc, rowb, rows, gi, per_of(128), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
     default: {
       const __bf16 *src[4] = {src_of(0), src_of(1), src_of(2), src_of(3)};
-      pf_gemm<1, 4, 1>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, lds, PF_DN_RBG);
+      pf_gemm<1, 4, 1, false, true>(T, src, a, sc, rowb, rows, gi, per_of(64), nsteps, H, nullptr, y, lds, PF_DN_RBG);
     } break;
   }
 }
@@ -743,7 +772,7 @@ __device__ __forceinline__ void pd_units(const PTile *__restrict__ tiles, const 
     if (GATEUP)                                                                                               \
       pf_gemm<2, NTV_, TILES, true>(T, src, ga, gs, rowb, rows, rb0, per, nsteps, O, hb3, nullptr, lds, 1);   \
     else                                                                                                      \
-      pf_gemm<1, NTV_, TILES, true>(T, src, da, ds, rowb, rows, rb0, per, nsteps, O, nullptr, y, lds, 1);     \
+      pf_gemm<1, NTV_, TILES, true, true>(T, src, da, ds, rowb, rows, rb0, per, nsteps, O, nullptr, y, lds, 1);     \
   }
     if (nt == 1)
       RBT_PD(1)
