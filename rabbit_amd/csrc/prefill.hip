@@ -384,18 +384,19 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
       ps[m][t] = sc[m] + (row0 + r) * rows;
       pl[m][t] = sc[m] + (row0 + (lane >> 2)) * rows + 16 * (lane & 3);
     }
-  // Scale lines: when a row's E8M0 bytes are 64 (K = 2048: four groups), one 16-byte load per lane
-  // and tile (row lane / 4, bytes 16 (lane % 4) .. +15) reads the tile's 16 rows x 64 bytes of the
-  // row block as whole lines, and each group's 16 bytes reach their MFMA lanes by shuffles. Loading
-  // each group's 16 bytes of a row on its own touched every 128-byte line four times, a group
-  // apart, and the weights streaming through the XCD's L2 in between evicted it: four fetches.
-  const bool sline = SL && rows == 64 && nsteps == 4 * G;  // SL: the down GEMMs
+  // Scale lines: a row's E8M0 bytes for four groups (2048 columns) are 64 contiguous bytes. One
+  // 16-byte load per lane and tile (row lane / 4, bytes 16 (lane % 4) .. +15 of the line) reads the
+  // tile's 16 rows x 64 bytes at once, and each group's 16 bytes reach their MFMA lanes by shuffles.
+  // Loading each group's 16 bytes of a row on its own touches every line four times, a group apart.
+  const int nlines = nsteps / (4 * G);  // lines per row of a row block
+  const bool sline = SL && nsteps % (4 * G) == 0 && rows == 64 * nlines;  // SL: the down GEMMs (the gate/up ones
+  // have no registers to spare at their occupancy)
   rbt_u4 sl[NM][TILES];
-  auto sl_load = [&](int rb) {
+  auto sl_load = [&](int rb, int j) {
 #pragma unroll
     for (int m = 0; m < NM; m++)
 #pragma unroll
-      for (int t = 0; t < TILES; t++) sl[m][t] = *(const rbt_gu4 *)(pl[m][t] + (long)rb * blk_s);
+      for (int t = 0; t < TILES; t++) sl[m][t] = *(const rbt_gu4 *)(pl[m][t] + (long)rb * blk_s + 64 * j);
   };
   // next group to fetch (past the end: the last group again, never used)
   int f_rb = 0, f_s = 0;
@@ -438,7 +439,7 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
     pf_stage_load<NTV>(s0, src, 0);
 #pragma unroll
     for (int d = 0; d < G; d++) stage_next(st[(d + 1) % G]);
-    if (sline) sl_load(0);
+    if (sline) sl_load(0, 0);
     fetch_group();
     pf_stage_store<NTV>(s0, bs[0]);
   }
@@ -456,14 +457,20 @@ __device__ __forceinline__ void pf_gemm(const PfTile &T, const __bf16 *const (&s
     if (sline) {
       // this group's 16 bytes of row r: lane 4 r + group holds them; the next row block's line
       // goes out once the last group's bytes are taken
-      const int gq = c_s / G, src = 4 * r + gq;
+      const int gq = c_s / G, src = 4 * r + (gq & 3);
 #pragma unroll
       for (int m = 0; m < NM; m++)
 #pragma unroll
         for (int t = 0; t < TILES; t++)
           cs[m][t] = rbt_u4{(uint32_t)__shfl((int)sl[m][t].x, src, 64), (uint32_t)__shfl((int)sl[m][t].y, src, 64),
                             (uint32_t)__shfl((int)sl[m][t].z, src, 64), (uint32_t)__shfl((int)sl[m][t].w, src, 64)};
-      if (gq == 3 && c_rb + 1 < per) sl_load(c_rb + 1);
+      if ((gq & 3) == 3) {
+        const int j = (gq >> 2) + 1;
+        if (j < nlines)
+          sl_load(c_rb, j);
+        else if (c_rb + 1 < per)
+          sl_load(c_rb + 1, 0);
+      }
     }
     // the group loaded a group ago -> this wave's LDS area (rows at PW_STRIDE)
 #pragma unroll
