@@ -352,16 +352,24 @@ def bench_layer(args, ctx, hip, cfg, pool_gb):
     log(f"[bench] {cfg.name}: timed {steps} tokens ({calls} calls): wall {wall * 1e3:.2f} ms "
         f"({us_tok:.2f} us/token), events {ev_ms:.2f} ms")
 
-    # eager passes: per-kernel durations, then the phase profile (streamed experts, exact folds)
+    # eager passes: the same calls without graphs (no profiling: the wall time per token, and the
+    # host's time to issue them, C-ABI call through ctypes included), then per-kernel durations,
+    # then the phase profile (streamed experts, exact folds)
+    ctx.sync()
+    t1 = time.perf_counter()
+    for c in range(wcalls, ncalls):
+        call(c)
+    t_issue = time.perf_counter() - t1
+    ctx.sync()
+    eager_us = (time.perf_counter() - t1) / steps * 1e6
+    issue_us = t_issue / calls * 1e6
     tab = kernel_table(ctx, lambda: [call(c) for c in range(wcalls, ncalls)])
     rows = per_call(tab, calls)
     ctx.profile_read(reset=True)
     ctx.profile_enable(True)
-    t1 = time.perf_counter()
     for c in range(wcalls, ncalls):
         call(c)
     ctx.sync()
-    eager_us = (time.perf_counter() - t1) / steps * 1e6
     prof = ctx.profile_read(reset=True)
     ctx.profile_enable(False)
     ids_np = ids_all.cpu().numpy().reshape(ncalls, S * k)[wcalls:]
@@ -418,6 +426,7 @@ def bench_layer(args, ctx, hip, cfg, pool_gb):
                  "note": "router + unique experts + shared expert + x/out over the whole call"},
         "kernels": kernels_json(rows),
         "eager_us_per_token": round(eager_us, 2),
+        "host_issue_us_per_call": round(issue_us, 2),
         "router_exact_recomputes": int(prof["ambiguous"]),
         "cpu_baseline": cpu,
     }

@@ -319,9 +319,12 @@ def test_moe_decode_grouped(ctx, orc, family, gated, lb, S, E, k):
 
 def test_moe_prefill_c4_full(ctx, orc):
     """C4: 512-token prefill of the Qwen3.8-shaped layer, all 512 experts resident. Ids of every
-    token bit-exact against the oracle's sequential-fp32 router; outputs of a token sample (each
-    token's row depends only on its own picks) within the bf16 prefill tolerance."""
+    token bit-exact against the oracle's sequential-fp32 router; the outputs of all 512 tokens
+    against the oracle's SIMD tier (the reference's order, every unique expert once over its
+    tokens) within the bf16 prefill tolerance, the whole call and every token's row."""
+    import os
     import rabbit_amd.workloads as W
+    from oracle import oracle as O
     from oracle.workload import HostLayer
     import torch
     cfg = W.CONFIGS["c4"]
@@ -336,9 +339,16 @@ def test_moe_prefill_c4_full(ctx, orc):
     got_ids = ids.cpu().numpy().reshape(S, k)
     eids, _ = host.route(x)
     assert np.array_equal(got_ids, eids)
-    sample = np.array([0, 1, 137, 300, 511])
-    exp, _, _ = host.forward(x[sample], simd=True)
-    got = out.cpu().numpy().reshape(S, cfg.hidden)[sample]
+    nthr = O.get_threads()
+    O.set_threads(min(16, os.cpu_count() or 1))  # the box's share of host cores
+    try:
+        exp, _, _ = host.forward(x, simd=True)
+    finally:
+        O.set_threads(nthr)
+    got = out.cpu().numpy().reshape(S, cfg.hidden)
+    exp = np.asarray(exp, np.float32).reshape(S, cfg.hidden)
     err = rel_l2(got, exp)
-    print(f"c4 sample rel_l2={err:.3e}")
+    worst = max(rel_l2(got[t], exp[t]) for t in range(S))
+    print(f"c4 rel_l2={err:.3e}, worst token {worst:.3e}")
     assert err < PREFILL_RTOL
+    assert worst < PREFILL_RTOL
