@@ -60,9 +60,14 @@ constexpr int GDN_MAXR = 16;  // state rows per thread held in registers (float4
 
 // One V head per workgroup of GDN_NT threads. Thread t owns the four columns 4 jq .. 4 jq + 3
 // (jq = t % (d_v / 4)) of rows i = g, g + G, ... (g = t / (d_v / 4), G = GDN_NT / (d_v / 4)); d_v is a
-// multiple of 4 with d_v / 4 dividing GDN_NT and d_v <= GDN_NT, d_k is even and d_k <= GDN_MAXR G. The head's state rows are requested first;
-// q, k, v and the gates are prepared while they arrive.
+// multiple of 4 with d_v / 4 dividing GDN_NT and d_v <= GDN_NT, d_k is even and d_k <= GDN_MAXR G.
+// q, k, v, z and the norm weight are requested first, then the head's state rows; the norms and gates
+// are prepared while the state arrives (loads complete in order, so those issued after the state
+// rows would wait for them).
+// NR > 0: every thread holds exactly NR rows (d_k = NR G), and the row loads are unconditional, so the
+// compiler's waits for the loads issued before them do not also wait for them.
 // act: the conv output after SiLU, [q (key_dim) | k (key_dim) | v (n_v d_v)].
+template <int NR>
 __global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states, const float *__restrict__ act,
                                                      int key_dim, int n_v, int n_k, int d_k, int d_v,
                                                      const float *__restrict__ z, const float *__restrict__ a,
@@ -77,31 +82,55 @@ __global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states,
   const int h = blockIdx.x, t = threadIdx.x;
   const int kh = h / (n_v / n_k);  // key_head_of (gdn.rs:62-65)
   const int jq = t % QN, g = t / QN;
-  const int nr = g < d_k ? (d_k - g + G - 1) / G : 0;
-  float4 *S4 = reinterpret_cast<float4 *>(states + (long)h * d_k * d_v);
-  float4 s[GDN_MAXR];
+  constexpr int MR = NR > 0 ? NR : GDN_MAXR;
+  const int nr = NR > 0 ? NR : g < d_k ? (d_k - g + G - 1) / G : 0;
+  // (clamped indices rather than branches, so that nothing here waits for the state rows)
+  const int ti = min(t, d_k - 1), tj = min(t, d_v - 1);
+  const float q0 = act[kh * d_k + ti], k0 = act[key_dim + kh * d_k + ti], v0 = act[2 * key_dim + h * d_v + tj];
+  const float zj = z[(long)h * d_v + tj], nwj = norm_w[tj];
+  const float ah = a[h], dth = dt_bias[h], alh = a_log[h], bh = b[h];
+  __builtin_amdgcn_sched_barrier(0);  // the state rows are requested only now
+  // this thread's rows: Sp[r * rs] is S[g + G r][4 jq .. 4 jq + 3] (32-bit offsets: the head's state
+  // is d_k d_v < 2^31 floats)
+  float4 *Sp = reinterpret_cast<float4 *>(states + (long)h * d_k * d_v) + g * QN + jq;
+  const int rs = G * QN;
+  float4 s[MR];
 #pragma unroll
-  for (int r = 0; r < GDN_MAXR; r++)
-    if (r < nr) s[r] = S4[(long)(g + G * r) * QN + jq];
-  for (int i = t; i < d_k; i += GDN_NT) {
+  for (int r = 0; r < MR; r++)
+    if (NR > 0 || r < nr) s[r] = Sp[r * rs];
+  // the values loaded first are taken here, before anything could move their loads after the rows'
+  // (threads past d_k or d_v store the same value as the last one)
+  float zv = zj, nw = nwj;
+  asm volatile("" : "+v"(zv), "+v"(nw));
+  qs[ti] = q0;
+  ks[ti] = k0;
+  vs[tj] = v0;
+  for (int i = t + GDN_NT; i < d_k; i += GDN_NT) {
     qs[i] = act[kh * d_k + i];
     ks[i] = act[key_dim + kh * d_k + i];
   }
-  for (int i = t; i < d_v; i += GDN_NT) vs[i] = act[2 * key_dim + h * d_v + i];
   __syncthreads();
   // prepare_qk (gdn.rs:110-118): l2_norm's sequential f32 sum of squares (kimi_linear/ops.rs:34-40)
   // for q on thread 0 and k on thread 64, the decay and write strength on thread 128
   if (t == 0 || t == 64) {
     float *v = t == 0 ? qs : ks;
     float ss = 0.0f;
-    for (int i = 0; i < d_k; i++) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
+    int i = 0;
+    for (; i + 16 <= d_k; i += 16) {  // in order; sixteen LDS reads in flight at a time
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) x[u] = v[i + u];
+#pragma unroll
+      for (int u = 0; u < 16; u++) ss = __fadd_rn(ss, __fmul_rn(x[u], x[u]));
+    }
+    for (; i < d_k; i++) ss = __fadd_rn(ss, __fmul_rn(v[i], v[i]));
     coef[t == 0 ? 0 : 1] = __fdiv_rn(1.0f, fmaxf(rbt_sqrt_rn(ss), 1e-6f));
   } else if (t == 128) {
     // alpha = exp(-exp(a_log) * softplus(a + dt_bias)), softplus(x) = max(x, 0) + ln_1p(exp(-|x|))
-    const float x = __fadd_rn(a[h], dt_bias[h]);
+    const float x = __fadd_rn(ah, dth);
     const float sp = __fadd_rn(fmaxf(x, 0.0f), (float)log1p((double)mx_exp(-fabsf(x))));
-    coef[2] = mx_exp(__fmul_rn(-mx_exp(a_log[h]), sp));
-    coef[3] = mx_sigmoid(b[h]);
+    coef[2] = mx_exp(__fmul_rn(-mx_exp(alh), sp));
+    coef[3] = mx_sigmoid(bh);
   }
   __syncthreads();
   const float qscale = __fdiv_rn(1.0f, rbt_sqrt_rn((float)d_k));
@@ -109,8 +138,8 @@ __global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states,
   // S *= alpha (kda.rs:140-144); c[j] = sum_i k_i S[i, j] (kda.rs:146-151)
   float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int r = 0; r < GDN_MAXR; r++)
-    if (r < nr) {
+  for (int r = 0; r < MR; r++)
+    if (NR > 0 || r < nr) {
       s[r] = make_float4(__fmul_rn(s[r].x, alpha), __fmul_rn(s[r].y, alpha), __fmul_rn(s[r].z, alpha),
                          __fmul_rn(s[r].w, alpha));
       const float ki = __fmul_rn(ks[g + G * r], sk);
@@ -133,15 +162,15 @@ __global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states,
                                 __fsub_rn(v4.w, cj.w));
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int r = 0; r < GDN_MAXR; r++)
-    if (r < nr) {
+  for (int r = 0; r < MR; r++)
+    if (NR > 0 || r < nr) {
       const int i = g + G * r;
       const float bk = __fmul_rn(beta, __fmul_rn(ks[i], sk));
       s[r].x = __fadd_rn(s[r].x, __fmul_rn(bk, dv.x));
       s[r].y = __fadd_rn(s[r].y, __fmul_rn(bk, dv.y));
       s[r].z = __fadd_rn(s[r].z, __fmul_rn(bk, dv.z));
       s[r].w = __fadd_rn(s[r].w, __fmul_rn(bk, dv.w));
-      S4[(long)i * QN + jq] = s[r];
+      Sp[r * rs] = s[r];
       const float qi = __fmul_rn(__fmul_rn(qs[i], sq), qscale);
       o.x = __fadd_rn(o.x, __fmul_rn(qi, s[r].x));
       o.y = __fadd_rn(o.y, __fmul_rn(qi, s[r].y));
@@ -156,22 +185,58 @@ __global__ __launch_bounds__(GDN_NT) void k_gdn_head(float *__restrict__ states,
     vs[t] = oj;
   }
   __syncthreads();
-  // head_output_gate_silu (gdn.rs:122-128): rmsnorm (kimi_linear/ops.rs:46-53, the f64 sum of
-  // squares in order) then * silu(z)
-  if (t == 0) {
+  // head_output_gate_silu (gdn.rs:122-128): rmsnorm (kimi_linear/ops.rs:46-53: an f64 sum of
+  // squares, here per lane of wave 0 then a butterfly; f64 sums of fp32 squares round to the same
+  // fp32 in any order but for rare ties) then * silu(z)
+  if (t < 64) {
     double ms = 0.0;
-    for (int i = 0; i < d_v; i++) ms += (double)vs[i] * (double)vs[i];
-    coef[0] = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)d_v), eps)));
+    for (int i = t; i < d_v; i += 64) ms += (double)vs[i] * (double)vs[i];
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) ms += __shfl_xor(ms, d, 64);
+    if (t == 0) coef[0] = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)d_v), eps)));
   }
   __syncthreads();
   if (t < d_v) {
     const float r = coef[0];
-    const float on = __fmul_rn(vs[t], __fmul_rn(r, norm_w[t]));
-    out[(long)h * d_v + t] = __fmul_rn(on, mx_silu(z[(long)h * d_v + t]));
+    const float on = __fmul_rn(vs[t], __fmul_rn(r, nw));
+    out[(long)h * d_v + t] = __fmul_rn(on, mx_silu(zv));
   }
 }
 
 // ---- GQA --------------------------------------------------------------------------------------
+// sin and cos of an fp32 angle (|x| < 2^22) in fp64, light on registers: x minus the nearest
+// multiple k of pi/2 (Cody and Waite's reduction with pi/2 split into three doubles; the first fma
+// is exact since x - k c1 is a multiple of 2^-52 below 1 in magnitude), then the Taylor series of
+// sin and cos on |r| <= pi/4 + ulp to degree 21 and 22 (truncation error below 2e-25), and the
+// quadrant k mod 4. Rounded to fp32, this gives the fp32 rounding of the exact values, as fp64
+// library calls do, without their large-argument paths.
+__device__ __forceinline__ void mx_sincos(float xf, float &sn, float &cs) {
+  constexpr double c1 = 1.5707963267948966, c2 = 6.123233995736766e-17, c3 = -1.4973849048591698e-33;
+  const double x = xf, k = rint(x * 0.6366197723675814);
+  double r = fma(-k, c1, x);
+  r = fma(-k, c2, r);
+  r = fma(-k, c3, r);
+  const double r2 = r * r;
+  // 1 / n! for n = 0 .. 22 (each factorial is exact in fp64, so each quotient is correctly rounded)
+  constexpr double f[23] = {1.0, 1.0, 1.0 / 2, 1.0 / 6, 1.0 / 24, 1.0 / 120, 1.0 / 720, 1.0 / 5040,
+                            1.0 / 40320, 1.0 / 362880, 1.0 / 3628800, 1.0 / 39916800, 1.0 / 479001600,
+                            1.0 / 6227020800.0, 1.0 / 87178291200.0, 1.0 / 1307674368000.0,
+                            1.0 / 20922789888000.0, 1.0 / 355687428096000.0, 1.0 / 6402373705728000.0,
+                            1.0 / 121645100408832000.0, 1.0 / 2432902008176640000.0,
+                            1.0 / 51090942171709440000.0, 1.0 / 1124000727777607680000.0};
+  // sin r = r sum_{n<=10} (-r^2)^n / (2n+1)!, cos r = sum_{n<=11} (-r^2)^n / (2n)!, by Horner
+  double ps = f[21], pc = -f[22];
+#pragma unroll
+  for (int n = 10; n >= 0; n--) {
+    if (n < 10) ps = (n & 1 ? -f[2 * n + 1] : f[2 * n + 1]) + r2 * ps;
+    pc = (n & 1 ? -f[2 * n] : f[2 * n]) + r2 * pc;
+  }
+  const double sr = r * ps, cr = pc;
+  const int q = (int)((long long)k & 3);
+  sn = (float)(q == 0 ? sr : q == 1 ? cr : q == 2 ? -sr : -cr);
+  cs = (float)(q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr);
+}
+
 // (1 + w) RMSNorm of one head_dim-wide row in LDS (qwen38/ops.rs:25-33: f64 sum of squares in order)
 // and the rotate-half RoPE of its first rope_dim entries (attention.rs:160-172), in place.
 __device__ void gqa_norm_rope(float *v, const float *__restrict__ w, int hd, float eps, int rope_dim, int pos,
@@ -179,7 +244,15 @@ __device__ void gqa_norm_rope(float *v, const float *__restrict__ w, int hd, flo
   const int t = threadIdx.x;
   if (t == 0) {
     double ms = 0.0;
-    for (int i = 0; i < hd; i++) ms += (double)v[i] * (double)v[i];
+    int i = 0;
+    for (; i + 16 <= hd; i += 16) {  // in order; sixteen LDS reads in flight at a time
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) x[u] = v[i + u];
+#pragma unroll
+      for (int u = 0; u < 16; u++) ms += (double)x[u] * (double)x[u];
+    }
+    for (; i < hd; i++) ms += (double)v[i] * (double)v[i];
     rs[0] = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)hd), eps)));
   }
   __syncthreads();
@@ -191,7 +264,8 @@ __device__ void gqa_norm_rope(float *v, const float *__restrict__ w, int hd, flo
     const float e = __fdiv_rn(__fmul_rn(-2.0f, (float)jj), (float)rope_dim);
     const float inv = (float)pow((double)theta, (double)e);
     const float ang = __fmul_rn((float)pos, inv);
-    const float sn = (float)sin((double)ang), cs = (float)cos((double)ang);
+    float sn, cs;
+    mx_sincos(ang, sn, cs);
     const float x0 = v[jj], x1 = v[jj + half];
     v[jj] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
     v[jj + half] = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(x0, sn));
@@ -365,22 +439,31 @@ __global__ __launch_bounds__(256) void k_gqa_combine(const float *__restrict__ p
   __syncthreads();
   if (t == 0) {
     float L = 0.0f;
-    for (int c = 0; c < nch; c++) L = __fadd_rn(L, lc[c]);
+    int c = 0;
+    for (; c + 16 <= nch; c += 16) {  // in order; sixteen LDS reads in flight at a time
+      float x[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) x[u] = lc[c + u];
+#pragma unroll
+      for (int u = 0; u < 16; u++) L = __fadd_rn(L, x[u]);
+    }
+    for (; c < nch; c++) L = __fadd_rn(L, lc[c]);
     tot[0] = L;
   }
   __syncthreads();
   const float L = tot[0];
   for (int d = t; d < hd; d += 256) {
-    // the chunks' terms in chunk order; their loads issued four at a time
+    // the chunks' terms in chunk order; their loads issued sixteen at a time (each batch waits
+    // one round trip to L2)
+    constexpr int CB = 16;
     float acc = 0.0f;
     int c = 0;
-    for (; c + 4 <= nch; c += 4) {
-      const float x0 = P0[c * stride + 4 + d], x1 = P0[(c + 1) * stride + 4 + d];
-      const float x2 = P0[(c + 2) * stride + 4 + d], x3 = P0[(c + 3) * stride + 4 + d];
-      acc = __fadd_rn(acc, __fmul_rn(x0, fc[c]));
-      acc = __fadd_rn(acc, __fmul_rn(x1, fc[c + 1]));
-      acc = __fadd_rn(acc, __fmul_rn(x2, fc[c + 2]));
-      acc = __fadd_rn(acc, __fmul_rn(x3, fc[c + 3]));
+    for (; c + CB <= nch; c += CB) {
+      float xv[CB];
+#pragma unroll
+      for (int u = 0; u < CB; u++) xv[u] = P0[(long)(c + u) * stride + 4 + d];
+#pragma unroll
+      for (int u = 0; u < CB; u++) acc = __fadd_rn(acc, __fmul_rn(xv[u], fc[c + u]));
     }
     for (; c < nch; c++) acc = __fadd_rn(acc, __fmul_rn(P0[c * stride + 4 + d], fc[c]));
     const float g = qg[(long)h * 2 * hd + hd + d];
@@ -402,7 +485,10 @@ hipError_t launch_gdn(const Ctx &c, float *conv_hist, const float *conv_w, int K
   const int key_dim = n_k * d_k, C = 2 * key_dim + n_v * d_v;
   launch_k(c, k_gdn_conv, dim3((C + 255) / 256), dim3(256), conv_hist, qkv_pre, conv_w, C, K, act);
   const unsigned lds = (unsigned)((2 * d_k + d_v + 4 * GDN_NT) * sizeof(float));
-  launch_ks(c, k_gdn_head, dim3(n_v), dim3(GDN_NT), lds, states, (const float *)act, key_dim, n_v, n_k, d_k, d_v, z, a,
+  const int G = GDN_NT / (d_v / 4);
+  auto head = d_k == 8 * G ? k_gdn_head<8> : d_k == 4 * G ? k_gdn_head<4> : d_k == 16 * G ? k_gdn_head<16>
+              : d_k == 2 * G ? k_gdn_head<2> : k_gdn_head<0>;
+  launch_ks(c, head, dim3(n_v), dim3(GDN_NT), lds, states, (const float *)act, key_dim, n_v, n_k, d_k, d_v, z, a,
             b, a_log, dt_bias, norm_w, eps, out);
   return hipGetLastError();
 }

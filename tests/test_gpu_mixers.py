@@ -21,11 +21,14 @@ def _t(a):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
 
 
-@pytest.mark.parametrize("n_v,n_k,d_k,d_v,steps", [(4, 2, 16, 8, 6), (8, 8, 32, 64, 4), (128, 16, 128, 128, 4)])
-def test_gdn_step_matches_oracle(ctx, orc, n_v, n_k, d_k, d_v, steps):
-    """Small shapes and Qwen 3.8's (128 V heads over 16 K heads, 128 x 128 state, conv_dim 20480)."""
+@pytest.mark.parametrize("n_v,n_k,d_k,d_v,steps,K", [(4, 2, 16, 8, 6, 4), (8, 8, 32, 64, 4, 4),
+                                                    (128, 16, 128, 128, 4, 4), (8, 2, 32, 64, 5, 3),
+                                                    (16, 4, 64, 512, 3, 4)])
+def test_gdn_step_matches_oracle(ctx, orc, n_v, n_k, d_k, d_v, steps, K):
+    """Small shapes and Qwen 3.8's (128 V heads over 16 K heads, 128 x 128 state, conv_dim 20480), with
+    conv kernels 4 and 3; the head kernel's row count per thread is fixed at 8 (Qwen 3.8) and 16
+    (head_v_dim 512) and runtime in the other cases."""
     import torch
-    K = 4
     rng = np.random.default_rng(n_v * 7 + d_k)
     key_dim = n_k * d_k
     conv_dim = 2 * key_dim + n_v * d_v
@@ -94,10 +97,12 @@ def test_gqa_step_matches_oracle(ctx, orc, n_heads, n_kv, hd, rope_dim, position
     print(f"gqa {n_heads}/{n_kv}x{hd}: worst rel-L2 {worst:.2e}")
 
 
-def test_gqa_step_long_cache(ctx, orc):
-    """Qwen 3.8's shape at positions 2000..2002 of a prefilled cache (32 score chunks)."""
-    worst = _gqa_case(ctx, orc, 64, 4, 256, 64, 3, prefill=2000, seed=5)
-    print(f"gqa long cache: worst rel-L2 {worst:.2e}")
+@pytest.mark.parametrize("prefill", [2000, 30000])
+def test_gqa_step_long_cache(ctx, orc, prefill):
+    """Qwen 3.8's shape at positions prefill..prefill+2 of a prefilled cache (32 and 469 score chunks;
+    RoPE angles up to 30002 radians)."""
+    worst = _gqa_case(ctx, orc, 64, 4, 256, 64, 3, prefill=prefill, seed=5)
+    print(f"gqa long cache at {prefill}: worst rel-L2 {worst:.2e}")
 
 
 def test_mixer_errors(ctx, orc):
