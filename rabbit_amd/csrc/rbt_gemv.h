@@ -495,9 +495,12 @@ __device__ __forceinline__ void proj1_body(PjLds &L, const uint8_t *__restrict__
   // the staging below waits for x only, not for the weights issued after it
   constexpr int XV = PJ_MAXC / 4 / (64 * NW);
   const int n4 = cols / 4;
-  float4 xv4[XV];
+  float4 xv4[XV], nw4[NORM ? XV : 1];
 #pragma unroll
   for (int k = 0; k < XV; k++) xv4[k] = ((const rbt_gf4 *)x)[min(t + 64 * NW * k, n4 - 1)];
+  if (NORM)  // the norm's weights too (loaded after the rows, waiting for them would wait for the rows)
+#pragma unroll
+    for (int k = 0; k < XV; k++) nw4[k] = ((const rbt_gf4 *)nw)[min(t + 64 * NW * k, n4 - 1)];
   __builtin_amdgcn_sched_barrier(0);
   // the wave's rows (clamped: a wave without rows re-reads row 0 and stores nothing)
   rbt_u4 wr[RW][NB];
@@ -547,7 +550,7 @@ __device__ __forceinline__ void proj1_body(PjLds &L, const uint8_t *__restrict__
     for (int k = 0; k < XV; k++) {
       const int i = t + 64 * NW * k;
       if (i < n4) {
-        const float4 g = ((const rbt_gf4 *)nw)[i];
+        const float4 g = nw4[k];
         float4 v = xv4[k];
         v.x = __fmul_rn(v.x, __fmul_rn(r, g.x));
         v.y = __fmul_rn(v.y, __fmul_rn(r, g.y));
