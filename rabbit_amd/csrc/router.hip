@@ -2388,7 +2388,7 @@ __device__ __forceinline__ void norm1p_chunks(LgLds<NR> &L, float4 (&xv)[RT_MAXH
 // key record). The rows' loads are issued together, then the rows are reduced two at a time.
 // With nw (the MoE sublayer), P.x is the raw token and every workgroup first normalises it
 // (rmsnorm_1p with weights nw, eps) for its rows; workgroup 0 writes the normalised token to xn.
-template <int RPW>
+template <int RPW, bool NORM>
 __device__ __forceinline__ void router1_body(LgLds<RPW == 1 ? 1 : 2> &L, const SelParams &P,
                                              const float *__restrict__ sgate, double *__restrict__ mid,
                                              double *__restrict__ bnd, float *__restrict__ sh_scale,
@@ -2399,14 +2399,14 @@ __device__ __forceinline__ void router1_body(LgLds<RPW == 1 ? 1 : 2> &L, const S
   const int H = P.H, E = P.E, nch = H / 1024;
   if (sgate == nullptr && b == 0 && t == 0) sh_scale[0] = 1.0f;
   const int Rn = E + (sgate != nullptr ? 1 : 0), r0 = RPW * b;
-  if (r0 >= Rn && !(nw != nullptr && b == 0)) return;
+  if (r0 >= Rn && !(NORM && b == 0)) return;
   const float4 *x4 = reinterpret_cast<const float4 *>(P.x);
   float4 xv[MC], w[RPW][MC], wv[MC];
   // the token (and the norm's weights) first: the memory counter retires loads in issue order, so
   // the norm waits for them only, not for the rows' loads behind them
 #pragma unroll
   for (int c = 0; c < MC; c++) xv[c] = x4[min(c, nch - 1) * 256 + t];
-  if (nw != nullptr) {
+  if (NORM) {
     const float4 *n4 = reinterpret_cast<const float4 *>(nw);
 #pragma unroll
     for (int c = 0; c < MC; c++) wv[c] = n4[min(c, nch - 1) * 256 + t];
@@ -2425,7 +2425,10 @@ __device__ __forceinline__ void router1_body(LgLds<RPW == 1 ? 1 : 2> &L, const S
       w[j][c] = make_float4(v[0], v[1], v[2], v[3]);
     }
   }
-  if (nw != nullptr) {
+  // (the norm below is kept after the rows' loads: placed before them, its use of the weights
+  // made the rows wait for the token and the weights to land)
+  __builtin_amdgcn_sched_barrier(0);
+  if (NORM) {
     norm1p_chunks<NR>(L, xv, wv, H, eps);
     if (b == 0) {
 #pragma unroll
@@ -2447,13 +2450,13 @@ __device__ __forceinline__ void router1_body(LgLds<RPW == 1 ? 1 : 2> &L, const S
   if (sgate != nullptr && r0 <= E && E < r0 + RPW && t == 0) sh_scale[0] = sigmoid_ref(__double2float_rn(mid[E]));
 }
 
-template <int RPW>
+template <int RPW, bool NORM>
 __global__ __launch_bounds__(256) void k_router1(SelParams P, const float *__restrict__ sgate,
                                                  double *__restrict__ mid, double *__restrict__ bnd,
                                                  float *__restrict__ sh_scale, KeyRec *__restrict__ rec,
                                                  const float *__restrict__ nw, float eps, float *__restrict__ xn) {
   __shared__ LgLds<RPW == 1 ? 1 : 2> L;
-  router1_body<RPW>(L, P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn, blockIdx.x);
+  router1_body<RPW, NORM>(L, P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn, blockIdx.x);
 }
 
 // One token of K3's latent MoE: the router rows' key records (router1_body, workgroups 0 .. E - 1)
@@ -2474,7 +2477,7 @@ __global__ __launch_bounds__(256) void k_router1_proj(SelParams P, double *__res
   if ((int)blockIdx.x >= P.E)
     proj1_body<I4G, false, NB, 4, 2>(U.pj, pd, ps, P.x, P.H, mh, xl, nullptr, 0.0f, blockIdx.x - P.E, npj);
   else
-    router1_body<1>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x);
+    router1_body<1, false>(U.lg, P, nullptr, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr, blockIdx.x);
 }
 
 // Certified logits of a decode batch, one (row, token) per workgroup: a smaller LDS footprint than
@@ -2925,9 +2928,11 @@ hipError_t launch_router1(const Ctx &c, const RouterArgs &a, const float *sgate,
   // critical path: C1's 513 rows take 9.5 us as 257 x 2 rows, 11.8 us as 129 x 4)
   const int rn = a.E + (sgate ? 1 : 0);
   if (rn <= 4 * c.num_cu)  // four one-row workgroups fit on a CU
-    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn);
+    launch_k(c, nw ? k_router1<1, true> : k_router1<1, false>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec,
+             nw, eps, xn);
   else
-    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nw, eps, xn);
+    launch_k(c, nw ? k_router1<2, true> : k_router1<2, false>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd,
+             sh_scale, rec, nw, eps, xn);
   return hipGetLastError();
 }
 
@@ -2935,8 +2940,8 @@ hipError_t launch_router1_latent(const Ctx &c, const RouterArgs &a, double *mid,
                                  void *rec_buf, int mh, int I) {
   if (!router1_latent_ok(a, c.num_cu, mh, I)) return hipErrorInvalidValue;
   const SelParams P = sel_params(a);
-  launch_k(c, k_router1<1>, dim3(a.E), dim3(256), P, nullptr, mid, bnd, sh_scale, reinterpret_cast<KeyRec *>(rec_buf),
-           nullptr, 0.0f, nullptr);
+  launch_k(c, k_router1<1, false>, dim3(a.E), dim3(256), P, nullptr, mid, bnd, sh_scale,
+           reinterpret_cast<KeyRec *>(rec_buf), nullptr, 0.0f, nullptr);
   return hipGetLastError();
 }
 
@@ -3058,9 +3063,9 @@ hipError_t launch_router1_any(const Ctx &c, const RouterArgs &a, double *mid, do
   KeyRec *rec = reinterpret_cast<KeyRec *>(rec_buf);
   const int rn = a.E + (sgate ? 1 : 0);
   if (rn <= 4 * c.num_cu)
-    launch_k(c, k_router1<1>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr);
+    launch_k(c, k_router1<1, false>, dim3(rn), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f, nullptr);
   else
-    launch_k(c, k_router1<2>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f,
+    launch_k(c, k_router1<2, false>, dim3((rn + 1) / 2), dim3(256), P, sgate, mid, bnd, sh_scale, rec, nullptr, 0.0f,
              nullptr);
   return hipGetLastError();
 }
