@@ -25,26 +25,6 @@ namespace rbt {
 
 constexpr int XV_W = 8;  // waves per workgroup (one item each)
 
-// The routing weight of expert `eid` for the single token (its first matching slot among ids[0..k),
-// glm52/moe.rs:465-470), or false when the token did not pick it. Wave-uniform.
-__device__ __forceinline__ bool single_weight(const int32_t *__restrict__ ids, const float *__restrict__ wts, int k,
-                                              int eid, float *wv) {
-  const int lane = threadIdx.x & 63;
-  bool hit = false;
-  int first = 64;
-  for (int j0 = 0; j0 < k; j0 += 64) {
-    const int j = j0 + lane;
-    const unsigned long long m = __ballot(j < k && ids[min(j, k - 1)] == eid);
-    if (m != 0) {
-      first = j0 + __ffsll(m) - 1;
-      hit = true;
-      break;
-    }
-  }
-  if (hit) *wv = wts[first];
-  return hit;
-}
-
 template <int NCH, int KS, bool GU, bool PIN>
 __global__ __launch_bounds__(64 * XV_W) void k_xgemv1(const uint8_t *__restrict__ d0, const uint8_t *__restrict__ s0,
                                                       const uint8_t *__restrict__ d1, const uint8_t *__restrict__ s1,
@@ -61,9 +41,13 @@ __global__ __launch_bounds__(64 * XV_W) void k_xgemv1(const uint8_t *__restrict_
   __shared__ float part[TPW][KS][4][NM];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, g = lane >> 4, col = lane & 15;
   const int rho = col >> 2, kap = col & 3;
-  // apply_single_expert: the token's weight for this expert (nothing to do if it did not pick it)
-  float wv = 1.0f;
-  if (ids != nullptr && !single_weight(ids, wts, k, eid, &wv)) return;
+  // apply_single_expert: lane j's routing slot (k <= 64) is requested first, with everything else,
+  // and looked at only after the products, before anything is stored (a token that did not pick the
+  // expert returns there): the check costs no trip to memory of its own. Without ids the loads read
+  // a valid address and go unused.
+  const int jl = min(lane, max(k, 1) - 1);
+  const int32_t idl = *(ids != nullptr ? ids + jl : reinterpret_cast<const int32_t *>(xin));
+  const float wtl = *(ids != nullptr ? wts + jl : reinterpret_cast<const float *>(xin));
   const int tile = blockIdx.x * TPW + w / KS, kp = w % KS;
   const int c0 = kp * NCH / KS, c1 = (kp + 1) * NCH / KS;  // this item's steps
   const long row0 = 4L * min(tile, O / 4 - 1);
@@ -137,6 +121,11 @@ __global__ __launch_bounds__(64 * XV_W) void k_xgemv1(const uint8_t *__restrict_
       for (int m = 0; m < NM; m++) xmma_s(wd[m][c], xe8m0((sd[m][c] >> sh) & 0xFFu), B, acc[m]);
     }
   }
+  // the token's weight for this expert: its first slot that holds eid (glm52/moe.rs:465-470), the same
+  // in every wave
+  const unsigned long long hit = __ballot(lane < k && idl == eid);
+  if (ids != nullptr && hit == 0) return;  // not picked: nothing to do
+  const float wv = ids != nullptr ? __shfl(wtl, (int)__ffsll(hit) - 1, 64) : 1.0f;
 #pragma unroll
   for (int m = 0; m < NM; m++) {
     const float v = row_dot(acc[m], col);
@@ -230,7 +219,7 @@ hipError_t launch_xexpert1(const Ctx &c, const RbtExpertDev &J, const float *x, 
                            const float *wts, int k, int eid, __bf16 *hp, float *out, const RbtAct &act) {
   if (!xexpert1_ok((size_t)d, (size_t)i, c.num_cu) || !J.gd || !J.ud || !J.dd || !J.gs || !J.us || !J.ds ||
       ((uintptr_t)x | (uintptr_t)J.gd | (uintptr_t)J.ud | (uintptr_t)J.dd) % 16 != 0 ||
-      ((uintptr_t)J.gs | (uintptr_t)J.us | (uintptr_t)J.ds) % 4 != 0 || k < 1)
+      ((uintptr_t)J.gs | (uintptr_t)J.us | (uintptr_t)J.ds) % 4 != 0 || k < 1 || k > 64)
     return hipErrorInvalidValue;
   const uint8_t *gs = (const uint8_t *)J.gs, *us = (const uint8_t *)J.us, *ds = (const uint8_t *)J.ds;
   const int ksg = xgemv1_ks(i, c.num_cu), ksd = xgemv1_ks(d, c.num_cu);
