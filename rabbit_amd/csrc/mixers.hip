@@ -237,66 +237,89 @@ __device__ __forceinline__ void mx_sincos(float xf, float &sn, float &cs) {
   cs = (float)(q == 0 ? cr : q == 1 ? -sr : q == 2 ? -cr : sr);
 }
 
-// (1 + w) RMSNorm of one head_dim-wide row in LDS (qwen38/ops.rs:25-33: f64 sum of squares in order)
-// and the rotate-half RoPE of its first rope_dim entries (attention.rs:160-172), in place.
-__device__ void gqa_norm_rope(float *v, const float *__restrict__ w, int hd, float eps, int rope_dim, int pos,
-                              float theta, float *rs) {
-  const int t = threadIdx.x;
-  if (t == 0) {
-    double ms = 0.0;
-    int i = 0;
-    for (; i + 16 <= hd; i += 16) {  // in order; sixteen LDS reads in flight at a time
-      float x[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++) x[u] = v[i + u];
-#pragma unroll
-      for (int u = 0; u < 16; u++) ms += (double)x[u] * (double)x[u];
-    }
-    for (; i < hd; i++) ms += (double)v[i] * (double)v[i];
-    rs[0] = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)hd), eps)));
-  }
-  __syncthreads();
-  const float r = rs[0];
-  for (int i = t; i < hd; i += blockDim.x) v[i] = __fmul_rn(v[i], __fmul_rn(r, __fadd_rn(1.0f, w[i])));
-  __syncthreads();
-  const int half = rope_dim / 2;
-  for (int jj = t; jj < half; jj += blockDim.x) {
-    const float e = __fdiv_rn(__fmul_rn(-2.0f, (float)jj), (float)rope_dim);
-    const float inv = (float)pow((double)theta, (double)e);
-    const float ang = __fmul_rn((float)pos, inv);
-    float sn, cs;
-    mx_sincos(ang, sn, cs);
-    const float x0 = v[jj], x1 = v[jj + half];
-    v[jj] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-    v[jj + half] = __fadd_rn(__fmul_rn(x1, cs), __fmul_rn(x0, sn));
-  }
-  __syncthreads();
-}
-
-// Workgroups [0, n_heads): query heads -> qp [n_heads, hd]; [n_heads, n_heads + n_kv): KV heads ->
-// cache row pos. blockDim >= 64, hd <= 1024.
+// One workgroup of 256 threads per head: workgroups [0, n_heads) take the query heads -> qp
+// [n_heads, hd]; [n_heads, n_heads + n_kv) the KV heads -> cache row pos. Each head's row gets the
+// (1 + w) RMSNorm (qwen38/ops.rs:25-33: f64 sum of squares in order) and the rotate-half RoPE of its
+// first rope_dim entries (attention.rs:160-172). NPT = entries per thread (hd <= 256 NPT).
+// Every global load is issued at entry (the row, the norm's weights and, for KV heads, the value
+// row; clamped indices, so none sits behind a branch), and the rotation's sines and cosines, which
+// depend on nothing loaded, are computed while those loads travel.
+template <int NPT>
 __global__ __launch_bounds__(256) void k_gqa_prep(const float *__restrict__ qg, const float *__restrict__ kin,
                                                   const float *__restrict__ vin, int n_heads, int n_kv, int hd,
                                                   const float *__restrict__ qn, const float *__restrict__ kn,
                                                   float eps, int rope_dim, int pos, float theta,
                                                   float *__restrict__ qp, float *__restrict__ kc,
                                                   float *__restrict__ vc) {
+  constexpr int NP = (NPT + 1) / 2;  // rotated pairs per thread (rope_dim / 2 <= hd / 2 <= 128 NPT)
   extern __shared__ float row[];
   __shared__ float rs[1];
   const int b = blockIdx.x, t = threadIdx.x;
   const bool query = b < n_heads;
-  const int kvh = b - n_heads;
+  const int kvh = query ? 0 : b - n_heads;  // query heads load KV head 0's value row and drop it
   const float *src = query ? qg + (long)b * 2 * hd : kin + (long)kvh * hd;
-  for (int i = t; i < hd; i += blockDim.x) row[i] = src[i];
+  const float *w = query ? qn : kn;
+  const float *vr = vin + (long)kvh * hd;
+  float xr[NPT], wr[NPT], vv[NPT];
+#pragma unroll
+  for (int k = 0; k < NPT; k++) xr[k] = src[min(t + 256 * k, hd - 1)];
+#pragma unroll
+  for (int k = 0; k < NPT; k++) wr[k] = w[min(t + 256 * k, hd - 1)];
+#pragma unroll
+  for (int k = 0; k < NPT; k++) vv[k] = vr[min(t + 256 * k, hd - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const int half = rope_dim / 2;
+  float sn[NP], cs[NP];
+#pragma unroll
+  for (int k = 0; k < NP; k++) {
+    const int jj = min(t + 256 * k, max(half, 1) - 1);
+    const float e = __fdiv_rn(__fmul_rn(-2.0f, (float)jj), (float)max(rope_dim, 2));
+    const float inv = (float)pow((double)theta, (double)e);
+    mx_sincos(__fmul_rn((float)pos, inv), sn[k], cs[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < NPT; k++)
+    if (t + 256 * k < hd) row[t + 256 * k] = xr[k];
   __syncthreads();
-  gqa_norm_rope(row, query ? qn : kn, hd, eps, rope_dim, pos, theta, rs);
+  if (t == 0) {
+    double ms = 0.0;
+    int i = 0;
+    for (; i + 32 <= hd; i += 32) {  // in order; 32 LDS reads in flight at a time
+      float x[32];
+#pragma unroll
+      for (int u = 0; u < 32; u++) x[u] = row[i + u];
+#pragma unroll
+      for (int u = 0; u < 32; u++) ms += (double)x[u] * (double)x[u];
+    }
+    for (; i < hd; i++) ms += (double)row[i] * (double)row[i];
+    rs[0] = __fdiv_rn(1.0f, rbt_sqrt_rn(__fadd_rn((float)(ms / (double)hd), eps)));
+  }
+  __syncthreads();
+  const float r = rs[0];
+#pragma unroll
+  for (int k = 0; k < NPT; k++)
+    if (t + 256 * k < hd) row[t + 256 * k] = __fmul_rn(xr[k], __fmul_rn(r, __fadd_rn(1.0f, wr[k])));
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < NP; k++) {
+    const int jj = t + 256 * k;
+    if (jj < half) {
+      const float x0 = row[jj], x1 = row[jj + half];
+      row[jj] = __fsub_rn(__fmul_rn(x0, cs[k]), __fmul_rn(x1, sn[k]));
+      row[jj + half] = __fadd_rn(__fmul_rn(x1, cs[k]), __fmul_rn(x0, sn[k]));
+    }
+  }
+  __syncthreads();
   const long kw = (long)n_kv * hd;
-  if (query) {
-    for (int i = t; i < hd; i += blockDim.x) qp[(long)b * hd + i] = row[i];
-  } else {
-    for (int i = t; i < hd; i += blockDim.x) {
+#pragma unroll
+  for (int k = 0; k < NPT; k++) {
+    const int i = t + 256 * k;
+    if (i >= hd) break;
+    if (query) {
+      qp[(long)b * hd + i] = row[i];
+    } else {
       kc[(long)pos * kw + (long)kvh * hd + i] = row[i];
-      vc[(long)pos * kw + (long)kvh * hd + i] = vin[(long)kvh * hd + i];
+      vc[(long)pos * kw + (long)kvh * hd + i] = vv[k];
     }
   }
 }
@@ -509,8 +532,9 @@ hipError_t launch_gqa(const Ctx &c, const float *qg, const float *k, const float
   if (!gqa_ok(n_heads, n_kv, hd, rope_dim) || pos < 0) return hipErrorInvalidValue;
   const int P = pos + 1, nch = (P + GQA_CHUNK - 1) / GQA_CHUNK;
   if ((size_t)nch * 2 * sizeof(float) > 48 * 1024) return hipErrorInvalidValue;  // the combine's chunk scales
-  launch_ks(c, k_gqa_prep, dim3(n_heads + n_kv), dim3(256), (unsigned)(hd * sizeof(float)), qg, k, v, n_heads, n_kv,
-            hd, qn, kn, eps, rope_dim, pos, theta, qp, kc, vc);
+  auto prep = hd <= 256 ? k_gqa_prep<1> : hd <= 512 ? k_gqa_prep<2> : k_gqa_prep<4>;
+  launch_ks(c, prep, dim3(n_heads + n_kv), dim3(256), (unsigned)(hd * sizeof(float)), qg, k, v, n_heads, n_kv, hd,
+            qn, kn, eps, rope_dim, pos, theta, qp, kc, vc);
   launch_k(c, k_gqa_chunk, dim3(n_kv, nch), dim3(256), (const float *)qp, (const float *)kc, (const float *)vc, P,
            n_heads, n_kv, hd, scale, part);
   launch_ks(c, k_gqa_combine, dim3(n_heads), dim3(256), (unsigned)(2 * nch * sizeof(float)), (const float *)part, qg,

@@ -89,18 +89,22 @@ def _gqa_case(ctx, orc, n_heads, n_kv, hd, rope_dim, positions, prefill=0, seed=
     return worst
 
 
-@pytest.mark.parametrize("n_heads,n_kv,hd,rope_dim,positions", [(8, 2, 64, 16, 9), (64, 4, 256, 64, 70)])
+@pytest.mark.parametrize("n_heads,n_kv,hd,rope_dim,positions", [(8, 2, 64, 16, 9), (64, 4, 256, 64, 70),
+                                                               (8, 2, 512, 320, 5), (4, 1, 1024, 1024, 3),
+                                                               (4, 2, 128, 0, 3)])
 def test_gqa_step_matches_oracle(ctx, orc, n_heads, n_kv, hd, rope_dim, positions):
     """Positions 0..positions-1 from an empty cache (70 positions: two score chunks); the second case is
-    Qwen 3.8's shape (64 query heads over 4 KV heads, head_dim 256, 64 rotated dims, theta 1e7)."""
+    Qwen 3.8's shape (64 query heads over 4 KV heads, head_dim 256, 64 rotated dims, theta 1e7); head
+    dims 512 and 1024 take two and four entries per thread (all 1024 rotated), and rope_dim 0 none."""
     worst = _gqa_case(ctx, orc, n_heads, n_kv, hd, rope_dim, positions)
     print(f"gqa {n_heads}/{n_kv}x{hd}: worst rel-L2 {worst:.2e}")
 
 
-@pytest.mark.parametrize("prefill", [2000, 30000])
+@pytest.mark.parametrize("prefill", [2000, 4000, 6200, 30000])
 def test_gqa_step_long_cache(ctx, orc, prefill):
-    """Qwen 3.8's shape at positions prefill..prefill+2 of a prefilled cache (32 and 469 score chunks;
-    RoPE angles up to 30002 radians)."""
+    """Qwen 3.8's shape at positions prefill..prefill+2 of a prefilled cache (32, 63, 97 and 469
+    score chunks: the combine's sixteen-chunk batches with and without a remainder, and more chunks
+    than threads; RoPE angles up to 30002 radians)."""
     worst = _gqa_case(ctx, orc, 64, 4, 256, 64, 3, prefill=prefill, seed=5)
     print(f"gqa long cache at {prefill}: worst rel-L2 {worst:.2e}")
 
