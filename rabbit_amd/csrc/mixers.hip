@@ -39,20 +39,39 @@ __device__ __forceinline__ float mx_sigmoid(float x) { return __fdiv_rn(1.0f, __
 
 // ---- Gated DeltaNet --------------------------------------------------------------------------
 // hist [C, K - 1] oldest first, w [C, K]: y[c] = silu(sum_t w[c,t] hist[c,t] + w[c,K-1] x[c]).
+// KT: the kernel size when it is known at compile time (its loads then all go out together, one
+// wait), 0 for any K.
+template <int KT>
 __global__ __launch_bounds__(256) void k_gdn_conv(float *__restrict__ hist, const float *__restrict__ x,
                                                   const float *__restrict__ w, int C, int K, float *__restrict__ y) {
   const int c = blockIdx.x * 256 + threadIdx.x;
   if (c >= C) return;
-  const int hl = K - 1;
+  const int hl = (KT > 0 ? KT : K) - 1;
   float *h = hist + (long)c * hl;
-  const float *wc = w + (long)c * K;
-  const float xc = x[c];
+  const float *wc = w + (long)c * (hl + 1);
   float acc = 0.0f;
-  for (int t = 0; t < hl; t++) acc = __fadd_rn(acc, __fmul_rn(wc[t], h[t]));
-  acc = __fadd_rn(acc, __fmul_rn(wc[hl], xc));
-  for (int t = 0; t + 1 < hl; t++) h[t] = h[t + 1];
-  if (hl > 0) h[hl - 1] = xc;
-  y[c] = mx_silu(acc);
+  if constexpr (KT > 0) {
+    float wv[KT], hv[KT > 1 ? KT - 1 : 1];
+#pragma unroll
+    for (int t = 0; t < KT; t++) wv[t] = wc[t];
+#pragma unroll
+    for (int t = 0; t < KT - 1; t++) hv[t] = h[t];
+    const float xc = x[c];
+#pragma unroll
+    for (int t = 0; t < KT - 1; t++) acc = __fadd_rn(acc, __fmul_rn(wv[t], hv[t]));
+    acc = __fadd_rn(acc, __fmul_rn(wv[KT - 1], xc));
+#pragma unroll
+    for (int t = 0; t + 1 < KT - 1; t++) h[t] = hv[t + 1];
+    if (KT > 1) h[KT - 2] = xc;
+    y[c] = mx_silu(acc);
+  } else {
+    const float xc = x[c];
+    for (int t = 0; t < hl; t++) acc = __fadd_rn(acc, __fmul_rn(wc[t], h[t]));
+    acc = __fadd_rn(acc, __fmul_rn(wc[hl], xc));
+    for (int t = 0; t + 1 < hl; t++) h[t] = h[t + 1];
+    if (hl > 0) h[hl - 1] = xc;
+    y[c] = mx_silu(acc);
+  }
 }
 
 constexpr int GDN_NT = 512;   // threads per head workgroup
@@ -506,7 +525,8 @@ hipError_t launch_gdn(const Ctx &c, float *conv_hist, const float *conv_w, int K
                       float *act, float *out) {
   if (!gdn_ok(n_v, n_k, d_k, d_v) || K < 1) return hipErrorInvalidValue;
   const int key_dim = n_k * d_k, C = 2 * key_dim + n_v * d_v;
-  launch_k(c, k_gdn_conv, dim3((C + 255) / 256), dim3(256), conv_hist, qkv_pre, conv_w, C, K, act);
+  launch_k(c, K == 4 ? k_gdn_conv<4> : K == 3 ? k_gdn_conv<3> : K == 2 ? k_gdn_conv<2> : k_gdn_conv<0>,
+           dim3((C + 255) / 256), dim3(256), conv_hist, qkv_pre, conv_w, C, K, act);
   const unsigned lds = (unsigned)((2 * d_k + d_v + 4 * GDN_NT) * sizeof(float));
   const int G = GDN_NT / (d_v / 4);
   auto head = d_k == 8 * G ? k_gdn_head<8> : d_k == 4 * G ? k_gdn_head<4> : d_k == 16 * G ? k_gdn_head<16>

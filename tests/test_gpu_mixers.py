@@ -23,11 +23,13 @@ def _t(a):
 
 @pytest.mark.parametrize("n_v,n_k,d_k,d_v,steps,K", [(4, 2, 16, 8, 6, 4), (8, 8, 32, 64, 4, 4),
                                                     (128, 16, 128, 128, 4, 4), (8, 2, 32, 64, 5, 3),
-                                                    (16, 4, 64, 512, 3, 4)])
+                                                    (16, 4, 64, 512, 3, 4), (4, 2, 16, 8, 5, 2),
+                                                    (4, 2, 16, 8, 7, 5)])
 def test_gdn_step_matches_oracle(ctx, orc, n_v, n_k, d_k, d_v, steps, K):
     """Small shapes and Qwen 3.8's (128 V heads over 16 K heads, 128 x 128 state, conv_dim 20480), with
-    conv kernels 4 and 3; the head kernel's row count per thread is fixed at 8 (Qwen 3.8) and 16
-    (head_v_dim 512) and runtime in the other cases."""
+    conv kernels 4, 3 and 2 (compiled for their size) and 5 (the conv kernel for any size); the head
+    kernel's row count per thread is fixed at 8 (Qwen 3.8) and 16 (head_v_dim 512) and runtime in the
+    other cases."""
     import torch
     rng = np.random.default_rng(n_v * 7 + d_k)
     key_dim = n_k * d_k
